@@ -1,0 +1,300 @@
+"""Benchmark of the nearest-neighbour hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
+
+Headline: one step = Chamfer forward + backward
+(ChamferDistance('mean') and its gradient) at B=32, N=M=8192, float32, inputs
+resident in HBM.  value = directed pair-distances per second (2*B*N*M per
+step) in G/s.  The roofline object covers the dominant kernel (the Chamfer
+forward kernel, timed with HIP events on the stream it runs on, inside the
+timed region): 9 FLOP per directed pair against the 157.3 TFLOP/s FP32
+vector peak.  The CPU baseline is the reference's CPU formulation of Chamfer
+(tests/test_chamfer.py:11-25 of the reference: broadcast, square, sum, min,
+plus autograd backward), chunked, on a bounded sample, on the host's cores.
+
+Secondary lines (other BASELINE configs, reported under "secondary"):
+knn_points c3, FPS c4 (ms), gather_points c4 fwd/bwd (GB/s), each with a
+bounded CPU baseline of the reference CPU kernels' restatement (oracle/).
+
+Prints exactly one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "torch-point-ops_amd"))
+sys.path.insert(0, REPO)
+
+FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+FLOP_PER_PAIR = 9  # 3 sub + 3 mul + 2 add + 1 compare per directed pair
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def host_cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------- GPU
+
+def time_steps(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def bench_chamfer(tpo, torch, steps, warmup):
+    import workloads
+
+    p1, p2 = workloads.chamfer_c2()
+    B, N, _ = p1.shape
+    M = p2.shape[1]
+    dev = torch.device("cuda:0")
+    a = p1.to(dev).requires_grad_(True)
+    b = p2.to(dev).requires_grad_(True)
+    fwd_ms = []
+
+    def step(record=False):
+        # ChamferDistance('mean') forward + backward through autograd; the
+        # events bracket the forward op, i.e. the chamfer forward kernel
+        if record:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+        d1, d2 = tpo.chamfer_distance(a, b)
+        if record:
+            e1.record()
+            fwd_ms.append((e0, e1))
+        loss = d1.mean() + d2.mean()
+        return torch.autograd.grad(loss, (a, b))
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(record=True)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / steps
+    fwd = sum(e0.elapsed_time(e1) for e0, e1 in fwd_ms) / len(fwd_ms) / 1e3
+    pairs = 2 * B * N * M
+    return dict(pairs=pairs, sec=sec, fwd_sec=fwd, B=B, N=N, M=M)
+
+
+def bench_knn(tpo, torch, steps):
+    import workloads
+
+    p1, p2, l1, l2 = workloads.knn_c3()
+    dev = torch.device("cuda:0")
+    a, b, la, lb = p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev)
+    mod = tpo.KNearestNeighbors(K=16, return_nn=True)
+    raw = lambda: torch.ops.torch_point_ops_knn.knn_forward(a, b, la, lb, 2, 16, -1)  # noqa
+    sec_mod = time_steps(lambda: mod(a, b, la, lb), steps, 2, torch)
+    sec_raw = time_steps(raw, steps, 2, torch)
+    pairs = int((l1 * l2).sum())
+    return dict(pairs=pairs, sec_module=sec_mod, sec_kernel=sec_raw)
+
+
+def bench_fps(tpo, torch, steps):
+    import workloads
+
+    pts = workloads.fps_c4().to("cuda:0")
+    sec = time_steps(lambda: tpo.furthest_point_sampling(pts, 4096), steps, 2, torch)
+    idx = tpo.furthest_point_sampling(pts, 4096)
+    feats, go = workloads.gather_c4()
+    f = feats.to("cuda:0")
+    g = go.to("cuda:0")
+    fwd = time_steps(lambda: torch.ops.torch_point_ops_fps.gather_points_forward(f, idx),
+                     steps * 10, 3, torch)
+    bwd = time_steps(lambda: torch.ops.torch_point_ops_fps.gather_points_backward(g, idx, 65536),
+                     steps * 10, 3, torch)
+    B, N, m = pts.shape[0], pts.shape[1], 4096
+    C, M = f.shape[1], 4096
+    return dict(fps_sec=sec, updates=B * N * (m - 1), gather_fwd_sec=fwd, gather_bwd_sec=bwd,
+                fwd_bytes=B * M * 8 + 2 * B * C * M * 4,
+                bwd_bytes=B * C * N * 4 + B * C * M * 4 + B * M * 8, idx=idx.cpu(), pts=pts.cpu())
+
+
+# --------------------------------------------------------------------- CPU
+
+def cpu_chamfer(torch, budget_s=12.0):
+    """Reference CPU formulation (test_chamfer.py:11-25) + autograd backward,
+    query-chunked, on whole clouds of config 2 until the budget is used."""
+    import workloads
+
+    p1, p2 = workloads.chamfer_c2()
+    threads = torch.get_num_threads()
+
+    def one_cloud(b):
+        a = p1[b:b + 1].clone().requires_grad_(True)
+        c = p2[b:b + 1].clone().requires_grad_(True)
+        mins1, mins2 = [], None
+        for s in range(0, a.shape[1], 512):
+            dm = ((a[:, s:s + 512].unsqueeze(2) - c.unsqueeze(1)) ** 2).sum(3)
+            mins1.append(dm.min(2).values)
+            m2 = dm.min(1).values
+            mins2 = m2 if mins2 is None else torch.minimum(mins2, m2)
+        d1 = torch.cat(mins1, 1)
+        loss = d1.mean() + mins2.mean()
+        loss.backward()
+
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        one_cloud(n % p1.shape[0])
+        n += 1
+        if time.perf_counter() - t0 > budget_s or n >= p1.shape[0]:
+            break
+    sec = time.perf_counter() - t0
+    pairs = 2 * n * p1.shape[1] * p2.shape[1]
+    return dict(value=pairs / sec / 1e9, unit="G pair-dists/s", cores=threads, kind="port",
+                sample=f"{n} of 32 clouds of config 2 (8192x8192 each, both directions, "
+                       f"fwd+bwd) with the reference tests' torch formulation, "
+                       f"512-query chunks, {threads} torch threads on {cpu_model()}")
+
+
+def cpu_knn(O, np, threads):
+    import workloads
+
+    p1, p2, l1, l2 = workloads.knn_c3()
+    q = 64  # queries per cloud
+    a = p1[:, :q].numpy()
+    ln1 = np.minimum(l1.numpy(), q)
+    t0 = time.perf_counter()
+    O.cpu_knn_fwd_f32(a, p2.numpy(), ln1, l2.numpy(), 16, 2, nthreads=threads)
+    sec = time.perf_counter() - t0
+    pairs = float((ln1 * l2.numpy()).sum())
+    return dict(value=pairs / sec / 1e9, unit="G pair-dists/s", cores=threads, kind="port",
+                sample=f"{q} queries per cloud x 8 clouds of config 3 (knn.cpp restated)")
+
+
+def cpu_fps(O, np, pts, threads):
+    nc = min(threads, pts.shape[0])
+    m = 512
+    t0 = time.perf_counter()
+    O.cpu_fps_f32(pts[:nc].numpy(), m, nthreads=nc)
+    sec = time.perf_counter() - t0
+    upd = nc * pts.shape[1] * (m - 1)
+    return dict(value=upd / sec / 1e9, unit="G point-updates/s", cores=nc, kind="port",
+                sample=f"{nc} clouds of config 4, first {m} samples, one thread per cloud "
+                       f"(fps.cpp restated)")
+
+
+# -------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build runs on a single MI355X "
+              "(the sharding design is described in DESIGN.md); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import torch_point_ops as tpo
+
+    log("[bench] chamfer c2 fwd+bwd")
+    ch = bench_chamfer(tpo, torch, args.steps, args.warmup)
+    value = ch["pairs"] / ch["sec"] / 1e9
+    achieved = FLOP_PER_PAIR * ch["pairs"] / ch["fwd_sec"] / 1e12
+    traffic = None
+    tfile = os.path.join(REPO, "profiles", "chamfer_fwd_c2_traffic.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+
+    out = {
+        "metric": "Chamfer/KNN G pair-dists/s & % FP32 VALU peak; FPS ms at N=64K->4K",
+        "value": round(value, 3),
+        "unit": "G pair-dists/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ch["sec"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (BASELINE configs[1] generator, seed 2)",
+        "config": {"workload": "chamfer_distance fwd+bwd, B=32, N=M=8192, D=3, fp32, "
+                               "ChamferDistance('mean') (BASELINE.json configs[1])",
+                   "global_batch": ch["B"], "points": [ch["N"], ch["M"]],
+                   "pairs_per_step": ch["pairs"], "parallelism": "single GPU"},
+        "roofline": {"bound": "valu", "kernel": "chamfer_fwd_kernel<float,8>",
+                     "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+                     "traffic": traffic, "fwd_kernel_ms": round(ch["fwd_sec"] * 1e3, 4),
+                     "flop_per_pair": FLOP_PER_PAIR},
+    }
+    threads = min(host_cores(), int(os.environ.get("OMP_NUM_THREADS", host_cores())))
+    if not args.no_cpu:
+        log("[bench] cpu baseline (chamfer)")
+        torch.set_num_threads(threads)
+        out["cpu_baseline"] = cpu_chamfer(torch)
+    if not args.no_secondary:
+        from oracle import oracle as O
+
+        sec = {}
+        log("[bench] knn c3")
+        kn = bench_knn(tpo, torch, max(3, args.steps // 4))
+        sec["knn_c3"] = {"G_pair_dists_per_s_kernel": round(kn["pairs"] / kn["sec_kernel"] / 1e9, 2),
+                         "G_pair_dists_per_s_module": round(kn["pairs"] / kn["sec_module"] / 1e9, 2),
+                         "ms_kernel": round(kn["sec_kernel"] * 1e3, 3),
+                         "ms_module_return_nn": round(kn["sec_module"] * 1e3, 3),
+                         "frac_fp32_peak": round(FLOP_PER_PAIR * kn["pairs"] / kn["sec_kernel"]
+                                                 / 1e12 / FP32_PEAK_TFLOPS, 4)}
+        log("[bench] fps + gather c4")
+        fp = bench_fps(tpo, torch, max(3, args.steps // 4))
+        sec["fps_c4"] = {"ms": round(fp["fps_sec"] * 1e3, 3),
+                         "G_point_updates_per_s": round(fp["updates"] / fp["fps_sec"] / 1e9, 2)}
+        sec["gather_c4"] = {
+            "fwd_us": round(fp["gather_fwd_sec"] * 1e6, 2),
+            "fwd_GBs": round(fp["fwd_bytes"] / fp["gather_fwd_sec"] / 1e9, 1),
+            "bwd_us": round(fp["gather_bwd_sec"] * 1e6, 2),
+            "bwd_GBs": round(fp["bwd_bytes"] / fp["gather_bwd_sec"] / 1e9, 1),
+            "bwd_frac_hbm": round(fp["bwd_bytes"] / fp["gather_bwd_sec"] / 1e9 / HBM_PEAK_GBS, 3)}
+        if not args.no_cpu:
+            log("[bench] cpu baselines (knn, fps)")
+            sec["knn_c3"]["cpu_baseline"] = cpu_knn(O, np, threads)
+            sec["fps_c4"]["cpu_baseline"] = cpu_fps(O, np, fp["pts"], threads)
+        out["secondary"] = sec
+    out["host"] = {"cpu": cpu_model(), "cores": threads,
+                   "gpu": torch.cuda.get_device_name(0)}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,152 @@
+/*
+ * tpo.h -- C ABI of libtpo_hip.so, the MI355X (gfx950) kernels behind the
+ * torch_point_ops operators chamfer / knn / fps / gather_points.
+ *
+ * Conventions for every entry point:
+ *   - all pointers are device pointers (hipMalloc / torch CUDA-device tensors)
+ *     to contiguous row-major arrays; `stream` is a hipStream_t (or NULL for
+ *     the default stream) and every call is asynchronous on it;
+ *   - no entry point allocates, frees or synchronises; buffers that need
+ *     scratch take a caller-provided workspace sized by a *_workspace_size()
+ *     query;
+ *   - outputs are written completely (no pre-zeroing needed);
+ *   - return 0 on success or a negative TPO_ERR_* code; tpo_last_error()
+ *     returns a thread-local description of the last failure;
+ *   - dtype is one of TPO_F32, TPO_F64, TPO_F16 (IEEE binary16), TPO_BF16
+ *     (only where stated).
+ * The functions keep no global mutable state and may be called from any
+ * thread.
+ */
+#ifndef TPO_H
+#define TPO_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  TPO_F32 = 0,
+  TPO_F64 = 1,
+  TPO_F16 = 2,
+  TPO_BF16 = 3
+};
+
+enum {
+  TPO_OK = 0,
+  TPO_ERR_ARG = -1,       /* bad size / argument */
+  TPO_ERR_DTYPE = -2,     /* dtype not supported by this entry point */
+  TPO_ERR_LAUNCH = -3,    /* HIP launch error (message from hipGetLastError) */
+  TPO_ERR_WORKSPACE = -4  /* workspace missing or too small */
+};
+
+/* Thread-local message for the last non-zero return on this thread. */
+const char* tpo_last_error(void);
+
+/* ABI version of this header (major << 16 | minor). */
+int tpo_abi_version(void);
+
+/*
+ * Chamfer forward.  Replaces chamfer_cuda_forward
+ * (torch_point_ops/chamfer/csrc/cuda/chamfer.cu:169-198), the CUDA-key body
+ * of torch_point_ops_chamfer::chamfer_forward (chamfer.cpp:35-36).
+ *   xyz1 (B,N,3), xyz2 (B,M,3) of `dtype` (F32/F64/F16)
+ *   dist1 (B,N), dist2 (B,M) of `dtype`: squared distance to the nearest
+ *   point of the other cloud; idx1 (B,N), idx2 (B,M) int32: the FIRST index
+ *   attaining it.  An empty other cloud gives dist 0, idx 0.
+ */
+int tpo_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2,
+                    int64_t B, int64_t N, int64_t M,
+                    void* dist1, void* dist2, int32_t* idx1, int32_t* idx2,
+                    void* stream);
+
+/*
+ * Chamfer backward.  Replaces chamfer_cuda_backward (chamfer.cu:236-271),
+ * torch_point_ops_chamfer::chamfer_backward (chamfer.cpp:37-38).
+ *   grad_dist1 (B,N), grad_dist2 (B,M) of `dtype`
+ *   grad_xyz1 (B,N,3), grad_xyz2 (B,M,3) of `dtype`:
+ *     grad_xyz1[i] =  2 g1[i] (x1_i - x2_idx1[i]) - sum_{j: idx2[j]=i} 2 g2[j] (x2_j - x1_i)
+ *   (and symmetrically), the scatter summed by atomics in unspecified order.
+ */
+int tpo_chamfer_bwd(int dtype, const void* xyz1, const void* xyz2,
+                    const int32_t* idx1, const int32_t* idx2,
+                    const void* grad_dist1, const void* grad_dist2,
+                    int64_t B, int64_t N, int64_t M,
+                    void* grad_xyz1, void* grad_xyz2, void* stream);
+
+/*
+ * KNN forward.  Replaces knn_cuda_forward
+ * (torch_point_ops/knn/csrc/cuda/knn.cu:295-398),
+ * torch_point_ops_knn::knn_forward (knn.cpp:168-169).
+ *   p1 (N,P1,D), p2 (N,P2,D) of `dtype` (F32/F64/F16); lengths1/lengths2 (N)
+ *   int64 (clamped to [0,P1] / [0,P2]); norm 1 or 2; K >= 1; version -1 for
+ *   automatic, 0..3 to force one of the reference's kernel semantics (an
+ *   invalid choice falls back to automatic, as the reference does).
+ *   idxs (N,P1,K) int64 and dists (N,P1,K) `dtype`, unsorted, laid out
+ *   exactly as the reference's MinK slots, including its padding rules:
+ *   rows >= lengths1 are (0,0); slots >= lengths2 are (0,0) for versions
+ *   2/3 and (-1,+inf) for versions 0/1.
+ *   If version_out is not NULL it receives the version that ran.
+ */
+int tpo_knn_fwd(int dtype, const void* p1, const void* p2,
+                const int64_t* lengths1, const int64_t* lengths2,
+                int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,
+                int norm, int version, int64_t* idxs, void* dists,
+                int* version_out, void* stream);
+
+/*
+ * KNN backward.  Replaces knn_cuda_backward (knn.cu:469-534),
+ * torch_point_ops_knn::knn_backward (knn.cpp:170-171).
+ *   idxs / grad_dists (N,P1,K); grad_p1 (N,P1,D), grad_p2 (N,P2,D) `dtype`.
+ *   Rows >= lengths1 and slots with idx == -1 contribute nothing; L2:
+ *   diff = (2 g)(p1 - p2); L1: diff = g sign(p1 - p2) with sign(0) = 0;
+ *   grad_p1 += diff, grad_p2[idx] -= diff.
+ */
+int tpo_knn_bwd(int dtype, const void* p1, const void* p2,
+                const int64_t* lengths1, const int64_t* lengths2,
+                const int64_t* idxs, int norm, const void* grad_dists,
+                int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,
+                void* grad_p1, void* grad_p2, void* stream);
+
+/*
+ * Furthest point sampling.  Replaces fps_cuda_forward
+ * (torch_point_ops/fps/csrc/cuda/fps.cu:273-315),
+ * torch_point_ops_fps::fps_forward (fps.cpp:159).
+ *   points (B,N,3) `dtype` (F32/F64/F16), 1 <= nsamples <= N;
+ *   idx (B,nsamples) int64, identical to the reference kernel including its
+ *   skip rule (|p|^2 <= 1e-3 never selected), start index 0 and tie order.
+ *   workspace: tpo_fps_workspace_size(dtype, B, N) bytes, 256-byte aligned.
+ */
+int64_t tpo_fps_workspace_size(int dtype, int64_t B, int64_t N);
+int tpo_fps_fwd(int dtype, const void* points, int64_t B, int64_t N,
+                int64_t nsamples, int64_t* idx,
+                void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * gather_points forward.  Replaces gather_points_cuda_forward
+ * (fps.cu:318-357), torch_point_ops_fps::gather_points_forward (fps.cpp:160).
+ *   points (B,C,N), idx (B,M) int64 in [0,N), out (B,C,M).  F32/F64/F16.
+ */
+int tpo_gather_fwd(int dtype, const void* points, const int64_t* idx,
+                   int64_t B, int64_t C, int64_t N, int64_t M, void* out,
+                   void* stream);
+
+/*
+ * gather_points backward.  Replaces gather_points_cuda_backward
+ * (fps.cu:360-404), torch_point_ops_fps::gather_points_backward
+ * (fps.cpp:161).
+ *   grad_out (B,C,M), idx (B,M) int64, grad_points (B,C,N):
+ *   zeros + scatter-add of grad_out at idx (duplicates sum).
+ *   workspace: tpo_gather_bwd_workspace_size(B, N) bytes.
+ */
+int64_t tpo_gather_bwd_workspace_size(int64_t B, int64_t N);
+int tpo_gather_bwd(int dtype, const void* grad_out, const int64_t* idx,
+                   int64_t B, int64_t C, int64_t N, int64_t M,
+                   void* grad_points, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TPO_H */

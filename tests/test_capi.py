@@ -1,0 +1,63 @@
+"""C ABI of libtpo_hip.so: loads, exports every symbol include/tpo.h declares,
+and rejects bad arguments before touching the GPU (no compute calls here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from tests.conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "tpo.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tpo_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib(tpo):
+    from torch_point_ops import _native
+
+    L = ctypes.CDLL(_native.HIP_LIB)
+    L.tpo_last_error.restype = ctypes.c_char_p
+    return L
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for must in ("tpo_chamfer_fwd", "tpo_chamfer_bwd", "tpo_knn_fwd", "tpo_knn_bwd",
+                 "tpo_fps_fwd", "tpo_fps_workspace_size", "tpo_gather_fwd", "tpo_gather_bwd",
+                 "tpo_gather_bwd_workspace_size", "tpo_last_error", "tpo_abi_version"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert lib.tpo_abi_version() >> 16 == 1
+
+
+def test_argument_errors_are_reported(lib):
+    P, I = ctypes.c_void_p, ctypes.c_int64
+    lib.tpo_knn_fwd.argtypes = [ctypes.c_int, P, P, P, P, I, I, I, I, I, ctypes.c_int,
+                                ctypes.c_int, P, P, P, P]
+    rc = lib.tpo_knn_fwd(0, None, None, None, None, 1, 4, 4, 3, 2, 3, -1, None, None, None, None)
+    assert rc == -1 and b"Norm must be 1 or 2" in lib.tpo_last_error()
+    lib.tpo_fps_fwd.argtypes = [ctypes.c_int, P, I, I, I, P, P, I, P]
+    assert lib.tpo_fps_fwd(0, None, 2, 10, 11, None, None, 0, None) == -1
+    assert b"nsamples" in lib.tpo_last_error()
+    lib.tpo_fps_workspace_size.argtypes = [ctypes.c_int, I, I]
+    lib.tpo_fps_workspace_size.restype = I
+    ws = lib.tpo_fps_workspace_size(0, 16, 65536)
+    assert ws >= 16 * 65536 * 20 and ws % 256 == 0
+    assert lib.tpo_fps_fwd(0, None, 2, 10, 5, None, None, 0, None) == -4  # no workspace
+    assert lib.tpo_fps_workspace_size(9, 1, 10) == -1
+    lib.tpo_chamfer_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, P, P, P, P, P]
+    assert lib.tpo_chamfer_fwd(0, None, None, -1, 3, 3, None, None, None, None, None) == -1
+    assert lib.tpo_chamfer_fwd(7, None, None, 0, 3, 3, None, None, None, None, None) == 0  # B=0
+    lib.tpo_gather_bwd_workspace_size.argtypes = [I, I]
+    lib.tpo_gather_bwd_workspace_size.restype = I
+    assert lib.tpo_gather_bwd_workspace_size(16, 65536) == 16 * 65536 * 4

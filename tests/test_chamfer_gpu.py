@@ -1,0 +1,218 @@
+"""Chamfer on the GPU vs the oracle (bit-exact distances and first-index argmin)
+and the reference test suite's semantics (tests/test_chamfer.py)."""
+import numpy as np
+import pytest
+import torch
+
+import workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def np_(t):
+    return t.detach().cpu().numpy()
+
+
+def assert_bits(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape and a.dtype == b.dtype
+    assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), \
+        f"{np.sum(a != b)} of {a.size} differ"
+
+
+def run_fwd(p1, p2, dev):
+    return torch.ops.torch_point_ops_chamfer.chamfer_forward(p1.to(dev), p2.to(dev))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
+def test_config1_forward_backward_vs_oracle(tpo, O, dev, dtype):
+    p1, p2 = workloads.chamfer_c1(dtype=dtype)
+    d1, d2, i1, i2 = run_fwd(p1, p2, dev)
+    e1, e2, j1, j2 = O.chamfer_fwd(np_(p1), np_(p2))
+    assert_bits(np_(d1), e1)
+    assert_bits(np_(d2), e2)
+    assert np.array_equal(np_(i1), j1) and np.array_equal(np_(i2), j2)
+    # backward of ChamferDistance('mean') (grad_dist = 1/N each)
+    a = p1.to(dev).requires_grad_(True)
+    b = p2.to(dev).requires_grad_(True)
+    tpo.ChamferDistance("mean")(a, b).backward()
+    g1 = np.full(e1.shape, 1.0 / e1.size, dtype=e1.dtype)
+    g2 = np.full(e2.shape, 1.0 / e2.size, dtype=e2.dtype)
+    ea, eb = O.chamfer_bwd(np_(p1), np_(p2), j1, j2, g1, g2, accum_f64=True)
+    tol = 1e-2 if dtype == torch.float16 else 1e-5
+    for got, ref in ((np_(a.grad), ea), (np_(b.grad), eb)):
+        scale = max(np.abs(ref).max(), 1e-30)
+        assert np.abs(got.astype(np.float64) - ref).max() <= tol * scale
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
+@pytest.mark.parametrize("B,N,M", [(1, 1, 1), (2, 5, 7), (3, 64, 1), (1, 513, 1000),
+                                   (2, 1000, 333), (4, 4097, 2049), (1, 20000, 17)])
+def test_forward_bit_exact_random_sizes(tpo, O, dev, dtype, B, N, M):
+    g = torch.Generator().manual_seed(B * 1000003 + N * 31 + M)
+    p1 = torch.randn(B, N, 3, generator=g).to(dtype)
+    p2 = torch.randn(B, M, 3, generator=g).to(dtype)
+    d1, d2, i1, i2 = run_fwd(p1, p2, dev)
+    e1, e2, j1, j2 = O.chamfer_fwd(np_(p1), np_(p2))
+    assert_bits(np_(d1), e1)
+    assert_bits(np_(d2), e2)
+    assert np.array_equal(np_(i1), j1) and np.array_equal(np_(i2), j2)
+
+
+def test_duplicates_first_index(tpo, O, dev):
+    g = torch.Generator().manual_seed(11)
+    p1 = torch.rand(2, 300, 3, generator=g)
+    p2 = torch.rand(2, 900, 3, generator=g)
+    p2[:, 700] = p2[:, 5]
+    p2[:, 333] = p2[:, 5]
+    p2[:, 100:200] = p2[:, 0:100]  # whole duplicated range
+    d1, _, i1, _ = run_fwd(p1, p2, dev)
+    e1, _, j1, _ = O.chamfer_fwd(np_(p1), np_(p2))
+    assert np.array_equal(np_(i1), j1)
+    assert not np.isin(np_(i1), [333, 700]).any() and not (np_(i1)[:, :] // 100 == 1).any()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_config2_subset_exact_and_full_properties(tpo, O, dev, dtype):
+    p1, p2 = workloads.chamfer_c2(dtype=dtype)
+    d1, d2, i1, i2 = run_fwd(p1, p2, dev)
+    # oracle on a subset of query rows (each row depends only on its query
+    # and the whole other cloud)
+    for b in (0, 31):
+        for qs, refs, d, i in ((p1, p2, d1, i1), (p2, p1, d2, i2)):
+            sel = slice(1000, 1512)
+            e, _, j, _ = O.chamfer_fwd(np_(qs[b:b + 1, sel]), np_(refs[b:b + 1]))
+            assert_bits(np_(d[b:b + 1, sel]), e)
+            assert np.array_equal(np_(i[b:b + 1, sel]), j)
+    # full size: indices in range, each distance attained at its index and
+    # no other point is closer (float64 check, tolerance above rounding)
+    for qs, refs, d, i in ((p1, p2, d1, i1), (p2, p1, d2, i2)):
+        assert int(i.min()) >= 0 and int(i.max()) < refs.shape[1]
+        q64 = qs.to(dev, torch.float64)
+        r64 = refs.to(dev, torch.float64)
+        at = ((torch.gather(r64, 1, i.long()[..., None].expand(-1, -1, 3)) - q64) ** 2).sum(-1)
+        tol = 5e-3 if dtype == torch.float16 else 1e-6
+        assert torch.allclose(at, d.double(), rtol=tol, atol=1e-7)
+        best = torch.cat([torch.cdist(q64[b:b + 1], r64[b:b + 1]).pow(2).min(-1).values
+                          for b in range(qs.shape[0])])
+        assert bool((at <= best * (1 + tol) + 1e-7).all())
+
+
+def test_backward_config2_vs_oracle(tpo, O, dev):
+    p1, p2 = workloads.chamfer_c2(B=4, N=4096)
+    a = p1.to(dev).requires_grad_(True)
+    b = p2.to(dev).requires_grad_(True)
+    tpo.ChamferDistance("mean")(a, b).backward()
+    _, _, j1, j2 = O.chamfer_fwd(np_(p1), np_(p2))
+    g1 = np.full(j1.shape, 1.0 / j1.size, np.float32)
+    g2 = np.full(j2.shape, 1.0 / j2.size, np.float32)
+    ea, eb = O.chamfer_bwd(np_(p1), np_(p2), j1, j2, g1, g2, accum_f64=True)
+    for got, ref in ((np_(a.grad), ea), (np_(b.grad), eb)):
+        assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+# ---- the reference test suite's checks (tests/test_chamfer.py) ----
+
+def torch_reference(p1, p2):
+    dm = ((p1.unsqueeze(2) - p2.unsqueeze(1)) ** 2).sum(3)
+    return dm.min(2).values, dm.min(1).values
+
+
+def test_reference_forward_and_known_values(tpo, dev):
+    g = torch.Generator().manual_seed(0)
+    p1 = torch.randn(1, 64, 3, generator=g).to(dev)
+    p2 = torch.randn(1, 128, 3, generator=g).to(dev)
+    d1, d2, _, _ = torch.ops.torch_point_ops_chamfer.chamfer_forward(p1, p2)
+    r1, r2 = torch_reference(p1, p2)
+    assert torch.allclose(d1, r1) and torch.allclose(d2, r2)
+    p = torch.tensor([[[0.0, 0.0, 0.0], [1.0, 1.0, 1.0]]], device=dev)
+    d1, d2, _, _ = torch.ops.torch_point_ops_chamfer.chamfer_forward(p, p.clone())
+    assert (d1 == 0).all() and (d2 == 0).all()
+    d1, d2, _, _ = torch.ops.torch_point_ops_chamfer.chamfer_forward(
+        torch.zeros(1, 1, 3, device=dev), torch.tensor([[[1.0, 2.0, 3.0]]], device=dev))
+    assert d1.item() == 14.0 and d2.item() == 14.0
+
+
+def test_empty_clouds(tpo, dev):
+    p1 = torch.randn(2, 10, 3, device=dev)
+    e = torch.empty(2, 0, 3, device=dev)
+    d1, d2, i1, i2 = torch.ops.torch_point_ops_chamfer.chamfer_forward(p1, e)
+    assert d1.shape == (2, 10) and d2.shape == (2, 0)
+    assert (d1 == 0).all() and (i1 == 0).all()
+    d1, d2, _, _ = torch.ops.torch_point_ops_chamfer.chamfer_forward(e, p1)
+    assert d1.shape == (2, 0) and d2.shape == (2, 10)
+    d1, d2, _, _ = torch.ops.torch_point_ops_chamfer.chamfer_forward(e, e)
+    assert d1.shape == (2, 0) and d2.shape == (2, 0)
+
+
+@pytest.mark.parametrize("B,N,M", [(1, 3, 4), (2, 5, 7), (1, 8, 6), (2, 6, 8), (1, 64, 128)])
+def test_gradients_vs_torch_reference(tpo, dev, B, N, M):
+    g = torch.Generator().manual_seed(N * M)
+    p1 = torch.randn(B, N, 3, generator=g).to(dev).requires_grad_(True)
+    p2 = torch.randn(B, M, 3, generator=g).to(dev).requires_grad_(True)
+    d1, d2 = tpo.chamfer_distance(p1, p2)
+    loss = d1.mean() + d2.mean()
+    ga, gb = torch.autograd.grad(loss, (p1, p2))
+    r1, r2 = torch_reference(p1, p2)
+    ref_loss = r1.mean() + r2.mean()
+    ra, rb = torch.autograd.grad(ref_loss, (p1, p2))
+    assert torch.allclose(loss, ref_loss, atol=1e-6)
+    assert torch.allclose(ga, ra, atol=1e-4) and torch.allclose(gb, rb, atol=1e-4)
+
+
+def test_gradcheck_float64(tpo, dev):
+    g = torch.Generator().manual_seed(5)
+    p1 = torch.randn(1, 4, 3, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
+    p2 = torch.randn(1, 5, 3, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
+    assert torch.autograd.gradcheck(tpo.chamfer_distance, (p1, p2), eps=1e-6, atol=1e-5,
+                                    rtol=1e-4, nondet_tol=1e-5, fast_mode=True,
+                                    check_batched_grad=False)
+    model = tpo.ChamferDistance(reduction="mean")
+    q1 = p1[:, :3].detach().clone().requires_grad_(True)
+    q2 = p2[:, :4].detach().clone().requires_grad_(True)
+    assert torch.autograd.gradcheck(model, (q1, q2), eps=1e-6, atol=1e-5, rtol=1e-4,
+                                    nondet_tol=1e-5, fast_mode=True, check_batched_grad=False)
+
+
+def test_opcheck_and_compile(tpo, dev):
+    from torch.library import opcheck
+
+    g = torch.Generator().manual_seed(6)
+    p1 = torch.randn(1, 3, 3, generator=g).to(dev)
+    p2 = torch.randn(1, 3, 3, generator=g).to(dev)
+    opcheck(torch.ops.torch_point_ops_chamfer.chamfer_forward.default, (p1, p2),
+            raise_exception=True)
+    model = tpo.ChamferDistance().to(dev)
+    a = torch.randn(1, 64, 3, generator=g).to(dev)
+    b = torch.randn(1, 128, 3, generator=g).to(dev)
+    assert torch.equal(model(a, b), torch.compile(model)(a, b))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.float64])
+def test_multi_precision_and_reductions(tpo, dev, dtype):
+    g = torch.Generator().manual_seed(7)
+    p1 = torch.randn(2, 10, 3, generator=g).to(dev, dtype)
+    p2 = torch.randn(2, 12, 3, generator=g).to(dev, dtype)
+    d1, d2 = tpo.chamfer_distance(p1, p2)
+    assert d1.dtype == dtype and d1.shape == (2, 10) and d2.shape == (2, 12)
+    a, b = p1.clone().requires_grad_(True), p2.clone().requires_grad_(True)
+    e1, e2 = tpo.chamfer_distance(a, b)
+    (e1.mean() + e2.mean()).backward()
+    assert torch.isfinite(a.grad).all() and torch.isfinite(b.grad).all()
+    for red in ("mean", "sum", None, "none"):
+        r = tpo.ChamferDistance(reduction=red)(p1, p2)
+        if red in (None, "none"):
+            assert len(r) == 2 and r[0].dtype == dtype
+        else:
+            assert r.dtype == dtype
+
+
+def test_non_contiguous_inputs(tpo, O, dev):
+    g = torch.Generator().manual_seed(8)
+    base = torch.randn(2, 3, 50, generator=g)
+    p1 = base.transpose(1, 2)  # (2, 50, 3) non-contiguous
+    p2 = torch.randn(2, 40, 3, generator=g)
+    d1, d2 = tpo.chamfer_distance(p1.to(dev), p2.to(dev))
+    e1, e2, _, _ = O.chamfer_fwd(np_(p1.contiguous()), np_(p2))
+    assert_bits(np_(d1), e1)
+    assert_bits(np_(d2), e2)

@@ -1,0 +1,229 @@
+"""KNN on the GPU vs the oracle: the raw op output (the reference's MinK slot
+layout, padding rules and distances) bit for bit, plus knn_points/knn_gather
+and the reference test suite's semantics (tests/test_knn.py)."""
+import numpy as np
+import pytest
+import torch
+
+import workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def np_(t):
+    return t.detach().cpu().numpy()
+
+
+def assert_same(got, ref):
+    got, ref = np.asarray(got), np.asarray(ref)
+    assert got.shape == ref.shape and got.dtype == ref.dtype
+    same = (got == ref) | (np.isnan(got) & np.isnan(ref)) if got.dtype.kind == "f" else got == ref
+    assert same.all(), f"{np.sum(~same)} of {got.size} differ"
+
+
+def raw(p1, p2, l1, l2, norm, K, version, dev):
+    return torch.ops.torch_point_ops_knn.knn_forward(p1.to(dev), p2.to(dev), l1.to(dev),
+                                                     l2.to(dev), norm, K, version)
+
+
+CASES = [
+    # dtype, N, P1, P2, D, K, norm, version
+    (torch.float32, 2, 100, 300, 3, 16, 2, -1),
+    (torch.float32, 3, 257, 129, 3, 1, 2, -1),
+    (torch.float32, 2, 64, 64, 3, 2, 2, -1),   # V3, sorted pair
+    (torch.float32, 2, 64, 64, 3, 2, 2, 2),    # V2, MinK
+    (torch.float32, 2, 70, 90, 3, 3, 1, 3),
+    (torch.float32, 2, 70, 90, 3, 32, 2, 2),
+    (torch.float32, 2, 50, 80, 3, 7, 2, 0),    # sentinel padding
+    (torch.float32, 2, 50, 80, 3, 5, 1, 1),
+    (torch.float32, 2, 40, 300, 3, 40, 2, -1),  # K > 32 -> V1, slots in memory
+    (torch.float32, 1, 33, 100, 5, 6, 2, -1),
+    (torch.float32, 1, 33, 100, 40, 9, 2, -1),   # V0, runtime D
+    (torch.float32, 1, 20, 64, 128, 32, 2, -1),  # config-5 shape class in fp32
+    (torch.float64, 2, 60, 130, 3, 10, 2, -1),
+    (torch.float64, 2, 60, 130, 3, 4, 1, -1),
+    (torch.float16, 2, 60, 130, 3, 8, 2, -1),
+    (torch.float16, 2, 60, 130, 3, 2, 1, -1),
+]
+
+
+@pytest.mark.parametrize("dtype,N,P1,P2,D,K,norm,version", CASES)
+def test_raw_forward_bit_exact(tpo, O, dev, dtype, N, P1, P2, D, K, norm, version):
+    g = torch.Generator().manual_seed(P1 * 7 + P2 * 13 + D + K)
+    p1 = torch.randn(N, P1, D, generator=g).to(dtype)
+    p2 = torch.randn(N, P2, D, generator=g).to(dtype)
+    l1 = torch.randint(P1 // 2, P1 + 1, (N,), generator=g)
+    l2 = torch.randint(max(1, K // 2), P2 + 1, (N,), generator=g)
+    l2[0] = min(P2, max(1, K - 1))  # a cloud shorter than K
+    idx, d = raw(p1, p2, l1, l2, norm, K, version, dev)
+    ei, ed = O.knn_fwd(np_(p1), np_(p2), np_(l1), np_(l2), norm=norm, K=K, version=version)
+    assert_same(np_(idx), ei)
+    assert_same(np_(d), ed)
+
+
+def test_quantised_ties_bit_exact(tpo, O, dev):
+    """Coordinates on a coarse grid: many exactly equal distances exercise the
+    first-max eviction and the strict-less rule."""
+    g = torch.Generator().manual_seed(21)
+    p1 = torch.randint(0, 4, (2, 200, 3), generator=g).float()
+    p2 = torch.randint(0, 4, (2, 500, 3), generator=g).float()
+    l = torch.tensor([200, 150]), torch.tensor([500, 333])
+    for K, v in ((16, -1), (2, -1), (2, 2), (4, 3), (5, 0), (40, -1)):
+        idx, d = raw(p1, p2, l[0], l[1], 2, K, v, dev)
+        ei, ed = O.knn_fwd(np_(p1), np_(p2), np_(l[0]), np_(l[1]), norm=2, K=K, version=v)
+        assert_same(np_(idx), ei)
+        assert_same(np_(d), ed)
+
+
+def test_config3_subset_exact_and_full_properties(tpo, O, dev):
+    p1, p2, l1, l2 = workloads.knn_c3()
+    idx, d = raw(p1, p2, l1, l2, 2, 16, -1, dev)
+    for n in (0, 7):
+        sel = slice(0, 256)
+        ln1 = torch.tensor([min(256, int(l1[n]))])
+        ei, ed = O.knn_fwd(np_(p1[n:n + 1, sel]), np_(p2[n:n + 1]), np_(ln1), np_(l2[n:n + 1]),
+                           norm=2, K=16)
+        assert_same(np_(idx[n:n + 1, sel]), ei)
+        assert_same(np_(d[n:n + 1, sel]), ed)
+    # full size: rows past lengths1 zero, indices inside lengths2, sorted
+    # distances match a float64 recomputation at the returned indices
+    si, sd = tpo.knn_points(p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev), K=16)
+    for n in range(p1.shape[0]):
+        a, b = int(l1[n]), int(l2[n])
+        assert (idx[n, a:] == 0).all() and (d[n, a:] == 0).all()
+        assert int(si[n, :a].min()) >= 0 and int(si[n, :a].max()) < b
+        assert bool((sd[n, :a, 1:] >= sd[n, :a, :-1]).all())
+        q = p1[n, :a].to(dev, torch.float64)
+        r = p2[n].to(dev, torch.float64)
+        at = ((r[si[n, :a]] - q[:, None]) ** 2).sum(-1)
+        assert torch.allclose(at, sd[n, :a].double(), rtol=1e-6, atol=1e-9)
+
+
+def test_knn_points_sorted_and_gather(tpo, O, dev):
+    g = torch.Generator().manual_seed(22)
+    p1 = torch.randn(3, 40, 3, generator=g)
+    p2 = torch.randn(3, 60, 3, generator=g)
+    l1 = torch.tensor([40, 20, 33])
+    l2 = torch.tensor([60, 3, 45])
+    idx, d = tpo.knn_points(p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev), K=5)
+    ei, ed = O.knn_fwd(np_(p1), np_(p2), np_(l1), np_(l2), K=5)
+    for n in range(3):
+        for i in range(int(l1[n])):
+            k = min(5, int(l2[n]))
+            order = np.argsort(ed[n, i, :k], kind="stable")
+            assert np.array_equal(np_(d[n, i, :k]), ed[n, i, :k][order])
+            assert np.array_equal(np_(idx[n, i, :k]), ei[n, i, :k][order])
+            assert (np_(d[n, i, k:]) == 0).all()
+    nn = tpo.knn_gather(p2.to(dev), idx, l2.to(dev))
+    for n in range(3):
+        for i in range(40):
+            for k in range(5):
+                if k < int(l2[n]):
+                    assert torch.equal(nn[n, i, k], p2[n, int(idx[n, i, k])].to(dev))
+                else:
+                    assert (nn[n, i, k] == 0).all()
+
+
+@pytest.mark.parametrize("norm", [1, 2])
+@pytest.mark.parametrize("version", [-1, 0])
+def test_backward_vs_oracle(tpo, O, dev, norm, version):
+    g = torch.Generator().manual_seed(23 + norm)
+    p1 = torch.randn(2, 300, 3, generator=g)
+    p2 = torch.randn(2, 200, 3, generator=g)
+    l1 = torch.tensor([300, 123])
+    l2 = torch.tensor([200, 5])
+    idx, _ = raw(p1, p2, l1, l2, norm, 8, version, dev)
+    gd = torch.rand(2, 300, 8, generator=g)
+    g1, g2 = torch.ops.torch_point_ops_knn.knn_backward(
+        p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev), idx, norm, gd.to(dev))
+    e1, e2 = O.knn_bwd(np_(p1), np_(p2), np_(l1), np_(l2), np_(idx), norm, np_(gd),
+                       accum_f64=True)
+    for got, ref in ((np_(g1), e1), (np_(g2), e2)):
+        assert np.abs(got - ref).max() <= 1e-5 * max(np.abs(ref).max(), 1e-30)
+
+
+# ---- the reference test suite's checks (tests/test_knn.py) ----
+
+def torch_reference_knn(p1, p2, K):
+    d = ((p1[:, :, None] - p2[:, None]) ** 2).sum(-1)
+    sd, si = d.sort(-1)
+    return si[..., :K], sd[..., :K]
+
+
+def test_reference_forward_and_known_values(tpo, dev):
+    g = torch.Generator().manual_seed(0)
+    p1 = torch.randn(2, 10, 3, generator=g).to(dev)
+    p2 = torch.randn(2, 15, 3, generator=g).to(dev)
+    for K in (1, 3, 5):
+        idx, d = tpo.knn_points(p1, p2, torch.full((2,), 10, device=dev),
+                                torch.full((2,), 15, device=dev), K=K)
+        ri, rd = torch_reference_knn(p1, p2, K)
+        assert torch.allclose(d, rd, atol=1e-5) and torch.equal(idx, ri)
+    a = torch.tensor([[[0.0, 0, 0], [1.0, 0, 0]]], device=dev)
+    b = torch.tensor([[[0.0, 0, 0], [0.5, 0, 0], [2.0, 0, 0]]], device=dev)
+    idx, d = tpo.knn_points(a, b, K=2)
+    assert idx.tolist() == [[[0, 1], [1, 0]]]
+    assert torch.allclose(d, torch.tensor([[[0.0, 0.25], [0.25, 1.0]]], device=dev))
+    q = torch.zeros(1, 1, 3, device=dev)
+    r = torch.tensor([[[1.0, 1, 1], [2.0, 0, 0]]], device=dev)
+    assert tpo.knn_points(q, r, norm=1, K=2)[1].tolist() == [[[2.0, 3.0]]]
+    assert tpo.knn_points(q, r, norm=2, K=2)[1].tolist() == [[[3.0, 4.0]]]
+
+
+def test_empty_clouds(tpo, dev):
+    p1 = torch.randn(2, 10, 3, device=dev)
+    e = torch.empty(2, 0, 3, device=dev)
+    idx, d = torch.ops.torch_point_ops_knn.knn_forward(
+        p1, e, torch.tensor([10, 10], device=dev), torch.tensor([0, 0], device=dev), 2, 3, -1)
+    assert idx.shape == (2, 10, 3) and (idx == 0).all() and (d == 0).all()
+    idx, d = torch.ops.torch_point_ops_knn.knn_forward(
+        e, p1, torch.tensor([0, 0], device=dev), torch.tensor([10, 10], device=dev), 2, 3, -1)
+    assert idx.shape == (2, 0, 3)
+
+
+def test_gradients_and_gradcheck(tpo, dev):
+    g = torch.Generator().manual_seed(9)
+    for B, N, M, K in ((1, 3, 4, 1), (2, 5, 7, 2), (1, 8, 6, 3), (1, 8, 12, 3)):
+        p1 = torch.randn(B, N, 3, generator=g).to(dev).requires_grad_(True)
+        p2 = torch.randn(B, M, 3, generator=g).to(dev).requires_grad_(True)
+        loss = tpo.knn_points(p1, p2, K=K)[1].mean()
+        ga, gb = torch.autograd.grad(loss, (p1, p2))
+        ref = torch_reference_knn(p1, p2, K)[1].mean()
+        ra, rb = torch.autograd.grad(ref, (p1, p2))
+        assert torch.allclose(loss, ref, atol=1e-6)
+        assert torch.allclose(ga, ra, atol=1e-4) and torch.allclose(gb, rb, atol=1e-4)
+    p1 = torch.randn(1, 4, 3, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
+    p2 = torch.randn(1, 5, 3, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
+    fn = lambda a, b: tpo.knn_points(a, b, K=2, return_sorted=False)[1].sum()  # noqa: E731
+    assert torch.autograd.gradcheck(fn, (p1, p2), eps=1e-6, atol=1e-5, rtol=1e-4,
+                                    nondet_tol=1e-5, fast_mode=True, check_batched_grad=False)
+
+
+def test_module_opcheck_compile_precision(tpo, dev):
+    from torch.library import opcheck
+
+    g = torch.Generator().manual_seed(10)
+    p1 = torch.randn(2, 8, 3, generator=g).to(dev)
+    p2 = torch.randn(2, 10, 3, generator=g).to(dev)
+    idx, d = tpo.KNearestNeighbors(K=3)(p1, p2)
+    assert idx.shape == (2, 8, 3) and d.shape == (2, 8, 3)
+    idx, d, nn = tpo.KNearestNeighbors(K=3, return_nn=True)(p1, p2)
+    assert nn.shape == (2, 8, 3, 3)
+    l = torch.tensor([3], device=dev)
+    opcheck(torch.ops.torch_point_ops_knn.knn_forward.default,
+            (p1[:1, :3].contiguous(), p2[:1, :3].contiguous(), l, l, 2, 2, -1),
+            raise_exception=True)
+    m = tpo.KNearestNeighbors(K=3).to(dev)
+    e, c = m(p1[:1], p2[:1]), torch.compile(m)(p1[:1], p2[:1])
+    assert torch.allclose(e[0], c[0]) and torch.allclose(e[1], c[1])
+    for dtype in (torch.float16, torch.float32, torch.float64):
+        a = p1.detach().to(dtype).clone().requires_grad_(True)
+        b = p2.detach().to(dtype).clone().requires_grad_(True)
+        idx, d = tpo.knn_points(a, b, K=3)
+        assert d.dtype == dtype and idx.dtype == torch.int64
+        d.mean().backward()
+        assert torch.isfinite(a.grad).all() and torch.isfinite(b.grad).all()
+    for v in (0, 1, 2, 3):
+        d_auto = tpo.knn_points(p1, p2, K=3)[1]
+        d_v = tpo.knn_points(p1, p2, K=3, version=v)[1]
+        assert torch.allclose(d_auto, d_v, atol=1e-5)

@@ -1,0 +1,404 @@
+"""Pins the CPU oracle (oracle/tpo_oracle.c) before it is trusted as checker.
+
+Each check is independent of the oracle's C code: the reference's own
+known-answer tests, exact rational arithmetic (tests/exact.py), numpy's
+float16 arithmetic, float64 brute force, closed forms and hand-derived tie
+cases that a plausible restatement mistake (wrong eviction slot, wrong tie
+order, missing rounding, wrong FMA order) would fail.
+"""
+import itertools
+
+import numpy as np
+import pytest
+
+from tests import exact
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ------------------------------------------------------------------ float16
+
+def test_f16_conversions_match_numpy(O):
+    h = np.arange(65536, dtype=np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = O.f16_bits_to_f32(h)
+    fin = ~np.isnan(ref)
+    assert np.array_equal(ref[fin].view(np.uint32), got[fin].view(np.uint32))
+    assert np.isnan(got[~fin]).all()
+    vals = ref[np.isfinite(ref)].astype(np.float64)
+    u = np.unique(vals)
+    mids = ((u[1:] + u[:-1]) / 2).astype(np.float32)  # exact ties
+    x = np.concatenate([
+        rng(0).standard_normal(200000).astype(np.float32) * np.float32(3e-5),
+        rng(1).standard_normal(200000).astype(np.float32) * np.float32(300),
+        mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf)),
+        np.array([65504, 65519.99, 65520, 1e6, -1e6, 1e-8, -6e-8, 0.0, -0.0], np.float32),
+    ])
+    with np.errstate(over="ignore"):
+        assert np.array_equal(x.astype(np.float16).view(np.uint16), O.f32_to_f16_bits(x))
+
+
+# ------------------------------------------------------------------ chamfer
+
+def test_chamfer_known_values(O):
+    # reference tests/test_chamfer.py:180-197
+    p = np.array([[[0.0, 0.0, 0.0], [1.0, 1.0, 1.0]]], np.float32)
+    d1, d2, i1, i2 = O.chamfer_fwd(p, p.copy())
+    assert (d1 == 0).all() and (d2 == 0).all()
+    assert i1.tolist() == [[0, 1]] and i2.tolist() == [[0, 1]]
+    d1, d2, _, _ = O.chamfer_fwd(np.zeros((1, 1, 3), np.float32),
+                                 np.array([[[1.0, 2.0, 3.0]]], np.float32))
+    assert d1[0, 0] == 14.0 and d2[0, 0] == 14.0
+
+
+def test_chamfer_f32_bits_exact_arithmetic(O):
+    r = rng(2)
+    a = r.standard_normal((1, 7, 3)).astype(np.float32)
+    b = r.standard_normal((1, 9, 3)).astype(np.float32)
+    d1, d2, i1, i2 = O.chamfer_fwd(a, b)
+    for (q, ref, d, idx) in ((a, b, d1, i1), (b, a, d2, i2)):
+        for j in range(q.shape[1]):
+            all_d = [exact.sq3_f32(*(exact.f32_sub(ref[0, k, c], q[0, j, c]) for c in range(3)))
+                     for k in range(ref.shape[1])]
+            m = min(all_d)
+            assert d[0, j].view(np.uint32) == np.float32(m).view(np.uint32)
+            assert idx[0, j] == all_d.index(m)  # first index of the minimum
+
+
+def test_chamfer_f64_and_f16_arithmetic(O):
+    r = rng(3)
+    a = r.standard_normal((1, 5, 3))
+    b = r.standard_normal((1, 6, 3))
+    d1, _, i1, _ = O.chamfer_fwd(a, b)
+    for j in range(5):
+        all_d = [exact.sq3_f64(*(b[0, k] - a[0, j])) for k in range(6)]
+        assert d1[0, j] == min(all_d) and i1[0, j] == all_d.index(min(all_d))
+    ah, bh = a.astype(np.float16), b.astype(np.float16)
+    d1, _, i1, _ = O.chamfer_fwd(ah, bh)
+    for j in range(5):
+        all_d = [exact.sq3_f16(*(bh[0, k] - ah[0, j])) for k in range(6)]
+        m = min(all_d)
+        assert d1[0, j] == m and i1[0, j] == all_d.index(m)
+
+
+def test_chamfer_brute_force_and_properties(O):
+    r = rng(4)
+    a = r.random((2, 300, 3)).astype(np.float32)
+    b = r.random((2, 700, 3)).astype(np.float32)
+    d1, d2, i1, i2 = O.chamfer_fwd(a, b)
+    full = ((a[:, :, None, :].astype(np.float64) - b[:, None, :, :]) ** 2).sum(-1)
+    np.testing.assert_allclose(d1, full.min(2), rtol=2e-6, atol=1e-12)
+    np.testing.assert_allclose(d2, full.min(1), rtol=2e-6, atol=1e-12)
+    picked = np.take_along_axis(full, i1[..., None].astype(np.int64), 2)[..., 0]
+    np.testing.assert_allclose(picked, full.min(2), rtol=2e-6, atol=1e-12)
+    # swap symmetry
+    e1, e2, j1, j2 = O.chamfer_fwd(b, a)
+    assert np.array_equal(e1, d2) and np.array_equal(e2, d1)
+    assert np.array_equal(j1, i2) and np.array_equal(j2, i1)
+    # exact duplicates in the reference cloud: the first copy wins
+    b2 = b.copy()
+    b2[:, 650] = b2[:, 11]
+    b2[:, 520] = b2[:, 11]
+    _, _, k1, _ = O.chamfer_fwd(a, b2)
+    assert not np.isin(k1, [520, 650]).any()
+
+
+def test_chamfer_empty_other_cloud(O):
+    a = rng(5).random((2, 10, 3)).astype(np.float32)
+    e = np.zeros((2, 0, 3), np.float32)
+    d1, d2, i1, i2 = O.chamfer_fwd(a, e)
+    assert d1.shape == (2, 10) and d2.shape == (2, 0)
+    assert (d1 == 0).all() and (i1 == 0).all()
+
+
+def test_chamfer_backward_closed_form(O):
+    r = rng(6)
+    a = r.standard_normal((2, 40, 3)).astype(np.float32)
+    b = r.standard_normal((2, 55, 3)).astype(np.float32)
+    _, _, i1, i2 = O.chamfer_fwd(a, b)
+    g1 = r.random((2, 40)).astype(np.float32)
+    g2 = r.random((2, 55)).astype(np.float32)
+    ga, gb = O.chamfer_bwd(a, b, i1, i2, g1, g2, accum_f64=True)
+    A, Bm = a.astype(np.float64), b.astype(np.float64)
+    ea, eb = np.zeros_like(A), np.zeros_like(Bm)
+    for bb in range(2):
+        c1 = 2 * g1[bb, :, None] * (A[bb] - Bm[bb, i1[bb]])
+        ea[bb] += c1
+        np.add.at(eb[bb], i1[bb], -c1)
+        c2 = 2 * g2[bb, :, None] * (Bm[bb] - A[bb, i2[bb]])
+        eb[bb] += c2
+        np.add.at(ea[bb], i2[bb], -c2)
+    np.testing.assert_allclose(ga, ea, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(gb, eb, rtol=1e-5, atol=1e-6)
+    sa, sb = O.chamfer_bwd(a, b, i1, i2, g1, g2, accum_f64=False)
+    np.testing.assert_allclose(sa, ga, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(sb, gb, rtol=1e-5, atol=1e-6)
+
+
+def test_chamfer_backward_finite_difference(O):
+    r = rng(7)
+    a = r.standard_normal((1, 6, 3))
+    b = r.standard_normal((1, 8, 3))
+    d1, d2, i1, i2 = O.chamfer_fwd(a, b)
+    ga, gb = O.chamfer_bwd(a, b, i1, i2, np.ones_like(d1), np.ones_like(d2))
+
+    def loss(x, y):
+        e1, e2, _, _ = O.chamfer_fwd(x, y)
+        return e1.sum() + e2.sum()
+
+    h = 1e-6
+    for arr, g in ((a, ga), (b, gb)):
+        for idx in itertools.product(range(1), range(arr.shape[1]), range(3)):
+            p, m = arr.copy(), arr.copy()
+            p[idx] += h
+            m[idx] -= h
+            num = (loss(p, b) - loss(m, b)) / (2 * h) if arr is a else (loss(a, p) - loss(a, m)) / (2 * h)
+            assert abs(num - g[idx]) < 1e-5
+
+
+# ---------------------------------------------------------------------- knn
+
+def test_knn_known_values(O):
+    # reference tests/test_knn.py:187-218
+    p1 = np.array([[[0.0, 0, 0], [1.0, 0, 0]]], np.float32)
+    p2 = np.array([[[0.0, 0, 0], [0.5, 0, 0], [2.0, 0, 0]]], np.float32)
+    idx, d = O.knn_fwd(p1, p2, K=2)
+    order = np.argsort(d, axis=2, kind="stable")
+    idx, d = np.take_along_axis(idx, order, 2), np.take_along_axis(d, order, 2)
+    assert idx.tolist() == [[[0, 1], [1, 0]]]
+    np.testing.assert_allclose(d, [[[0.0, 0.25], [0.25, 1.0]]])
+    # reference tests/test_knn.py:251-285
+    q = np.zeros((1, 1, 3), np.float32)
+    r = np.array([[[1.0, 1, 1], [2.0, 0, 0]]], np.float32)
+    _, d1 = O.knn_fwd(q, r, K=2, norm=1)
+    _, d2 = O.knn_fwd(q, r, K=2, norm=2)
+    assert sorted(d1[0, 0].tolist()) == [2.0, 3.0]
+    assert sorted(d2[0, 0].tolist()) == [3.0, 4.0]
+
+
+def test_knn_choose_version(O):
+    # dispatch.cuh:114-147
+    assert O.knn_choose_version(3, 1) == 3
+    assert O.knn_choose_version(3, 4) == 3
+    assert O.knn_choose_version(3, 5) == 2
+    assert O.knn_choose_version(8, 32) == 2
+    assert O.knn_choose_version(3, 33) == 1
+    assert O.knn_choose_version(32, 64) == 1
+    assert O.knn_choose_version(33, 1) == 0
+    assert O.knn_choose_version(128, 32) == 0
+    assert O.knn_choose_version(3, 16, 3) == 2   # invalid explicit -> automatic
+    assert O.knn_choose_version(3, 16, 0) == 0
+    assert O.knn_choose_version(3, 16, 1) == 1
+
+
+def test_knn_mink_tie_semantics(O):
+    """Hand-derived from mink.cuh: MinK evicts the FIRST slot holding the max;
+    RegisterMinK<2> keeps a sorted pair and shifts on a new minimum."""
+    q = np.zeros((1, 1, 3), np.float32)
+    r = np.array([[[1.0, 0, 0], [0, 1.0, 0], [0.5, 0, 0]]], np.float32)  # d = 1, 1, 0.25
+    i2, d2 = O.knn_fwd(q, r, K=2, version=2)
+    assert i2.tolist() == [[[2, 1]]] and d2.tolist() == [[[0.25, 1.0]]]
+    i3, d3 = O.knn_fwd(q, r, K=2, version=3)
+    assert i3.tolist() == [[[2, 0]]] and d3.tolist() == [[[0.25, 1.0]]]
+    # equal distance never evicts: refs 3,4 tie with the current max
+    r = np.array([[[0.5, 0, 0], [1.0, 0, 0], [0.2, 0, 0], [0, 1.0, 0], [0, 0, 1.0]]], np.float32)
+    i, _ = O.knn_fwd(q, r, K=2, version=2)
+    assert i.tolist() == [[[0, 2]]]
+    # K=3 generic layout: slots (0,1,2) then ref3 (d=.01) replaces the first max (slot 1)
+    r = np.array([[[0.3, 0, 0], [0.9, 0, 0], [0.9, 0, 0], [0.1, 0, 0]]], np.float32)
+    i, d = O.knn_fwd(q, r, K=3, version=3)
+    assert i.tolist() == [[[0, 3, 2]]]
+
+
+def test_knn_padding_rules(O):
+    r = rng(8)
+    p1 = r.standard_normal((2, 5, 3)).astype(np.float32)
+    p2 = r.standard_normal((2, 6, 3)).astype(np.float32)
+    l1 = np.array([3, 5])
+    l2 = np.array([2, 6])
+    for v, pad_i, pad_d in ((0, -1, np.inf), (1, -1, np.inf), (2, 0, 0.0)):
+        idx, d = O.knn_fwd(p1, p2, l1, l2, K=4, version=v)
+        assert (idx[0, 3:] == 0).all() and (d[0, 3:] == 0).all()  # rows >= lengths1
+        assert (idx[0, :3, 2:] == pad_i).all() and (d[0, :3, 2:] == pad_d).all()
+        assert (idx[0, :3, :2] >= 0).all() and (idx[0, :3, :2] < 2).all()
+        assert (idx[1] >= 0).all()
+
+
+def test_knn_brute_force(O):
+    r = rng(9)
+    for dt, D, K, norm, v in ((np.float32, 3, 5, 2, -1), (np.float32, 3, 16, 2, 2),
+                              (np.float64, 4, 7, 1, -1), (np.float32, 40, 9, 2, 0),
+                              (np.float32, 10, 3, 2, 1)):
+        p1 = r.standard_normal((2, 30, D)).astype(dt)
+        p2 = r.standard_normal((2, 80, D)).astype(dt)
+        idx, d = O.knn_fwd(p1, p2, K=K, norm=norm, version=v)
+        diff = p1[:, :, None, :].astype(np.float64) - p2[:, None, :, :]
+        full = (diff ** 2).sum(-1) if norm == 2 else np.abs(diff).sum(-1)
+        ref_idx = np.argsort(full, axis=2, kind="stable")[:, :, :K]
+        order = np.argsort(d, axis=2, kind="stable")
+        got = np.take_along_axis(idx, order, 2)
+        assert np.array_equal(got, ref_idx)
+        np.testing.assert_allclose(np.sort(d, 2), np.take_along_axis(full, ref_idx, 2), rtol=1e-5)
+
+
+def test_knn_f32_bits_exact_arithmetic(O):
+    r = rng(10)
+    p1 = r.standard_normal((1, 3, 3)).astype(np.float32)
+    p2 = r.standard_normal((1, 5, 3)).astype(np.float32)
+    idx, d = O.knn_fwd(p1, p2, K=5)
+    for j in range(3):
+        for s in range(5):
+            k = idx[0, j, s]
+            e = exact.knn_l2_f32([exact.f32_sub(p1[0, j, c], p2[0, k, c]) for c in range(3)])
+            assert d[0, j, s].view(np.uint32) == np.float32(e).view(np.uint32)
+
+
+def test_knn_backward_closed_form(O):
+    r = rng(11)
+    p1 = r.standard_normal((2, 12, 3)).astype(np.float32)
+    p2 = r.standard_normal((2, 15, 3)).astype(np.float32)
+    l1, l2 = np.array([12, 7]), np.array([15, 2])
+    for norm in (1, 2):
+        idx, _ = O.knn_fwd(p1, p2, l1, l2, K=4, norm=norm, version=0)  # -1 padding
+        g = r.random((2, 12, 4)).astype(np.float32)
+        g1, g2 = O.knn_bwd(p1, p2, l1, l2, idx, norm, g, accum_f64=True)
+        e1 = np.zeros((2, 12, 3))
+        e2 = np.zeros((2, 15, 3))
+        for n in range(2):
+            for i in range(l1[n]):
+                for k in range(4):
+                    j = idx[n, i, k]
+                    if j < 0:
+                        continue
+                    dv = p1[n, i].astype(np.float64) - p2[n, j]
+                    c = 2 * g[n, i, k] * dv if norm == 2 else g[n, i, k] * np.sign(dv)
+                    e1[n, i] += c
+                    e2[n, j] -= c
+        np.testing.assert_allclose(g1, e1, rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(g2, e2, rtol=1e-5, atol=1e-6)
+
+
+def test_knn_cpu_baseline_restatement(O):
+    """knn.cpp semantics: ascending (dist, idx), padding -1, rows sorted."""
+    r = rng(12)
+    p1 = r.standard_normal((2, 20, 3)).astype(np.float32)
+    p2 = r.standard_normal((2, 50, 3)).astype(np.float32)
+    l1, l2 = np.array([20, 10]), np.array([50, 3])
+    idx, d = O.cpu_knn_fwd_f32(p1, p2, l1, l2, K=5)
+    full = ((p1[:, :, None, :].astype(np.float64) - p2[:, None, :, :]) ** 2).sum(-1)
+    for n in range(2):
+        ref = np.argsort(full[n, :, :l2[n]], axis=1, kind="stable")[:, :5]
+        k = min(5, l2[n])
+        assert np.array_equal(idx[n, :l1[n], :k], ref[:l1[n], :k])
+        assert (idx[n, :l1[n], k:] == -1).all() and (idx[n, l1[n]:] == -1).all()
+    i8, d8 = O.cpu_knn_fwd_f32(p1, p2, l1, l2, K=5, nthreads=4)
+    assert np.array_equal(i8, idx) and np.array_equal(d8, d)
+
+
+# ---------------------------------------------------------------------- fps
+
+def fps_f64(points, m):
+    """Plain furthest point sampling in float64 (no ties expected)."""
+    n = points.shape[0]
+    temp = np.full(n, 1e10)
+    valid = (points.astype(np.float64) ** 2).sum(1) > 1e-3
+    out = [0]
+    for _ in range(1, m):
+        d = ((points - points[out[-1]]) ** 2).sum(1)
+        temp = np.where(valid, np.minimum(temp, d), temp)
+        cand = np.where(valid, temp, -1.0)
+        out.append(int(np.argmax(cand)))
+    return out
+
+
+def test_fps_block_size_and_rank(O):
+    assert [O.fps_block_size(n) for n in (1, 2, 3, 7, 20, 511, 512, 513, 65536)] == \
+        [1, 2, 2, 4, 16, 256, 512, 512, 512]
+    # bit-reversed thread order: N=7 -> BS=4, per=2
+    assert [O.fps_rank(k, 7) for k in range(7)] == [0, 4, 2, 6, 1, 5, 3]
+
+
+def test_fps_tie_order_literal_tree_vs_closed_form(O):
+    """Origin first, then six points at distance exactly 1: every one ties.
+    The reference's tree reduction picks the lowest rank (k=4 for N=7), not
+    the lowest index."""
+    pts = np.array([[[0, 0, 0], [1, 0, 0], [-1, 0, 0], [0, 1, 0], [0, -1, 0], [0, 0, 1],
+                     [0, 0, -1]]], np.float32)
+    idx = O.fps(pts, 2)
+    ranks = [O.fps_rank(k, 7) for k in range(1, 7)]
+    assert idx[0, 1] == 1 + int(np.argmin(ranks)) == 4
+    # larger symmetric case: 2^10 points on a circle of equal radius around
+    # the start point; the closed form must agree with the literal tree
+    ang = np.arange(1023) * (2 * np.pi / 1023)
+    circ = np.stack([np.cos(ang), np.sin(ang), np.zeros_like(ang)], 1)
+    pts = np.concatenate([np.zeros((1, 3)), circ]).astype(np.float32)[None]
+    d = np.array([exact.sq3_f32(*pts[0, k]) for k in range(1, 1024)], np.float32)
+    ties = np.flatnonzero(d == d.max()) + 1
+    assert len(ties) > 1
+    idx = O.fps(pts, 2)
+    assert idx[0, 1] == ties[np.argmin([O.fps_rank(int(k), 1024) for k in ties])]
+
+
+def test_fps_known_configurations(O):
+    # all-degenerate cloud -> every sample is index 0 (test_fps.py:889-910)
+    pts = (rng(13).standard_normal((1, 20, 3)) * 1e-6).astype(np.float32)
+    assert (O.fps(pts, 8) == 0).all()
+    # degenerate points are never selected (test_fps.py:462-475)
+    pts = rng(14).standard_normal((1, 10, 3)).astype(np.float32)
+    pts[0, 5:8] = 1e-4
+    idx = O.fps(pts, 5)
+    assert len(set(idx[0].tolist())) == 5 and not set(idx[0].tolist()) & {5, 6, 7}
+    # 5x5 grid in z=0 (test_fps.py:442-460)
+    x = np.linspace(-1, 1, 5)
+    g = np.stack(np.meshgrid(x, x, indexing="ij"), -1).reshape(-1, 2)
+    pts = np.concatenate([g, np.zeros((25, 1))], 1).astype(np.float32)[None]
+    idx = O.fps(pts, 5)
+    assert idx[0, 0] == 0 and len(set(idx[0].tolist())) == 5
+
+
+def test_fps_brute_force(O):
+    r = rng(15)
+    for n, m in ((20, 5), (100, 30), (1000, 200)):
+        pts = r.standard_normal((2, n, 3)).astype(np.float32)
+        idx = O.fps(pts, m)
+        for b in range(2):
+            assert idx[b].tolist() == fps_f64(pts[b].astype(np.float64), m)
+    # float64 and float16 inputs follow the same selection on well-separated data
+    pts = r.standard_normal((1, 60, 3))
+    assert O.fps(pts, 20)[0].tolist() == fps_f64(pts[0], 20)
+    assert O.fps(pts.astype(np.float16), 10)[0, 0] == 0
+
+
+def test_fps_cpu_baseline_restatement(O):
+    """fps.cpp semantics (the reference tests' reference_fps_cpu loop)."""
+    r = rng(16)
+    pts = r.standard_normal((3, 50, 3)).astype(np.float32)
+    idx = O.cpu_fps_f32(pts, 12)
+    for b in range(3):
+        assert idx[b].tolist() == fps_f64(pts[b].astype(np.float64), 12)
+    assert np.array_equal(O.cpu_fps_f32(pts, 12, nthreads=3), idx)
+    # CPU semantics select degenerate points first (FLT_MAX distance)
+    pts[0, 7] = 0.0
+    assert O.cpu_fps_f32(pts, 3)[0, 1] == 7
+
+
+# ------------------------------------------------------------------- gather
+
+def test_gather_closed_form(O):
+    r = rng(17)
+    pts = r.standard_normal((2, 6, 20)).astype(np.float32)
+    idx = r.integers(0, 20, (2, 8))
+    out = O.gather_fwd(pts, idx)
+    assert np.array_equal(out, np.take_along_axis(pts, idx[:, None, :].repeat(6, 1), 2))
+    go = r.standard_normal((2, 6, 8)).astype(np.float32)
+    gp = O.gather_bwd(go, idx, 20, accum_f64=True)
+    e = np.zeros((2, 6, 20))
+    for b in range(2):
+        np.add.at(e[b].T, idx[b], go[b].T.astype(np.float64))
+    np.testing.assert_allclose(gp, e, rtol=1e-6, atol=1e-6)
+    assert np.array_equal(O.cpu_gather_fwd_f32(pts, idx), out)
+    np.testing.assert_allclose(O.cpu_gather_bwd_f32(go, idx, 20), e, rtol=1e-6, atol=1e-6)
+    with pytest.raises(ValueError):
+        O.gather_fwd(pts, np.full((2, 8), 20))

@@ -1,0 +1,188 @@
+// gather.hip -- gather_points forward/backward for gfx950 (HBM-bound).
+//
+// Forward (replaces gather_points_kernel, fps.cu:63-76): one thread per
+// (cloud, sample, group of 8 channels) reads its index once and gathers the
+// channels; stores are coalesced along the sample axis.
+// Backward (replaces zeros + gather_points_grad_kernel, fps.cu:79-98,376):
+// instead of a full zero-fill followed by scattered atomics, build a per-cloud
+// inverse map pos[b, n] = smallest sample j with idx[b, j] == n, then write
+// grad_points in ONE dense, coalesced pass (grad_out[b,c,pos] or 0).  Samples
+// that repeat an index (j > pos) are added afterwards with atomics, which is
+// the reference's accumulation for duplicates.  For unique indices every
+// value equals the reference's 0 + g exactly.
+// Indices outside [0, N) are ignored (forward writes 0); the reference reads
+// out of bounds there.
+#include "tpo_common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace tpo {
+
+constexpr int GATHER_CGROUP = 8;
+
+template <typename T>
+__global__ __launch_bounds__(256) void gather_fwd_kernel(const T* __restrict__ pts,
+                                                         const int64_t* __restrict__ idx,
+                                                         int64_t B, int64_t C, int64_t N,
+                                                         int64_t M, T* __restrict__ out) {
+  const int64_t ncg = (C + GATHER_CGROUP - 1) / GATHER_CGROUP;
+  const int64_t total = B * ncg * M;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t j = t % M;
+    const int64_t bc = t / M;
+    const int64_t cg = bc % ncg, b = bc / ncg;
+    const int64_t a = idx[b * M + j];
+    const bool ok = a >= 0 && a < N;
+    const int64_t c0 = cg * GATHER_CGROUP;
+    const int64_t cn = min((int64_t)GATHER_CGROUP, C - c0);
+    T v[GATHER_CGROUP];
+#pragma unroll
+    for (int c = 0; c < GATHER_CGROUP; ++c)
+      v[c] = (c < cn && ok) ? pts[((b * C) + c0 + c) * N + a] : (T)0;
+#pragma unroll
+    for (int c = 0; c < GATHER_CGROUP; ++c)
+      if (c < cn) out[((b * C) + c0 + c) * M + j] = v[c];
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* __restrict__ p, int64_t n,
+                                                       int32_t v) {
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n;
+       t += (int64_t)gridDim.x * blockDim.x)
+    p[t] = v;
+}
+
+// pos[b, idx[b, j]] = min over j
+__global__ __launch_bounds__(256) void gather_inverse_kernel(const int64_t* __restrict__ idx,
+                                                             int64_t B, int64_t N, int64_t M,
+                                                             int32_t* __restrict__ pos) {
+  const int64_t total = B * M;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = t / M, j = t - b * M;
+    const int64_t a = idx[t];
+    if (a >= 0 && a < N) atomicMin(pos + b * N + a, (int32_t)j);
+  }
+}
+
+// grad_points[b, c, n] = pos >= 0 ? grad_out[b, c, pos] : 0, one thread per
+// (b, n), looping over channels (stores coalesced along n).
+template <typename T>
+__global__ __launch_bounds__(256) void gather_bwd_dense_kernel(const T* __restrict__ go,
+                                                               const int32_t* __restrict__ pos,
+                                                               int64_t B, int64_t C, int64_t N,
+                                                               int64_t M, T* __restrict__ gp) {
+  const int64_t total = B * N;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = t / N, n = t - b * N;
+    const int32_t p = pos[t];
+    const bool hit = p != 0x7fffffff;
+    const T* __restrict__ src = go + b * C * M + (hit ? p : 0);
+    T* __restrict__ dst = gp + b * C * N + n;
+    int64_t c = 0;
+    for (; c + 4 <= C; c += 4) {
+      T v0 = hit ? src[(c + 0) * M] : (T)0;
+      T v1 = hit ? src[(c + 1) * M] : (T)0;
+      T v2 = hit ? src[(c + 2) * M] : (T)0;
+      T v3 = hit ? src[(c + 3) * M] : (T)0;
+      dst[(c + 0) * N] = v0;
+      dst[(c + 1) * N] = v1;
+      dst[(c + 2) * N] = v2;
+      dst[(c + 3) * N] = v3;
+    }
+    for (; c < C; ++c) dst[c * N] = hit ? src[c * M] : (T)0;
+  }
+}
+
+// samples whose index repeats an earlier sample's: atomic add
+template <typename T>
+__global__ __launch_bounds__(256) void gather_bwd_dup_kernel(const T* __restrict__ go,
+                                                             const int64_t* __restrict__ idx,
+                                                             const int32_t* __restrict__ pos,
+                                                             int64_t B, int64_t C, int64_t N,
+                                                             int64_t M, T* __restrict__ gp) {
+  const int64_t total = B * M;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = t / M, j = t - b * M;
+    const int64_t a = idx[t];
+    if (a < 0 || a >= N) continue;
+    if (pos[b * N + a] == (int32_t)j) continue;
+    for (int64_t c = 0; c < C; ++c) atomic_add(gp + (b * C + c) * N + a, go[(b * C + c) * M + j]);
+  }
+}
+
+static unsigned grid_for(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 1 << 20) g = 1 << 20;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+template <typename T>
+static void fwd(const void* pts, const int64_t* idx, int64_t B, int64_t C, int64_t N, int64_t M,
+                void* out, hipStream_t s) {
+  const int64_t total = B * ((C + GATHER_CGROUP - 1) / GATHER_CGROUP) * M;
+  hipLaunchKernelGGL(gather_fwd_kernel<T>, dim3(grid_for(total)), dim3(256), 0, s,
+                     (const T*)pts, idx, B, C, N, M, (T*)out);
+}
+
+template <typename T>
+static void bwd(const void* go, const int64_t* idx, int64_t B, int64_t C, int64_t N, int64_t M,
+                void* gp, int32_t* pos, hipStream_t s) {
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for(B * N)), dim3(256), 0, s, pos, B * N,
+                     (int32_t)0x7fffffff);
+  if (M > 0)
+    hipLaunchKernelGGL(gather_inverse_kernel, dim3(grid_for(B * M)), dim3(256), 0, s, idx, B, N,
+                       M, pos);
+  hipLaunchKernelGGL(gather_bwd_dense_kernel<T>, dim3(grid_for(B * N)), dim3(256), 0, s,
+                     (const T*)go, pos, B, C, N, M, (T*)gp);
+  if (M > 0)
+    hipLaunchKernelGGL(gather_bwd_dup_kernel<T>, dim3(grid_for(B * M)), dim3(256), 0, s,
+                       (const T*)go, idx, pos, B, C, N, M, (T*)gp);
+}
+
+}  // namespace tpo
+
+using namespace tpo;
+
+extern "C" int tpo_gather_fwd(int dtype, const void* points, const int64_t* idx, int64_t B,
+                              int64_t C, int64_t N, int64_t M, void* out, void* stream) {
+  if (B < 0 || C < 0 || N < 0 || M < 0)
+    return set_error(TPO_ERR_ARG, "tpo_gather_fwd: negative size");
+  if (B == 0 || C == 0 || M == 0) return TPO_OK;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case TPO_F32: fwd<float>(points, idx, B, C, N, M, out, s); break;
+    case TPO_F64: fwd<double>(points, idx, B, C, N, M, out, s); break;
+    case TPO_F16: fwd<half_t>(points, idx, B, C, N, M, out, s); break;
+    default: return set_error(TPO_ERR_DTYPE, "tpo_gather_fwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("tpo_gather_fwd");
+}
+
+extern "C" int64_t tpo_gather_bwd_workspace_size(int64_t B, int64_t N) {
+  if (B < 0 || N < 0) return -1;
+  return ((B * N * 4 + 255) / 256) * 256;
+}
+
+extern "C" int tpo_gather_bwd(int dtype, const void* grad_out, const int64_t* idx, int64_t B,
+                              int64_t C, int64_t N, int64_t M, void* grad_points, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+  if (B < 0 || C < 0 || N < 0 || M < 0 || N >= ((int64_t)1 << 31) || M >= ((int64_t)1 << 31))
+    return set_error(TPO_ERR_ARG, "tpo_gather_bwd: bad sizes");
+  if (B == 0 || C == 0 || N == 0) return TPO_OK;
+  if (!workspace || workspace_bytes < B * N * 4)
+    return set_error(TPO_ERR_WORKSPACE, "tpo_gather_bwd: workspace of %lld bytes < %lld",
+                     (long long)workspace_bytes, (long long)(B * N * 4));
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* pos = (int32_t*)workspace;
+  switch (dtype) {
+    case TPO_F32: bwd<float>(grad_out, idx, B, C, N, M, grad_points, pos, s); break;
+    case TPO_F64: bwd<double>(grad_out, idx, B, C, N, M, grad_points, pos, s); break;
+    case TPO_F16: bwd<half_t>(grad_out, idx, B, C, N, M, grad_points, pos, s); break;
+    default: return set_error(TPO_ERR_DTYPE, "tpo_gather_bwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("tpo_gather_bwd");
+}

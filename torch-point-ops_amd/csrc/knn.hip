@@ -1,0 +1,424 @@
+// knn.hip -- K nearest neighbours (forward/backward) for gfx950.
+//
+// Forward (replaces KNearestNeighborKernelV0..V3, knn.cu:16-227).
+//   One query per lane; the wave's 64 queries belong to one cloud, so the
+//   reference cloud is walked in the same order by every lane and each
+//   reference point is a wave-uniform scalar load (SGPRs, no LDS).
+//   The output must be the reference's MinK slot layout (mink.cuh:77-121),
+//   which depends on the whole insertion history, so every lane replays the
+//   MinK process exactly: the first K references fill the slots in order; a
+//   later reference replaces the FIRST slot holding the maximum when it is
+//   strictly smaller.  To keep the wave from executing the O(K) slot update
+//   whenever any one lane needs it, references are processed in chunks of 32:
+//   the distances of a chunk are compared against the lane's current maximum
+//   into a 32-bit candidate mask (the maximum only decreases, so the mask is
+//   a superset of the real insertions); then each lane walks its own
+//   candidates in index order, re-checking against the updated maximum.  The
+//   wave pays for max-over-lanes(candidates per chunk), which after the first
+//   few hundred references is 0-2 per chunk.
+//   Version semantics (dispatch.cuh:106-147): all versions select the same
+//   set except version 3 with K == 2 (RegisterMinK<2>, mink.cuh:212-265,
+//   keeps the pair sorted); versions 0/1 pad missing slots with (-1, +inf),
+//   versions 2/3 with (0, 0); rows >= lengths1 are (0, 0).
+//   K > 32 (versions 0/1 only) keeps the slots in the output rows, like the
+//   reference's global-memory MinK.
+// Backward (replaces KNearestNeighborBackwardKernel, knn.cu:400-466).
+//   One thread per query row sums its K contributions to grad_p1 in
+//   registers (plain stores, every row written) and scatters -diff onto
+//   grad_p2 with hardware atomics (grad_p2 zero-filled first).
+#include "tpo_common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace tpo {
+namespace {
+
+constexpr int KNN_CHUNK = 32;
+
+template <typename T>
+__global__ __launch_bounds__(256) void fill_kernel(T* __restrict__ p, int64_t n, T v) {
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n;
+       t += (int64_t)gridDim.x * blockDim.x)
+    p[t] = v;
+}
+
+// Distance between the lane's query and reference r (knn.cu:148-158).
+// DT > 0: compile-time dimension, query in registers; DT == 0: runtime D,
+// query read through qp.
+template <typename T, int DT, int NORM>
+__device__ __forceinline__ T knn_dist(const T* qr, const T* __restrict__ qp,
+                                      const T* __restrict__ r, int D) {
+  T acc = (T)0;
+  if constexpr (DT > 0) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      const T diff = (T)(qr[d] - r[d]);
+      acc = NORM == 2 ? knn_acc2(acc, diff, d == 0) : knn_acc1(acc, diff, d == 0);
+    }
+  } else {
+    for (int d = 0; d < D; ++d) {
+      const T diff = (T)(qp[d] - r[d]);
+      acc = NORM == 2 ? knn_acc2(acc, diff, d == 0) : knn_acc1(acc, diff, d == 0);
+    }
+  }
+  return acc;
+}
+
+// First slot holding the maximum among slots [0, K) (mink.cuh:96-104).
+template <typename T, int KC>
+__device__ __forceinline__ void first_max(const T (&sd)[KC], int K, T& m, int& ms) {
+  m = sd[0];
+  ms = 0;
+#pragma unroll
+  for (int s = 1; s < KC; ++s) {
+    if (s < K && sd[s] > m) {
+      m = sd[s];
+      ms = s;
+    }
+  }
+}
+
+template <typename T, int DT, int NORM, int KC>
+__global__ __launch_bounds__(256) void knn_fwd_kernel(
+    const T* __restrict__ p1, const T* __restrict__ p2, const int64_t* __restrict__ len1,
+    const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb, int pad_sentinel,
+    int sorted2, int64_t* __restrict__ idxs, T* __restrict__ dists) {
+  const int n = blockIdx.x / nqb;
+  const int q = (blockIdx.x - n * nqb) * 256 + threadIdx.x;
+  if (q >= P1) return;
+  int64_t l1 = len1[n], l2 = len2[n];
+  l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+  l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
+  const int L2 = (int)l2;
+  const size_t row = (size_t)n * P1 + q;
+  int64_t* __restrict__ io = idxs + row * K;
+  T* __restrict__ dout = dists + row * K;
+  if (q >= l1) {  // never written by the reference: its zeros
+    for (int s = 0; s < K; ++s) {
+      io[s] = 0;
+      dout[s] = (T)0;
+    }
+    return;
+  }
+  const int Dd = DT > 0 ? DT : D;
+  const T* __restrict__ qp = p1 + row * Dd;
+  const T* __restrict__ rp = p2 + (size_t)n * P2 * Dd;
+  T qr[DT > 0 ? DT : 1];
+  if constexpr (DT > 0) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d) qr[d] = qp[d];
+  }
+
+  T sd[KC];
+  int si[KC];
+  int size = 0;
+  if (sorted2) {
+    // RegisterMinK<.., 2>::add, mink.cuh:221-248
+    T d0 = Lim<T>::inf(), d1 = Lim<T>::inf();
+    int i0 = -1, i1 = -1;
+    for (int j = 0; j < L2; ++j) {
+      const T d = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)j * Dd, D);
+      if (j == 0) {
+        d0 = d;
+        i0 = 0;
+      } else if (d < d0) {  // shift down, new pair head
+        d1 = d0;
+        i1 = i0;
+        d0 = d;
+        i0 = j;
+      } else if (j == 1 || d < d1) {  // second slot (always taken for j == 1)
+        d1 = d;
+        i1 = j;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < KC; ++s) {
+      sd[s] = s == 0 ? d0 : d1;
+      si[s] = s == 0 ? i0 : i1;
+    }
+    size = L2 < 2 ? L2 : 2;
+  } else {
+    // fill phase: slot s <- reference s
+    const int fill = L2 < K ? L2 : K;
+#pragma unroll
+    for (int s = 0; s < KC; ++s) {
+      if (s < fill) {
+        sd[s] = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)s * Dd, D);
+        si[s] = s;
+      } else {
+        sd[s] = Lim<T>::inf();
+        si[s] = -1;
+      }
+    }
+    size = fill;
+    if (L2 > K) {
+      T thr;
+      int ms;
+      first_max<T, KC>(sd, K, thr, ms);
+      for (int j0 = K; j0 < L2; j0 += KNN_CHUNK) {
+        const int cn = min(KNN_CHUNK, L2 - j0);
+        uint32_t mask = 0;
+        if (cn == KNN_CHUNK) {
+#pragma unroll
+          for (int c = 0; c < KNN_CHUNK; ++c) {
+            const T d = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)(j0 + c) * Dd, D);
+            mask |= (d < thr) ? (1u << c) : 0u;
+          }
+        } else {
+          for (int c = 0; c < cn; ++c) {
+            const T d = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)(j0 + c) * Dd, D);
+            mask |= (d < thr) ? (1u << c) : 0u;
+          }
+        }
+        while (mask) {
+          const int c = __builtin_ctz(mask);
+          mask &= mask - 1;
+          const int j = j0 + c;
+          const T d = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)j * Dd, D);
+          if (d < thr) {
+#pragma unroll
+            for (int s = 0; s < KC; ++s) {
+              if (s == ms) {
+                sd[s] = d;
+                si[s] = j;
+              }
+            }
+            first_max<T, KC>(sd, K, thr, ms);
+          }
+        }
+      }
+    }
+  }
+  const int64_t pad_i = pad_sentinel ? -1 : 0;
+  const T pad_d = pad_sentinel ? Lim<T>::inf() : (T)0;
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    if (s < K) {
+      io[s] = s < size ? (int64_t)si[s] : pad_i;
+      dout[s] = s < size ? sd[s] : pad_d;
+    }
+  }
+}
+
+// K > 32: MinK held in the output row (the reference's V0/V1 layout).
+template <typename T, int NORM>
+__global__ __launch_bounds__(256) void knn_fwd_global_kernel(
+    const T* __restrict__ p1, const T* __restrict__ p2, const int64_t* __restrict__ len1,
+    const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb,
+    int64_t* __restrict__ idxs, T* __restrict__ dists) {
+  const int n = blockIdx.x / nqb;
+  const int q = (blockIdx.x - n * nqb) * 256 + threadIdx.x;
+  if (q >= P1) return;
+  int64_t l1 = len1[n], l2 = len2[n];
+  l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+  l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
+  const size_t row = (size_t)n * P1 + q;
+  int64_t* __restrict__ io = idxs + row * K;
+  T* __restrict__ dout = dists + row * K;
+  if (q >= l1) {
+    for (int s = 0; s < K; ++s) {
+      io[s] = 0;
+      dout[s] = (T)0;
+    }
+    return;
+  }
+  for (int s = 0; s < K; ++s) {  // mink.cuh:83-86
+    io[s] = -1;
+    dout[s] = Lim<T>::inf();
+  }
+  const T* __restrict__ qp = p1 + row * D;
+  const T* __restrict__ rp = p2 + (size_t)n * P2 * D;
+  T thr = Lim<T>::inf();
+  int ms = 0, size = 0;
+  for (int j = 0; j < (int)l2; ++j) {
+    const T d = knn_dist<T, 0, NORM>(nullptr, qp, rp + (size_t)j * D, D);
+    if (size < K) {
+      dout[size] = d;
+      io[size] = j;
+      ++size;
+      if (size == K) {
+        thr = dout[0];
+        ms = 0;
+        for (int s = 1; s < K; ++s)
+          if (dout[s] > thr) {
+            thr = dout[s];
+            ms = s;
+          }
+      }
+    } else if (d < thr) {
+      dout[ms] = d;
+      io[ms] = j;
+      thr = dout[0];
+      ms = 0;
+      for (int s = 1; s < K; ++s)
+        if (dout[s] > thr) {
+          thr = dout[s];
+          ms = s;
+        }
+    }
+  }
+}
+
+template <typename T, int NORM>
+__global__ __launch_bounds__(256) void knn_bwd_kernel(
+    const T* __restrict__ p1, const T* __restrict__ p2, const int64_t* __restrict__ len1,
+    const int64_t* __restrict__ idxs, const T* __restrict__ gd, int64_t N, int64_t P1, int64_t P2,
+    int64_t D, int64_t K, T* __restrict__ gp1, T* __restrict__ gp2) {
+  const int64_t total = N * P1;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = t / P1, q = t - n * P1;
+    int64_t l1 = len1[n];
+    l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+    const bool active = q < l1;
+    for (int64_t d = 0; d < D; ++d) {
+      T acc = (T)0;
+      if (active) {
+        const T v1 = p1[t * D + d];
+        for (int64_t k = 0; k < K; ++k) {
+          const int64_t r = idxs[t * K + k];
+          if (r < 0 || r >= P2) continue;  // -1 padding (knn.cu:439); others invalid
+          const T g = gd[t * K + k];
+          const T v2 = p2[(n * P2 + r) * D + d];
+          T diff;
+          if (NORM == 1) {  // knn.cu:445-448
+            const T sign = v1 > v2 ? (T)1 : (v1 == v2 ? (T)0 : (T)-1);
+            diff = (T)(g * sign);
+          } else {
+            diff = (T)((T)((T)2 * g) * (T)(v1 - v2));
+          }
+          acc = (T)(acc + diff);
+          atomic_add(gp2 + (n * P2 + r) * D + d, (T)(-diff));
+        }
+      }
+      gp1[t * D + d] = acc;
+    }
+  }
+}
+
+unsigned grid_for(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 1 << 20) g = 1 << 20;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+template <typename T, int DT, int NORM, int KC>
+void launch_fwd_kc(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
+                   int P1, int P2, int D, int K, int pad, int sorted2, int64_t* idxs, void* dists,
+                   hipStream_t s) {
+  const int nqb = (P1 + 255) / 256;
+  hipLaunchKernelGGL((knn_fwd_kernel<T, DT, NORM, KC>), dim3(N * nqb), dim3(256), 0, s,
+                     (const T*)p1, (const T*)p2, l1, l2, P1, P2, D, K, nqb, pad, sorted2, idxs,
+                     (T*)dists);
+}
+
+template <typename T, int DT, int NORM>
+void launch_fwd_dt(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
+                   int P1, int P2, int D, int K, int pad, int sorted2, int64_t* idxs, void* dists,
+                   hipStream_t s) {
+  if (K <= 4) launch_fwd_kc<T, DT, NORM, 4>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  else if (K <= 8) launch_fwd_kc<T, DT, NORM, 8>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  else if (K <= 16) launch_fwd_kc<T, DT, NORM, 16>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  else launch_fwd_kc<T, DT, NORM, 32>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+}
+
+template <typename T, int NORM>
+void launch_fwd_norm(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
+                     int P1, int P2, int D, int K, int pad, int sorted2, int64_t* idxs,
+                     void* dists, hipStream_t s) {
+  if (K > 32) {
+    const int nqb = (P1 + 255) / 256;
+    hipLaunchKernelGGL((knn_fwd_global_kernel<T, NORM>), dim3(N * nqb), dim3(256), 0, s,
+                       (const T*)p1, (const T*)p2, l1, l2, P1, P2, D, K, nqb, idxs, (T*)dists);
+  } else if (D == 3) {
+    launch_fwd_dt<T, 3, NORM>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  } else {
+    launch_fwd_dt<T, 0, NORM>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  }
+}
+
+template <typename T>
+void launch_fwd(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
+                int P1, int P2, int D, int K, int norm, int pad, int sorted2, int64_t* idxs,
+                void* dists, hipStream_t s) {
+  if (norm == 1) launch_fwd_norm<T, 1>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  else launch_fwd_norm<T, 2>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+}
+
+template <typename T>
+void launch_bwd(const void* p1, const void* p2, const int64_t* l1, const int64_t* idxs,
+                const void* gd, int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K, int norm,
+                void* gp1, void* gp2, hipStream_t s) {
+  hipLaunchKernelGGL(fill_kernel<T>, dim3(grid_for(N * P2 * D)), dim3(256), 0, s, (T*)gp2,
+                     N * P2 * D, (T)0);
+  if (norm == 1)
+    hipLaunchKernelGGL((knn_bwd_kernel<T, 1>), dim3(grid_for(N * P1)), dim3(256), 0, s,
+                       (const T*)p1, (const T*)p2, l1, idxs, (const T*)gd, N, P1, P2, D, K,
+                       (T*)gp1, (T*)gp2);
+  else
+    hipLaunchKernelGGL((knn_bwd_kernel<T, 2>), dim3(grid_for(N * P1)), dim3(256), 0, s,
+                       (const T*)p1, (const T*)p2, l1, idxs, (const T*)gd, N, P1, P2, D, K,
+                       (T*)gp1, (T*)gp2);
+}
+
+// dispatch.cuh:114-147
+bool check_version(int v, int64_t D, int64_t K) {
+  if (v == 0) return true;
+  if (v == 1) return D >= 1 && D <= 32;
+  if (v == 2) return D >= 1 && D <= 8 && K >= 1 && K <= 32;
+  if (v == 3) return D >= 1 && D <= 8 && K >= 1 && K <= 4;
+  return false;
+}
+int choose_version(int64_t D, int64_t K) {
+  for (int v = 3; v >= 1; --v)
+    if (check_version(v, D, K)) return v;
+  return 0;
+}
+
+}  // namespace
+}  // namespace tpo
+
+using namespace tpo;
+
+extern "C" int tpo_knn_fwd(int dtype, const void* p1, const void* p2, const int64_t* lengths1,
+                           const int64_t* lengths2, int64_t N, int64_t P1, int64_t P2, int64_t D,
+                           int64_t K, int norm, int version, int64_t* idxs, void* dists,
+                           int* version_out, void* stream) {
+  if (N < 0 || P1 < 0 || P2 < 0 || D < 1 || K < 0 || N >= (1 << 20) || P1 >= (1 << 30) ||
+      P2 >= (1 << 30) || D >= (1 << 20) || K >= (1 << 20))
+    return set_error(TPO_ERR_ARG, "tpo_knn_fwd: bad sizes");
+  if (norm != 1 && norm != 2) return set_error(TPO_ERR_ARG, "Norm must be 1 or 2.");
+  // knn.cu:332-338: invalid explicit versions are replaced by the automatic one
+  int v = (version >= 0 && check_version(version, D, K)) ? version : choose_version(D, K);
+  if (version_out) *version_out = v;
+  if (N == 0 || P1 == 0 || K == 0) return TPO_OK;
+  const int pad = v <= 1;
+  const int sorted2 = (v == 3 && K == 2);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case TPO_F32: launch_fwd<float>(p1, p2, lengths1, lengths2, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
+    case TPO_F64: launch_fwd<double>(p1, p2, lengths1, lengths2, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
+    case TPO_F16: launch_fwd<half_t>(p1, p2, lengths1, lengths2, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
+    default: return set_error(TPO_ERR_DTYPE, "tpo_knn_fwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("tpo_knn_fwd");
+}
+
+extern "C" int tpo_knn_bwd(int dtype, const void* p1, const void* p2, const int64_t* lengths1,
+                           const int64_t* lengths2, const int64_t* idxs, int norm,
+                           const void* grad_dists, int64_t N, int64_t P1, int64_t P2, int64_t D,
+                           int64_t K, void* grad_p1, void* grad_p2, void* stream) {
+  (void)lengths2;
+  if (N < 0 || P1 < 0 || P2 < 0 || D < 1 || K < 0)
+    return set_error(TPO_ERR_ARG, "tpo_knn_bwd: bad sizes");
+  if (norm != 1 && norm != 2) return set_error(TPO_ERR_ARG, "Norm must be 1 or 2.");
+  if (N == 0 || (P1 == 0 && P2 == 0)) return TPO_OK;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case TPO_F32: launch_bwd<float>(p1, p2, lengths1, idxs, grad_dists, N, P1, P2, D, K, norm, grad_p1, grad_p2, s); break;
+    case TPO_F64: launch_bwd<double>(p1, p2, lengths1, idxs, grad_dists, N, P1, P2, D, K, norm, grad_p1, grad_p2, s); break;
+    case TPO_F16: launch_bwd<half_t>(p1, p2, lengths1, idxs, grad_dists, N, P1, P2, D, K, norm, grad_p1, grad_p2, s); break;
+    default: return set_error(TPO_ERR_DTYPE, "tpo_knn_bwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("tpo_knn_bwd");
+}

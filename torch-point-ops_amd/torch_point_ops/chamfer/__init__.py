@@ -1,0 +1,68 @@
+"""Chamfer distance (reference: torch_point_ops/chamfer/__init__.py:1-75).
+
+torch.ops.torch_point_ops_chamfer.chamfer_forward / chamfer_backward run the
+gfx950 kernels of libtpo_hip.so; this module adds the autograd formula and
+the FakeTensor kernels, as the reference does.
+"""
+import torch
+
+from .. import _C  # noqa: F401
+
+
+def _chamfer_backward(ctx, grad_dist1, grad_dist2, grad_idx1, grad_idx2):
+    # index outputs carry no gradient (reference chamfer/__init__.py:6-11)
+    xyz1, xyz2, idx1, idx2 = ctx.saved_tensors
+    return torch.ops.torch_point_ops_chamfer.chamfer_backward(
+        xyz1, xyz2, idx1, idx2, grad_dist1, grad_dist2
+    )
+
+
+def _chamfer_setup_context(ctx, inputs, output):
+    xyz1, xyz2 = inputs
+    _d1, _d2, idx1, idx2 = output
+    ctx.save_for_backward(xyz1, xyz2, idx1, idx2)
+
+
+torch.library.register_autograd(
+    "torch_point_ops_chamfer::chamfer_forward",
+    _chamfer_backward,
+    setup_context=_chamfer_setup_context,
+)
+
+
+@torch.library.register_fake("torch_point_ops_chamfer::chamfer_forward")
+def _chamfer_forward_fake(xyz1, xyz2):
+    b, n = xyz1.shape[0], xyz1.shape[1]
+    m = xyz2.shape[1]
+    like = dict(device=xyz1.device)
+    return (
+        torch.empty(b, n, dtype=xyz1.dtype, **like),
+        torch.empty(b, m, dtype=xyz1.dtype, **like),
+        torch.empty(b, n, dtype=torch.int32, **like),
+        torch.empty(b, m, dtype=torch.int32, **like),
+    )
+
+
+@torch.library.register_fake("torch_point_ops_chamfer::chamfer_backward")
+def _chamfer_backward_fake(xyz1, xyz2, idx1, idx2, grad_dist1, grad_dist2):
+    return torch.empty_like(xyz1), torch.empty_like(xyz2)
+
+
+def chamfer_distance(xyz1: torch.Tensor, xyz2: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Squared distance from every point to its nearest neighbour in the other cloud.
+
+    Args:
+        xyz1: (B, N, 3) point cloud 1.
+        xyz2: (B, M, 3) point cloud 2.
+
+    Returns:
+        dist1 (B, N) and dist2 (B, M), in the input dtype.  Inputs need not be
+        contiguous.
+    """
+    d1, d2, _i1, _i2 = torch.ops.torch_point_ops_chamfer.chamfer_forward(
+        xyz1.contiguous(), xyz2.contiguous()
+    )
+    return d1, d2
+
+
+from .chamfer import ChamferDistance  # noqa: E402
