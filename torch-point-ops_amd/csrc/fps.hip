@@ -67,10 +67,17 @@ template <> struct FpsConst<half_t> {
   __device__ static float tiny() { return 1e-3f; }
 };
 
+// One sorted point: coordinates and meta = rank | FPS_INVALID-if-skipped,
+// loaded as a single 16-byte access for float.
+template <typename T> struct FpsRec {
+  T x, y, z;
+  uint32_t meta;
+};
+
 struct FpsLayout {
   int64_t np;      // padded points per cloud = nb * s
   int64_t stride;  // bytes per cloud
-  int64_t off_x, off_y, off_z, off_t, off_m;
+  int64_t off_r, off_t;
 };
 
 template <typename T>
@@ -81,11 +88,8 @@ __host__ __device__ inline FpsLayout fps_layout(int64_t n) {
   L.np = nb * s;
   auto al = [](int64_t v) { return (v + 255) / 256 * 256; };
   int64_t o = 0;
-  L.off_x = o; o += al(L.np * (int64_t)sizeof(T));
-  L.off_y = o; o += al(L.np * (int64_t)sizeof(T));
-  L.off_z = o; o += al(L.np * (int64_t)sizeof(T));
+  L.off_r = o; o += al(L.np * (int64_t)sizeof(FpsRec<T>));
   L.off_t = o; o += al(L.np * (int64_t)sizeof(T));
-  L.off_m = o; o += al(L.np * 4);
   L.stride = o;
   return L;
 }
@@ -97,39 +101,95 @@ __device__ __forceinline__ uint32_t spread3(uint32_t v) {  // 4 bits -> every th
   return v;
 }
 
-template <typename V>
-__device__ __forceinline__ bool better(V va, uint32_t ra, V vb, uint32_t rb) {
-  return va > vb || (va == vb && ra < rb);
+// ------------------------------------------------------------ candidates
+// A candidate is (running-min value, rank); the better one has the larger
+// value, then the lower rank.  For float/half values (all >= +0) it is packed
+// into one 64-bit key, (value bits << 32) | (0xffffffff - rank), so "better"
+// is an unsigned compare and 0 means "no candidate"; wave reductions then run
+// on DPP lane swizzles.  double values keep a (value, rank) pair.
+struct CandF {
+  uint64_t k;
+};
+struct CandD {
+  double v;
+  uint32_t r;
+};
+template <typename T> struct FpsCand { typedef CandF type; };
+template <> struct FpsCand<double> { typedef CandD type; };
+
+__device__ __forceinline__ CandF cand_make(float v, uint32_t r, CandF*) {
+  return {((uint64_t)__float_as_uint(v) << 32) | (uint64_t)(0xffffffffu - r)};
 }
+__device__ __forceinline__ CandD cand_make(double v, uint32_t r, CandD*) { return {v, r}; }
+__device__ __forceinline__ CandF cand_none(CandF*) { return {0}; }
+__device__ __forceinline__ CandD cand_none(CandD*) { return {-1.0, 0xffffffffu}; }
+__device__ __forceinline__ bool cand_gt(CandF a, CandF b) { return a.k > b.k; }
+__device__ __forceinline__ bool cand_gt(CandD a, CandD b) {
+  return a.v > b.v || (a.v == b.v && a.r < b.r);
+}
+__device__ __forceinline__ bool cand_eq(CandF a, CandF b) { return a.k == b.k; }
+__device__ __forceinline__ bool cand_eq(CandD a, CandD b) { return a.v == b.v && a.r == b.r; }
+__device__ __forceinline__ bool cand_valid(CandF a) { return a.k != 0; }
+__device__ __forceinline__ bool cand_valid(CandD a) { return a.v >= 0.0; }
+__device__ __forceinline__ float cand_val(CandF a) { return __uint_as_float((uint32_t)(a.k >> 32)); }
+__device__ __forceinline__ double cand_val(CandD a) { return a.v; }
+__device__ __forceinline__ uint32_t cand_rank(CandF a) { return 0xffffffffu - (uint32_t)a.k; }
+__device__ __forceinline__ uint32_t cand_rank(CandD a) { return a.r; }
 
-template <typename V>
-__device__ __forceinline__ V shfl_xor_v(V v, int m) { return __shfl_xor(v, m, 64); }
-
-// Reduce (val, rank) to the wave's best; returns the best lane's values in
-// every lane and the index of (one) lane holding it.
-template <typename V>
-__device__ __forceinline__ int wave_best(V& val, uint32_t& rank) {
-  V bv = val;
-  uint32_t br = rank;
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t dpp_umax(uint32_t v) {
+  // folds into one v_max_u32_dpp; lanes of masked-off rows keep v
+  const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xf, false);
+  return o > v ? o : v;
+}
+// max over the 64 lanes (all active), in every lane
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+  v = dpp_umax<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v = dpp_umax<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+  v = dpp_umax<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_umax<0x140, 0xf>(v);  // row_mirror: each lane holds its row's max
+  v = dpp_umax<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+  v = dpp_umax<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+// Best candidate of the whole wave: the largest value word, then the largest
+// rank word among the lanes holding that value.
+__device__ __forceinline__ CandF wave_best(CandF c) {
+  const uint32_t hi = (uint32_t)(c.k >> 32);
+  const uint32_t mh = wave_umax(hi);
+  const uint32_t ml = wave_umax(hi == mh ? (uint32_t)c.k : 0u);
+  return {((uint64_t)mh << 32) | ml};
+}
+__device__ __forceinline__ CandD wave_best(CandD c) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
-    const V ov = shfl_xor_v(bv, m);
-    const uint32_t orr = (uint32_t)__shfl_xor((int)br, m, 64);
-    if (better(ov, orr, bv, br)) {
-      bv = ov;
-      br = orr;
-    }
+    const CandD o = {__shfl_xor(c.v, m, 64), (uint32_t)__shfl_xor((int)c.r, m, 64)};
+    if (cand_gt(o, c)) c = o;
   }
-  const uint64_t hit = __ballot(val == bv && rank == br);
-  val = bv;
-  rank = br;
-  return hit ? __builtin_ctzll(hit) : 0;
+  return c;
+}
+__device__ __forceinline__ CandD row0_best(CandD c) {
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1) {
+    const CandD o = {__shfl_xor(c.v, m, 64), (uint32_t)__shfl_xor((int)c.r, m, 64)};
+    if (cand_gt(o, c)) c = o;
+  }
+  return {__shfl(c.v, 0, 64), (uint32_t)__shfl((int)c.r, 0, 64)};
 }
 
-__device__ __forceinline__ float bcast(float v, int lane) { return __shfl(v, lane, 64); }
+__device__ __forceinline__ float bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
 __device__ __forceinline__ double bcast(double v, int lane) { return __shfl(v, lane, 64); }
 __device__ __forceinline__ half_t bcast(half_t v, int lane) {
-  return (half_t)__shfl((float)v, lane, 64);  // exact round trip
+  return (half_t)bcast((float)v, lane);  // exact round trip
+}
+
+// first lane whose candidate equals c (c is wave-uniform and held by a lane)
+template <typename C>
+__device__ __forceinline__ int lane_of(C mine, C c) {
+  const uint64_t hit = __ballot(cand_eq(mine, c));
+  return hit ? __builtin_ctzll(hit) : 0;
 }
 
 template <typename T>
@@ -141,9 +201,12 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
   __shared__ uint32_t s_cnt[FPS_CELLS];
   __shared__ uint32_t s_part[FPS_THREADS / 64];
   __shared__ V s_red[6][FPS_WAVES];
-  __shared__ V s_bv[2][FPS_WAVES];
-  __shared__ uint32_t s_br[2][FPS_WAVES];
-  __shared__ T s_bx[2][FPS_WAVES], s_by[2][FPS_WAVES], s_bz[2][FPS_WAVES];
+  struct WaveBest {
+    typename FpsCand<T>::type c;
+    T x, y, z;
+  };
+  __shared__ WaveBest s_wb[2][FPS_WAVES];
+  __shared__ unsigned long long s_gkey[3];
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
@@ -151,11 +214,8 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
   const int s_sz = (int)(64 * ((N + 64 * FPS_THREADS - 1) / (64 * FPS_THREADS)));
   const int nb = (N + s_sz - 1) / s_sz;
   char* base = ws + (size_t)b * L.stride;
-  T* __restrict__ xs = (T*)(base + L.off_x);
-  T* __restrict__ ys = (T*)(base + L.off_y);
-  T* __restrict__ zs = (T*)(base + L.off_z);
+  FpsRec<T>* __restrict__ recs = (FpsRec<T>*)(base + L.off_r);
   T* __restrict__ ts = (T*)(base + L.off_t);
-  uint32_t* __restrict__ ms = (uint32_t*)(base + L.off_m);
   const T* __restrict__ P = pts + (size_t)b * N * 3;
   int64_t* __restrict__ out = idx_out + (size_t)b * m;
 
@@ -186,6 +246,7 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     }
   }
   for (int c = tid; c < FPS_CELLS; c += FPS_THREADS) s_cnt[c] = 0;
+  if (tid < 3) s_gkey[tid] = 0;
   __syncthreads();
   float glo[3], gscale[3];
 #pragma unroll
@@ -249,26 +310,24 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     const uint32_t t = (uint32_t)(k & (bs - 1));
     const uint32_t rev = bs_bits ? (__builtin_bitreverse32(t) >> (32 - bs_bits)) : 0u;
     const uint32_t rank = rev * (uint32_t)per + (uint32_t)(k / bs);
-    xs[pos] = x;
-    ys[pos] = y;
-    zs[pos] = z;
+    recs[pos] = FpsRec<T>{x, y, z, rank | (valid ? 0u : FPS_INVALID)};
     ts[pos] = init;
-    ms[pos] = rank | (valid ? 0u : FPS_INVALID);
   }
   for (int64_t k = N + tid; k < L.np; k += FPS_THREADS) {
-    xs[k] = (T)0;
-    ys[k] = (T)0;
-    zs[k] = (T)0;
+    recs[k] = FpsRec<T>{(T)0, (T)0, (T)0, FPS_INVALID};
     ts[k] = (T)0;
-    ms[k] = FPS_INVALID;
   }
   __syncthreads();
 
-  // ---- 3. bucket summaries: lane owns bucket sb = w*64 + lane ----
-  const int sb = w * 64 + lane;
+  // ---- 3. bucket summaries ----
+  // Lane l of wave w owns bucket sb = l * 16 + w: buckets adjacent in Morton
+  // order (hence in space) belong to different waves, so the few buckets a new
+  // sample touches are spread over the workgroup instead of queueing in one wave.
+  typedef typename FpsCand<T>::type C;
+  C* const ctag = nullptr;
+  const int sb = lane * FPS_WAVES + w;
   V blo[3], bhi[3];
-  V bval = (V)-1;
-  uint32_t brank = 0xffffffffu;
+  C bbest = cand_none(ctag);
   T bx = (T)0, by = (T)0, bz = (T)0;
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
@@ -278,35 +337,43 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
   if (sb < nb) {
     for (int i = 0; i < s_sz; ++i) {
       const int pos = sb * s_sz + i;
-      const uint32_t mt = ms[pos];
+      const FpsRec<T> rc = recs[pos];
+      const uint32_t mt = rc.meta;
       if (mt & FPS_INVALID) continue;
-      const T x = xs[pos], y = ys[pos], z = zs[pos];
+      const T x = rc.x, y = rc.y, z = rc.z;
       blo[0] = x < blo[0] ? (V)x : blo[0];
       blo[1] = y < blo[1] ? (V)y : blo[1];
       blo[2] = z < blo[2] ? (V)z : blo[2];
       bhi[0] = x > bhi[0] ? (V)x : bhi[0];
       bhi[1] = y > bhi[1] ? (V)y : bhi[1];
       bhi[2] = z > bhi[2] ? (V)z : bhi[2];
-      if (better((V)init, mt, bval, brank)) {
-        bval = (V)init;
-        brank = mt;
+      const C cand = cand_make((V)init, mt, ctag);
+      if (cand_gt(cand, bbest)) {
+        bbest = cand;
         bx = x;
         by = y;
         bz = z;
       }
     }
   }
+  // the wave's best bucket (uniform)
+  C wbest = wave_best(bbest);
+  int wlane = lane_of(bbest, wbest);
+  T wx = bcast(bx, wlane), wy = bcast(by, wlane), wz = bcast(bz, wlane);
 
   // ---- 4. the sampling loop ----
   T ox = P[0], oy = P[1], oz = P[2];
   if (tid == 0) out[0] = 0;
   const V margin = (V)FpsConst<T>::margin();
   const V tiny = (V)FpsConst<T>::tiny();
+  constexpr int BATCH = 4;
   for (int j = 1; j < m; ++j) {
+    // A bucket can be skipped when the new sample is provably farther from
+    // every point in it than that point's running minimum.
     bool touch = false;
-    if (bval >= (V)0) {
-      V lb2 = (V)0;
+    if (cand_valid(bbest)) {
       const V o3[3] = {(V)ox, (V)oy, (V)oz};
+      V lb2 = (V)0;
 #pragma unroll
       for (int c = 0; c < 3; ++c) {
         V e = blo[c] - o3[c];
@@ -315,89 +382,110 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
         e = e > (V)0 ? e : (V)0;
         lb2 += e * e;
       }
-      touch = !(lb2 * ((V)1 - margin) > bval && lb2 > tiny);
+      touch = !(lb2 * ((V)1 - margin) > (V)cand_val(bbest) && lb2 > tiny);
     }
     uint64_t tm = __ballot(touch);
+    const bool rereduce = (tm >> wlane) & 1;
     while (tm) {
-      const int bit = __builtin_ctzll(tm);
-      tm &= tm - 1;
-      const int bk = w * 64 + bit;
-      V cv = (V)-1;
-      uint32_t cr = 0xffffffffu;
-      T cx = (T)0, cy = (T)0, cz = (T)0;
+      // up to BATCH touched buckets: their loads are issued together, then
+      // each present bucket is updated and re-reduced
+      int bits[BATCH];
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        bits[u] = tm ? __builtin_ctzll(tm) : -1;
+        tm &= tm ? tm - 1 : 0;
+      }
       for (int p0 = 0; p0 < s_sz; p0 += 64) {
-        const int pos = bk * s_sz + p0 + lane;
-        const uint32_t mt = ms[pos];
-        if (!(mt & FPS_INVALID)) {
-          const T x = xs[pos], y = ys[pos], z = zs[pos];
-          const T t = ts[pos];
-          const T d = sq3((T)(x - ox), (T)(y - oy), (T)(z - oz));  // fps.cu:145
-          const T t2 = d < t ? d : t;                                // fps.cu:146
-          if (t2 != t) ts[pos] = t2;
-          if (better((V)t2, mt, cv, cr)) {
-            cv = (V)t2;
-            cr = mt;
-            cx = x;
-            cy = y;
-            cz = z;
+        FpsRec<T> rc[BATCH];
+        T t[BATCH];
+        int pos[BATCH];
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+          if (bits[u] >= 0) {
+            pos[u] = (bits[u] * FPS_WAVES + w) * s_sz + p0 + lane;
+            rc[u] = recs[pos[u]];
+            t[u] = ts[pos[u]];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+          if (bits[u] < 0) continue;
+          C cand = cand_none(ctag);
+          if (!(rc[u].meta & FPS_INVALID)) {
+            const T d = sq3((T)(rc[u].x - ox), (T)(rc[u].y - oy), (T)(rc[u].z - oz));  // fps.cu:145
+            const T t2 = d < t[u] ? d : t[u];                                           // fps.cu:146
+            if (t2 != t[u]) ts[pos[u]] = t2;
+            cand = cand_make((V)t2, rc[u].meta, ctag);
+          }
+          const C best = wave_best(cand);
+          const int wl = lane_of(cand, best);
+          const T cx = bcast(rc[u].x, wl), cy = bcast(rc[u].y, wl), cz = bcast(rc[u].z, wl);
+          // passes after the first (buckets larger than 64) keep the max
+          if (lane == bits[u] && (p0 == 0 || cand_gt(best, bbest))) {
+            bbest = best;
+            bx = cx;
+            by = cy;
+            bz = cz;
           }
         }
       }
-      const int wl = wave_best(cv, cr);
-      cx = bcast(cx, wl);
-      cy = bcast(cy, wl);
-      cz = bcast(cz, wl);
-      if (lane == bit) {
-        bval = cv;
-        brank = cr;
-        bx = cx;
-        by = cy;
-        bz = cz;
-      }
     }
-    // wave best over its buckets, then the workgroup best
-    V wv = bval;
-    uint32_t wr = brank;
-    const int wl = wave_best(wv, wr);
-    const T wx = bcast(bx, wl), wy = bcast(by, wl), wz = bcast(bz, wl);
+    if (rereduce) {  // the wave's best bucket changed; otherwise wbest stands
+      wbest = wave_best(bbest);
+      wlane = lane_of(bbest, wbest);
+      wx = bcast(bx, wlane);
+      wy = bcast(by, wlane);
+      wz = bcast(bz, wlane);
+    }
     const int par = j & 1;
-    if (lane == 0) {
-      s_bv[par][w] = wv;
-      s_br[par][w] = wr;
-      s_bx[par][w] = wx;
-      s_by[par][w] = wy;
-      s_bz[par][w] = wz;
-    }
-    __syncthreads();
-    V gv = s_bv[par][0];
-    uint32_t gr = s_br[par][0];
-    int gw = 0;
-#pragma unroll
-    for (int v2 = 1; v2 < FPS_WAVES; ++v2) {
-      const V vv = s_bv[par][v2];
-      const uint32_t rr = s_br[par][v2];
-      if (better(vv, rr, gv, gr)) {
-        gv = vv;
-        gr = rr;
-        gw = v2;
+    C g;
+    int gw;
+    WaveBest mine = {cand_none(ctag), (T)0, (T)0, (T)0};
+    if constexpr (sizeof(C) == 8) {
+      // Packed keys: every wave folds its best into one LDS word with an
+      // atomic max; slots rotate over 3 iterations so the reset of the next
+      // slot (before this barrier) never races with its readers (before the
+      // previous barrier) or its writers (after this barrier).
+      if (tid == 0) s_gkey[(j + 1) % 3] = 0;
+      if (lane == 0) {
+        atomicMax(&s_gkey[j % 3], (unsigned long long)wbest.k);
+        s_wb[par][w] = WaveBest{wbest, wx, wy, wz};
       }
+      __syncthreads();
+      if (lane < FPS_WAVES) mine = s_wb[par][lane];  // issued with the key read
+      g = C{s_gkey[j % 3]};
+      gw = lane_of(mine.c, g);
+    } else {
+      if (lane == 0) s_wb[par][w] = WaveBest{wbest, wx, wy, wz};
+      __syncthreads();
+      if (lane < FPS_WAVES) mine = s_wb[par][lane];
+      g = row0_best(mine.c);
+      gw = lane_of(mine.c, g);
     }
-    int64_t k;
-    if (gv < (V)0) {  // nothing participates: the reference's index 0
-      k = 0;
+    // the rank is decoded to an index after the loop, off the critical path
+    if (!cand_valid(g)) {  // nothing participates: the reference's index 0
       ox = P[0];
       oy = P[1];
       oz = P[2];
+      if (tid == 0) out[j] = -1;
     } else {
-      const uint32_t r = gr & ~FPS_INVALID;
-      const uint32_t q = r / (uint32_t)per, rem = r - q * (uint32_t)per;
-      const uint32_t t = bs_bits ? (__builtin_bitreverse32(q) >> (32 - bs_bits)) : 0u;
-      k = (int64_t)t + (int64_t)rem * bs;
-      ox = s_bx[par][gw];
-      oy = s_by[par][gw];
-      oz = s_bz[par][gw];
+      ox = bcast(mine.x, gw);
+      oy = bcast(mine.y, gw);
+      oz = bcast(mine.z, gw);
+      if (tid == 0) out[j] = (int64_t)cand_rank(g);
     }
-    if (tid == 0) out[j] = k;
+  }
+  // rank -> point index: rank = bitrev(k mod BS) * per + k / BS
+  __syncthreads();
+  for (int j = 1 + tid; j < m; j += FPS_THREADS) {
+    const int64_t r = out[j];
+    int64_t k = 0;
+    if (r >= 0) {
+      const uint32_t q = (uint32_t)r / (uint32_t)per, rem = (uint32_t)r - q * (uint32_t)per;
+      const uint32_t tq = bs_bits ? (__builtin_bitreverse32(q) >> (32 - bs_bits)) : 0u;
+      k = (int64_t)tq + (int64_t)rem * bs;
+    }
+    out[j] = k;
   }
 }
 
