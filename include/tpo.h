@@ -88,12 +88,17 @@ int tpo_chamfer_bwd(int dtype, const void* xyz1, const void* xyz2,
  *   rows >= lengths1 are (0,0); slots >= lengths2 are (0,0) for versions
  *   2/3 and (-1,+inf) for versions 0/1.
  *   If version_out is not NULL it receives the version that ran.
+ *   workspace (optional, tpo_knn_workspace_size(N, P1) bytes) lets the
+ *   kernel process queries in spatial order, which is faster; results are
+ *   identical with or without it.
  */
+int64_t tpo_knn_workspace_size(int64_t N, int64_t P1);
 int tpo_knn_fwd(int dtype, const void* p1, const void* p2,
                 const int64_t* lengths1, const int64_t* lengths2,
                 int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,
                 int norm, int version, int64_t* idxs, void* dists,
-                int* version_out, void* stream);
+                int* version_out, void* workspace, int64_t workspace_bytes,
+                void* stream);
 
 /*
  * KNN backward.  Replaces knn_cuda_backward (knn.cu:469-534),

@@ -43,8 +43,9 @@ def test_every_declared_symbol_is_exported(lib):
 def test_argument_errors_are_reported(lib):
     P, I = ctypes.c_void_p, ctypes.c_int64
     lib.tpo_knn_fwd.argtypes = [ctypes.c_int, P, P, P, P, I, I, I, I, I, ctypes.c_int,
-                                ctypes.c_int, P, P, P, P]
-    rc = lib.tpo_knn_fwd(0, None, None, None, None, 1, 4, 4, 3, 2, 3, -1, None, None, None, None)
+                                ctypes.c_int, P, P, P, P, I, P]
+    rc = lib.tpo_knn_fwd(0, None, None, None, None, 1, 4, 4, 3, 2, 3, -1, None, None, None, None,
+                         0, None)
     assert rc == -1 and b"Norm must be 1 or 2" in lib.tpo_last_error()
     lib.tpo_fps_fwd.argtypes = [ctypes.c_int, P, I, I, I, P, P, I, P]
     assert lib.tpo_fps_fwd(0, None, 2, 10, 11, None, None, 0, None) == -1
@@ -58,6 +59,9 @@ def test_argument_errors_are_reported(lib):
     lib.tpo_chamfer_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, P, P, P, P, P]
     assert lib.tpo_chamfer_fwd(0, None, None, -1, 3, 3, None, None, None, None, None) == -1
     assert lib.tpo_chamfer_fwd(7, None, None, 0, 3, 3, None, None, None, None, None) == 0  # B=0
+    lib.tpo_knn_workspace_size.argtypes = [I, I]
+    lib.tpo_knn_workspace_size.restype = I
+    assert lib.tpo_knn_workspace_size(8, 16384) == 8 * 16384 * 4
     lib.tpo_gather_bwd_workspace_size.argtypes = [I, I]
     lib.tpo_gather_bwd_workspace_size.restype = I
     assert lib.tpo_gather_bwd_workspace_size(16, 65536) == 16 * 65536 * 4

@@ -15,9 +15,15 @@
 //   index.  Chunks merge in LDS in index order with strict-less, so ties go to
 //   the lowest index -- the reference's rule (chamfer.cu:69-72, 159-162).
 // Backward (replaces chamfer_dist_grad_kernel, chamfer.cu:200-234).
-//   Pass 1 stores the direct term of every point (grad_q = 2 g (q - r_idx)),
-//   which also initialises both outputs; pass 2 scatters the negated terms
-//   onto the matched points with hardware float atomics.
+//   grad_q[i] = 2 g_i (q_i - r_idx[i]) - sum over the other cloud's points j
+//   matched to i of 2 g_j (r_j - q_i).  When one cloud's gradient fits in LDS
+//   (<= 12288 points, float/half) a 1024-thread workgroup per (cloud, batch)
+//   accumulates the scattered terms with LDS atomics, adds its points' direct
+//   terms and writes every element once: no global atomics, no zero-fill.
+//   (float16: terms are computed in half like the reference, accumulated in
+//   float and rounded once.)  Otherwise pass 1 stores the direct terms (which
+//   initialises both outputs) and pass 2 scatters the negated terms with
+//   hardware atomics, like the reference.
 #include <stdio.h>
 
 #include "tpo_common.hpp"
@@ -28,6 +34,18 @@ namespace tpo {
 
 constexpr int CH_WAVES = 4;
 constexpr int CH_TILE = 16;
+
+// Copy a wave-uniform (SGPR) value into a VGPR.  On gfx950 a VALU op with an
+// SGPR source issues at 4 cycles per wave64 instruction, while VGPR-only
+// FP32 ops issue at ~2.3-2.7; one v_mov per reference coordinate, shared by
+// the Q queries of the lane, lets every subtraction use VGPR operands.
+__device__ __forceinline__ float to_vgpr(float s) {
+  float v;
+  asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(s));
+  return v;
+}
+__device__ __forceinline__ double to_vgpr(double s) { return s; }
+__device__ __forceinline__ half_t to_vgpr(half_t s) { return s; }
 
 __device__ __forceinline__ float vmin(float a, float b) { return __builtin_fminf(a, b); }
 __device__ __forceinline__ double vmin(double a, double b) { return __builtin_fmin(a, b); }
@@ -79,7 +97,7 @@ __global__ __launch_bounds__(256) void chamfer_fwd_kernel(
     const T* __restrict__ r = rp + 3 * t0;
 #pragma unroll
     for (int j = 0; j < CH_TILE; ++j) {
-      const T rx = r[3 * j], ry = r[3 * j + 1], rz = r[3 * j + 2];
+      const T rx = to_vgpr(r[3 * j]), ry = to_vgpr(r[3 * j + 1]), rz = to_vgpr(r[3 * j + 2]);
 #pragma unroll
       for (int i = 0; i < Q; ++i)
         tmin[i] = vmin(tmin[i], sq3((T)(rx - qx[i]), (T)(ry - qy[i]), (T)(rz - qz[i])));
@@ -213,6 +231,51 @@ __global__ __launch_bounds__(256) void chamfer_bwd_scatter_kernel(
   }
 }
 
+constexpr int CH_BWD_LDS_FLOATS = 36864;  // 144 KiB: 12288 points x 3
+
+template <typename T>
+__global__ __launch_bounds__(1024) void chamfer_bwd_fused_kernel(
+    const T* __restrict__ xyz1, const T* __restrict__ xyz2, const int32_t* __restrict__ idx1,
+    const int32_t* __restrict__ idx2, const T* __restrict__ gd1, const T* __restrict__ gd2, int N,
+    int M, T* __restrict__ g1, T* __restrict__ g2) {
+  __shared__ float acc[CH_BWD_LDS_FLOATS];
+  const int c = blockIdx.x & 1;  // 0: gradient of cloud 1, 1: of cloud 2
+  const int b = blockIdx.x >> 1;
+  const int n_own = c ? M : N, n_oth = c ? N : M;
+  const T* __restrict__ own = (c ? xyz2 : xyz1) + (size_t)b * n_own * 3;
+  const T* __restrict__ oth = (c ? xyz1 : xyz2) + (size_t)b * n_oth * 3;
+  const int32_t* __restrict__ idx_own = (c ? idx2 : idx1) + (size_t)b * n_own;
+  const int32_t* __restrict__ idx_oth = (c ? idx1 : idx2) + (size_t)b * n_oth;
+  const T* __restrict__ gd_own = (c ? gd2 : gd1) + (size_t)b * n_own;
+  const T* __restrict__ gd_oth = (c ? gd1 : gd2) + (size_t)b * n_oth;
+  T* __restrict__ out = (c ? g2 : g1) + (size_t)b * n_own * 3;
+
+  for (int i = threadIdx.x; i < 3 * n_own; i += 1024) acc[i] = 0.f;
+  __syncthreads();
+  // other cloud's points j whose nearest point is i (chamfer.cu:229-231 of
+  // the other direction): acc[i] += -(g_j (r_j - q_i))
+  for (int j = threadIdx.x; j < n_oth; j += 1024) {
+    const int i = idx_oth[j];
+    if (i < 0 || i >= n_own) continue;
+    const T g = (T)(gd_oth[j] * (T)2);
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      atomicAdd(&acc[3 * i + k], -(float)(T)(g * (T)(oth[3 * j + k] - own[3 * i + k])));
+  }
+  __syncthreads();
+  // direct term of the own points (chamfer.cu:226-228)
+  for (int i = threadIdx.x; i < n_own; i += 1024) {
+    const int j2 = idx_own[i];
+    const bool ok = j2 >= 0 && j2 < n_oth;
+    const T g = (T)(gd_own[i] * (T)2);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const T d = ok ? (T)(g * (T)(own[3 * i + k] - oth[3 * j2 + k])) : (T)0;
+      out[3 * i + k] = (T)(acc[3 * i + k] + (float)d);
+    }
+  }
+}
+
 template <typename T, int Q>
 static void launch_fwd(const void* x1, const void* x2, int B, int N, int M, void* d1, void* d2,
                        int32_t* i1, int32_t* i2, hipStream_t s) {
@@ -240,6 +303,12 @@ static void bwd_dispatch(const void* x1, const void* x2, const int32_t* i1, cons
                          void* g1, void* g2, hipStream_t s) {
   const int64_t total = B * (N + M);
   if (total == 0) return;
+  if (sizeof(T) <= 4 && 3 * std::max(N, M) <= CH_BWD_LDS_FLOATS && 2 * B < (1 << 30)) {
+    hipLaunchKernelGGL(chamfer_bwd_fused_kernel<T>, dim3((unsigned)(2 * B)), dim3(1024), 0, s,
+                       (const T*)x1, (const T*)x2, i1, i2, (const T*)gd1, (const T*)gd2, (int)N,
+                       (int)M, (T*)g1, (T*)g2);
+    return;
+  }
   const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
   hipLaunchKernelGGL(chamfer_bwd_direct_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s,
                      (const T*)x1, (const T*)x2, i1, i2, (const T*)gd1, (const T*)gd2, B, N, M,

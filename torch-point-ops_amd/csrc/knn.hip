@@ -78,14 +78,183 @@ __device__ __forceinline__ void first_max(const T (&sd)[KC], int K, T& m, int& m
   }
 }
 
+// Broadcast a wave-uniform value into a VGPR so the subtractions that use it
+// are VGPR-only VALU ops (an SGPR source costs 4 cycles per wave64 op).
+__device__ __forceinline__ float to_vgpr(float s) {
+  float v;
+  asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(s));
+  return v;
+}
+__device__ __forceinline__ double to_vgpr(double s) { return s; }
+__device__ __forceinline__ half_t to_vgpr(half_t s) { return s; }
+
+// mask = 2 * mask + (d < thr): one compare and one add-with-carry.
+__device__ __forceinline__ uint32_t push_lt(uint32_t mask, float d, float thr) {
+  uint32_t r;
+  asm("v_cmp_lt_f32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %3, %3, vcc"
+      : "=v"(r)
+      : "v"(d), "v"(thr), "v"(mask)
+      : "vcc");
+  return r;
+}
+__device__ __forceinline__ uint32_t push_lt(uint32_t mask, double d, double thr) {
+  return mask + mask + (uint32_t)(d < thr);
+}
+__device__ __forceinline__ uint32_t push_lt(uint32_t mask, half_t d, half_t thr) {
+  return mask + mask + (uint32_t)(d < thr);
+}
+
+// Per-lane select between two registers by a lane mask (bit set -> b).  Kept
+// as v_cndmask so the compiler cannot turn the select tree below back into a
+// dynamically indexed (stack) array.
+__device__ __forceinline__ uint32_t csel_u32(uint64_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(m));
+  return r;
+}
+__device__ __forceinline__ float csel(uint64_t m, float a, float b) {
+  return __uint_as_float(csel_u32(m, __float_as_uint(a), __float_as_uint(b)));
+}
+__device__ __forceinline__ double csel(uint64_t m, double a, double b) {
+  const uint64_t x = __double_as_longlong(a), y = __double_as_longlong(b);
+  const uint64_t lo = csel_u32(m, (uint32_t)x, (uint32_t)y);
+  const uint64_t hi = csel_u32(m, (uint32_t)(x >> 32), (uint32_t)(y >> 32));
+  return __longlong_as_double((long long)((hi << 32) | lo));
+}
+__device__ __forceinline__ half_t csel(uint64_t m, half_t a, half_t b) {
+  const uint32_t x = __builtin_bit_cast(uint16_t, a), y = __builtin_bit_cast(uint16_t, b);
+  return __builtin_bit_cast(half_t, (uint16_t)csel_u32(m, x, y));
+}
+
+// d[c] for a per-lane c in [0, 32): a 5-level select tree over registers
+// (one ballot per level, 31 selects).  Inactive lanes take no part: both the
+// ballots and the selects run under the current exec mask.
+template <typename T>
+__device__ __forceinline__ T select32(const T (&d)[KNN_CHUNK], int c) {
+  T a[16], b[8], e[4], f[2];
+  const uint64_t m0 = __ballot(c & 1), m1 = __ballot(c & 2), m2 = __ballot(c & 4);
+  const uint64_t m3 = __ballot(c & 8), m4 = __ballot(c & 16);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) a[i] = csel(m0, d[2 * i], d[2 * i + 1]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) b[i] = csel(m1, a[2 * i], a[2 * i + 1]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) e[i] = csel(m2, b[2 * i], b[2 * i + 1]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) f[i] = csel(m3, e[2 * i], e[2 * i + 1]);
+  return csel(m4, f[0], f[1]);
+}
+
+// Per cloud, the valid queries (row < lengths1) in Morton order of a 16^3
+// grid over their bounding box.  The order only decides which queries share
+// a wave: neighbouring queries share their nearest references, so the MinK
+// insertions of a wave's lanes coincide and the candidate loop below runs
+// fewer iterations.  Results are bit-identical in any order.
+constexpr int KNN_GRID = 16;
+constexpr int KNN_CELLS = KNN_GRID * KNN_GRID * KNN_GRID;
+
+template <typename T>
+__global__ __launch_bounds__(1024) void knn_order_kernel(const T* __restrict__ p1,
+                                                         const int64_t* __restrict__ len1, int P1,
+                                                         int32_t* __restrict__ order) {
+  __shared__ uint32_t cnt[KNN_CELLS];
+  __shared__ float red[6][16];
+  __shared__ uint32_t part[16];
+  const int n = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int64_t l1 = len1[n];
+  const int L1 = (int)(l1 < 0 ? 0 : (l1 > P1 ? P1 : l1));
+  const T* __restrict__ P = p1 + (size_t)n * P1 * 3;
+  int32_t* __restrict__ out = order + (size_t)n * P1;
+  float lo[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
+  float hi[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  for (int k = tid; k < L1; k += 1024)
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const float v = (float)P[3 * k + c];
+      lo[c] = fminf(lo[c], v);
+      hi[c] = fmaxf(hi[c], v);
+    }
+#pragma unroll
+  for (int c = 0; c < 3; ++c)
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      lo[c] = fminf(lo[c], __shfl_xor(lo[c], m, 64));
+      hi[c] = fmaxf(hi[c], __shfl_xor(hi[c], m, 64));
+    }
+  if (lane == 0)
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      red[c][w] = lo[c];
+      red[3 + c][w] = hi[c];
+    }
+  for (int c = tid; c < KNN_CELLS; c += 1024) cnt[c] = 0;
+  __syncthreads();
+  float glo[3], gs[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    float a = __builtin_inff(), z = -__builtin_inff();
+    for (int v = 0; v < 16; ++v) {
+      a = fminf(a, red[c][v]);
+      z = fmaxf(z, red[3 + c][v]);
+    }
+    glo[c] = a;
+    const float ext = z - a;
+    gs[c] = (ext > 0.f && ext < __builtin_inff()) ? (float)KNN_GRID / ext : 0.f;
+  }
+  auto cell_of = [&](int k) -> uint32_t {
+    uint32_t code = 0;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const float f = ((float)P[3 * k + c] - glo[c]) * gs[c];
+      int i = (f == f) ? (int)f : 0;
+      i = i < 0 ? 0 : (i > KNN_GRID - 1 ? KNN_GRID - 1 : i);
+      uint32_t v = (uint32_t)i;
+      v = (v | (v << 4)) & 0x0c3;
+      v = (v | (v << 2)) & 0x249;
+      code |= v << c;
+    }
+    return code;
+  };
+  for (int k = tid; k < L1; k += 1024) atomicAdd(&cnt[cell_of(k)], 1u);
+  __syncthreads();
+  {  // exclusive scan, 4 cells per thread
+    uint32_t v[4], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = cnt[tid * 4 + i];
+      sum += v[i];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) part[w] = incl;
+    __syncthreads();
+    uint32_t run = incl - sum;
+    for (int v2 = 0; v2 < w; ++v2) run += part[v2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      cnt[tid * 4 + i] = run;
+      run += v[i];
+    }
+  }
+  __syncthreads();
+  for (int k = tid; k < L1; k += 1024) out[atomicAdd(&cnt[cell_of(k)], 1u)] = k;
+  for (int k = L1 + tid; k < P1; k += 1024) out[k] = k;  // rows past lengths1 keep their place
+}
+
 template <typename T, int DT, int NORM, int KC>
 __global__ __launch_bounds__(256) void knn_fwd_kernel(
     const T* __restrict__ p1, const T* __restrict__ p2, const int64_t* __restrict__ len1,
-    const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb, int pad_sentinel,
-    int sorted2, int64_t* __restrict__ idxs, T* __restrict__ dists) {
+    const int64_t* __restrict__ len2, const int32_t* __restrict__ order, int P1, int P2, int D,
+    int K, int nqb, int pad_sentinel, int sorted2, int64_t* __restrict__ idxs,
+    T* __restrict__ dists) {
   const int n = blockIdx.x / nqb;
-  const int q = (blockIdx.x - n * nqb) * 256 + threadIdx.x;
-  if (q >= P1) return;
+  const int i = (blockIdx.x - n * nqb) * 256 + threadIdx.x;  // position in processing order
+  if (i >= P1) return;
+  const int q = order ? order[(size_t)n * P1 + i] : i;  // query row handled by this lane
   int64_t l1 = len1[n], l2 = len2[n];
   l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
   l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
@@ -157,30 +326,44 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
       first_max<T, KC>(sd, K, thr, ms);
       for (int j0 = K; j0 < L2; j0 += KNN_CHUNK) {
         const int cn = min(KNN_CHUNK, L2 - j0);
+        // distances of the chunk stay in registers; bit (cn-1-c) of mask
+        // flags reference j0+c as a candidate against the current maximum
+        T dch[KNN_CHUNK];
         uint32_t mask = 0;
         if (cn == KNN_CHUNK) {
 #pragma unroll
           for (int c = 0; c < KNN_CHUNK; ++c) {
-            const T d = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)(j0 + c) * Dd, D);
-            mask |= (d < thr) ? (1u << c) : 0u;
+            const T* __restrict__ r = rp + (size_t)(j0 + c) * Dd;
+            if constexpr (DT == 3) {
+              const T rv[3] = {to_vgpr(r[0]), to_vgpr(r[1]), to_vgpr(r[2])};
+              dch[c] = knn_dist<T, DT, NORM>(qr, qp, rv, D);
+            } else {
+              dch[c] = knn_dist<T, DT, NORM>(qr, qp, r, D);
+            }
+            mask = push_lt(mask, dch[c], thr);
           }
         } else {
-          for (int c = 0; c < cn; ++c) {
-            const T d = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)(j0 + c) * Dd, D);
-            mask |= (d < thr) ? (1u << c) : 0u;
+#pragma unroll
+          for (int c = 0; c < KNN_CHUNK; ++c) {
+            if (c < cn) {
+              dch[c] = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)(j0 + c) * Dd, D);
+              mask = push_lt(mask, dch[c], thr);
+            } else {
+              dch[c] = Lim<T>::inf();
+            }
           }
         }
         while (mask) {
-          const int c = __builtin_ctz(mask);
-          mask &= mask - 1;
-          const int j = j0 + c;
-          const T d = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)j * Dd, D);
+          const int top = 31 - __builtin_clz(mask);  // earliest candidate first
+          mask ^= 1u << top;
+          const int c = cn - 1 - top;
+          const T d = select32(dch, c);
           if (d < thr) {
 #pragma unroll
             for (int s = 0; s < KC; ++s) {
               if (s == ms) {
                 sd[s] = d;
-                si[s] = j;
+                si[s] = j0 + c;
               }
             }
             first_max<T, KC>(sd, K, thr, ms);
@@ -303,46 +486,49 @@ unsigned grid_for(int64_t n) {
 }
 
 template <typename T, int DT, int NORM, int KC>
-void launch_fwd_kc(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
-                   int P1, int P2, int D, int K, int pad, int sorted2, int64_t* idxs, void* dists,
-                   hipStream_t s) {
+void launch_fwd_kc(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
+                   const int32_t* order, int N, int P1, int P2, int D, int K, int pad,
+                   int sorted2, int64_t* idxs, void* dists, hipStream_t s) {
   const int nqb = (P1 + 255) / 256;
   hipLaunchKernelGGL((knn_fwd_kernel<T, DT, NORM, KC>), dim3(N * nqb), dim3(256), 0, s,
-                     (const T*)p1, (const T*)p2, l1, l2, P1, P2, D, K, nqb, pad, sorted2, idxs,
-                     (T*)dists);
+                     (const T*)p1, (const T*)p2, l1, l2, order, P1, P2, D, K, nqb, pad, sorted2,
+                     idxs, (T*)dists);
 }
 
 template <typename T, int DT, int NORM>
-void launch_fwd_dt(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
-                   int P1, int P2, int D, int K, int pad, int sorted2, int64_t* idxs, void* dists,
-                   hipStream_t s) {
-  if (K <= 4) launch_fwd_kc<T, DT, NORM, 4>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
-  else if (K <= 8) launch_fwd_kc<T, DT, NORM, 8>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
-  else if (K <= 16) launch_fwd_kc<T, DT, NORM, 16>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
-  else launch_fwd_kc<T, DT, NORM, 32>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+void launch_fwd_dt(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
+                   const int32_t* order, int N, int P1, int P2, int D, int K, int pad,
+                   int sorted2, int64_t* idxs, void* dists, hipStream_t s) {
+  if (K <= 4) launch_fwd_kc<T, DT, NORM, 4>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  else if (K <= 8) launch_fwd_kc<T, DT, NORM, 8>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  else if (K <= 16) launch_fwd_kc<T, DT, NORM, 16>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  else launch_fwd_kc<T, DT, NORM, 32>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
 }
 
 template <typename T, int NORM>
-void launch_fwd_norm(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
-                     int P1, int P2, int D, int K, int pad, int sorted2, int64_t* idxs,
-                     void* dists, hipStream_t s) {
+void launch_fwd_norm(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
+                     int32_t* order, int N, int P1, int P2, int D, int K, int pad, int sorted2,
+                     int64_t* idxs, void* dists, hipStream_t s) {
   if (K > 32) {
     const int nqb = (P1 + 255) / 256;
     hipLaunchKernelGGL((knn_fwd_global_kernel<T, NORM>), dim3(N * nqb), dim3(256), 0, s,
                        (const T*)p1, (const T*)p2, l1, l2, P1, P2, D, K, nqb, idxs, (T*)dists);
   } else if (D == 3) {
-    launch_fwd_dt<T, 3, NORM>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+    if (order)
+      hipLaunchKernelGGL(knn_order_kernel<T>, dim3(N), dim3(1024), 0, s, (const T*)p1, l1, P1,
+                         order);
+    launch_fwd_dt<T, 3, NORM>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
   } else {
-    launch_fwd_dt<T, 0, NORM>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+    launch_fwd_dt<T, 0, NORM>(p1, p2, l1, l2, nullptr, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
   }
 }
 
 template <typename T>
-void launch_fwd(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
-                int P1, int P2, int D, int K, int norm, int pad, int sorted2, int64_t* idxs,
-                void* dists, hipStream_t s) {
-  if (norm == 1) launch_fwd_norm<T, 1>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
-  else launch_fwd_norm<T, 2>(p1, p2, l1, l2, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+void launch_fwd(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
+                int32_t* order, int N, int P1, int P2, int D, int K, int norm, int pad,
+                int sorted2, int64_t* idxs, void* dists, hipStream_t s) {
+  if (norm == 1) launch_fwd_norm<T, 1>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+  else launch_fwd_norm<T, 2>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
 }
 
 template <typename T>
@@ -380,10 +566,16 @@ int choose_version(int64_t D, int64_t K) {
 
 using namespace tpo;
 
+extern "C" int64_t tpo_knn_workspace_size(int64_t N, int64_t P1) {
+  if (N < 0 || P1 < 0) return -1;
+  return ((N * P1 * 4 + 255) / 256) * 256;
+}
+
 extern "C" int tpo_knn_fwd(int dtype, const void* p1, const void* p2, const int64_t* lengths1,
                            const int64_t* lengths2, int64_t N, int64_t P1, int64_t P2, int64_t D,
                            int64_t K, int norm, int version, int64_t* idxs, void* dists,
-                           int* version_out, void* stream) {
+                           int* version_out, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
   if (N < 0 || P1 < 0 || P2 < 0 || D < 1 || K < 0 || N >= (1 << 20) || P1 >= (1 << 30) ||
       P2 >= (1 << 30) || D >= (1 << 20) || K >= (1 << 20))
     return set_error(TPO_ERR_ARG, "tpo_knn_fwd: bad sizes");
@@ -394,11 +586,13 @@ extern "C" int tpo_knn_fwd(int dtype, const void* p1, const void* p2, const int6
   if (N == 0 || P1 == 0 || K == 0) return TPO_OK;
   const int pad = v <= 1;
   const int sorted2 = (v == 3 && K == 2);
+  // the query ordering is an optimisation: without workspace, keep row order
+  int32_t* order = (workspace && workspace_bytes >= N * P1 * 4) ? (int32_t*)workspace : nullptr;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case TPO_F32: launch_fwd<float>(p1, p2, lengths1, lengths2, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
-    case TPO_F64: launch_fwd<double>(p1, p2, lengths1, lengths2, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
-    case TPO_F16: launch_fwd<half_t>(p1, p2, lengths1, lengths2, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
+    case TPO_F32: launch_fwd<float>(p1, p2, lengths1, lengths2, order, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
+    case TPO_F64: launch_fwd<double>(p1, p2, lengths1, lengths2, order, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
+    case TPO_F16: launch_fwd<half_t>(p1, p2, lengths1, lengths2, order, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
     default: return set_error(TPO_ERR_DTYPE, "tpo_knn_fwd: unsupported dtype %d", dtype);
   }
   return check_launch("tpo_knn_fwd");

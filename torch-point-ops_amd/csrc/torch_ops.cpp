@@ -137,9 +137,12 @@ std::tuple<at::Tensor, at::Tensor> knn_forward_hip(const at::Tensor& p1_in,
   const at::Tensor p1 = p1_in.contiguous(), p2 = p2_in.contiguous();
   const at::Tensor l1 = lengths1_in.contiguous(), l2 = lengths2_in.contiguous();
   const int dt = dtype_code(p1, "knn_forward");
+  const int64_t ws = tpo_knn_workspace_size(N, P1);
+  at::Tensor work = at::empty({ws > 0 ? ws : 1}, p1.options().dtype(at::kByte));
   check_rc(tpo_knn_fwd(dt, p1.data_ptr(), p2.data_ptr(), l1.data_ptr<int64_t>(),
                        l2.data_ptr<int64_t>(), N, P1, P2, D, K, (int)norm, (int)version,
-                       idxs.data_ptr<int64_t>(), dists.data_ptr(), nullptr, stream_of(p1)),
+                       idxs.data_ptr<int64_t>(), dists.data_ptr(), nullptr, work.data_ptr(), ws,
+                       stream_of(p1)),
            "knn_forward");
   return {idxs, dists};
 }
