@@ -111,6 +111,89 @@ def test_backward_config2_vs_oracle(tpo, O, dev):
         assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
 
 
+# ---- edge cases of the float filter (expanded-form ranking + exact re-scan)
+# and of the NaN rule of the reference's 512-reference stages
+
+def assert_same(a, b):
+    """Bitwise equality, except that NaN matches NaN whatever its payload."""
+    a, b = np.asarray(a), np.asarray(b)
+    na, nb = np.isnan(a), np.isnan(b)
+    assert np.array_equal(na, nb), f"NaN pattern differs: {np.sum(na != nb)}"
+    assert_bits(np.where(na, 0, a).astype(a.dtype), np.where(nb, 0, b).astype(b.dtype))
+
+
+def check_vs_oracle(O, dev, p1, p2):
+    d1, d2, i1, i2 = run_fwd(p1, p2, dev)
+    e1, e2, j1, j2 = O.chamfer_fwd(np_(p1), np_(p2))
+    assert_same(np_(d1), e1)
+    assert_same(np_(d2), e2)
+    assert np.array_equal(np_(i1), j1) and np.array_equal(np_(i2), j2)
+    return np_(i1), np_(i2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
+def test_lattice_ties_across_tiles(tpo, O, dev, dtype):
+    # shuffled integer lattice; half-integer queries are equidistant from up to
+    # 8 lattice points that sit in different tiles and chunks
+    g = torch.Generator().manual_seed(21)
+    ax = torch.arange(12.0)
+    lat = torch.stack(torch.meshgrid(ax, ax, ax, indexing="ij"), -1).reshape(1, -1, 3)
+    p2 = lat[:, torch.randperm(lat.shape[1], generator=g)]
+    p1 = torch.randint(0, 23, (1, 3000, 3), generator=g).float() / 2
+    check_vs_oracle(O, dev, p1.to(dtype), p2.to(dtype))
+
+
+@pytest.mark.parametrize("offset", [1e2, 1e3, 3e4])
+def test_far_from_origin_float(tpo, O, dev, offset):
+    # |q|^2 large against the spacing: the filter window admits many tiles and
+    # most queries take the exact wave scan; at 3e4 many distances tie exactly
+    g = torch.Generator().manual_seed(int(offset))
+    p1 = torch.rand(2, 3000, 3, generator=g) + offset
+    p2 = torch.rand(2, 2500, 3, generator=g) + offset
+    check_vs_oracle(O, dev, p1, p2)
+
+
+@pytest.mark.parametrize("scale", [1e-10, 1e-19, 1e-30])
+def test_tiny_coordinates_float(tpo, O, dev, scale):
+    g = torch.Generator().manual_seed(3)
+    p1 = torch.randn(2, 1500, 3, generator=g) * scale
+    p2 = torch.randn(2, 1300, 3, generator=g) * scale
+    check_vs_oracle(O, dev, p1, p2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_huge_coordinates(tpo, O, dev, dtype):
+    g = torch.Generator().manual_seed(4)
+    p1 = torch.randn(3, 700, 3, generator=g, dtype=torch.float64)
+    p2 = torch.randn(3, 1100, 3, generator=g, dtype=torch.float64)
+    p2[0, 5] = 2.0 ** 61              # beyond the filter's 2^60 bound
+    p2[1, 900, 1] = 1e30              # squares overflow in float
+    p1[1, 3, 0] = -1e25               # query with huge coordinate
+    p1[2, 17] = p2[2, 40] * 2.0 ** 70
+    check_vs_oracle(O, dev, p1.to(dtype), p2.to(dtype))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
+def test_nonfinite_coordinates_follow_reference(tpo, O, dev, dtype):
+    g = torch.Generator().manual_seed(5)
+    B, N, M = 6, 600, 1500
+    p1 = torch.randn(B, N, 3, generator=g)
+    p2 = torch.randn(B, M, 3, generator=g)
+    inf, nan = float("inf"), float("nan")
+    p2[0, 0, 1] = nan                 # D(0) NaN: every query of batch 0 -> (NaN, 0)
+    p2[1, 512, 0] = nan               # stage head: refs 512..1023 never count
+    p2[1, 800] = p1[1, 7]             # ... including the exact match of query 7
+    p2[2, 700, 2] = nan               # non-head NaN: only ref 700 drops out
+    p2[3, 300, 0] = inf               # inf reference
+    p2[3, 301, 0] = -inf
+    p1[4, 9, 2] = nan                 # NaN query
+    p1[4, 10, 0] = inf                # inf query: inf - inf with p2[4, 0]
+    p2[4, 0, 0] = inf
+    p1[5, :, :] = inf                 # every distance inf or NaN
+    i1, i2 = check_vs_oracle(O, dev, p1.to(dtype), p2.to(dtype))
+    assert (i1[0] == 0).all() and not np.isin(i1[1], np.arange(512, 1024)).any()
+
+
 # ---- the reference test suite's checks (tests/test_chamfer.py) ----
 
 def torch_reference(p1, p2):

@@ -3,17 +3,19 @@
 // Forward (replaces chamfer_dist_kernel, chamfer.cu:36-167).
 //   One launch covers both directions.  A workgroup owns 64*Q query points
 //   (Q per lane, held in VGPRs) of one (direction, cloud) and its 4 waves split
-//   the reference cloud into 4 contiguous chunks.  Each wave streams its chunk
-//   through SGPRs (wave-uniform scalar loads, no LDS traffic in the hot loop),
-//   so the inner loop is 6 VALU ops per pair (3 sub, mul, 2 fma) plus half a
-//   v_min3 for the running minimum.
-//   First-index argmin without per-pair index bookkeeping: per tile of 16
-//   references keep only the tile minimum; a tile replaces the running best
-//   only when strictly smaller (so the earliest tile holding the minimum wins);
-//   at the end the winning tile is re-scanned with the identical formula and
-//   the first position whose distance equals the minimum bit-for-bit is the
-//   index.  Chunks merge in LDS in index order with strict-less, so ties go to
-//   the lowest index -- the reference's rule (chamfer.cu:69-72, 159-162).
+//   the reference cloud into 4 contiguous chunks; chunk results merge in LDS in
+//   index order with strict-less, so ties go to the lowest index -- the
+//   reference's rule (chamfer.cu:69-72, 159-162).
+//   float: chamfer_fwd_filter_kernel ranks references by the expanded form
+//   |r|^2 - 2 q.r (3 FMAs per pair) and proves with a per-query error window
+//   that the reference formula's first-index minimum lies in the best tile of
+//   16, which it then re-scans exactly; queries the window cannot decide are
+//   re-scanned exactly by the whole wave.
+//   double / half: chamfer_fwd_kernel evaluates the reference formula per
+//   pair (3 sub, mul, 2 fma, streamed through SGPRs), keeps only per-tile
+//   minima and re-scans the winning tile for the first index.
+//   Non-finite coordinates take the exact wave-wide scan, which follows the
+//   reference's handling of NaN distances (chunk_scan).
 // Backward (replaces chamfer_dist_grad_kernel, chamfer.cu:200-234).
 //   grad_q[i] = 2 g_i (q_i - r_idx[i]) - sum over the other cloud's points j
 //   matched to i of 2 g_j (r_j - q_i).  When one cloud's gradient fits in LDS
@@ -50,6 +52,70 @@ __device__ __forceinline__ half_t to_vgpr(half_t s) { return s; }
 __device__ __forceinline__ float vmin(float a, float b) { return __builtin_fminf(a, b); }
 __device__ __forceinline__ double vmin(double a, double b) { return __builtin_fmin(a, b); }
 __device__ __forceinline__ half_t vmin(half_t a, half_t b) { return __builtin_fminf16(a, b); }
+
+template <typename T>
+__device__ __forceinline__ T ref_d(T qx, T qy, T qz, const T* __restrict__ r) {
+  return sq3((T)(r[0] - qx), (T)(r[1] - qy), (T)(r[2] - qz));
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ double wave_min(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmin(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ half_t wave_min(half_t v) { return (half_t)wave_min((float)v); }
+__device__ __forceinline__ int wave_imin(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+  return v;
+}
+
+// The reference's result for one query over the references [c0, c1),
+// computed by the whole wave (lanes stride the references).  chamfer.cu:55-82
+// takes the first element of each 512-reference stage unconditionally and
+// later ones on strict less; a stage replaces the stored result only when
+// that is strictly greater (:159-162).  With finite distances this is the
+// first index of the minimum.  With NaN distances: reference j counts only
+// if neither D(j) nor D(512*floor(j/512)) is NaN, and a NaN D(0) makes the
+// answer (NaN, 0).  Returns the minimum and first index over the counted
+// references of the range ((+inf, INT_MAX) when none counts), or (NaN, 0).
+template <typename T>
+__device__ void chunk_scan(T qx, T qy, T qz, const T* __restrict__ rp, int c0, int c1, int lane,
+                           T& out_d, int& out_i) {
+  T d_ = Lim<T>::inf();
+  int i_ = 0x7fffffff;
+  for (int j = c0 + lane; j < c1; j += 64) {
+    const T d = ref_d(qx, qy, qz, rp + 3 * j);
+    const int h = j & ~511;
+    const T dh = h == j ? d : ref_d(qx, qy, qz, rp + 3 * h);
+    if (d == d && dh == dh && (d < d_ || (d == d_ && i_ == 0x7fffffff))) {
+      d_ = d;
+      i_ = j;
+    }
+  }
+  T md = wave_min(d_);
+  int mi = wave_imin(d_ == md ? i_ : 0x7fffffff);
+  if (c0 == 0) {
+    const T d0 = ref_d(qx, qy, qz, rp);
+    if (d0 != d0) {
+      md = d0;
+      mi = 0;
+    }
+  }
+  out_d = md;
+  out_i = mi;
+}
+
+// x - x is 0 exactly when x is finite (inf - inf and NaN - NaN are NaN).
+template <typename T>
+__device__ __forceinline__ bool finite3(const T* __restrict__ p) {
+  return (T)(p[0] - p[0]) == (T)0 && (T)(p[1] - p[1]) == (T)0 && (T)(p[2] - p[2]) == (T)0;
+}
 
 template <typename T, int Q>
 __global__ __launch_bounds__(256) void chamfer_fwd_kernel(
@@ -127,24 +193,55 @@ __global__ __launch_bounds__(256) void chamfer_fwd_kernel(
     }
   }
 
-  // Recover the first index inside the winning tile (same formula, same bits).
+  // With finite coordinates no distance is NaN (overflow gives +inf), so the
+  // first index of the minimum is the reference's answer: recover it inside
+  // the winning tile (same formula, same bits).  Non-finite coordinates in
+  // the chunk (or its first 512-stage head) or the query: chunk_scan.
+  bool rfin = true;
+  for (int j = c0 + lane; j < c1; j += 64) rfin = rfin && finite3(rp + 3 * j);
+  if (c0 < c1 && (c0 & 511) != 0) rfin = rfin && finite3(rp + 3 * (c0 & ~511));
+  const bool rbad = __ballot(!rfin) != 0;
+  int found[Q];
+  uint64_t amb[Q];
 #pragma unroll
   for (int i = 0; i < Q; ++i) {
-    int found = 0x7fffffff;
-    if (c0 < c1) {
+    int gq = qb * 64 * Q + i * 64 + lane;
+    gq = gq < nq ? gq : nq - 1;
+    const bool a = c0 < c1 && (rbad || !finite3(qp + 3 * gq));
+    amb[i] = __ballot(a);
+    found[i] = 0x7fffffff;
+    if (c0 < c1 && !a) {
       const int tb = bt[i];
-      for (int k = 0; k < CH_TILE; ++k) {
-        const int j = tb + k;
-        if (j < c1 && found == 0x7fffffff) {
-          const T d = sq3((T)(rp[3 * j] - qx[i]), (T)(rp[3 * j + 1] - qy[i]),
-                          (T)(rp[3 * j + 2] - qz[i]));
-          if (d == best[i]) found = j;
+      const int te = min(tb + CH_TILE, c1);
+      for (int j = tb; j < te; ++j) {
+        if (ref_d(qx[i], qy[i], qz[i], rp + 3 * j) == best[i]) {
+          found[i] = j;
+          break;
         }
       }
-      if (found == 0x7fffffff) found = c0;  // all-NaN chunk: keep its first index
     }
+  }
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    uint64_t m = amb[i];
+    while (m) {
+      const int l = __builtin_ctzll(m);
+      m &= m - 1;
+      int gq = qb * 64 * Q + i * 64 + l;
+      gq = gq < nq ? gq : nq - 1;
+      T md;
+      int mi;
+      chunk_scan(qp[3 * gq], qp[3 * gq + 1], qp[3 * gq + 2], rp, c0, c1, lane, md, mi);
+      if (lane == l) {
+        best[i] = md;
+        found[i] = mi;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
     s_d[w][i * 64 + lane] = best[i];
-    s_i[w][i * 64 + lane] = found;
+    s_i[w][i * 64 + lane] = found[i];
   }
   __syncthreads();
 
@@ -169,6 +266,212 @@ __global__ __launch_bounds__(256) void chamfer_fwd_kernel(
     }
     dout[gq] = bd;
     iout[gq] = bi;
+  }
+}
+
+// ------------------------------------------------- forward, float: filter
+// Expanded-form filter (float).  For query q and reference r
+//   A(r) = |r|^2 - 2 q.r = fma(-2qx, rx, fma(-2qy, ry, fma(-2qz, rz, |r|^2)))
+// costs 3 FMAs per pair instead of the reference formula's 6 VALU ops.  With
+// u = 2^-24 and every coordinate below 2^60 in magnitude (so nothing
+// overflows), A(r) differs from D(r) - |q|^2, D being the reference formula's
+// float result, by at most
+//   E(r) <= 6u(|r|^2 + |q||r|) + 5u D(r) <= 21u|q|^2 + 20u D(r)
+// (four roundings in A; the reference formula's relative error is <= 5u since
+// all its terms are non-negative; |r| <= |q| + sqrt(D)).  Per tile of 16
+// references the kernel keeps the tile minimum of A, per query the best tile
+// (strictly smaller replaces, so the earliest wins) and `second`, the
+// minimum over every other tile.  With a* the best value and
+//   W = 2^-18 (|q|^2 + max(a* + |q|^2, 0)) + 2^-120,
+// W >= E(r*) + E(ra) for an exact minimiser r* and the approximate one ra
+// (the 2^-120 term covers gradual underflow), so A(r*) <= a* + W.  Hence if
+// second > a* + W every exact minimiser lies in the best tile, which is
+// re-scanned with the reference formula: same bits, first index.  Otherwise
+// (a near-tie across tiles, NaN/Inf or a coordinate >= 2^60 in the wave's
+// chunk or the query, an empty chunk) the whole wave re-scans that query's
+// chunk with the reference formula, lanes striding the references.
+//   The references reach the lanes through a wave-private LDS block: each
+// lane loads one reference and computes |r|^2 once, and every pair then
+// reads it back as one broadcast ds_read_b128, so the per-pair VALU work is
+// the 3 FMAs, half a v_min3 and the per-tile bookkeeping.
+constexpr uint32_t CH_BIG = 0x5d800000u;  // float bits of 2^60
+
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+
+template <int Q>
+__global__ __launch_bounds__(256) void chamfer_fwd_filter_kernel(
+    const float* __restrict__ xyz1, const float* __restrict__ xyz2, int B, int N, int M,
+    int nqb1, int nqb2, float* __restrict__ dist1, float* __restrict__ dist2,
+    int32_t* __restrict__ idx1, int32_t* __restrict__ idx2) {
+  __shared__ float4 s_ref[CH_WAVES][64];
+  __shared__ float s_d[CH_WAVES][64 * Q];
+  __shared__ int s_i[CH_WAVES][64 * Q];
+
+  int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int g1 = B * nqb1;
+  const int dir = lb >= g1;
+  if (dir) lb -= g1;
+  const int nqb = dir ? nqb2 : nqb1;
+  const int b = lb / nqb;
+  const int qb = lb - b * nqb;
+  const int nq = dir ? M : N;
+  const int nr = dir ? N : M;
+  const float* __restrict__ qp = (dir ? xyz2 : xyz1) + (size_t)b * nq * 3;
+  const float* __restrict__ rp = (dir ? xyz1 : xyz2) + (size_t)b * nr * 3;
+
+  const int w = wave_id(), lane = lane_id();
+  const int chunk = ((nr + CH_WAVES * 64 - 1) / (CH_WAVES * 64)) * 64;
+  const int c0 = min(nr, w * chunk);
+  const int c1 = min(nr, c0 + chunk);
+
+  float bd[Q];
+  int bi[Q];
+  if (c0 < c1) {
+    float qx2[Q], qy2[Q], qz2[Q], best[Q], second[Q];
+    int bt[Q];
+    uint32_t qbig = 0;  // bit i: query i has a non-finite or >= 2^60 coordinate
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      int gq = qb * 64 * Q + i * 64 + lane;
+      gq = gq < nq ? gq : nq - 1;
+      const float x = qp[3 * gq], y = qp[3 * gq + 1], z = qp[3 * gq + 2];
+      qx2[i] = -2.f * x;
+      qy2[i] = -2.f * y;
+      qz2[i] = -2.f * z;
+      if (max(abs_bits(x), max(abs_bits(y), abs_bits(z))) >= CH_BIG) qbig |= 1u << i;
+      best[i] = Lim<float>::inf();
+      second[i] = Lim<float>::inf();
+      bt[i] = c0;
+    }
+    uint32_t rbig = 0;
+    float nx = 0.f, ny = 0.f, nz = 0.f;
+    if (c0 + lane < c1) {
+      nx = rp[3 * (c0 + lane)];
+      ny = rp[3 * (c0 + lane) + 1];
+      nz = rp[3 * (c0 + lane) + 2];
+    }
+    for (int blk = c0; blk < c1; blk += 64) {
+      const float x = nx, y = ny, z = nz;
+      rbig = max(rbig, max(abs_bits(x), max(abs_bits(y), abs_bits(z))));
+      // references past the chunk: A = +inf, never a tile minimum
+      const float rr = blk + lane < c1 ? sq3(x, y, z) : Lim<float>::inf();
+      s_ref[w][lane] = make_float4(x, y, z, rr);
+      __builtin_amdgcn_wave_barrier();
+      const int jn = blk + 64 + lane;
+      if (jn < c1) {
+        nx = rp[3 * jn];
+        ny = rp[3 * jn + 1];
+        nz = rp[3 * jn + 2];
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float tmin[Q];
+#pragma unroll
+        for (int i = 0; i < Q; ++i) tmin[i] = Lim<float>::inf();
+#pragma unroll
+        for (int jj = 0; jj < CH_TILE; ++jj) {
+          const float4 r = s_ref[w][CH_TILE * t + jj];
+#pragma unroll
+          for (int i = 0; i < Q; ++i)
+            tmin[i] = fminf(tmin[i], __builtin_fmaf(qx2[i], r.x,
+                                                    __builtin_fmaf(qy2[i], r.y,
+                                                                   __builtin_fmaf(qz2[i], r.z, r.w))));
+        }
+        const int t0 = blk + CH_TILE * t;
+#pragma unroll
+        for (int i = 0; i < Q; ++i) {
+          const bool lt = tmin[i] < best[i];
+          second[i] = lt ? best[i] : fminf(second[i], tmin[i]);
+          best[i] = lt ? tmin[i] : best[i];
+          bt[i] = lt ? t0 : bt[i];
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    // the 512-stage head of c0 decides whether the chunk's first references
+    // count (NaN rule of chunk_scan), so it joins the check
+    if ((c0 & 511) != 0) {
+      const float* h = rp + 3 * (c0 & ~511);
+      rbig = max(rbig, max(abs_bits(h[0]), max(abs_bits(h[1]), abs_bits(h[2]))));
+    }
+    const bool rbad = __ballot(rbig >= CH_BIG) != 0;
+
+    uint64_t amb[Q];
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const float qq = 0.25f * sq3(qx2[i], qy2[i], qz2[i]);
+      const float W = __builtin_fmaf(0x1p-18f, qq + fmaxf(best[i] + qq, 0.f), 0x1p-120f);
+      const bool a = rbad || ((qbig >> i) & 1u) || !(second[i] > best[i] + W);
+      amb[i] = __ballot(a);
+      float d_ = Lim<float>::inf();
+      int i_ = 0x7fffffff;
+      if (!a) {  // all exact minimisers are in tile bt: first index of its minimum
+        const float x = -0.5f * qx2[i], y = -0.5f * qy2[i], z = -0.5f * qz2[i];
+        const int te = min(bt[i] + CH_TILE, c1);
+        for (int j = bt[i]; j < te; ++j) {
+          const float d = ref_d(x, y, z, rp + 3 * j);
+          if (d < d_) {
+            d_ = d;
+            i_ = j;
+          }
+        }
+      }
+      bd[i] = d_;
+      bi[i] = i_;
+    }
+    // ambiguous queries: the wave scans the chunk for one query at a time
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      uint64_t m = amb[i];
+      while (m) {
+        const int l = __builtin_ctzll(m);
+        m &= m - 1;
+        int gq = qb * 64 * Q + i * 64 + l;
+        gq = gq < nq ? gq : nq - 1;
+        float md;
+        int mi;
+        chunk_scan(qp[3 * gq], qp[3 * gq + 1], qp[3 * gq + 2], rp, c0, c1, lane, md, mi);
+        if (lane == l) {
+          bd[i] = md;
+          bi[i] = mi;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      bd[i] = Lim<float>::inf();
+      bi[i] = 0x7fffffff;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    s_d[w][i * 64 + lane] = bd[i];
+    s_i[w][i * 64 + lane] = bi[i];
+  }
+  __syncthreads();
+
+  float* __restrict__ dout = (dir ? dist2 : dist1) + (size_t)b * nq;
+  int32_t* __restrict__ iout = (dir ? idx2 : idx1) + (size_t)b * nq;
+  for (int e = threadIdx.x; e < 64 * Q; e += 256) {
+    const int gq = qb * 64 * Q + e;
+    if (gq >= nq) continue;
+    float d = s_d[0][e];
+    int ix = s_i[0][e];
+#pragma unroll
+    for (int v = 1; v < CH_WAVES; ++v) {
+      const float dv = s_d[v][e];
+      if (dv < d) {
+        d = dv;
+        ix = s_i[v][e];
+      }
+    }
+    if (ix == 0x7fffffff) {  // empty reference cloud
+      d = 0.f;
+      ix = 0;
+    }
+    dout[gq] = d;
+    iout[gq] = ix;
   }
 }
 
@@ -286,15 +589,33 @@ static void launch_fwd(const void* x1, const void* x2, int B, int N, int M, void
                      (const T*)x2, B, N, M, nqb1, nqb2, (T*)d1, (T*)d2, i1, i2);
 }
 
+template <int Q>
+static void launch_fwd_filter(const void* x1, const void* x2, int B, int N, int M, void* d1,
+                              void* d2, int32_t* i1, int32_t* i2, hipStream_t s) {
+  const int nqb1 = (N + 64 * Q - 1) / (64 * Q), nqb2 = (M + 64 * Q - 1) / (64 * Q);
+  const int grid = B * (nqb1 + nqb2);
+  if (grid == 0) return;
+  hipLaunchKernelGGL((chamfer_fwd_filter_kernel<Q>), dim3(grid), dim3(256), 0, s,
+                     (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2, (float*)d1,
+                     (float*)d2, i1, i2);
+}
+
 template <typename T>
 static void fwd_dispatch(const void* x1, const void* x2, int B, int N, int M, void* d1, void* d2,
                          int32_t* i1, int32_t* i2, hipStream_t s) {
   // Largest per-lane query count that still gives >= 2 workgroups per CU.
   const int64_t q = (int64_t)B * ((int64_t)N + M);
-  if (q >= (int64_t)512 * 64 * 8) launch_fwd<T, 8>(x1, x2, B, N, M, d1, d2, i1, i2, s);
-  else if (q >= (int64_t)512 * 64 * 4) launch_fwd<T, 4>(x1, x2, B, N, M, d1, d2, i1, i2, s);
-  else if (q >= (int64_t)512 * 64 * 2) launch_fwd<T, 2>(x1, x2, B, N, M, d1, d2, i1, i2, s);
-  else launch_fwd<T, 1>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+  if constexpr (sizeof(T) == 4) {
+    if (q >= (int64_t)512 * 64 * 8) launch_fwd_filter<8>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    else if (q >= (int64_t)512 * 64 * 4) launch_fwd_filter<4>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    else if (q >= (int64_t)512 * 64 * 2) launch_fwd_filter<2>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    else launch_fwd_filter<1>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+  } else {
+    if (q >= (int64_t)512 * 64 * 8) launch_fwd<T, 8>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    else if (q >= (int64_t)512 * 64 * 4) launch_fwd<T, 4>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    else if (q >= (int64_t)512 * 64 * 2) launch_fwd<T, 2>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    else launch_fwd<T, 1>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+  }
 }
 
 template <typename T>
