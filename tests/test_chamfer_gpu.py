@@ -111,6 +111,26 @@ def test_backward_config2_vs_oracle(tpo, O, dev):
         assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.float64])
+@pytest.mark.parametrize("B,N,M", [(2, 20000, 17), (1, 70000, 900), (3, 4097, 5000)])
+def test_backward_slices_and_two_pass_vs_oracle(tpo, O, dev, dtype, B, N, M):
+    # sliced LDS accumulation (several slices per cloud, ragged last slice)
+    # and, for 70000 points, the two-pass global-atomic path
+    g = torch.Generator().manual_seed(N + M)
+    p1 = torch.randn(B, N, 3, generator=g).to(dtype)
+    p2 = torch.randn(B, M, 3, generator=g).to(dtype)
+    gd1 = torch.rand(B, N, generator=g).to(dtype)
+    gd2 = torch.rand(B, M, generator=g).to(dtype)
+    _, _, j1, j2 = O.chamfer_fwd(np_(p1), np_(p2))
+    ea, eb = O.chamfer_bwd(np_(p1), np_(p2), j1, j2, np_(gd1), np_(gd2), accum_f64=True)
+    ga, gb = torch.ops.torch_point_ops_chamfer.chamfer_backward(
+        p1.to(dev), p2.to(dev), torch.from_numpy(j1).to(dev), torch.from_numpy(j2).to(dev),
+        gd1.to(dev), gd2.to(dev))
+    tol = 2e-2 if dtype == torch.float16 else (1e-5 if dtype == torch.float32 else 1e-12)
+    for got, ref in ((np_(ga), ea), (np_(gb), eb)):
+        assert np.abs(got.astype(np.float64) - ref).max() <= tol * max(np.abs(ref).max(), 1e-30)
+
+
 # ---- edge cases of the float filter (expanded-form ranking + exact re-scan)
 # and of the NaN rule of the reference's 512-reference stages
 

@@ -44,6 +44,9 @@ HIPCC_FLAGS = [
     f"-I{INCLUDE}",
 ]
 
+# Per-file additions (none at present).
+HIPCC_FILE_FLAGS: dict = {}
+
 
 def _run(cmd, verbose):
     if verbose:
@@ -65,7 +68,8 @@ def build_hip_lib(jobs: int = 8, verbose: bool = False) -> str:
     for src in HIP_SOURCES:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIPCC_FLAGS, *HIPCC_FILE_FLAGS.get(src, []), "-c",
+                     os.path.join(CSRC, src), "-o", obj])
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     out = os.path.join(PKG, "libtpo_hip.so")

@@ -18,24 +18,25 @@
 //   reference's handling of NaN distances (chunk_scan).
 // Backward (replaces chamfer_dist_grad_kernel, chamfer.cu:200-234).
 //   grad_q[i] = 2 g_i (q_i - r_idx[i]) - sum over the other cloud's points j
-//   matched to i of 2 g_j (r_j - q_i).  When one cloud's gradient fits in LDS
-//   (<= 12288 points, float/half) a 1024-thread workgroup per (cloud, batch)
-//   accumulates the scattered terms with LDS atomics, adds its points' direct
-//   terms and writes every element once: no global atomics, no zero-fill.
+//   matched to i of 2 g_j (r_j - q_i).  float/half: a workgroup per (batch,
+//   cloud, slice of <= 4096 points) holds the slice's gradient in LDS,
+//   accumulates the scattered terms that land in it with LDS atomics, adds
+//   its points' direct terms and writes every element once: no global
+//   atomics, no zero-fill.
 //   (float16: terms are computed in half like the reference, accumulated in
 //   float and rounded once.)  Otherwise pass 1 stores the direct terms (which
 //   initialises both outputs) and pass 2 scatters the negated terms with
 //   hardware atomics, like the reference.
 #include <stdio.h>
 
+#include <algorithm>
+
+#include "chamfer_common.hpp"
 #include "tpo_common.hpp"
 
 #pragma clang fp contract(off)
 
 namespace tpo {
-
-constexpr int CH_WAVES = 4;
-constexpr int CH_TILE = 16;
 
 // Copy a wave-uniform (SGPR) value into a VGPR.  On gfx950 a VALU op with an
 // SGPR source issues at 4 cycles per wave64 instruction, while VGPR-only
@@ -52,70 +53,6 @@ __device__ __forceinline__ half_t to_vgpr(half_t s) { return s; }
 __device__ __forceinline__ float vmin(float a, float b) { return __builtin_fminf(a, b); }
 __device__ __forceinline__ double vmin(double a, double b) { return __builtin_fmin(a, b); }
 __device__ __forceinline__ half_t vmin(half_t a, half_t b) { return __builtin_fminf16(a, b); }
-
-template <typename T>
-__device__ __forceinline__ T ref_d(T qx, T qy, T qz, const T* __restrict__ r) {
-  return sq3((T)(r[0] - qx), (T)(r[1] - qy), (T)(r[2] - qz));
-}
-
-__device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o));
-  return v;
-}
-__device__ __forceinline__ double wave_min(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmin(v, __shfl_xor(v, o));
-  return v;
-}
-__device__ __forceinline__ half_t wave_min(half_t v) { return (half_t)wave_min((float)v); }
-__device__ __forceinline__ int wave_imin(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
-  return v;
-}
-
-// The reference's result for one query over the references [c0, c1),
-// computed by the whole wave (lanes stride the references).  chamfer.cu:55-82
-// takes the first element of each 512-reference stage unconditionally and
-// later ones on strict less; a stage replaces the stored result only when
-// that is strictly greater (:159-162).  With finite distances this is the
-// first index of the minimum.  With NaN distances: reference j counts only
-// if neither D(j) nor D(512*floor(j/512)) is NaN, and a NaN D(0) makes the
-// answer (NaN, 0).  Returns the minimum and first index over the counted
-// references of the range ((+inf, INT_MAX) when none counts), or (NaN, 0).
-template <typename T>
-__device__ void chunk_scan(T qx, T qy, T qz, const T* __restrict__ rp, int c0, int c1, int lane,
-                           T& out_d, int& out_i) {
-  T d_ = Lim<T>::inf();
-  int i_ = 0x7fffffff;
-  for (int j = c0 + lane; j < c1; j += 64) {
-    const T d = ref_d(qx, qy, qz, rp + 3 * j);
-    const int h = j & ~511;
-    const T dh = h == j ? d : ref_d(qx, qy, qz, rp + 3 * h);
-    if (d == d && dh == dh && (d < d_ || (d == d_ && i_ == 0x7fffffff))) {
-      d_ = d;
-      i_ = j;
-    }
-  }
-  T md = wave_min(d_);
-  int mi = wave_imin(d_ == md ? i_ : 0x7fffffff);
-  if (c0 == 0) {
-    const T d0 = ref_d(qx, qy, qz, rp);
-    if (d0 != d0) {
-      md = d0;
-      mi = 0;
-    }
-  }
-  out_d = md;
-  out_i = mi;
-}
-
-// x - x is 0 exactly when x is finite (inf - inf and NaN - NaN are NaN).
-template <typename T>
-__device__ __forceinline__ bool finite3(const T* __restrict__ p) {
-  return (T)(p[0] - p[0]) == (T)0 && (T)(p[1] - p[1]) == (T)0 && (T)(p[2] - p[2]) == (T)0;
-}
 
 template <typename T, int Q>
 __global__ __launch_bounds__(256) void chamfer_fwd_kernel(
@@ -250,20 +187,9 @@ __global__ __launch_bounds__(256) void chamfer_fwd_kernel(
   for (int e = threadIdx.x; e < 64 * Q; e += 256) {
     const int gq = qb * 64 * Q + e;
     if (gq >= nq) continue;
-    T bd = s_d[0][e];
-    int bi = s_i[0][e];
-#pragma unroll
-    for (int v = 1; v < CH_WAVES; ++v) {
-      const T d = s_d[v][e];
-      if (d < bd) {
-        bd = d;
-        bi = s_i[v][e];
-      }
-    }
-    if (bi == 0x7fffffff) {  // empty reference cloud: zeros, as the reference's init
-      bd = (T)0;
-      bi = 0;
-    }
+    T bd;
+    int bi;
+    merge_chunks<T, 64 * Q>(&s_d[0][e], &s_i[0][e], bd, bi);
     dout[gq] = bd;
     iout[gq] = bi;
   }
@@ -294,10 +220,6 @@ __global__ __launch_bounds__(256) void chamfer_fwd_kernel(
 // lane loads one reference and computes |r|^2 once, and every pair then
 // reads it back as one broadcast ds_read_b128, so the per-pair VALU work is
 // the 3 FMAs, half a v_min3 and the per-tile bookkeeping.
-constexpr uint32_t CH_BIG = 0x5d800000u;  // float bits of 2^60
-
-__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
-
 template <int Q>
 __global__ __launch_bounds__(256) void chamfer_fwd_filter_kernel(
     const float* __restrict__ xyz1, const float* __restrict__ xyz2, int B, int N, int M,
@@ -344,11 +266,12 @@ __global__ __launch_bounds__(256) void chamfer_fwd_filter_kernel(
       bt[i] = c0;
     }
     uint32_t rbig = 0;
-    float nx = 0.f, ny = 0.f, nz = 0.f;
-    if (c0 + lane < c1) {
-      nx = rp[3 * (c0 + lane)];
-      ny = rp[3 * (c0 + lane) + 1];
-      nz = rp[3 * (c0 + lane) + 2];
+    float nx, ny, nz;
+    {
+      const int j = min(c0 + lane, c1 - 1);
+      nx = rp[3 * j];
+      ny = rp[3 * j + 1];
+      nz = rp[3 * j + 2];
     }
     for (int blk = c0; blk < c1; blk += 64) {
       const float x = nx, y = ny, z = nz;
@@ -357,12 +280,10 @@ __global__ __launch_bounds__(256) void chamfer_fwd_filter_kernel(
       const float rr = blk + lane < c1 ? sq3(x, y, z) : Lim<float>::inf();
       s_ref[w][lane] = make_float4(x, y, z, rr);
       __builtin_amdgcn_wave_barrier();
-      const int jn = blk + 64 + lane;
-      if (jn < c1) {
-        nx = rp[3 * jn];
-        ny = rp[3 * jn + 1];
-        nz = rp[3 * jn + 2];
-      }
+      const int jn = min(blk + 64 + lane, c1 - 1);  // unconditional prefetch
+      nx = rp[3 * jn];
+      ny = rp[3 * jn + 1];
+      nz = rp[3 * jn + 2];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         float tmin[Q];
@@ -456,20 +377,9 @@ __global__ __launch_bounds__(256) void chamfer_fwd_filter_kernel(
   for (int e = threadIdx.x; e < 64 * Q; e += 256) {
     const int gq = qb * 64 * Q + e;
     if (gq >= nq) continue;
-    float d = s_d[0][e];
-    int ix = s_i[0][e];
-#pragma unroll
-    for (int v = 1; v < CH_WAVES; ++v) {
-      const float dv = s_d[v][e];
-      if (dv < d) {
-        d = dv;
-        ix = s_i[v][e];
-      }
-    }
-    if (ix == 0x7fffffff) {  // empty reference cloud
-      d = 0.f;
-      ix = 0;
-    }
+    float d;
+    int ix;
+    merge_chunks<float, 64 * Q>(&s_d[0][e], &s_i[0][e], d, ix);
     dout[gq] = d;
     iout[gq] = ix;
   }
@@ -534,17 +444,26 @@ __global__ __launch_bounds__(256) void chamfer_bwd_scatter_kernel(
   }
 }
 
-constexpr int CH_BWD_LDS_FLOATS = 36864;  // 144 KiB: 12288 points x 3
+// One workgroup per (batch, cloud, slice of that cloud's points): the slice's
+// gradient rows live in LDS; the workgroup scans the other cloud's nearest
+// indices and accumulates, with LDS atomics, the terms that land in its
+// slice; then it adds its points' direct terms and writes each element once.
+constexpr int CH_BWD_SLICE_MAX = 4096;  // points per slice (48 KiB of LDS)
+constexpr int CH_BWD_MAX_SLICES = 16;   // beyond this the 2-pass path is cheaper
 
 template <typename T>
-__global__ __launch_bounds__(1024) void chamfer_bwd_fused_kernel(
+__global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
     const T* __restrict__ xyz1, const T* __restrict__ xyz2, const int32_t* __restrict__ idx1,
     const int32_t* __restrict__ idx2, const T* __restrict__ gd1, const T* __restrict__ gd2, int N,
-    int M, T* __restrict__ g1, T* __restrict__ g2) {
-  __shared__ float acc[CH_BWD_LDS_FLOATS];
-  const int c = blockIdx.x & 1;  // 0: gradient of cloud 1, 1: of cloud 2
-  const int b = blockIdx.x >> 1;
+    int M, int S, T* __restrict__ g1, T* __restrict__ g2) {
+  extern __shared__ float acc[];
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int sl = lb % S;
+  const int c = (lb / S) & 1;  // 0: gradient of cloud 1, 1: of cloud 2
+  const int b = lb / (2 * S);
   const int n_own = c ? M : N, n_oth = c ? N : M;
+  const int span = (n_own + S - 1) / S;
+  const int lo = min(n_own, sl * span), hi = min(n_own, lo + span);
   const T* __restrict__ own = (c ? xyz2 : xyz1) + (size_t)b * n_own * 3;
   const T* __restrict__ oth = (c ? xyz1 : xyz2) + (size_t)b * n_oth * 3;
   const int32_t* __restrict__ idx_own = (c ? idx2 : idx1) + (size_t)b * n_own;
@@ -553,28 +472,28 @@ __global__ __launch_bounds__(1024) void chamfer_bwd_fused_kernel(
   const T* __restrict__ gd_oth = (c ? gd1 : gd2) + (size_t)b * n_oth;
   T* __restrict__ out = (c ? g2 : g1) + (size_t)b * n_own * 3;
 
-  for (int i = threadIdx.x; i < 3 * n_own; i += 1024) acc[i] = 0.f;
+  for (int i = threadIdx.x; i < 3 * (hi - lo); i += 256) acc[i] = 0.f;
   __syncthreads();
-  // other cloud's points j whose nearest point is i (chamfer.cu:229-231 of
-  // the other direction): acc[i] += -(g_j (r_j - q_i))
-  for (int j = threadIdx.x; j < n_oth; j += 1024) {
+  // other cloud's points j whose nearest point i is in [lo, hi)
+  // (chamfer.cu:229-231 of the other direction): acc[i] += -(g_j (r_j - q_i))
+  for (int j = threadIdx.x; j < n_oth; j += 256) {
     const int i = idx_oth[j];
-    if (i < 0 || i >= n_own) continue;
+    if (i < lo || i >= hi) continue;
     const T g = (T)(gd_oth[j] * (T)2);
 #pragma unroll
     for (int k = 0; k < 3; ++k)
-      atomicAdd(&acc[3 * i + k], -(float)(T)(g * (T)(oth[3 * j + k] - own[3 * i + k])));
+      atomicAdd(&acc[3 * (i - lo) + k], -(float)(T)(g * (T)(oth[3 * j + k] - own[3 * i + k])));
   }
   __syncthreads();
-  // direct term of the own points (chamfer.cu:226-228)
-  for (int i = threadIdx.x; i < n_own; i += 1024) {
+  // direct term of the slice's points (chamfer.cu:226-228)
+  for (int i = lo + threadIdx.x; i < hi; i += 256) {
     const int j2 = idx_own[i];
     const bool ok = j2 >= 0 && j2 < n_oth;
     const T g = (T)(gd_own[i] * (T)2);
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
       const T d = ok ? (T)(g * (T)(own[3 * i + k] - oth[3 * j2 + k])) : (T)0;
-      out[3 * i + k] = (T)(acc[3 * i + k] + (float)d);
+      out[3 * i + k] = (T)(acc[3 * (i - lo) + k] + (float)d);
     }
   }
 }
@@ -624,11 +543,19 @@ static void bwd_dispatch(const void* x1, const void* x2, const int32_t* i1, cons
                          void* g1, void* g2, hipStream_t s) {
   const int64_t total = B * (N + M);
   if (total == 0) return;
-  if (sizeof(T) <= 4 && 3 * std::max(N, M) <= CH_BWD_LDS_FLOATS && 2 * B < (1 << 30)) {
-    hipLaunchKernelGGL(chamfer_bwd_fused_kernel<T>, dim3((unsigned)(2 * B)), dim3(1024), 0, s,
-                       (const T*)x1, (const T*)x2, i1, i2, (const T*)gd1, (const T*)gd2, (int)N,
-                       (int)M, (T*)g1, (T*)g2);
-    return;
+  if (sizeof(T) <= 4) {
+    // slices: enough for one cloud's slice to fit LDS and for ~512 workgroups
+    const int64_t nmax = std::max(N, M);
+    int64_t S = (nmax + CH_BWD_SLICE_MAX - 1) / CH_BWD_SLICE_MAX;
+    const int64_t want = (512 + 2 * B - 1) / (2 * B);
+    S = std::max(S, std::min({want, std::max<int64_t>(1, nmax / 512), (int64_t)CH_BWD_MAX_SLICES}));
+    if (S <= CH_BWD_MAX_SLICES && 2 * B * S < (1 << 30)) {
+      const int64_t span = (nmax + S - 1) / S;
+      hipLaunchKernelGGL(chamfer_bwd_fused_kernel<T>, dim3((unsigned)(2 * B * S)), dim3(256),
+                         (size_t)(3 * span * sizeof(float)), s, (const T*)x1, (const T*)x2, i1, i2,
+                         (const T*)gd1, (const T*)gd2, (int)N, (int)M, (int)S, (T*)g1, (T*)g2);
+      return;
+    }
   }
   const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
   hipLaunchKernelGGL(chamfer_bwd_direct_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s,
