@@ -220,7 +220,9 @@ __global__ __launch_bounds__(256) void chamfer_fwd_kernel(
 // lane loads one reference and computes |r|^2 once, and every pair then
 // reads it back as one broadcast ds_read_b128, so the per-pair VALU work is
 // the 3 FMAs, half a v_min3 and the per-tile bookkeeping.
-template <int Q>
+constexpr int CH_FTILE = 16;  // references per tile of the filter kernel
+
+template <int Q, int TT>
 __global__ __launch_bounds__(256) void chamfer_fwd_filter_kernel(
     const float* __restrict__ xyz1, const float* __restrict__ xyz2, int B, int N, int M,
     int nqb1, int nqb2, float* __restrict__ dist1, float* __restrict__ dist2,
@@ -285,20 +287,19 @@ __global__ __launch_bounds__(256) void chamfer_fwd_filter_kernel(
       ny = rp[3 * jn + 1];
       nz = rp[3 * jn + 2];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < 64 / TT; ++t) {
         float tmin[Q];
 #pragma unroll
-        for (int i = 0; i < Q; ++i) tmin[i] = Lim<float>::inf();
+        for (int jj = 0; jj < TT; ++jj) {
+          const float4 r = s_ref[w][TT * t + jj];
 #pragma unroll
-        for (int jj = 0; jj < CH_TILE; ++jj) {
-          const float4 r = s_ref[w][CH_TILE * t + jj];
-#pragma unroll
-          for (int i = 0; i < Q; ++i)
-            tmin[i] = fminf(tmin[i], __builtin_fmaf(qx2[i], r.x,
-                                                    __builtin_fmaf(qy2[i], r.y,
-                                                                   __builtin_fmaf(qz2[i], r.z, r.w))));
+          for (int i = 0; i < Q; ++i) {
+            const float a = __builtin_fmaf(qx2[i], r.x,
+                                           __builtin_fmaf(qy2[i], r.y, __builtin_fmaf(qz2[i], r.z, r.w)));
+            tmin[i] = jj == 0 ? a : fminf(tmin[i], a);
+          }
         }
-        const int t0 = blk + CH_TILE * t;
+        const int t0 = blk + TT * t;
 #pragma unroll
         for (int i = 0; i < Q; ++i) {
           const bool lt = tmin[i] < best[i];
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(256) void chamfer_fwd_filter_kernel(
       int i_ = 0x7fffffff;
       if (!a) {  // all exact minimisers are in tile bt: first index of its minimum
         const float x = -0.5f * qx2[i], y = -0.5f * qy2[i], z = -0.5f * qz2[i];
-        const int te = min(bt[i] + CH_TILE, c1);
+        const int te = min(bt[i] + TT, c1);
         for (int j = bt[i]; j < te; ++j) {
           const float d = ref_d(x, y, z, rp + 3 * j);
           if (d < d_) {
@@ -508,13 +509,13 @@ static void launch_fwd(const void* x1, const void* x2, int B, int N, int M, void
                      (const T*)x2, B, N, M, nqb1, nqb2, (T*)d1, (T*)d2, i1, i2);
 }
 
-template <int Q>
+template <int Q, int TT>
 static void launch_fwd_filter(const void* x1, const void* x2, int B, int N, int M, void* d1,
                               void* d2, int32_t* i1, int32_t* i2, hipStream_t s) {
   const int nqb1 = (N + 64 * Q - 1) / (64 * Q), nqb2 = (M + 64 * Q - 1) / (64 * Q);
   const int grid = B * (nqb1 + nqb2);
   if (grid == 0) return;
-  hipLaunchKernelGGL((chamfer_fwd_filter_kernel<Q>), dim3(grid), dim3(256), 0, s,
+  hipLaunchKernelGGL((chamfer_fwd_filter_kernel<Q, TT>), dim3(grid), dim3(256), 0, s,
                      (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2, (float*)d1,
                      (float*)d2, i1, i2);
 }
@@ -525,10 +526,10 @@ static void fwd_dispatch(const void* x1, const void* x2, int B, int N, int M, vo
   // Largest per-lane query count that still gives >= 2 workgroups per CU.
   const int64_t q = (int64_t)B * ((int64_t)N + M);
   if constexpr (sizeof(T) == 4) {
-    if (q >= (int64_t)512 * 64 * 8) launch_fwd_filter<8>(x1, x2, B, N, M, d1, d2, i1, i2, s);
-    else if (q >= (int64_t)512 * 64 * 4) launch_fwd_filter<4>(x1, x2, B, N, M, d1, d2, i1, i2, s);
-    else if (q >= (int64_t)512 * 64 * 2) launch_fwd_filter<2>(x1, x2, B, N, M, d1, d2, i1, i2, s);
-    else launch_fwd_filter<1>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    if (q >= (int64_t)512 * 64 * 8) launch_fwd_filter<8, CH_FTILE>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    else if (q >= (int64_t)512 * 64 * 4) launch_fwd_filter<4, CH_FTILE>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    else if (q >= (int64_t)512 * 64 * 2) launch_fwd_filter<2, CH_FTILE>(x1, x2, B, N, M, d1, d2, i1, i2, s);
+    else launch_fwd_filter<1, CH_FTILE>(x1, x2, B, N, M, d1, d2, i1, i2, s);
   } else {
     if (q >= (int64_t)512 * 64 * 8) launch_fwd<T, 8>(x1, x2, B, N, M, d1, d2, i1, i2, s);
     else if (q >= (int64_t)512 * 64 * 4) launch_fwd<T, 4>(x1, x2, B, N, M, d1, d2, i1, i2, s);

@@ -2,7 +2,10 @@
 //
 // Forward (replaces gather_points_kernel, fps.cu:63-76): one thread per
 // (cloud, sample, group of 8 channels) reads its index once and gathers the
-// channels; stores are coalesced along the sample axis.
+// channels; stores are coalesced along the sample axis.  With many samples
+// per row most cache lines of a row hold a sample, so the cost is the lines
+// fetched: the workgroups of one (cloud, channel group) are numbered onto one
+// XCD (xcd_logical_block), so each line comes from HBM into one L2 once.
 // Backward (replaces zeros + gather_points_grad_kernel, fps.cu:79-98,376):
 // instead of a full zero-fill followed by scattered atomics, build a per-cloud
 // inverse map pos[b, n] = smallest sample j with idx[b, j] == n, then write
@@ -27,8 +30,8 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(const T* __restrict__ p
                                                          int64_t M, T* __restrict__ out) {
   const int64_t ncg = (C + GATHER_CGROUP - 1) / GATHER_CGROUP;
   const int64_t total = B * ncg * M;
-  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
-       t += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t t = (int64_t)xcd_logical_block(blockIdx.x, gridDim.x) * 256 + threadIdx.x;
+       t < total; t += (int64_t)gridDim.x * 256) {
     const int64_t j = t % M;
     const int64_t bc = t / M;
     const int64_t cg = bc % ncg, b = bc / ncg;
@@ -120,11 +123,20 @@ static unsigned grid_for(int64_t n) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
+// Grid for the XCD-numbered kernels: a multiple of 8 (the XCD count) so that
+// xcd_logical_block applies; surplus workgroups find no work.
+static unsigned grid_for_xcd(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 1 << 20) g = 1 << 20;
+  g = (g + 7) & ~(int64_t)7;
+  return (unsigned)(g < 8 ? 8 : g);
+}
+
 template <typename T>
 static void fwd(const void* pts, const int64_t* idx, int64_t B, int64_t C, int64_t N, int64_t M,
                 void* out, hipStream_t s) {
   const int64_t total = B * ((C + GATHER_CGROUP - 1) / GATHER_CGROUP) * M;
-  hipLaunchKernelGGL(gather_fwd_kernel<T>, dim3(grid_for(total)), dim3(256), 0, s,
+  hipLaunchKernelGGL(gather_fwd_kernel<T>, dim3(grid_for_xcd(total)), dim3(256), 0, s,
                      (const T*)pts, idx, B, C, N, M, (T*)out);
 }
 
