@@ -55,11 +55,27 @@ int tpo_abi_version(void);
  *   dist1 (B,N), dist2 (B,M) of `dtype`: squared distance to the nearest
  *   point of the other cloud; idx1 (B,N), idx2 (B,M) int32: the FIRST index
  *   attaining it.  An empty other cloud gives dist 0, idx 0.
+ *   workspace (optional, tpo_chamfer_workspace_size() bytes, 256-byte
+ *   aligned; size 0 means none is used): with it, float clouds of at least
+ *   2048 points each are searched with exact spatial pruning, which is much
+ *   faster on clustered or spread-out data; results are identical with or
+ *   without it.
  */
+int64_t tpo_chamfer_workspace_size(int dtype, int64_t B, int64_t N, int64_t M);
 int tpo_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2,
                     int64_t B, int64_t N, int64_t M,
                     void* dist1, void* dist2, int32_t* idx1, int32_t* idx2,
-                    void* stream);
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Diagnostic, no counterpart in the reference: after a tpo_chamfer_fwd call
+ * that used the workspace (same dtype and sizes), writes to the device
+ * int64 `pairs` the number of (query, reference) pairs the pruned search
+ * evaluated (a brute-force search evaluates 2*B*N*M).  Asynchronous on
+ * `stream`.
+ */
+int tpo_chamfer_pairs_evaluated(int dtype, const void* workspace, int64_t B,
+                                int64_t N, int64_t M, int64_t* pairs, void* stream);
 
 /*
  * Chamfer backward.  Replaces chamfer_cuda_backward (chamfer.cu:236-271),

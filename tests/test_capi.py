@@ -28,7 +28,8 @@ def lib(tpo):
 
 def test_header_declares_the_boundary():
     names = declared_functions()
-    for must in ("tpo_chamfer_fwd", "tpo_chamfer_bwd", "tpo_knn_fwd", "tpo_knn_bwd",
+    for must in ("tpo_chamfer_fwd", "tpo_chamfer_bwd", "tpo_chamfer_workspace_size",
+                 "tpo_chamfer_pairs_evaluated", "tpo_knn_fwd", "tpo_knn_bwd",
                  "tpo_fps_fwd", "tpo_fps_workspace_size", "tpo_gather_fwd", "tpo_gather_bwd",
                  "tpo_gather_bwd_workspace_size", "tpo_last_error", "tpo_abi_version"):
         assert must in names
@@ -37,7 +38,7 @@ def test_header_declares_the_boundary():
 def test_every_declared_symbol_is_exported(lib):
     missing = [n for n in declared_functions() if not hasattr(lib, n)]
     assert not missing, missing
-    assert lib.tpo_abi_version() >> 16 == 1
+    assert lib.tpo_abi_version() >> 16 == 2
 
 
 def test_argument_errors_are_reported(lib):
@@ -56,9 +57,19 @@ def test_argument_errors_are_reported(lib):
     assert ws >= 16 * 65536 * 20 and ws % 256 == 0
     assert lib.tpo_fps_fwd(0, None, 2, 10, 5, None, None, 0, None) == -4  # no workspace
     assert lib.tpo_fps_workspace_size(9, 1, 10) == -1
-    lib.tpo_chamfer_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, P, P, P, P, P]
-    assert lib.tpo_chamfer_fwd(0, None, None, -1, 3, 3, None, None, None, None, None) == -1
-    assert lib.tpo_chamfer_fwd(7, None, None, 0, 3, 3, None, None, None, None, None) == 0  # B=0
+    lib.tpo_chamfer_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, P, P, P, P, P, I, P]
+    assert lib.tpo_chamfer_fwd(0, None, None, -1, 3, 3, None, None, None, None, None, 0,
+                               None) == -1
+    assert lib.tpo_chamfer_fwd(7, None, None, 0, 3, 3, None, None, None, None, None, 0,
+                               None) == 0  # B=0
+    lib.tpo_chamfer_workspace_size.argtypes = [ctypes.c_int, I, I, I]
+    lib.tpo_chamfer_workspace_size.restype = I
+    assert lib.tpo_chamfer_workspace_size(0, 32, 8192, 8192) > 32 * 16384 * 20
+    assert lib.tpo_chamfer_workspace_size(0, 2, 100, 8192) == 0    # too small to prune
+    assert lib.tpo_chamfer_workspace_size(1, 32, 8192, 8192) == 0  # float only
+    assert lib.tpo_chamfer_workspace_size(0, -1, 3, 3) == -1
+    lib.tpo_chamfer_pairs_evaluated.argtypes = [ctypes.c_int, P, I, I, I, P, P]
+    assert lib.tpo_chamfer_pairs_evaluated(0, None, 2, 4096, 4096, None, None) == -1
     lib.tpo_knn_workspace_size.argtypes = [I, I]
     lib.tpo_knn_workspace_size.restype = I
     assert lib.tpo_knn_workspace_size(8, 16384) == 8 * 16384 * 4

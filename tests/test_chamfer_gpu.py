@@ -214,6 +214,98 @@ def test_nonfinite_coordinates_follow_reference(tpo, O, dev, dtype):
     assert (i1[0] == 0).all() and not np.isin(i1[1], np.arange(512, 1024)).any()
 
 
+# ---- the spatially pruned float path (both clouds >= 2048 points)
+
+def _pruned_case(kind, g):
+    if kind == "uniform":
+        return torch.rand(2, 3000, 3, generator=g), torch.rand(2, 2500, 3, generator=g)
+    if kind == "blobs":
+        return workloads.chamfer_c2(seed=9, B=2, N=4096)
+    if kind == "flat":  # zero extent along z: every point in one cell layer
+        p1 = torch.rand(2, 2100, 3, generator=g)
+        p2 = torch.rand(2, 2600, 3, generator=g)
+        p1[..., 2] = 0.5
+        p2[..., 2] = 0.5
+        return p1, p2
+    if kind == "single_point":  # zero extent in every axis, all distances tie
+        return torch.full((1, 2048, 3), 0.25), torch.full((1, 2100, 3), 0.75)
+    if kind == "apart":  # query cloud far from the reference cloud
+        return torch.rand(2, 2500, 3, generator=g) + 10.0, torch.rand(2, 3100, 3, generator=g)
+    if kind == "duplicates":
+        p1 = torch.rand(2, 2048, 3, generator=g)
+        p2 = torch.cat([p1[:, :1024], p1[:, :1024], p1[:, 1000:1100]], 1)[:, torch.randperm(2148, generator=g)]
+        return p1, p2
+    if kind == "lattice":
+        ax = torch.arange(16.0)
+        lat = torch.stack(torch.meshgrid(ax, ax, ax, indexing="ij"), -1).reshape(1, -1, 3)
+        p2 = lat[:, torch.randperm(lat.shape[1], generator=g)]
+        p1 = torch.randint(0, 31, (1, 3000, 3), generator=g).float() / 2
+        return p1, p2
+    if kind == "line":
+        t = torch.rand(1, 4000, 1, generator=g)
+        return t * torch.tensor([1.0, 2.0, -1.0]), torch.rand(1, 2500, 1, generator=g) * torch.tensor([1.0, 2.0, -1.0])
+    if kind == "tiny":
+        return torch.randn(1, 2500, 3, generator=g) * 1e-19, torch.randn(1, 2200, 3, generator=g) * 1e-19
+    if kind == "offset":
+        return torch.rand(1, 2500, 3, generator=g) + 3e4, torch.rand(1, 2200, 3, generator=g) + 3e4
+    if kind == "huge":
+        p1, p2 = torch.randn(2, 2300, 3, generator=g), torch.randn(2, 2400, 3, generator=g)
+        p2[0, 77] = 2.0 ** 62
+        p1[1, 5, 1] = -1e30
+        return p1, p2
+    if kind == "nonfinite":
+        p1, p2 = torch.randn(3, 2100, 3, generator=g), torch.randn(3, 2600, 3, generator=g)
+        p2[0, 1000, 0] = float("nan")   # reference cloud with a NaN: every query re-scanned
+        p2[1, 0, 2] = float("nan")      # D(0) NaN
+        p1[2, 7, 1] = float("inf")      # one query non-finite
+        return p1, p2
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["uniform", "blobs", "flat", "single_point", "apart",
+                                  "duplicates", "lattice", "line", "tiny", "offset", "huge",
+                                  "nonfinite"])
+def test_pruned_forward_vs_oracle(tpo, O, dev, kind):
+    g = torch.Generator().manual_seed(len(kind))
+    p1, p2 = _pruned_case(kind, g)
+    assert min(p1.shape[1], p2.shape[1]) >= 2048
+    check_vs_oracle(O, dev, p1.float(), p2.float())
+
+
+def test_pruned_equals_dense_and_counts_pairs(tpo, dev):
+    import ctypes
+    from torch_point_ops import _native
+
+    lib = ctypes.CDLL(_native.HIP_LIB)
+    P, I = ctypes.c_void_p, ctypes.c_int64
+    lib.tpo_chamfer_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, P, P, P, P, P, I, P]
+    lib.tpo_chamfer_workspace_size.argtypes = [ctypes.c_int, I, I, I]
+    lib.tpo_chamfer_workspace_size.restype = I
+    lib.tpo_chamfer_pairs_evaluated.argtypes = [ctypes.c_int, P, I, I, I, P, P]
+    p1, p2 = (t.to(dev) for t in workloads.chamfer_c2())
+    B, N, M = p1.shape[0], p1.shape[1], p2.shape[1]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    ws = torch.empty(lib.tpo_chamfer_workspace_size(0, B, N, M), dtype=torch.uint8, device=dev)
+    for w in (None, ws):
+        d1, d2 = torch.empty(B, N, device=dev), torch.empty(B, M, device=dev)
+        i1 = torch.empty(B, N, dtype=torch.int32, device=dev)
+        i2 = torch.empty(B, M, dtype=torch.int32, device=dev)
+        rc = lib.tpo_chamfer_fwd(0, p1.data_ptr(), p2.data_ptr(), B, N, M, d1.data_ptr(),
+                                 d2.data_ptr(), i1.data_ptr(), i2.data_ptr(),
+                                 None if w is None else w.data_ptr(),
+                                 0 if w is None else w.numel(), stream)
+        assert rc == 0
+        outs.append((d1, d2, i1, i2))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    pairs = torch.zeros(1, dtype=torch.int64, device=dev)
+    assert lib.tpo_chamfer_pairs_evaluated(0, ws.data_ptr(), B, N, M, pairs.data_ptr(),
+                                           stream) == 0
+    n = int(pairs.item())
+    assert 0 < n < 2 * B * N * M
+
+
 # ---- the reference test suite's checks (tests/test_chamfer.py) ----
 
 def torch_reference(p1, p2):

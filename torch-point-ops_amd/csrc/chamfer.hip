@@ -571,9 +571,19 @@ static void bwd_dispatch(const void* x1, const void* x2, const int32_t* i1, cons
 
 using namespace tpo;
 
+static bool prune_applies(int dtype, int64_t B, int64_t N, int64_t M) {
+  return dtype == TPO_F32 && B > 0 && N >= CH_PRUNE_MIN && M >= CH_PRUNE_MIN;
+}
+
+extern "C" int64_t tpo_chamfer_workspace_size(int dtype, int64_t B, int64_t N, int64_t M) {
+  if (B < 0 || N < 0 || M < 0) return -1;
+  return prune_applies(dtype, B, N, M) ? chamfer_prune_workspace(B, N, M) : 0;
+}
+
 extern "C" int tpo_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2, int64_t B,
                                int64_t N, int64_t M, void* dist1, void* dist2, int32_t* idx1,
-                               int32_t* idx2, void* stream) {
+                               int32_t* idx2, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
   if (B < 0 || N < 0 || M < 0 || N >= (1 << 28) || M >= (1 << 28) ||
       B * (N + M) >= ((int64_t)1 << 31))
     return set_error(TPO_ERR_ARG, "tpo_chamfer_fwd: bad sizes B=%lld N=%lld M=%lld",
@@ -582,6 +592,15 @@ extern "C" int tpo_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2, in
   if ((N > 0 && (!xyz1 || !dist1 || !idx1)) || (M > 0 && (!xyz2 || !dist2 || !idx2)))
     return set_error(TPO_ERR_ARG, "tpo_chamfer_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
+  if (workspace && prune_applies(dtype, B, N, M)) {
+    const int64_t need = chamfer_prune_workspace(B, N, M);
+    if (workspace_bytes < need)
+      return set_error(TPO_ERR_WORKSPACE, "tpo_chamfer_fwd: workspace of %lld bytes < %lld",
+                       (long long)workspace_bytes, (long long)need);
+    launch_chamfer_fwd_prune(xyz1, xyz2, (int)B, (int)N, (int)M, dist1, dist2, idx1, idx2,
+                             workspace, s);
+    return check_launch("tpo_chamfer_fwd");
+  }
   switch (dtype) {
     case TPO_F32: fwd_dispatch<float>(xyz1, xyz2, (int)B, (int)N, (int)M, dist1, dist2, idx1, idx2, s); break;
     case TPO_F64: fwd_dispatch<double>(xyz1, xyz2, (int)B, (int)N, (int)M, dist1, dist2, idx1, idx2, s); break;
@@ -589,6 +608,15 @@ extern "C" int tpo_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2, in
     default: return set_error(TPO_ERR_DTYPE, "tpo_chamfer_fwd: unsupported dtype %d", dtype);
   }
   return check_launch("tpo_chamfer_fwd");
+}
+
+extern "C" int tpo_chamfer_pairs_evaluated(int dtype, const void* workspace, int64_t B,
+                                           int64_t N, int64_t M, int64_t* pairs, void* stream) {
+  if (!workspace || !pairs || !prune_applies(dtype, B, N, M))
+    return set_error(TPO_ERR_ARG,
+                     "tpo_chamfer_pairs_evaluated: no pruned forward for these arguments");
+  launch_chamfer_prune_stats(workspace, B, N, M, pairs, (hipStream_t)stream);
+  return check_launch("tpo_chamfer_pairs_evaluated");
 }
 
 extern "C" int tpo_chamfer_bwd(int dtype, const void* xyz1, const void* xyz2,

@@ -1,0 +1,431 @@
+// chamfer_grid.hip -- Chamfer forward for float clouds by exact grid search
+// (replaces chamfer_dist_kernel, chamfer.cu:36-167, when the caller provides
+// a workspace and both clouds have at least CH_PRUNE_MIN points).
+//
+// 1. chamfer_grid_sort_kernel, one workgroup per (batch, cloud): the cloud's
+//    bounding box, a counting sort of its points into a 16^3 grid of cells
+//    (cells in Morton order, so neighbouring cells are mostly close in
+//    memory), the sorted points as (x, y, z, original index) and the start of
+//    every cell.
+// 2. chamfer_grid_search_kernel: one lane per query, queries taken in the
+//    sorted (Morton) order of their own cloud so a wave's lanes search nearby
+//    cells.  A lane visits the cells of the reference grid in Chebyshev rings
+//    around its query's cell and evaluates every point of a visited cell
+//    with the reference formula (chamfer.cu:64-67, same bits), keeping the
+//    smallest (distance, original index) -- the reference's first-index rule.
+//    A cell is skipped, and the ring walk stops, once a lower bound of the
+//    squared distance to anything left, rounded down by 2^-20 relative,
+//    exceeds the best distance found: the reference's float distance of any
+//    such point is then strictly larger (its relative error is <= 5u), so
+//    neither a smaller distance nor a tie with a lower index is skipped.
+//    Cell boxes are widened by 2^-20 (|lo| + extent) per side, which covers
+//    the rounding of the cell assignment.
+// 3. Queries with a coordinate that is non-finite or >= 2^60 in magnitude,
+//    and every query of a reference cloud holding such a coordinate, are
+//    scanned over the whole reference cloud in original order by chunk_scan
+//    (the reference's NaN rule included).
+// Results are identical to the reference's; the work depends on the data
+// (clustered and spread clouds need a few dozen points per query, a cloud
+// squeezed into one cell degrades to a full scan).  Each wave records the
+// number of points it evaluated (tpo_chamfer_pairs_evaluated sums them).
+#include <algorithm>
+#include <mutex>
+
+#include "chamfer_common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace tpo {
+
+constexpr int CG_GRID = 16;  // cells per axis
+constexpr int CG_CELLS = CG_GRID * CG_GRID * CG_GRID;
+constexpr int CG_WG = 256;        // queries per workgroup, global-memory search
+constexpr int CG_WG_LDS = 1024;   // queries per workgroup, LDS search
+constexpr int CG_LDS_POINTS = 8192;  // largest reference cloud staged in LDS
+
+__host__ __device__ inline int64_t cg_pad(int64_t n) { return (n + 63) & ~(int64_t)63; }
+
+// Byte offsets of the workspace regions (all 256-byte aligned).
+struct CgLayout {
+  int64_t hdr;     // 2B x 16 floats: lo[3], hi[3], cells per unit[3], cell size[3], bad
+  int64_t pts;     // float4 per padded point: sorted (x, y, z, original index bits)
+  int64_t cstart;  // (CG_CELLS + 1) int32 per cloud: first sorted position of a cell
+  int64_t rank;    // int32 per point: rank within its cell (sort scratch)
+  int64_t stats;   // int32 per search wave: points evaluated
+  int64_t total;
+};
+
+static int64_t cg_align(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+static bool cg_use_lds(int64_t N, int64_t M) {
+  return cg_pad(N) <= CG_LDS_POINTS && cg_pad(M) <= CG_LDS_POINTS;
+}
+static int cg_wg(int64_t N, int64_t M) { return cg_use_lds(N, M) ? CG_WG_LDS : CG_WG; }
+static int64_t cg_grid_size(int64_t B, int64_t N, int64_t M) {
+  const int wg = cg_wg(N, M);
+  return B * ((N + wg - 1) / wg + (M + wg - 1) / wg);
+}
+
+static CgLayout cg_layout(int64_t B, int64_t N, int64_t M) {
+  const int64_t P = cg_pad(N) + cg_pad(M);
+  CgLayout L;
+  int64_t o = 0;
+  L.hdr = o;
+  o = cg_align(o + 2 * B * 16 * 4);
+  L.pts = o;
+  o = cg_align(o + B * P * 16);
+  L.cstart = o;
+  o = cg_align(o + 2 * B * (CG_CELLS + 1) * 4);
+  L.rank = o;
+  o = cg_align(o + B * P * 4);
+  L.stats = o;
+  o = cg_align(o + cg_grid_size(B, N, M) * (cg_wg(N, M) / 64) * 4);
+  L.total = o;
+  return L;
+}
+
+__device__ __forceinline__ uint32_t cg_spread(uint32_t v) {  // 4 bits -> every third bit
+  v = (v | (v << 4)) & 0x0c3u;
+  v = (v | (v << 2)) & 0x249u;
+  return v;
+}
+
+__device__ __forceinline__ int cg_axis_cell(float p, float lo, float sc) {
+  const float f = (p - lo) * sc;
+  return is_nan(f) ? 0 : (int)fminf(fmaxf(f, 0.f), (float)(CG_GRID - 1));
+}
+
+__device__ __forceinline__ uint32_t cg_code(int cx, int cy, int cz) {
+  return cg_spread((uint32_t)cx) | (cg_spread((uint32_t)cy) << 1) | (cg_spread((uint32_t)cz) << 2);
+}
+
+__global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
+    const float* __restrict__ xyz1, const float* __restrict__ xyz2, int N, int M,
+    char* __restrict__ ws, CgLayout L) {
+  __shared__ uint32_t cnt[CG_CELLS];
+  __shared__ float red[6][16];
+  __shared__ uint32_t part[16];
+  __shared__ uint32_t s_bad;
+  const int c = blockIdx.x & 1, b = blockIdx.x >> 1;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int n = c ? M : N;
+  const int64_t PN = cg_pad(N), PM = cg_pad(M);
+  const int64_t base = (int64_t)b * (PN + PM) + (c ? PN : 0);
+  const float* __restrict__ P = (c ? xyz2 : xyz1) + (size_t)b * n * 3;
+  float* __restrict__ hdr = reinterpret_cast<float*>(ws + L.hdr) + (size_t)blockIdx.x * 16;
+  float4* __restrict__ pts = reinterpret_cast<float4*>(ws + L.pts) + base;
+  int32_t* __restrict__ cstart =
+      reinterpret_cast<int32_t*>(ws + L.cstart) + (size_t)blockIdx.x * (CG_CELLS + 1);
+  int32_t* __restrict__ rank = reinterpret_cast<int32_t*>(ws + L.rank) + base;
+
+  // bounding box (NaN ignored) and the bad flag (non-finite or >= 2^60)
+  if (tid == 0) s_bad = 0;
+  float lo[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
+  float hi[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  uint32_t big = 0;
+  for (int k = tid; k < n; k += 1024)
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      const float v = P[3 * k + a];
+      big = max(big, abs_bits(v));
+      lo[a] = fminf(lo[a], v);
+      hi[a] = fmaxf(hi[a], v);
+    }
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      lo[a] = fminf(lo[a], __shfl_xor(lo[a], m));
+      hi[a] = fmaxf(hi[a], __shfl_xor(hi[a], m));
+    }
+  if (lane == 0)
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      red[a][w] = lo[a];
+      red[3 + a][w] = hi[a];
+    }
+  for (int k = tid; k < CG_CELLS; k += 1024) cnt[k] = 0;
+  __syncthreads();
+  if (big >= CH_BIG) atomicOr(&s_bad, 1u);
+  float glo[3], ghi[3], gs[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    float x = __builtin_inff(), z = -__builtin_inff();
+    for (int v = 0; v < 16; ++v) {
+      x = fminf(x, red[a][v]);
+      z = fmaxf(z, red[3 + a][v]);
+    }
+    if (!is_finite(x) || !is_finite(z)) x = z = 0.f;  // empty or all-NaN axis
+    glo[a] = x;
+    ghi[a] = z;
+    const float ext = z - x;
+    gs[a] = (ext > 0.f && is_finite(ext)) ? (float)CG_GRID / ext : 0.f;
+  }
+  for (int k = tid; k < n; k += 1024) {
+    const uint32_t code = cg_code(cg_axis_cell(P[3 * k], glo[0], gs[0]),
+                                  cg_axis_cell(P[3 * k + 1], glo[1], gs[1]),
+                                  cg_axis_cell(P[3 * k + 2], glo[2], gs[2]));
+    rank[k] = (int32_t)atomicAdd(&cnt[code], 1u);
+  }
+  __syncthreads();
+  {  // exclusive scan of the cell counts, 4 cells per thread
+    uint32_t v[4], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = cnt[tid * 4 + i];
+      sum += v[i];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) part[w] = incl;
+    __syncthreads();
+    uint32_t run = incl - sum;
+    for (int v2 = 0; v2 < w; ++v2) run += part[v2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      cnt[tid * 4 + i] = run;
+      cstart[tid * 4 + i] = (int32_t)run;
+      run += v[i];
+    }
+    if (tid == 1023) cstart[CG_CELLS] = (int32_t)run;
+  }
+  __syncthreads();
+  for (int k = tid; k < n; k += 1024) {
+    const float x = P[3 * k], y = P[3 * k + 1], z = P[3 * k + 2];
+    const uint32_t code = cg_code(cg_axis_cell(x, glo[0], gs[0]), cg_axis_cell(y, glo[1], gs[1]),
+                                  cg_axis_cell(z, glo[2], gs[2]));
+    pts[cnt[code] + rank[k]] = make_float4(x, y, z, __int_as_float(k));
+  }
+  for (int pos = n + tid; pos < cg_pad(n); pos += 1024)
+    pts[pos] = make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
+  if (tid == 0) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      hdr[a] = glo[a];
+      hdr[3 + a] = ghi[a];
+      hdr[6 + a] = gs[a];
+      hdr[9 + a] = gs[a] > 0.f ? (ghi[a] - glo[a]) / (float)CG_GRID : 0.f;
+    }
+    hdr[12] = __uint_as_float(s_bad);
+  }
+}
+
+// LDS: the reference cloud's sorted points and cell starts are first copied to
+// LDS by the (1024-thread) workgroup, which then searches at LDS latency; used
+// when they fit (up to CG_LDS_POINTS points).
+template <bool LDS, int WG>
+__global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
+    const float* __restrict__ xyz1, const float* __restrict__ xyz2, int B, int N, int M,
+    int nqb1, int nqb2, const char* __restrict__ ws, CgLayout L, float* __restrict__ dist1,
+    float* __restrict__ dist2, int32_t* __restrict__ idx1, int32_t* __restrict__ idx2) {
+  extern __shared__ float4 s_pts[];
+  const int bid = xcd_logical_block(blockIdx.x, gridDim.x);
+  int lb = bid;
+  const int g1 = B * nqb1;
+  const int dir = lb >= g1;
+  if (dir) lb -= g1;
+  const int nqb = dir ? nqb2 : nqb1;
+  const int b = lb / nqb;
+  const int qb = lb - b * nqb;
+  const int nq = dir ? M : N;
+  const int nr = dir ? N : M;
+  const int cq = dir, cr = 1 - dir;  // query / reference cloud
+  const int64_t PN = cg_pad(N), PM = cg_pad(M);
+  const int64_t base_q = (int64_t)b * (PN + PM) + (cq ? PN : 0);
+  const int64_t base_r = (int64_t)b * (PN + PM) + (cr ? PN : 0);
+  const float4* __restrict__ qs = reinterpret_cast<const float4*>(ws + L.pts) + base_q;
+  const float4* __restrict__ rs_g = reinterpret_cast<const float4*>(ws + L.pts) + base_r;
+  const int32_t* __restrict__ cs_g =
+      reinterpret_cast<const int32_t*>(ws + L.cstart) + (size_t)(2 * b + cr) * (CG_CELLS + 1);
+  const float4* rs = rs_g;
+  const int32_t* cstart = cs_g;
+  if constexpr (LDS) {
+    const int np = (int)cg_pad(nr);
+    int32_t* s_cs = reinterpret_cast<int32_t*>(s_pts + np);
+    for (int k = threadIdx.x; k < np; k += WG) s_pts[k] = rs_g[k];
+    for (int k = threadIdx.x; k <= CG_CELLS; k += WG) s_cs[k] = cs_g[k];
+    __syncthreads();
+    rs = s_pts;
+    cstart = s_cs;
+  }
+  const float* __restrict__ h = reinterpret_cast<const float*>(ws + L.hdr) + (2 * b + cr) * 16;
+  const float* __restrict__ rp = (dir ? xyz1 : xyz2) + (size_t)b * nr * 3;  // original order
+  const float* __restrict__ qp = (dir ? xyz2 : xyz1) + (size_t)b * nq * 3;
+  float* __restrict__ dout = (dir ? dist2 : dist1) + (size_t)b * nq;
+  int32_t* __restrict__ iout = (dir ? idx2 : idx1) + (size_t)b * nq;
+
+  const int lane = lane_id(), w = wave_id();
+  const int pos = qb * WG + (int)threadIdx.x;
+  const bool valid = pos < nq;
+  const float4 q = qs[min(pos, nq - 1)];
+  const int oq = __float_as_int(q.w);
+  const bool rbad = __float_as_uint(h[12]) != 0u;
+  const bool qbad = max(abs_bits(q.x), max(abs_bits(q.y), abs_bits(q.z))) >= CH_BIG;
+  const bool fallback = valid && (rbad || qbad);
+  int examined = 0;
+
+  if (valid && !fallback) {
+    const float glo[3] = {h[0], h[1], h[2]}, ghi[3] = {h[3], h[4], h[5]};
+    const float gs[3] = {h[6], h[7], h[8]}, cs[3] = {h[9], h[10], h[11]};
+    const float qv[3] = {q.x, q.y, q.z};
+    int ci[3], ga[3];
+    float eps[3], m[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      ga[a] = gs[a] > 0.f ? CG_GRID : 1;
+      ci[a] = gs[a] > 0.f ? cg_axis_cell(qv[a], glo[a], gs[a]) : 0;
+      eps[a] = 0x1p-20f * (__builtin_fabsf(glo[a]) + (ghi[a] - glo[a])) + 0x1p-126f;
+      // distance from the query to the nearer face of its own cell (0 outside)
+      const float clo = ga[a] > 1 ? glo[a] + (float)ci[a] * cs[a] : glo[a];
+      const float chi = ga[a] > 1 ? glo[a] + (float)(ci[a] + 1) * cs[a] : ghi[a];
+      m[a] = fmaxf(fminf(qv[a] - clo, chi - qv[a]) - eps[a], 0.f);
+    }
+    int rmax = 0;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) rmax = max(rmax, max(ci[a], ga[a] - 1 - ci[a]));
+    float bd = Lim<float>::inf();
+    int bi = 0x7fffffff;
+    for (int r = 0; r <= rmax; ++r) {
+      if (r > 0) {  // lower bound for every cell of ring r and beyond
+        float lr = Lim<float>::inf();
+#pragma unroll
+        for (int a = 0; a < 3; ++a)
+          if (ga[a] > 1) lr = fminf(lr, fmaxf((float)(r - 1) * cs[a] + m[a], 0.f));
+        if (lr * lr * (1.f - 0x1p-20f) > bd) break;
+      }
+      const int z0 = max(-r, -ci[2]), z1 = min(r, ga[2] - 1 - ci[2]);
+      const int y0 = max(-r, -ci[1]), y1 = min(r, ga[1] - 1 - ci[1]);
+      for (int dz = z0; dz <= z1; ++dz)
+        for (int dy = y0; dy <= y1; ++dy) {
+          const bool full = dz == -r || dz == r || dy == -r || dy == r;
+          const int x0 = max(-r, -ci[0]), x1 = min(r, ga[0] - 1 - ci[0]);
+          for (int dx = x0; dx <= x1; ++dx) {
+            if (!full && dx != -r && dx != r) {  // interior of the ring: jump to its far side
+              if (dx < r) dx = r - 1;
+              continue;
+            }
+            const int cc[3] = {ci[0] + dx, ci[1] + dy, ci[2] + dz};
+            float gap[3];
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+              const float clo = (ga[a] > 1 ? glo[a] + (float)cc[a] * cs[a] : glo[a]) - eps[a];
+              const float chi = (ga[a] > 1 ? glo[a] + (float)(cc[a] + 1) * cs[a] : ghi[a]) + eps[a];
+              gap[a] = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
+            }
+            if (sq3(gap[0], gap[1], gap[2]) * (1.f - 0x1p-20f) > bd) continue;
+            const uint32_t code = cg_code(cc[0], cc[1], cc[2]);
+            const int j1 = cstart[code + 1];
+            int j = cstart[code];
+            for (; j + 1 < j1; j += 2) {  // two loads in flight
+              const float4 p0 = rs[j], p1 = rs[j + 1];
+              const float d0 = sq3((float)(p0.x - q.x), (float)(p0.y - q.y), (float)(p0.z - q.z));
+              const float d1 = sq3((float)(p1.x - q.x), (float)(p1.y - q.y), (float)(p1.z - q.z));
+              const int o0 = __float_as_int(p0.w), o1 = __float_as_int(p1.w);
+              if (d0 < bd || (d0 == bd && o0 < bi)) {
+                bd = d0;
+                bi = o0;
+              }
+              if (d1 < bd || (d1 == bd && o1 < bi)) {
+                bd = d1;
+                bi = o1;
+              }
+            }
+            if (j < j1) {
+              const float4 p = rs[j];
+              const float d = sq3((float)(p.x - q.x), (float)(p.y - q.y), (float)(p.z - q.z));
+              const int oi = __float_as_int(p.w);
+              if (d < bd || (d == bd && oi < bi)) {
+                bd = d;
+                bi = oi;
+              }
+            }
+            examined += j1 - cstart[code];
+          }
+        }
+    }
+    dout[oq] = bd;
+    iout[oq] = bi;
+  }
+  {  // points evaluated by this wave
+    int e = examined;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o);
+    if (lane == 0)
+      reinterpret_cast<int32_t*>(const_cast<char*>(ws) + L.stats)[(size_t)bid * (WG / 64) + w] = e;
+  }
+  // queries that need the reference's full rule: the wave scans one at a time
+  uint64_t fb = __ballot(fallback);
+  while (fb) {
+    const int l = __builtin_ctzll(fb);
+    fb &= fb - 1;
+    const int o = __shfl(oq, l);
+    float md;
+    int mi;
+    chunk_scan(qp[3 * o], qp[3 * o + 1], qp[3 * o + 2], rp, 0, nr, lane, md, mi);
+    if (mi == 0x7fffffff) {  // no reference counts: cannot happen with nr > 0
+      md = 0.f;
+      mi = 0;
+    }
+    if (lane == 0) {
+      dout[o] = md;
+      iout[o] = mi;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void chamfer_stats_kernel(const int32_t* __restrict__ stats,
+                                                            int64_t n, int64_t* __restrict__ out) {
+  __shared__ int64_t part[4];
+  int64_t s = 0;
+  for (int64_t k = threadIdx.x; k < n; k += 256) s += stats[k];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = part[0] + part[1] + part[2] + part[3];
+}
+
+int64_t chamfer_prune_workspace(int64_t B, int64_t N, int64_t M) {
+  return cg_layout(B, N, M).total;
+}
+
+void launch_chamfer_fwd_prune(const void* x1, const void* x2, int B, int N, int M, void* d1,
+                              void* d2, int32_t* i1, int32_t* i2, void* ws, hipStream_t s) {
+  const CgLayout L = cg_layout(B, N, M);
+  hipLaunchKernelGGL(chamfer_grid_sort_kernel, dim3(2 * B), dim3(1024), 0, s, (const float*)x1,
+                     (const float*)x2, N, M, (char*)ws, L);
+  if (cg_use_lds(N, M)) {
+    constexpr int WG = CG_WG_LDS;
+    const int nqb1 = (N + WG - 1) / WG, nqb2 = (M + WG - 1) / WG;
+    const size_t lds = (size_t)std::max(cg_pad(N), cg_pad(M)) * 16 + (CG_CELLS + 1) * 4;
+    static std::once_flag attr_once;  // dynamic LDS beyond the default limit
+    std::call_once(attr_once, [] {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&chamfer_grid_search_kernel<true, WG>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                CG_LDS_POINTS * 16 + (CG_CELLS + 1) * 4);
+    });
+    hipLaunchKernelGGL((chamfer_grid_search_kernel<true, WG>), dim3(B * (nqb1 + nqb2)), dim3(WG),
+                       lds, s, (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2,
+                       (const char*)ws, L, (float*)d1, (float*)d2, i1, i2);
+  } else {
+    constexpr int WG = CG_WG;
+    const int nqb1 = (N + WG - 1) / WG, nqb2 = (M + WG - 1) / WG;
+    hipLaunchKernelGGL((chamfer_grid_search_kernel<false, WG>), dim3(B * (nqb1 + nqb2)), dim3(WG),
+                       0, s, (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2,
+                       (const char*)ws, L, (float*)d1, (float*)d2, i1, i2);
+  }
+}
+
+void launch_chamfer_prune_stats(const void* ws, int64_t B, int64_t N, int64_t M, int64_t* out,
+                                hipStream_t s) {
+  const CgLayout L = cg_layout(B, N, M);
+  hipLaunchKernelGGL(chamfer_stats_kernel, dim3(1), dim3(256), 0, s,
+                     reinterpret_cast<const int32_t*>((const char*)ws + L.stats),
+                     cg_grid_size(B, N, M) * (cg_wg(N, M) / 64), out);
+}
+
+}  // namespace tpo

@@ -66,9 +66,12 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> chamfer_forward_hip(
   at::Tensor dist2 = at::empty({B, M}, xyz1.options());
   at::Tensor idx1 = at::empty({B, N}, xyz1.options().dtype(at::kInt));
   at::Tensor idx2 = at::empty({B, M}, xyz1.options().dtype(at::kInt));
+  const int64_t ws_bytes = tpo_chamfer_workspace_size(dt, B, N, M);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes}, xyz1.options().dtype(at::kByte));
   check_rc(tpo_chamfer_fwd(dt, xyz1.data_ptr(), xyz2.data_ptr(), B, N, M, dist1.data_ptr(),
                            dist2.data_ptr(), idx1.data_ptr<int32_t>(), idx2.data_ptr<int32_t>(),
-                           stream_of(xyz1)),
+                           ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(xyz1)),
            "chamfer_forward");
   return {dist1, dist2, idx1, idx2};
 }
