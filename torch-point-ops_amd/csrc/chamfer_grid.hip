@@ -3,23 +3,25 @@
 // a workspace and both clouds have at least CH_PRUNE_MIN points).
 //
 // 1. chamfer_grid_sort_kernel, one workgroup per (batch, cloud): the cloud's
-//    bounding box, a counting sort of its points into a 16^3 grid of cells
+//    bounding box, a counting sort of its points into a 32^3 grid of cells
 //    (cells in Morton order, so neighbouring cells are mostly close in
 //    memory), the sorted points as (x, y, z, original index) and the start of
 //    every cell.
 // 2. chamfer_grid_search_kernel: one lane per query, queries taken in the
 //    sorted (Morton) order of their own cloud so a wave's lanes search nearby
-//    cells.  A lane visits the cells of the reference grid in Chebyshev rings
-//    around its query's cell and evaluates every point of a visited cell
-//    with the reference formula (chamfer.cu:64-67, same bits), keeping the
+//    cells.  A lane walks Chebyshev rings of cells around its query's cell
+//    until it has a candidate, then visits the box of cells that can hold a
+//    point within the best distance found (cell assignment is monotone in
+//    each coordinate, and the box is widened by 2^-19 relative plus the
+//    rounding of its bounds), evaluating every point of a visited cell with
+//    the reference formula (chamfer.cu:64-67, same bits) and keeping the
 //    smallest (distance, original index) -- the reference's first-index rule.
-//    A cell is skipped, and the ring walk stops, once a lower bound of the
-//    squared distance to anything left, rounded down by 2^-20 relative,
-//    exceeds the best distance found: the reference's float distance of any
-//    such point is then strictly larger (its relative error is <= 5u), so
-//    neither a smaller distance nor a tie with a lower index is skipped.
-//    Cell boxes are widened by 2^-20 (|lo| + extent) per side, which covers
-//    the rounding of the cell assignment.
+//    A cell is skipped when a lower bound of its squared distance, rounded
+//    down by 2^-20 relative, exceeds the best distance: the reference's float
+//    distance of any of its points is then strictly larger (its relative
+//    error is <= 5u), so neither a smaller distance nor a tie with a lower
+//    index is missed.  Cell boxes are widened by 2^-20 (|lo| + extent) per
+//    side, which covers the rounding of the cell assignment.
 // 3. Queries with a coordinate that is non-finite or >= 2^60 in magnitude,
 //    and every query of a reference cloud holding such a coordinate, are
 //    scanned over the whole reference cloud in original order by chunk_scan
@@ -37,7 +39,7 @@
 
 namespace tpo {
 
-constexpr int CG_GRID = 16;  // cells per axis
+constexpr int CG_GRID = 32;  // cells per axis
 constexpr int CG_CELLS = CG_GRID * CG_GRID * CG_GRID;
 constexpr int CG_WG = 256;        // queries per workgroup, global-memory search
 constexpr int CG_WG_LDS = 1024;   // queries per workgroup, LDS search
@@ -84,9 +86,10 @@ static CgLayout cg_layout(int64_t B, int64_t N, int64_t M) {
   return L;
 }
 
-__device__ __forceinline__ uint32_t cg_spread(uint32_t v) {  // 4 bits -> every third bit
-  v = (v | (v << 4)) & 0x0c3u;
-  v = (v | (v << 2)) & 0x249u;
+__device__ __forceinline__ uint32_t cg_spread(uint32_t v) {  // 5 bits -> every third bit
+  v = (v | (v << 8)) & 0x100fu;
+  v = (v | (v << 4)) & 0x10c3u;
+  v = (v | (v << 2)) & 0x1249u;
   return v;
 }
 
@@ -168,11 +171,12 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     rank[k] = (int32_t)atomicAdd(&cnt[code], 1u);
   }
   __syncthreads();
-  {  // exclusive scan of the cell counts, 4 cells per thread
-    uint32_t v[4], sum = 0;
+  {  // exclusive scan of the cell counts, CPT cells per thread
+    constexpr int CPT = CG_CELLS / 1024;
+    uint32_t v[CPT], sum = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = cnt[tid * 4 + i];
+    for (int i = 0; i < CPT; ++i) {
+      v[i] = cnt[tid * CPT + i];
       sum += v[i];
     }
     uint32_t incl = sum;
@@ -186,9 +190,9 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     uint32_t run = incl - sum;
     for (int v2 = 0; v2 < w; ++v2) run += part[v2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      cnt[tid * 4 + i] = run;
-      cstart[tid * 4 + i] = (int32_t)run;
+    for (int i = 0; i < CPT; ++i) {
+      cnt[tid * CPT + i] = run;
+      cstart[tid * CPT + i] = (int32_t)run;
       run += v[i];
     }
     if (tid == 1023) cstart[CG_CELLS] = (int32_t)run;
@@ -214,9 +218,9 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   }
 }
 
-// LDS: the reference cloud's sorted points and cell starts are first copied to
-// LDS by the (1024-thread) workgroup, which then searches at LDS latency; used
-// when they fit (up to CG_LDS_POINTS points).
+// LDS: the reference cloud's sorted points are first copied to LDS by the
+// (1024-thread) workgroup, which then reads them at LDS latency; used when
+// they fit (up to CG_LDS_POINTS points).  Cell starts are read from memory.
 template <bool LDS, int WG>
 __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     const float* __restrict__ xyz1, const float* __restrict__ xyz2, int B, int N, int M,
@@ -245,12 +249,9 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
   const int32_t* cstart = cs_g;
   if constexpr (LDS) {
     const int np = (int)cg_pad(nr);
-    int32_t* s_cs = reinterpret_cast<int32_t*>(s_pts + np);
     for (int k = threadIdx.x; k < np; k += WG) s_pts[k] = rs_g[k];
-    for (int k = threadIdx.x; k <= CG_CELLS; k += WG) s_cs[k] = cs_g[k];
     __syncthreads();
     rs = s_pts;
-    cstart = s_cs;
   }
   const float* __restrict__ h = reinterpret_cast<const float*>(ws + L.hdr) + (2 * b + cr) * 16;
   const float* __restrict__ rp = (dir ? xyz1 : xyz2) + (size_t)b * nr * 3;  // original order
@@ -273,80 +274,94 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     const float gs[3] = {h[6], h[7], h[8]}, cs[3] = {h[9], h[10], h[11]};
     const float qv[3] = {q.x, q.y, q.z};
     int ci[3], ga[3];
-    float eps[3], m[3];
+    float eps[3];
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
       ga[a] = gs[a] > 0.f ? CG_GRID : 1;
       ci[a] = gs[a] > 0.f ? cg_axis_cell(qv[a], glo[a], gs[a]) : 0;
       eps[a] = 0x1p-20f * (__builtin_fabsf(glo[a]) + (ghi[a] - glo[a])) + 0x1p-126f;
-      // distance from the query to the nearer face of its own cell (0 outside)
-      const float clo = ga[a] > 1 ? glo[a] + (float)ci[a] * cs[a] : glo[a];
-      const float chi = ga[a] > 1 ? glo[a] + (float)(ci[a] + 1) * cs[a] : ghi[a];
-      m[a] = fmaxf(fminf(qv[a] - clo, chi - qv[a]) - eps[a], 0.f);
     }
     int rmax = 0;
 #pragma unroll
     for (int a = 0; a < 3; ++a) rmax = max(rmax, max(ci[a], ga[a] - 1 - ci[a]));
     float bd = Lim<float>::inf();
     int bi = 0x7fffffff;
-    for (int r = 0; r <= rmax; ++r) {
-      if (r > 0) {  // lower bound for every cell of ring r and beyond
-        float lr = Lim<float>::inf();
+    // evaluate every point of cell cc unless its box is farther than bd
+    auto visit = [&](int cx, int cy, int cz) {
+      const int cc[3] = {cx, cy, cz};
+      float gap[3];
 #pragma unroll
-        for (int a = 0; a < 3; ++a)
-          if (ga[a] > 1) lr = fminf(lr, fmaxf((float)(r - 1) * cs[a] + m[a], 0.f));
-        if (lr * lr * (1.f - 0x1p-20f) > bd) break;
+      for (int a = 0; a < 3; ++a) {
+        const float clo = (ga[a] > 1 ? glo[a] + (float)cc[a] * cs[a] : glo[a]) - eps[a];
+        const float chi = (ga[a] > 1 ? glo[a] + (float)(cc[a] + 1) * cs[a] : ghi[a]) + eps[a];
+        gap[a] = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
       }
+      if (sq3(gap[0], gap[1], gap[2]) * (1.f - 0x1p-20f) > bd) return;
+      const uint32_t code = cg_code(cx, cy, cz);
+      const int j0 = cstart[code], j1 = cstart[code + 1];
+      int j = j0;
+      for (; j + 1 < j1; j += 2) {  // two loads in flight
+        const float4 p0 = rs[j], p1 = rs[j + 1];
+        const float d0 = sq3((float)(p0.x - q.x), (float)(p0.y - q.y), (float)(p0.z - q.z));
+        const float d1 = sq3((float)(p1.x - q.x), (float)(p1.y - q.y), (float)(p1.z - q.z));
+        const int o0 = __float_as_int(p0.w), o1 = __float_as_int(p1.w);
+        if (d0 < bd || (d0 == bd && o0 < bi)) {
+          bd = d0;
+          bi = o0;
+        }
+        if (d1 < bd || (d1 == bd && o1 < bi)) {
+          bd = d1;
+          bi = o1;
+        }
+      }
+      if (j < j1) {
+        const float4 p = rs[j];
+        const float d = sq3((float)(p.x - q.x), (float)(p.y - q.y), (float)(p.z - q.z));
+        const int oi = __float_as_int(p.w);
+        if (d < bd || (d == bd && oi < bi)) {
+          bd = d;
+          bi = oi;
+        }
+      }
+      examined += j1 - j0;
+    };
+    // phase 1: Chebyshev rings around the query's cell until a point is found
+    int rdone = -1;
+    for (int r = 0; r <= rmax && bd == Lim<float>::inf(); ++r) {
       const int z0 = max(-r, -ci[2]), z1 = min(r, ga[2] - 1 - ci[2]);
       const int y0 = max(-r, -ci[1]), y1 = min(r, ga[1] - 1 - ci[1]);
+      const int x0 = max(-r, -ci[0]), x1 = min(r, ga[0] - 1 - ci[0]);
       for (int dz = z0; dz <= z1; ++dz)
         for (int dy = y0; dy <= y1; ++dy) {
           const bool full = dz == -r || dz == r || dy == -r || dy == r;
-          const int x0 = max(-r, -ci[0]), x1 = min(r, ga[0] - 1 - ci[0]);
           for (int dx = x0; dx <= x1; ++dx) {
             if (!full && dx != -r && dx != r) {  // interior of the ring: jump to its far side
               if (dx < r) dx = r - 1;
               continue;
             }
-            const int cc[3] = {ci[0] + dx, ci[1] + dy, ci[2] + dz};
-            float gap[3];
-#pragma unroll
-            for (int a = 0; a < 3; ++a) {
-              const float clo = (ga[a] > 1 ? glo[a] + (float)cc[a] * cs[a] : glo[a]) - eps[a];
-              const float chi = (ga[a] > 1 ? glo[a] + (float)(cc[a] + 1) * cs[a] : ghi[a]) + eps[a];
-              gap[a] = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
-            }
-            if (sq3(gap[0], gap[1], gap[2]) * (1.f - 0x1p-20f) > bd) continue;
-            const uint32_t code = cg_code(cc[0], cc[1], cc[2]);
-            const int j1 = cstart[code + 1];
-            int j = cstart[code];
-            for (; j + 1 < j1; j += 2) {  // two loads in flight
-              const float4 p0 = rs[j], p1 = rs[j + 1];
-              const float d0 = sq3((float)(p0.x - q.x), (float)(p0.y - q.y), (float)(p0.z - q.z));
-              const float d1 = sq3((float)(p1.x - q.x), (float)(p1.y - q.y), (float)(p1.z - q.z));
-              const int o0 = __float_as_int(p0.w), o1 = __float_as_int(p1.w);
-              if (d0 < bd || (d0 == bd && o0 < bi)) {
-                bd = d0;
-                bi = o0;
-              }
-              if (d1 < bd || (d1 == bd && o1 < bi)) {
-                bd = d1;
-                bi = o1;
-              }
-            }
-            if (j < j1) {
-              const float4 p = rs[j];
-              const float d = sq3((float)(p.x - q.x), (float)(p.y - q.y), (float)(p.z - q.z));
-              const int oi = __float_as_int(p.w);
-              if (d < bd || (d == bd && oi < bi)) {
-                bd = d;
-                bi = oi;
-              }
-            }
-            examined += j1 - cstart[code];
+            visit(ci[0] + dx, ci[1] + dy, ci[2] + dz);
           }
         }
+      rdone = r;
     }
+    // phase 2: the box of cells within the best distance (cell assignment is
+    // monotone in each coordinate, so the box holds every point within it);
+    // cells of the rings already walked are skipped
+    int blo[3], bhi[3];
+    const float rad = __builtin_sqrtf(bd) * (1.f + 0x1p-19f);
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      const float ra = rad + eps[a] + 0x1p-20f * __builtin_fabsf(qv[a]);
+      blo[a] = ga[a] > 1 ? cg_axis_cell(qv[a] - ra, glo[a], gs[a]) : 0;
+      bhi[a] = ga[a] > 1 ? cg_axis_cell(qv[a] + ra, glo[a], gs[a]) : 0;
+    }
+    for (int cz = blo[2]; cz <= bhi[2]; ++cz)
+      for (int cy = blo[1]; cy <= bhi[1]; ++cy)
+        for (int cx = blo[0]; cx <= bhi[0]; ++cx) {
+          const int cheb = max(abs(cx - ci[0]), max(abs(cy - ci[1]), abs(cz - ci[2])));
+          if (cheb <= rdone) continue;
+          visit(cx, cy, cz);
+        }
     dout[oq] = bd;
     iout[oq] = bi;
   }
@@ -401,12 +416,12 @@ void launch_chamfer_fwd_prune(const void* x1, const void* x2, int B, int N, int 
   if (cg_use_lds(N, M)) {
     constexpr int WG = CG_WG_LDS;
     const int nqb1 = (N + WG - 1) / WG, nqb2 = (M + WG - 1) / WG;
-    const size_t lds = (size_t)std::max(cg_pad(N), cg_pad(M)) * 16 + (CG_CELLS + 1) * 4;
+    const size_t lds = (size_t)std::max(cg_pad(N), cg_pad(M)) * 16;
     static std::once_flag attr_once;  // dynamic LDS beyond the default limit
     std::call_once(attr_once, [] {
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&chamfer_grid_search_kernel<true, WG>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                CG_LDS_POINTS * 16 + (CG_CELLS + 1) * 4);
+                                CG_LDS_POINTS * 16);
     });
     hipLaunchKernelGGL((chamfer_grid_search_kernel<true, WG>), dim3(B * (nqb1 + nqb2)), dim3(WG),
                        lds, s, (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2,
