@@ -79,19 +79,10 @@ def bench_chamfer(tpo, torch, steps, warmup):
     dev = torch.device("cuda:0")
     a = p1.to(dev).requires_grad_(True)
     b = p2.to(dev).requires_grad_(True)
-    fwd_ms = []
 
-    def step(record=False):
-        # ChamferDistance('mean') forward + backward through autograd; the
-        # events bracket the forward op, i.e. the chamfer forward kernel
-        if record:
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record()
+    def step():
+        # ChamferDistance('mean') forward + backward through autograd
         d1, d2 = tpo.chamfer_distance(a, b)
-        if record:
-            e1.record()
-            fwd_ms.append((e0, e1))
         loss = d1.mean() + d2.mean()
         return torch.autograd.grad(loss, (a, b))
 
@@ -100,12 +91,62 @@ def bench_chamfer(tpo, torch, steps, warmup):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        step(record=True)
+        step()
     torch.cuda.synchronize()
     sec = (time.perf_counter() - t0) / steps
-    fwd = sum(e0.elapsed_time(e1) for e0, e1 in fwd_ms) / len(fwd_ms) / 1e3
-    pairs = 2 * B * N * M
-    return dict(pairs=pairs, sec=sec, fwd_sec=fwd, B=B, N=N, M=M)
+    out = dict(pairs=2 * B * N * M, sec=sec, B=B, N=N, M=M)
+    out.update(chamfer_forward_paths(torch, a.detach(), b.detach(), steps))
+    return out
+
+
+def chamfer_forward_paths(torch, p1, p2, reps):
+    """The forward alone through the C ABI, HIP events on the stream it runs
+    on: with a workspace (exact grid search: sort + search launches) and
+    without (dense filter kernel), plus the pairs the grid search evaluated."""
+    import ctypes
+
+    from torch_point_ops import _native
+
+    lib = ctypes.CDLL(_native.HIP_LIB)
+    P, I = ctypes.c_void_p, ctypes.c_int64
+    lib.tpo_chamfer_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, P, P, P, P, P, I, P]
+    lib.tpo_chamfer_workspace_size.argtypes = [ctypes.c_int, I, I, I]
+    lib.tpo_chamfer_workspace_size.restype = I
+    lib.tpo_chamfer_pairs_evaluated.argtypes = [ctypes.c_int, P, I, I, I, P, P]
+    B, N, M = p1.shape[0], p1.shape[1], p2.shape[1]
+    dev = p1.device
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    d1, d2 = torch.empty(B, N, device=dev), torch.empty(B, M, device=dev)
+    i1 = torch.empty(B, N, dtype=torch.int32, device=dev)
+    i2 = torch.empty(B, M, dtype=torch.int32, device=dev)
+    ws = torch.empty(lib.tpo_chamfer_workspace_size(0, B, N, M), dtype=torch.uint8, device=dev)
+
+    def run(w):
+        rc = lib.tpo_chamfer_fwd(0, p1.data_ptr(), p2.data_ptr(), B, N, M, d1.data_ptr(),
+                                 d2.data_ptr(), i1.data_ptr(), i2.data_ptr(),
+                                 None if w is None else w.data_ptr(),
+                                 0 if w is None else w.numel(), sp)
+        assert rc == 0
+
+    res = {}
+    for name, w in (("grid", ws), ("dense", None)):
+        for _ in range(3):
+            run(w)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            run(w)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res[name + "_fwd_sec"] = e0.elapsed_time(e1) / reps / 1e3
+    run(ws)
+    pairs = torch.zeros(1, dtype=torch.int64, device=dev)
+    assert lib.tpo_chamfer_pairs_evaluated(0, ws.data_ptr(), B, N, M, pairs.data_ptr(), sp) == 0
+    torch.cuda.synchronize()
+    res["pairs_evaluated"] = int(pairs.item())
+    return res
 
 
 def bench_knn(tpo, torch, steps):
@@ -262,7 +303,9 @@ def main():
     log("[bench] chamfer c2 fwd+bwd")
     ch = bench_chamfer(tpo, torch, args.steps, args.warmup)
     value = ch["pairs"] / ch["sec"] / 1e9
-    achieved = FLOP_PER_PAIR * ch["pairs"] / ch["fwd_sec"] / 1e12
+    achieved = FLOP_PER_PAIR * ch["pairs"] / ch["grid_fwd_sec"] / 1e12
+    executed = FLOP_PER_PAIR * ch["pairs_evaluated"] / ch["grid_fwd_sec"] / 1e12
+    dense = FLOP_PER_PAIR * ch["pairs"] / ch["dense_fwd_sec"] / 1e12
     traffic = None
     tfile = os.path.join(REPO, "profiles", "chamfer_fwd_c2_traffic.json")
     if os.path.exists(tfile):
@@ -285,11 +328,20 @@ def main():
                                "ChamferDistance('mean') (BASELINE.json configs[1])",
                    "global_batch": ch["B"], "points": [ch["N"], ch["M"]],
                    "pairs_per_step": ch["pairs"], "parallelism": "single GPU"},
-        "roofline": {"bound": "valu", "kernel": "chamfer_fwd_filter_kernel<8>",
+        "roofline": {"bound": "valu",
+                     "kernel": "chamfer_grid_sort_kernel + chamfer_grid_search_kernel",
                      "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
-                     "traffic": traffic, "fwd_kernel_ms": round(ch["fwd_sec"] * 1e3, 4),
-                     "flop_per_pair": FLOP_PER_PAIR},
+                     "traffic": traffic, "fwd_ms": round(ch["grid_fwd_sec"] * 1e3, 4),
+                     "flop_per_pair": FLOP_PER_PAIR, "algorithmic_pairs": ch["pairs"],
+                     "pairs_evaluated": ch["pairs_evaluated"],
+                     "executed_tflops": round(executed, 4),
+                     "executed_frac": round(executed / FP32_PEAK_TFLOPS, 5),
+                     "note": "achieved = 9 FLOP x all 2BNM directed pairs / forward time; the "
+                             "exact grid search evaluates only pairs_evaluated of them, so frac "
+                             "> 1 means less work than brute force (executed_* is the VALU "
+                             "use); the brute-force kernel's own roofline is "
+                             "secondary.chamfer_dense_c2"},
     }
     threads = min(host_cores(), int(os.environ.get("OMP_NUM_THREADS", host_cores())))
     if not args.no_cpu:
@@ -299,7 +351,9 @@ def main():
     if not args.no_secondary:
         from oracle import oracle as O
 
-        sec = {}
+        sec = {"chamfer_dense_c2": {
+            "kernel": "chamfer_fwd_filter_kernel<8,16>", "fwd_ms": round(ch["dense_fwd_sec"] * 1e3, 4),
+            "achieved_tflops": round(dense, 3), "frac_fp32_peak": round(dense / FP32_PEAK_TFLOPS, 4)}}
         log("[bench] knn c3")
         kn = bench_knn(tpo, torch, max(3, args.steps // 4))
         sec["knn_c3"] = {"G_pair_dists_per_s_kernel": round(kn["pairs"] / kn["sec_kernel"] / 1e9, 2),

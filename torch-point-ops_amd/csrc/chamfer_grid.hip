@@ -31,7 +31,6 @@
 // squeezed into one cell degrades to a full scan).  Each wave records the
 // number of points it evaluated (tpo_chamfer_pairs_evaluated sums them).
 #include <algorithm>
-#include <mutex>
 
 #include "chamfer_common.hpp"
 
@@ -41,9 +40,8 @@ namespace tpo {
 
 constexpr int CG_GRID = 32;  // cells per axis
 constexpr int CG_CELLS = CG_GRID * CG_GRID * CG_GRID;
-constexpr int CG_WG = 256;        // queries per workgroup, global-memory search
-constexpr int CG_WG_LDS = 1024;   // queries per workgroup, LDS search
-constexpr int CG_LDS_POINTS = 8192;  // largest reference cloud staged in LDS
+constexpr int CG_WG = 256;    // queries per search workgroup
+constexpr int CG_UNROLL = 2;  // points of a cell loaded together
 
 __host__ __device__ inline int64_t cg_pad(int64_t n) { return (n + 63) & ~(int64_t)63; }
 
@@ -59,13 +57,8 @@ struct CgLayout {
 
 static int64_t cg_align(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-static bool cg_use_lds(int64_t N, int64_t M) {
-  return cg_pad(N) <= CG_LDS_POINTS && cg_pad(M) <= CG_LDS_POINTS;
-}
-static int cg_wg(int64_t N, int64_t M) { return cg_use_lds(N, M) ? CG_WG_LDS : CG_WG; }
 static int64_t cg_grid_size(int64_t B, int64_t N, int64_t M) {
-  const int wg = cg_wg(N, M);
-  return B * ((N + wg - 1) / wg + (M + wg - 1) / wg);
+  return B * ((N + CG_WG - 1) / CG_WG + (M + CG_WG - 1) / CG_WG);
 }
 
 static CgLayout cg_layout(int64_t B, int64_t N, int64_t M) {
@@ -81,7 +74,7 @@ static CgLayout cg_layout(int64_t B, int64_t N, int64_t M) {
   L.rank = o;
   o = cg_align(o + B * P * 4);
   L.stats = o;
-  o = cg_align(o + cg_grid_size(B, N, M) * (cg_wg(N, M) / 64) * 4);
+  o = cg_align(o + cg_grid_size(B, N, M) * (CG_WG / 64) * 4);
   L.total = o;
   return L;
 }
@@ -102,10 +95,17 @@ __device__ __forceinline__ uint32_t cg_code(int cx, int cy, int cz) {
   return cg_spread((uint32_t)cx) | (cg_spread((uint32_t)cy) << 1) | (cg_spread((uint32_t)cz) << 2);
 }
 
+// The histogram is stored with one padding word per 32 cells, so the scan's
+// per-thread runs of 32 consecutive cells fall in different LDS banks.
+__device__ __forceinline__ int cg_hidx(uint32_t code) { return (int)(code + (code >> 5)); }
+
+// PPT > 0: every thread keeps its (at most PPT) points in registers across the
+// passes (n <= 1024 * PPT); PPT == 0: the passes reload from memory.
+template <int PPT>
 __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     const float* __restrict__ xyz1, const float* __restrict__ xyz2, int N, int M,
     char* __restrict__ ws, CgLayout L) {
-  __shared__ uint32_t cnt[CG_CELLS];
+  __shared__ uint32_t cnt[CG_CELLS + CG_CELLS / 32];
   __shared__ float red[6][16];
   __shared__ uint32_t part[16];
   __shared__ uint32_t s_bad;
@@ -121,19 +121,47 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
       reinterpret_cast<int32_t*>(ws + L.cstart) + (size_t)blockIdx.x * (CG_CELLS + 1);
   int32_t* __restrict__ rank = reinterpret_cast<int32_t*>(ws + L.rank) + base;
 
+  constexpr int R = PPT > 0 ? PPT : 1;
+  float px[R], py[R], pz[R];
+  if constexpr (PPT > 0) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int k = min(tid + 1024 * i, n - 1);  // duplicates of the last point: harmless below
+      px[i] = P[3 * k];
+      py[i] = P[3 * k + 1];
+      pz[i] = P[3 * k + 2];
+    }
+  }
+  auto point = [&](int i, int k, float& x, float& y, float& z) {
+    if constexpr (PPT > 0) {
+      x = px[i];
+      y = py[i];
+      z = pz[i];
+    } else {
+      x = P[3 * k];
+      y = P[3 * k + 1];
+      z = P[3 * k + 2];
+    }
+  };
+  const int iters = PPT > 0 ? PPT : (n + 1023) / 1024;
+
   // bounding box (NaN ignored) and the bad flag (non-finite or >= 2^60)
   if (tid == 0) s_bad = 0;
   float lo[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
   float hi[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
   uint32_t big = 0;
-  for (int k = tid; k < n; k += 1024)
+  for (int i = 0; i < iters; ++i) {
+    const int k = tid + 1024 * i;
+    if (k >= n) break;
+    float v[3];
+    point(i, k, v[0], v[1], v[2]);
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
-      const float v = P[3 * k + a];
-      big = max(big, abs_bits(v));
-      lo[a] = fminf(lo[a], v);
-      hi[a] = fmaxf(hi[a], v);
+      big = max(big, abs_bits(v[a]));
+      lo[a] = fminf(lo[a], v[a]);
+      hi[a] = fmaxf(hi[a], v[a]);
     }
+  }
 #pragma unroll
   for (int a = 0; a < 3; ++a)
 #pragma unroll
@@ -147,7 +175,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
       red[a][w] = lo[a];
       red[3 + a][w] = hi[a];
     }
-  for (int k = tid; k < CG_CELLS; k += 1024) cnt[k] = 0;
+  for (int k = tid; k < CG_CELLS + CG_CELLS / 32; k += 1024) cnt[k] = 0;
   __syncthreads();
   if (big >= CH_BIG) atomicOr(&s_bad, 1u);
   float glo[3], ghi[3], gs[3];
@@ -164,19 +192,27 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     const float ext = z - x;
     gs[a] = (ext > 0.f && is_finite(ext)) ? (float)CG_GRID / ext : 0.f;
   }
-  for (int k = tid; k < n; k += 1024) {
-    const uint32_t code = cg_code(cg_axis_cell(P[3 * k], glo[0], gs[0]),
-                                  cg_axis_cell(P[3 * k + 1], glo[1], gs[1]),
-                                  cg_axis_cell(P[3 * k + 2], glo[2], gs[2]));
-    rank[k] = (int32_t)atomicAdd(&cnt[code], 1u);
+  auto code_of = [&](float x, float y, float z) {
+    return cg_code(cg_axis_cell(x, glo[0], gs[0]), cg_axis_cell(y, glo[1], gs[1]),
+                   cg_axis_cell(z, glo[2], gs[2]));
+  };
+  uint32_t rk[R];
+  for (int i = 0; i < iters; ++i) {
+    const int k = tid + 1024 * i;
+    if (k >= n) break;
+    float x, y, z;
+    point(i, k, x, y, z);
+    const uint32_t r = atomicAdd(&cnt[cg_hidx(code_of(x, y, z))], 1u);
+    if constexpr (PPT > 0) rk[i] = r;
+    else rank[k] = (int32_t)r;
   }
   __syncthreads();
-  {  // exclusive scan of the cell counts, CPT cells per thread
+  {  // exclusive scan of the cell counts, CPT consecutive cells per thread
     constexpr int CPT = CG_CELLS / 1024;
     uint32_t v[CPT], sum = 0;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      v[i] = cnt[tid * CPT + i];
+      v[i] = cnt[cg_hidx(tid * CPT + i)];
       sum += v[i];
     }
     uint32_t incl = sum;
@@ -191,18 +227,20 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     for (int v2 = 0; v2 < w; ++v2) run += part[v2];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      cnt[tid * CPT + i] = run;
-      cstart[tid * CPT + i] = (int32_t)run;
+      cnt[cg_hidx(tid * CPT + i)] = run;
       run += v[i];
     }
     if (tid == 1023) cstart[CG_CELLS] = (int32_t)run;
   }
   __syncthreads();
-  for (int k = tid; k < n; k += 1024) {
-    const float x = P[3 * k], y = P[3 * k + 1], z = P[3 * k + 2];
-    const uint32_t code = cg_code(cg_axis_cell(x, glo[0], gs[0]), cg_axis_cell(y, glo[1], gs[1]),
-                                  cg_axis_cell(z, glo[2], gs[2]));
-    pts[cnt[code] + rank[k]] = make_float4(x, y, z, __int_as_float(k));
+  for (int k = tid; k < CG_CELLS; k += 1024) cstart[k] = (int32_t)cnt[cg_hidx(k)];  // coalesced
+  for (int i = 0; i < iters; ++i) {
+    const int k = tid + 1024 * i;
+    if (k >= n) break;
+    float x, y, z;
+    point(i, k, x, y, z);
+    const uint32_t r = PPT > 0 ? rk[i] : (uint32_t)rank[k];
+    pts[cnt[cg_hidx(code_of(x, y, z))] + r] = make_float4(x, y, z, __int_as_float(k));
   }
   for (int pos = n + tid; pos < cg_pad(n); pos += 1024)
     pts[pos] = make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
@@ -218,15 +256,11 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   }
 }
 
-// LDS: the reference cloud's sorted points are first copied to LDS by the
-// (1024-thread) workgroup, which then reads them at LDS latency; used when
-// they fit (up to CG_LDS_POINTS points).  Cell starts are read from memory.
-template <bool LDS, int WG>
+template <int WG>
 __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     const float* __restrict__ xyz1, const float* __restrict__ xyz2, int B, int N, int M,
     int nqb1, int nqb2, const char* __restrict__ ws, CgLayout L, float* __restrict__ dist1,
     float* __restrict__ dist2, int32_t* __restrict__ idx1, int32_t* __restrict__ idx2) {
-  extern __shared__ float4 s_pts[];
   const int bid = xcd_logical_block(blockIdx.x, gridDim.x);
   int lb = bid;
   const int g1 = B * nqb1;
@@ -242,17 +276,9 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
   const int64_t base_q = (int64_t)b * (PN + PM) + (cq ? PN : 0);
   const int64_t base_r = (int64_t)b * (PN + PM) + (cr ? PN : 0);
   const float4* __restrict__ qs = reinterpret_cast<const float4*>(ws + L.pts) + base_q;
-  const float4* __restrict__ rs_g = reinterpret_cast<const float4*>(ws + L.pts) + base_r;
-  const int32_t* __restrict__ cs_g =
+  const float4* __restrict__ rs = reinterpret_cast<const float4*>(ws + L.pts) + base_r;
+  const int32_t* __restrict__ cstart =
       reinterpret_cast<const int32_t*>(ws + L.cstart) + (size_t)(2 * b + cr) * (CG_CELLS + 1);
-  const float4* rs = rs_g;
-  const int32_t* cstart = cs_g;
-  if constexpr (LDS) {
-    const int np = (int)cg_pad(nr);
-    for (int k = threadIdx.x; k < np; k += WG) s_pts[k] = rs_g[k];
-    __syncthreads();
-    rs = s_pts;
-  }
   const float* __restrict__ h = reinterpret_cast<const float*>(ws + L.hdr) + (2 * b + cr) * 16;
   const float* __restrict__ rp = (dir ? xyz1 : xyz2) + (size_t)b * nr * 3;  // original order
   const float* __restrict__ qp = (dir ? xyz2 : xyz1) + (size_t)b * nq * 3;
@@ -299,28 +325,20 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
       if (sq3(gap[0], gap[1], gap[2]) * (1.f - 0x1p-20f) > bd) return;
       const uint32_t code = cg_code(cx, cy, cz);
       const int j0 = cstart[code], j1 = cstart[code + 1];
-      int j = j0;
-      for (; j + 1 < j1; j += 2) {  // two loads in flight
-        const float4 p0 = rs[j], p1 = rs[j + 1];
-        const float d0 = sq3((float)(p0.x - q.x), (float)(p0.y - q.y), (float)(p0.z - q.z));
-        const float d1 = sq3((float)(p1.x - q.x), (float)(p1.y - q.y), (float)(p1.z - q.z));
-        const int o0 = __float_as_int(p0.w), o1 = __float_as_int(p1.w);
-        if (d0 < bd || (d0 == bd && o0 < bi)) {
-          bd = d0;
-          bi = o0;
-        }
-        if (d1 < bd || (d1 == bd && o1 < bi)) {
-          bd = d1;
-          bi = o1;
-        }
-      }
-      if (j < j1) {
-        const float4 p = rs[j];
-        const float d = sq3((float)(p.x - q.x), (float)(p.y - q.y), (float)(p.z - q.z));
-        const int oi = __float_as_int(p.w);
-        if (d < bd || (d == bd && oi < bi)) {
-          bd = d;
-          bi = oi;
+      for (int j = j0; j < j1; j += CG_UNROLL) {
+        // CG_UNROLL loads in flight; positions past the cell repeat its last
+        // point, whose second evaluation cannot change the result
+        float4 p[CG_UNROLL];
+#pragma unroll
+        for (int u = 0; u < CG_UNROLL; ++u) p[u] = rs[min(j + u, j1 - 1)];
+#pragma unroll
+        for (int u = 0; u < CG_UNROLL; ++u) {
+          const float d = sq3((float)(p[u].x - q.x), (float)(p[u].y - q.y), (float)(p[u].z - q.z));
+          const int oi = __float_as_int(p[u].w);
+          // branch-free (d, index) minimum
+          const bool take = (d < bd) | ((d == bd) & (oi < bi));
+          bd = take ? d : bd;
+          bi = take ? oi : bi;
         }
       }
       examined += j1 - j0;
@@ -411,28 +429,16 @@ int64_t chamfer_prune_workspace(int64_t B, int64_t N, int64_t M) {
 void launch_chamfer_fwd_prune(const void* x1, const void* x2, int B, int N, int M, void* d1,
                               void* d2, int32_t* i1, int32_t* i2, void* ws, hipStream_t s) {
   const CgLayout L = cg_layout(B, N, M);
-  hipLaunchKernelGGL(chamfer_grid_sort_kernel, dim3(2 * B), dim3(1024), 0, s, (const float*)x1,
-                     (const float*)x2, N, M, (char*)ws, L);
-  if (cg_use_lds(N, M)) {
-    constexpr int WG = CG_WG_LDS;
-    const int nqb1 = (N + WG - 1) / WG, nqb2 = (M + WG - 1) / WG;
-    const size_t lds = (size_t)std::max(cg_pad(N), cg_pad(M)) * 16;
-    static std::once_flag attr_once;  // dynamic LDS beyond the default limit
-    std::call_once(attr_once, [] {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&chamfer_grid_search_kernel<true, WG>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                CG_LDS_POINTS * 16);
-    });
-    hipLaunchKernelGGL((chamfer_grid_search_kernel<true, WG>), dim3(B * (nqb1 + nqb2)), dim3(WG),
-                       lds, s, (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2,
-                       (const char*)ws, L, (float*)d1, (float*)d2, i1, i2);
-  } else {
-    constexpr int WG = CG_WG;
-    const int nqb1 = (N + WG - 1) / WG, nqb2 = (M + WG - 1) / WG;
-    hipLaunchKernelGGL((chamfer_grid_search_kernel<false, WG>), dim3(B * (nqb1 + nqb2)), dim3(WG),
-                       0, s, (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2,
-                       (const char*)ws, L, (float*)d1, (float*)d2, i1, i2);
-  }
+  if (std::max(N, M) <= 1024 * 8)
+    hipLaunchKernelGGL(chamfer_grid_sort_kernel<8>, dim3(2 * B), dim3(1024), 0, s,
+                       (const float*)x1, (const float*)x2, N, M, (char*)ws, L);
+  else
+    hipLaunchKernelGGL(chamfer_grid_sort_kernel<0>, dim3(2 * B), dim3(1024), 0, s,
+                       (const float*)x1, (const float*)x2, N, M, (char*)ws, L);
+  const int nqb1 = (N + CG_WG - 1) / CG_WG, nqb2 = (M + CG_WG - 1) / CG_WG;
+  hipLaunchKernelGGL((chamfer_grid_search_kernel<CG_WG>), dim3(B * (nqb1 + nqb2)), dim3(CG_WG), 0,
+                     s, (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2, (const char*)ws,
+                     L, (float*)d1, (float*)d2, i1, i2);
 }
 
 void launch_chamfer_prune_stats(const void* ws, int64_t B, int64_t N, int64_t M, int64_t* out,
@@ -440,7 +446,7 @@ void launch_chamfer_prune_stats(const void* ws, int64_t B, int64_t N, int64_t M,
   const CgLayout L = cg_layout(B, N, M);
   hipLaunchKernelGGL(chamfer_stats_kernel, dim3(1), dim3(256), 0, s,
                      reinterpret_cast<const int32_t*>((const char*)ws + L.stats),
-                     cg_grid_size(B, N, M) * (cg_wg(N, M) / 64), out);
+                     cg_grid_size(B, N, M) * (CG_WG / 64), out);
 }
 
 }  // namespace tpo
