@@ -95,20 +95,26 @@ int tpo_chamfer_bwd(int dtype, const void* xyz1, const void* xyz2,
  * KNN forward.  Replaces knn_cuda_forward
  * (torch_point_ops/knn/csrc/cuda/knn.cu:295-398),
  * torch_point_ops_knn::knn_forward (knn.cpp:168-169).
- *   p1 (N,P1,D), p2 (N,P2,D) of `dtype` (F32/F64/F16); lengths1/lengths2 (N)
- *   int64 (clamped to [0,P1] / [0,P2]); norm 1 or 2; K >= 1; version -1 for
+ *   p1 (N,P1,D), p2 (N,P2,D) of `dtype`; lengths1/lengths2 (N) int64
+ *   (clamped to [0,P1] / [0,P2]); norm 1 or 2; K >= 1; version -1 for
  *   automatic, 0..3 to force one of the reference's kernel semantics (an
  *   invalid choice falls back to automatic, as the reference does).
- *   idxs (N,P1,K) int64 and dists (N,P1,K) `dtype`, unsorted, laid out
- *   exactly as the reference's MinK slots, including its padding rules:
- *   rows >= lengths1 are (0,0); slots >= lengths2 are (0,0) for versions
- *   2/3 and (-1,+inf) for versions 0/1.
+ *   F32/F64/F16: idxs (N,P1,K) int64 and dists (N,P1,K) `dtype`, unsorted,
+ *   laid out exactly as the reference's MinK slots, including its padding
+ *   rules: rows >= lengths1 are (0,0); slots >= lengths2 are (0,0) for
+ *   versions 2/3 and (-1,+inf) for versions 0/1.  workspace is optional
+ *   (tpo_knn_workspace_size bytes): with it the queries are processed in
+ *   spatial order, which is faster; results are identical.
+ *   BF16 (no reference kernel; the reference raises): norm 2, D % 8 == 0,
+ *   8 <= D <= 128, K <= 32, points 16-byte aligned, workspace required.
+ *   Squared distances |q|^2 + |r|^2 - 2 q.r in float (q.r on the matrix
+ *   cores), clamped at 0; each row's K nearest sorted by (distance, index),
+ *   dists rounded to bfloat16; rows >= lengths1 and slots >= lengths2 are
+ *   (0,0).  version is ignored and version_out receives -1.
  *   If version_out is not NULL it receives the version that ran.
- *   workspace (optional, tpo_knn_workspace_size(N, P1) bytes) lets the
- *   kernel process queries in spatial order, which is faster; results are
- *   identical with or without it.
  */
-int64_t tpo_knn_workspace_size(int64_t N, int64_t P1);
+int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int64_t P2,
+                               int64_t D, int64_t K, int norm);
 int tpo_knn_fwd(int dtype, const void* p1, const void* p2,
                 const int64_t* lengths1, const int64_t* lengths2,
                 int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,

@@ -70,9 +70,14 @@ def test_argument_errors_are_reported(lib):
     assert lib.tpo_chamfer_workspace_size(0, -1, 3, 3) == -1
     lib.tpo_chamfer_pairs_evaluated.argtypes = [ctypes.c_int, P, I, I, I, P, P]
     assert lib.tpo_chamfer_pairs_evaluated(0, None, 2, 4096, 4096, None, None) == -1
-    lib.tpo_knn_workspace_size.argtypes = [I, I]
+    lib.tpo_knn_workspace_size.argtypes = [ctypes.c_int, I, I, I, I, I, ctypes.c_int]
     lib.tpo_knn_workspace_size.restype = I
-    assert lib.tpo_knn_workspace_size(8, 16384) == 8 * 16384 * 4
+    assert lib.tpo_knn_workspace_size(0, 8, 16384, 16384, 3, 16, 2) == 8 * 16384 * 4
+    assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 128, 32, 2) == 4 * (4096 + 65536) * 4
+    assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 128, 32, 1) == 0  # no bf16 L1 kernel
+    assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 130, 32, 2) == 0  # D % 8 != 0
+    assert lib.tpo_knn_fwd(3, None, None, None, None, 1, 4, 4, 3, 2, 2, -1, None, None, None,
+                           None, 0, None) == -2  # bf16 with D=3: unsupported
     lib.tpo_gather_bwd_workspace_size.argtypes = [I, I]
     lib.tpo_gather_bwd_workspace_size.restype = I
     assert lib.tpo_gather_bwd_workspace_size(16, 65536) == 16 * 65536 * 4

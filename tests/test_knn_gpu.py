@@ -227,3 +227,102 @@ def test_module_opcheck_compile_precision(tpo, dev):
         d_auto = tpo.knn_points(p1, p2, K=3)[1]
         d_v = tpo.knn_points(p1, p2, K=3, version=v)[1]
         assert torch.allclose(d_auto, d_v, atol=1e-5)
+
+
+# ------------------------------------------------------- bfloat16 (extension)
+# The reference raises for bfloat16.  The matrix-core kernel (norm 2, D % 8 ==
+# 0, D <= 128, K <= 32) computes |q|^2 + |r|^2 - 2 q.r in float; it is checked
+# against a float64 brute force on the bfloat16-rounded inputs: membership of
+# the K nearest is exact outside an error band around the K-th distance that
+# bounds the float computation, order is ascending, distances agree to the
+# bfloat16 rounding.  (Parity with the reference is unpinned: it has no
+# bfloat16 result to compare with.)
+
+def bf16_expected(q, r, l1, l2, K):
+    """float64 squared distances of the bf16 values, per batch (N, P1, P2)."""
+    qd = q.to(torch.float64)
+    rd = r.to(torch.float64)
+    return torch.cdist(qd, rd) ** 2
+
+
+def check_bf16_knn(idx, d, q, r, l1, l2, K):
+    idx, d = idx.cpu(), d.cpu().to(torch.float64)
+    exact = bf16_expected(q, r, l1, l2, K)
+    D = q.shape[2]
+    qq = (q.to(torch.float64) ** 2).sum(-1)
+    rr = (r.to(torch.float64) ** 2).sum(-1)
+    for n in range(q.shape[0]):
+        L1, L2 = int(l1[n]), int(l2[n])
+        assert (idx[n, L1:] == 0).all() and (d[n, L1:] == 0).all()
+        k_real = min(K, L2)
+        assert (idx[n, :L1, k_real:] == 0).all() and (d[n, :L1, k_real:] == 0).all()
+        if L1 == 0 or k_real == 0:
+            continue
+        ex = exact[n, :L1, :L2]
+        got = idx[n, :L1, :k_real]
+        assert int(got.min()) >= 0 and int(got.max()) < L2
+        assert all(len(set(row.tolist())) == k_real for row in got)
+        kth = ex.sort(-1).values[:, k_real - 1:k_real]
+        # error of the float expansion: a few roundings of |q|^2 + |r|^2 + 2|q.r|
+        band = 8 * (D + 4) * 2.0 ** -24 * (qq[n, :L1, None] + rr[n, None, :L2].max() + 2 * (qq[n, :L1, None] * rr[n, None, :L2].max()).sqrt())
+        gd = torch.gather(ex, 1, got)
+        assert bool((gd <= kth + band).all()), "a returned point is outside the K nearest"
+        must = ex < (kth - band)
+        has = torch.zeros_like(must)
+        has.scatter_(1, got, True)
+        assert bool((~must | has).all()), "a point clearly inside the K nearest is missing"
+        dd = d[n, :L1, :k_real]
+        assert bool((dd[:, 1:] >= dd[:, :-1]).all()), "not sorted ascending"
+        assert torch.allclose(dd, gd, rtol=2 ** -7, atol=1e-6 + float(band.max()))
+
+
+@pytest.mark.parametrize("N,P1,P2,D,K", [(2, 100, 1000, 128, 32), (1, 64, 513, 64, 16),
+                                         (2, 50, 300, 40, 5), (1, 33, 90, 8, 1),
+                                         (2, 70, 200, 96, 20)])
+def test_bf16_matrix_core_knn(tpo, dev, N, P1, P2, D, K):
+    g = torch.Generator().manual_seed(N * 1000 + P1 + P2 + D + K)
+    q = torch.randn(N, P1, D, generator=g).to(torch.bfloat16)
+    r = torch.randn(N, P2, D, generator=g).to(torch.bfloat16)
+    l1 = torch.randint(P1 // 2, P1 + 1, (N,), generator=g)
+    l2 = torch.randint(K, P2 + 1, (N,), generator=g)
+    if N > 1:
+        l2[1] = max(1, K // 2)  # fewer references than K
+    idx, d = raw(q, r, l1, l2, 2, K, -1, dev)
+    assert idx.dtype == torch.int64 and d.dtype == torch.bfloat16
+    check_bf16_knn(idx, d, q, r, l1, l2, K)
+
+
+def test_bf16_config5_subset(tpo, dev):
+    q, r = workloads.knn_c5()
+    B, P1, D = q.shape
+    l1 = torch.full((B,), P1, dtype=torch.int64)
+    l2 = torch.full((B,), r.shape[1], dtype=torch.int64)
+    idx, d = raw(q, r, l1, l2, 2, 32, -1, dev)
+    sel = torch.arange(0, P1, 61)  # 68 query rows per cloud, checked against float64
+    check_bf16_knn(idx[:, sel], d[:, sel], q[:, sel], r, torch.full((B,), len(sel)), l2, 32)
+
+
+def test_bf16_knn_points_and_fallbacks(tpo, dev):
+    g = torch.Generator().manual_seed(77)
+    q = torch.randn(2, 40, 64, generator=g).to(torch.bfloat16).to(dev)
+    r = torch.randn(2, 300, 64, generator=g).to(torch.bfloat16).to(dev)
+    idx, dists, nn = tpo.KNearestNeighbors(K=8, return_nn=True)(q, r)
+    assert dists.dtype == torch.bfloat16 and nn.shape == (2, 40, 8, 64)
+    assert bool((dists[..., 1:] >= dists[..., :-1]).all())
+    _, ref = tpo.knn_points(q.float(), r.float(), K=8)
+    assert torch.allclose(dists.float(), ref, rtol=2 ** -6, atol=1e-3)
+    # routes computed in float on the widened values: L1, D not a multiple of 8
+    for (D, norm) in ((64, 1), (3, 2)):
+        qa = torch.randn(2, 30, D, generator=g).to(torch.bfloat16)
+        ra = torch.randn(2, 90, D, generator=g).to(torch.bfloat16)
+        l1 = torch.tensor([30, 20])
+        l2 = torch.tensor([90, 5])
+        i_b, d_b = raw(qa, ra, l1, l2, norm, 6, -1, dev)
+        i_f, d_f = raw(qa.float(), ra.float(), l1, l2, norm, 6, -1, dev)
+        assert torch.equal(i_b, i_f) and torch.equal(d_b, d_f.to(torch.bfloat16))
+    # backward in float, rounded once
+    a = q.detach().clone().requires_grad_(True)
+    b = r.detach().clone().requires_grad_(True)
+    tpo.knn_points(a, b, K=4)[1].float().sum().backward()
+    assert a.grad.dtype == torch.bfloat16 and torch.isfinite(a.grad.float()).all()
+    assert torch.isfinite(b.grad.float()).all()

@@ -28,6 +28,15 @@
 //   grad_p2 with hardware atomics (grad_p2 zero-filled first).
 #include "tpo_common.hpp"
 
+namespace tpo {
+// knn_bf16.hip
+int64_t knn_bf16_workspace(int64_t N, int64_t P1, int64_t P2);
+bool knn_bf16_supported(int64_t D, int64_t K, int norm);
+void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
+                     int P1, int P2, int D, int K, int64_t* idxs, void* dists, void* ws,
+                     hipStream_t s);
+}  // namespace tpo
+
 #pragma clang fp contract(off)
 
 namespace tpo {
@@ -566,8 +575,10 @@ int choose_version(int64_t D, int64_t K) {
 
 using namespace tpo;
 
-extern "C" int64_t tpo_knn_workspace_size(int64_t N, int64_t P1) {
-  if (N < 0 || P1 < 0) return -1;
+extern "C" int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int64_t P2,
+                                          int64_t D, int64_t K, int norm) {
+  if (N < 0 || P1 < 0 || P2 < 0 || D < 1 || K < 0) return -1;
+  if (dtype == TPO_BF16) return knn_bf16_supported(D, K, norm) ? knn_bf16_workspace(N, P1, P2) : 0;
   return ((N * P1 * 4 + 255) / 256) * 256;
 }
 
@@ -580,6 +591,24 @@ extern "C" int tpo_knn_fwd(int dtype, const void* p1, const void* p2, const int6
       P2 >= (1 << 30) || D >= (1 << 20) || K >= (1 << 20))
     return set_error(TPO_ERR_ARG, "tpo_knn_fwd: bad sizes");
   if (norm != 1 && norm != 2) return set_error(TPO_ERR_ARG, "Norm must be 1 or 2.");
+  if (dtype == TPO_BF16) {  // matrix-core path (knn_bf16.hip); no reference version applies
+    if (version_out) *version_out = -1;
+    if (!knn_bf16_supported(D, K, norm))
+      return set_error(TPO_ERR_DTYPE,
+                       "tpo_knn_fwd: bfloat16 needs norm 2, D %% 8 == 0, 8 <= D <= 128, "
+                       "1 <= K <= 32 (got norm %d, D %lld, K %lld)",
+                       norm, (long long)D, (long long)K);
+    if (N == 0 || P1 == 0) return TPO_OK;
+    if (((uintptr_t)p1 | (uintptr_t)p2) & 15)
+      return set_error(TPO_ERR_ARG, "tpo_knn_fwd: bfloat16 points must be 16-byte aligned");
+    const int64_t need = knn_bf16_workspace(N, P1, P2);
+    if (!workspace || workspace_bytes < need)
+      return set_error(TPO_ERR_WORKSPACE, "tpo_knn_fwd: workspace of %lld bytes < %lld",
+                       (long long)workspace_bytes, (long long)need);
+    launch_knn_bf16(p1, p2, lengths1, lengths2, (int)N, (int)P1, (int)P2, (int)D, (int)K, idxs,
+                    dists, workspace, (hipStream_t)stream);
+    return check_launch("tpo_knn_fwd");
+  }
   // knn.cu:332-338: invalid explicit versions are replaced by the automatic one
   int v = (version >= 0 && check_version(version, D, K)) ? version : choose_version(D, K);
   if (version_out) *version_out = v;

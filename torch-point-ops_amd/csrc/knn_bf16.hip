@@ -1,0 +1,258 @@
+// knn_bf16.hip -- K nearest neighbours for bfloat16 points on the matrix
+// cores (the high-D path; the reference's knn_cuda_forward, knn.cu:295-398,
+// has no bfloat16 kernel and raises for it).
+//
+// Distances are squared L2 in float: d = |q|^2 + |r|^2 - 2 q.r, with the
+// bfloat16 products exact in float, q.r summed by v_mfma_f32_32x32x16_bf16 and
+// |q|^2, |r|^2 by a float FMA chain (knn_bf16_norms_kernel); d is clamped at 0.
+// Each query's K nearest are returned sorted by (distance, index), distances
+// rounded to bfloat16; rows past lengths1 and slots past lengths2 are (0, 0)
+// as in the reference's version-2 layout.
+//
+// Layout of one v_mfma_f32_32x32x16_bf16 (checked on the device): lane l
+// supplies 8 consecutive k of row/column l%32, k = 8(l/32)..8(l/32)+7, and
+// receives column l%32, rows 8(v/4) + 4(l/32) + v%4 for v = 0..15.  Queries
+// are the 32 columns of a workgroup, references the rows of 32-point tiles;
+// the workgroup's 4 waves take every 4th tile.  Each lane thus sees 16
+// references per tile for its query and keeps its own sorted list of the KC
+// best (KC >= K): a candidate below the list's last entry is inserted by a
+// branch-free network.  References reach a lane in increasing index order, so
+// strict-less insertion keeps the lower index first among equal distances.
+// At the end the 8 lists of a query (2 lanes x 4 waves) are merged in LDS.
+#include "tpo_common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace tpo {
+
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
+typedef float f16v_t __attribute__((ext_vector_type(16)));
+
+constexpr int KB_Q = 32;  // queries per workgroup (MFMA columns)
+constexpr int KB_T = 32;  // references per tile (MFMA rows)
+constexpr int KB_WAVES = 4;
+
+__host__ __device__ inline int64_t kb_pad(int64_t n) { return (n + 31) & ~(int64_t)31; }
+
+// out[r] = sum over d of p[r][d]^2 in float (rows of D bfloat16, D % 8 == 0)
+__global__ __launch_bounds__(256) void knn_bf16_norms_kernel(const __bf16* __restrict__ p,
+                                                             int64_t rows, int64_t stride_out,
+                                                             int64_t rows_per_batch, int D,
+                                                             float* __restrict__ out) {
+  for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < rows;
+       r += (int64_t)gridDim.x * 256) {
+    const bf8_t* x = reinterpret_cast<const bf8_t*>(p + r * D);
+    float acc = 0.f;
+    for (int d = 0; d < D / 8; ++d) {
+      const bf8_t v = x[d];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = (float)v[e];
+        acc = __builtin_fmaf(f, f, acc);
+      }
+    }
+    const int64_t b = r / rows_per_batch;
+    out[b * stride_out + (r - b * rows_per_batch)] = acc;
+  }
+}
+
+__device__ __forceinline__ uint32_t kb_csel(uint64_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(m));
+  return r;
+}
+
+// v[c] for a per-lane c in [0, 16): a 4-level select tree over registers (one
+// ballot per level) so the array is never indexed through memory.
+__device__ __forceinline__ float kb_select16(const float (&v)[16], int c) {
+  const uint64_t m0 = __ballot(c & 1), m1 = __ballot(c & 2), m2 = __ballot(c & 4),
+                 m3 = __ballot(c & 8);
+  uint32_t a[8], b[4], e[2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = kb_csel(m0, __float_as_uint(v[2 * i]), __float_as_uint(v[2 * i + 1]));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = kb_csel(m1, a[2 * i], a[2 * i + 1]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) e[i] = kb_csel(m2, b[2 * i], b[2 * i + 1]);
+  return __uint_as_float(kb_csel(m3, e[0], e[1]));
+}
+
+template <int KS, int KC>
+__global__ __launch_bounds__(256) void knn_bf16_kernel(
+    const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
+    const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb,
+    const float* __restrict__ qn, const float* __restrict__ rn, int64_t* __restrict__ idxs,
+    __bf16* __restrict__ dists) {
+  __shared__ float s_ld[KB_Q][2 * KB_WAVES][KC];
+  __shared__ int s_li[KB_Q][2 * KB_WAVES][KC];
+
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int n = lb / nqb, qb = lb - n * nqb;
+  int64_t l1 = len1[n], l2 = len2[n];
+  l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+  l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
+  const int L2 = (int)l2;
+  const int w = wave_id(), lane = lane_id(), j = lane & 31, h = lane >> 5;
+  const int q = qb * KB_Q + j;
+  const int qc = min(q, P1 - 1);
+
+  // column operand: query qc, dims 16s + 8h .. 16s + 8h + 7 (zero past D)
+  const __bf16* __restrict__ qp = p1 + ((size_t)n * P1 + qc) * D;
+  bf8_t bq[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int d0 = 16 * s + 8 * h;
+    bq[s] = d0 < D ? *reinterpret_cast<const bf8_t*>(qp + d0) : bf8_t{};
+  }
+  const float qq = qn[(size_t)n * kb_pad(P1) + qc];
+  const __bf16* __restrict__ rb = p2 + (size_t)n * P2 * D;
+  const float* __restrict__ rr = rn + (size_t)n * kb_pad(P2);
+
+  float ld[KC];
+  int li[KC];
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    ld[s] = Lim<float>::inf();
+    li[s] = 0x7fffffff;
+  }
+
+  const int ntiles = (L2 + KB_T - 1) / KB_T;
+  for (int t = w; t < ntiles; t += KB_WAVES) {
+    const int base = t * KB_T;
+    const __bf16* __restrict__ ra = rb + (size_t)min(base + j, L2 - 1) * D;
+    f16v_t acc = {};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int d0 = 16 * s + 8 * h;
+      const bf8_t a = d0 < D ? *reinterpret_cast<const bf8_t*>(ra + d0) : bf8_t{};
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], acc, 0, 0, 0);
+    }
+    float dv[16];
+    uint32_t mask = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 r4 = *reinterpret_cast<const float4*>(rr + base + 8 * g + 4 * h);
+      const float rv[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = 4 * g + e;
+        const int i = 8 * g + 4 * h + e;
+        float d = fmaxf(__builtin_fmaf(-2.f, acc[v], qq + rv[e]), 0.f);
+        d = base + i < L2 ? d : Lim<float>::inf();
+        dv[v] = d;
+        mask |= (d < ld[KC - 1] ? 1u : 0u) << v;
+      }
+    }
+    while (mask) {  // candidates in increasing reference order
+      const int v = __builtin_ctz(mask);
+      mask &= mask - 1;
+      const float d = kb_select16(dv, v);
+      const int id = base + 8 * (v >> 2) + 4 * h + (v & 3);
+      // sorted insertion (no-op when d >= the last entry)
+      bool c[KC];
+#pragma unroll
+      for (int s = 0; s < KC; ++s) c[s] = d < ld[s];
+#pragma unroll
+      for (int s = KC - 1; s > 0; --s) {
+        ld[s] = c[s - 1] ? ld[s - 1] : (c[s] ? d : ld[s]);
+        li[s] = c[s - 1] ? li[s - 1] : (c[s] ? id : li[s]);
+      }
+      ld[0] = c[0] ? d : ld[0];
+      li[0] = c[0] ? id : li[0];
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    s_ld[j][2 * w + h][s] = ld[s];
+    s_li[j][2 * w + h][s] = li[s];
+  }
+  __syncthreads();
+
+  // merge the 8 sorted lists of query j (threads 0..31), smallest (d, index) first
+  if (threadIdx.x < KB_Q && q < P1) {
+    const size_t row = (size_t)n * P1 + q;
+    int64_t* __restrict__ io = idxs + row * K;
+    __bf16* __restrict__ dout = dists + row * K;
+    if (q >= l1) {
+      for (int k = 0; k < K; ++k) {
+        io[k] = 0;
+        dout[k] = (__bf16)0.f;
+      }
+    } else {
+      int ptr[2 * KB_WAVES] = {};
+      for (int k = 0; k < K; ++k) {
+        float bd = Lim<float>::inf();
+        int bi = 0x7fffffff, bl = 0;
+#pragma unroll
+        for (int L = 0; L < 2 * KB_WAVES; ++L) {
+          const int p = ptr[L];
+          const float d = p < KC ? s_ld[j][L][p] : Lim<float>::inf();
+          const int i = p < KC ? s_li[j][L][p] : 0x7fffffff;
+          if (d < bd || (d == bd && i < bi)) {
+            bd = d;
+            bi = i;
+            bl = L;
+          }
+        }
+#pragma unroll
+        for (int L = 0; L < 2 * KB_WAVES; ++L) ptr[L] += L == bl ? 1 : 0;
+        const bool real = bi != 0x7fffffff;  // fewer than K references
+        io[k] = real ? (int64_t)bi : 0;
+        dout[k] = real ? (__bf16)bd : (__bf16)0.f;
+      }
+    }
+  }
+}
+
+int64_t knn_bf16_workspace(int64_t N, int64_t P1, int64_t P2) {
+  return ((N * (kb_pad(P1) + kb_pad(P2)) * 4 + 255) / 256) * 256;
+}
+
+bool knn_bf16_supported(int64_t D, int64_t K, int norm) {
+  return norm == 2 && D % 8 == 0 && D >= 8 && D <= 128 && K >= 1 && K <= 32;
+}
+
+template <int KS, int KC>
+static void kb_launch(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
+                      int N, int P1, int P2, int D, int K, const float* qn, const float* rn,
+                      int64_t* idxs, void* dists, hipStream_t s) {
+  const int nqb = (P1 + KB_Q - 1) / KB_Q;
+  hipLaunchKernelGGL((knn_bf16_kernel<KS, KC>), dim3(N * nqb), dim3(256), 0, s,
+                     (const __bf16*)p1, (const __bf16*)p2, l1, l2, P1, P2, D, K, nqb, qn, rn, idxs,
+                     (__bf16*)dists);
+}
+
+template <int KC>
+static void kb_dispatch_ks(int ks, const void* p1, const void* p2, const int64_t* l1,
+                           const int64_t* l2, int N, int P1, int P2, int D, int K, const float* qn,
+                           const float* rn, int64_t* idxs, void* dists, hipStream_t s) {
+  switch (ks) {
+    case 1: kb_launch<1, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+    case 2: kb_launch<2, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+    case 3: kb_launch<3, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+    case 4: kb_launch<4, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+    case 5: kb_launch<5, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+    case 6: kb_launch<6, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+    case 7: kb_launch<7, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+    default: kb_launch<8, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+  }
+}
+
+void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
+                     int P1, int P2, int D, int K, int64_t* idxs, void* dists, void* ws,
+                     hipStream_t s) {
+  float* qn = reinterpret_cast<float*>(ws);
+  float* rn = qn + (size_t)N * kb_pad(P1);
+  const int64_t r1 = (int64_t)N * P1, r2 = (int64_t)N * P2;
+  if (r1 > 0)
+    hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)std::min<int64_t>((r1 + 255) / 256, 65536)),
+                       dim3(256), 0, s, (const __bf16*)p1, r1, kb_pad(P1), (int64_t)P1, D, qn);
+  if (r2 > 0)
+    hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)std::min<int64_t>((r2 + 255) / 256, 65536)),
+                       dim3(256), 0, s, (const __bf16*)p2, r2, kb_pad(P2), (int64_t)P2, D, rn);
+  const int ks = (D + 15) / 16;
+  if (K <= 16) kb_dispatch_ks<16>(ks, p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s);
+  else kb_dispatch_ks<32>(ks, p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s);
+}
+
+}  // namespace tpo

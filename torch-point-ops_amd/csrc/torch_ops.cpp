@@ -35,6 +35,11 @@ int dtype_code(const at::Tensor& t, const char* op) {
   return -1;
 }
 
+// A tensor whose data starts on a 16-byte boundary (a copy if it does not).
+at::Tensor aligned16(const at::Tensor& t) {
+  return ((uintptr_t)t.data_ptr() & 15) ? t.clone(at::MemoryFormat::Contiguous) : t;
+}
+
 void* stream_of(const at::Tensor& t) {
   return (void*)c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
 }
@@ -137,10 +142,28 @@ std::tuple<at::Tensor, at::Tensor> knn_forward_hip(const at::Tensor& p1_in,
   TORCH_CHECK(p1_in.scalar_type() == p2_in.scalar_type(), "p1 and p2 dtypes differ");
   TORCH_CHECK(lengths1_in.scalar_type() == at::kLong && lengths2_in.scalar_type() == at::kLong,
               "lengths must be int64");
-  const at::Tensor p1 = p1_in.contiguous(), p2 = p2_in.contiguous();
   const at::Tensor l1 = lengths1_in.contiguous(), l2 = lengths2_in.contiguous();
+  if (p1_in.scalar_type() == at::kBFloat16) {
+    // bfloat16 (the reference raises): matrix-core kernel where it applies,
+    // otherwise the float kernels on the exactly widened values
+    const int64_t wsb = tpo_knn_workspace_size(TPO_BF16, N, P1, P2, D, K, (int)norm);
+    if (wsb > 0) {
+      const at::Tensor p1 = aligned16(p1_in.contiguous()), p2 = aligned16(p2_in.contiguous());
+      at::Tensor work = at::empty({wsb}, p1.options().dtype(at::kByte));
+      check_rc(tpo_knn_fwd(TPO_BF16, p1.data_ptr(), p2.data_ptr(), l1.data_ptr<int64_t>(),
+                           l2.data_ptr<int64_t>(), N, P1, P2, D, K, (int)norm, (int)version,
+                           idxs.data_ptr<int64_t>(), dists.data_ptr(), nullptr,
+                           work.data_ptr(), wsb, stream_of(p1)),
+               "knn_forward");
+      return {idxs, dists};
+    }
+    auto r = knn_forward_hip(p1_in.to(at::kFloat), p2_in.to(at::kFloat), lengths1_in,
+                             lengths2_in, norm, K, version);
+    return {std::get<0>(r), std::get<1>(r).to(at::kBFloat16)};
+  }
+  const at::Tensor p1 = p1_in.contiguous(), p2 = p2_in.contiguous();
   const int dt = dtype_code(p1, "knn_forward");
-  const int64_t ws = tpo_knn_workspace_size(N, P1);
+  const int64_t ws = tpo_knn_workspace_size(dt, N, P1, P2, D, K, (int)norm);
   at::Tensor work = at::empty({ws > 0 ? ws : 1}, p1.options().dtype(at::kByte));
   check_rc(tpo_knn_fwd(dt, p1.data_ptr(), p2.data_ptr(), l1.data_ptr<int64_t>(),
                        l2.data_ptr<int64_t>(), N, P1, P2, D, K, (int)norm, (int)version,
@@ -174,6 +197,11 @@ std::tuple<at::Tensor, at::Tensor> knn_backward_hip(const at::Tensor& p1_in,
     g1.zero_();
     g2.zero_();
     return {g1, g2};
+  }
+  if (p1_in.scalar_type() == at::kBFloat16) {  // computed in float, rounded once
+    auto r = knn_backward_hip(p1_in.to(at::kFloat), p2_in.to(at::kFloat), lengths1_in,
+                              lengths2_in, idxs_in, norm, grad_dists_in.to(at::kFloat));
+    return {std::get<0>(r).to(at::kBFloat16), std::get<1>(r).to(at::kBFloat16)};
   }
   const at::Tensor p1 = p1_in.contiguous(), p2 = p2_in.contiguous();
   const at::Tensor l1 = lengths1_in.contiguous(), l2 = lengths2_in.contiguous();
