@@ -33,6 +33,7 @@ sys.path.insert(0, REPO)
 
 FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0  # dense MFMA
 FLOP_PER_PAIR = 9  # 3 sub + 3 mul + 2 add + 1 compare per directed pair
 
 
@@ -163,6 +164,25 @@ def bench_knn(tpo, torch, steps):
     return dict(pairs=pairs, sec_module=sec_mod, sec_kernel=sec_raw)
 
 
+def bench_knn_c5(tpo, torch, steps):
+    """Config 5: high-D KNN, bfloat16 inputs on the matrix cores; also one run
+    of the reference-semantics float kernel (version 0) on the widened inputs."""
+    import workloads
+
+    q, r = workloads.knn_c5()
+    dev = torch.device("cuda:0")
+    a, b = q.to(dev), r.to(dev)
+    B, P1, D = a.shape
+    P2 = b.shape[1]
+    la = torch.full((B,), P1, dtype=torch.int64, device=dev)
+    lb = torch.full((B,), P2, dtype=torch.int64, device=dev)
+    op = torch.ops.torch_point_ops_knn.knn_forward
+    sec = time_steps(lambda: op(a, b, la, lb, 2, 32, -1), steps, 2, torch)
+    af, bf = a.float(), b.float()
+    sec_f32 = time_steps(lambda: op(af, bf, la, lb, 2, 32, -1), 1, 1, torch)
+    return dict(pairs=B * P1 * P2, D=D, sec=sec, sec_f32=sec_f32)
+
+
 def bench_fps(tpo, torch, steps):
     import workloads
 
@@ -236,6 +256,24 @@ def cpu_knn(O, np, threads):
                 sample=f"{q} queries per cloud x 8 clouds of config 3 (knn.cpp restated)")
 
 
+def cpu_knn_c5(O, np, threads):
+    import workloads
+
+    q, r = workloads.knn_c5()
+    nq = 16  # queries per cloud
+    a = q[:, :nq].float().numpy()
+    b = r.float().numpy()
+    ln1 = np.full(a.shape[0], nq, dtype=np.int64)
+    ln2 = np.full(a.shape[0], b.shape[1], dtype=np.int64)
+    t0 = time.perf_counter()
+    O.cpu_knn_fwd_f32(a, b, ln1, ln2, 32, 2, nthreads=threads)
+    sec = time.perf_counter() - t0
+    pairs = float(a.shape[0] * nq * b.shape[1])
+    return dict(value=pairs / sec / 1e9, unit="G pair-dists/s", cores=threads, kind="port",
+                sample=f"{nq} queries per cloud x 4 clouds of config 5 widened to float "
+                       f"(knn.cpp restated; the reference CPU path has no bfloat16)")
+
+
 def cpu_fps(O, np, pts, threads):
     nc = min(threads, pts.shape[0])
     m = 512
@@ -259,6 +297,9 @@ def profile_run(tpo, torch, reps=5):
     dev = torch.device("cuda:0")
     p1, p2 = (t.to(dev).requires_grad_(True) for t in workloads.chamfer_c2())
     k1, k2, l1, l2 = (t.to(dev) for t in workloads.knn_c3())
+    h1, h2 = (t.to(dev) for t in workloads.knn_c5())
+    hl1 = torch.full((h1.shape[0],), h1.shape[1], dtype=torch.int64, device=dev)
+    hl2 = torch.full((h1.shape[0],), h2.shape[1], dtype=torch.int64, device=dev)
     pts = workloads.fps_c4().to(dev)
     feats, go = (t.to(dev) for t in workloads.gather_c4())
     src = torch.randn(64 << 20, device=dev)  # 256 MiB of float32
@@ -267,6 +308,7 @@ def profile_run(tpo, torch, reps=5):
         d1, d2 = tpo.chamfer_distance(p1, p2)
         torch.autograd.grad(d1.mean() + d2.mean(), (p1, p2))
         torch.ops.torch_point_ops_knn.knn_forward(k1, k2, l1, l2, 2, 16, -1)
+        torch.ops.torch_point_ops_knn.knn_forward(h1, h2, hl1, hl2, 2, 32, -1)
         idx = tpo.furthest_point_sampling(pts, 4096)
         torch.ops.torch_point_ops_fps.gather_points_forward(feats, idx)
         torch.ops.torch_point_ops_fps.gather_points_backward(go, idx, 65536)
@@ -362,6 +404,14 @@ def main():
                          "ms_module_return_nn": round(kn["sec_module"] * 1e3, 3),
                          "frac_fp32_peak": round(FLOP_PER_PAIR * kn["pairs"] / kn["sec_kernel"]
                                                  / 1e12 / FP32_PEAK_TFLOPS, 4)}
+        log("[bench] knn c5 (bf16, matrix cores)")
+        k5 = bench_knn_c5(tpo, torch, max(3, args.steps // 4))
+        mfma = 2 * k5["D"] * k5["pairs"] / k5["sec"] / 1e12
+        sec["knn_c5_bf16"] = {"ms": round(k5["sec"] * 1e3, 3),
+                              "G_pair_dists_per_s": round(k5["pairs"] / k5["sec"] / 1e9, 2),
+                              "mfma_tflops": round(mfma, 2),
+                              "frac_bf16_dense_peak": round(mfma / BF16_PEAK_TFLOPS, 4),
+                              "ms_float_reference_semantics": round(k5["sec_f32"] * 1e3, 3)}
         log("[bench] fps + gather c4")
         fp = bench_fps(tpo, torch, max(3, args.steps // 4))
         sec["fps_c4"] = {"ms": round(fp["fps_sec"] * 1e3, 3),
@@ -376,6 +426,7 @@ def main():
             log("[bench] cpu baselines (knn, fps)")
             sec["knn_c3"]["cpu_baseline"] = cpu_knn(O, np, threads)
             sec["fps_c4"]["cpu_baseline"] = cpu_fps(O, np, fp["pts"], threads)
+            sec["knn_c5_bf16"]["cpu_baseline"] = cpu_knn_c5(O, np, threads)
         out["secondary"] = sec
     out["host"] = {"cpu": cpu_model(), "cores": threads,
                    "gpu": torch.cuda.get_device_name(0)}

@@ -40,6 +40,9 @@ CASES = [
     (torch.float32, 1, 33, 100, 5, 6, 2, -1),
     (torch.float32, 1, 33, 100, 40, 9, 2, -1),   # V0, runtime D
     (torch.float32, 1, 20, 64, 128, 32, 2, -1),  # config-5 shape class in fp32
+    (torch.float32, 2, 40, 100, 64, 10, 2, -1),  # D = 64 held in VGPRs
+    (torch.float32, 1, 30, 80, 128, 5, 1, -1),
+    (torch.float32, 2, 30, 70, 64, 3, 1, 2),     # invalid forced version -> automatic
     (torch.float64, 2, 60, 130, 3, 10, 2, -1),
     (torch.float64, 2, 60, 130, 3, 4, 1, -1),
     (torch.float16, 2, 60, 130, 3, 8, 2, -1),

@@ -528,6 +528,16 @@ void launch_fwd_norm(const void* p1, const void* p2, const int64_t* l1, const in
                          order);
     launch_fwd_dt<T, 3, NORM>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
   } else {
+    if constexpr (sizeof(T) == 4) {  // common high-D widths: float query held in VGPRs
+      if (D == 128) {
+        launch_fwd_dt<T, 128, NORM>(p1, p2, l1, l2, nullptr, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+        return;
+      }
+      if (D == 64) {
+        launch_fwd_dt<T, 64, NORM>(p1, p2, l1, l2, nullptr, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
+        return;
+      }
+    }
     launch_fwd_dt<T, 0, NORM>(p1, p2, l1, l2, nullptr, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
   }
 }
