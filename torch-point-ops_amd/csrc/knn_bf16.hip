@@ -18,7 +18,10 @@
 // best (KC >= K): a candidate below the list's last entry is inserted by a
 // branch-free network.  References reach a lane in increasing index order, so
 // strict-less insertion keeps the lower index first among equal distances.
-// At the end the 8 lists of a query (2 lanes x 4 waves) are merged in LDS.
+// Candidates are first queued per lane in LDS (in index order) and inserted
+// in bulk when some lane's queue is about to overflow, so one pass of the
+// insertion network serves every lane that has work.  At the end the 8 lists
+// of a query (2 lanes x 4 waves) are merged in LDS.
 #include "tpo_common.hpp"
 
 #pragma clang fp contract(off)
@@ -56,25 +59,21 @@ __global__ __launch_bounds__(256) void knn_bf16_norms_kernel(const __bf16* __res
   }
 }
 
-__device__ __forceinline__ uint32_t kb_csel(uint64_t m, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(m));
-  return r;
-}
+constexpr int KB_QCAP = 16;  // queued candidates per lane
 
-// v[c] for a per-lane c in [0, 16): a 4-level select tree over registers (one
-// ballot per level) so the array is never indexed through memory.
-__device__ __forceinline__ float kb_select16(const float (&v)[16], int c) {
-  const uint64_t m0 = __ballot(c & 1), m1 = __ballot(c & 2), m2 = __ballot(c & 4),
-                 m3 = __ballot(c & 8);
-  uint32_t a[8], b[4], e[2];
+template <int KC>
+__device__ __forceinline__ void kb_insert(float (&ld)[KC], int (&li)[KC], float d, int id) {
+  // sorted insertion; a no-op when d is not below the last entry
+  bool c[KC];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) a[i] = kb_csel(m0, __float_as_uint(v[2 * i]), __float_as_uint(v[2 * i + 1]));
+  for (int s = 0; s < KC; ++s) c[s] = d < ld[s];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) b[i] = kb_csel(m1, a[2 * i], a[2 * i + 1]);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) e[i] = kb_csel(m2, b[2 * i], b[2 * i + 1]);
-  return __uint_as_float(kb_csel(m3, e[0], e[1]));
+  for (int s = KC - 1; s > 0; --s) {
+    ld[s] = c[s - 1] ? ld[s - 1] : (c[s] ? d : ld[s]);
+    li[s] = c[s - 1] ? li[s - 1] : (c[s] ? id : li[s]);
+  }
+  ld[0] = c[0] ? d : ld[0];
+  li[0] = c[0] ? id : li[0];
 }
 
 template <int KS, int KC>
@@ -83,8 +82,19 @@ __global__ __launch_bounds__(256) void knn_bf16_kernel(
     const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb,
     const float* __restrict__ qn, const float* __restrict__ rn, int64_t* __restrict__ idxs,
     __bf16* __restrict__ dists) {
-  __shared__ float s_ld[KB_Q][2 * KB_WAVES][KC];
-  __shared__ int s_li[KB_Q][2 * KB_WAVES][KC];
+  // per-lane candidate queues during the scan, the 8 lists of each query after
+  struct Queues {
+    float d[KB_WAVES][KB_QCAP][64];
+    int i[KB_WAVES][KB_QCAP][64];
+  };
+  struct Lists {
+    float d[KB_Q][2 * KB_WAVES][KC];
+    int i[KB_Q][2 * KB_WAVES][KC];
+  };
+  __shared__ union {
+    Queues q;
+    Lists l;
+  } sm;
 
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const int n = lb / nqb, qb = lb - n * nqb;
@@ -115,6 +125,22 @@ __global__ __launch_bounds__(256) void knn_bf16_kernel(
     ld[s] = Lim<float>::inf();
     li[s] = 0x7fffffff;
   }
+  int nq_ = 0;  // queued candidates of this lane
+  // insert the queue in order: each pass a lane first skips (cheaply) the
+  // entries no longer below its list's last one, then inserts its next entry,
+  // so the passes number the largest count of useful insertions in the wave
+  auto drain = [&]() {
+    int k = 0;
+    for (;;) {
+      while (k < nq_ && !(sm.q.d[w][k][lane] < ld[KC - 1])) ++k;
+      if (__ballot(k < nq_) == 0) break;
+      if (k < nq_) {
+        kb_insert<KC>(ld, li, sm.q.d[w][k][lane], sm.q.i[w][k][lane]);
+        ++k;
+      }
+    }
+    nq_ = 0;
+  };
 
   const int ntiles = (L2 + KB_T - 1) / KB_T;
   for (int t = w; t < ntiles; t += KB_WAVES) {
@@ -128,7 +154,8 @@ __global__ __launch_bounds__(256) void knn_bf16_kernel(
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], acc, 0, 0, 0);
     }
     float dv[16];
-    uint32_t mask = 0;
+    int pc = 0;
+    const float thr = ld[KC - 1];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const float4 r4 = *reinterpret_cast<const float4*>(rr + base + 8 * g + 4 * h);
@@ -140,31 +167,25 @@ __global__ __launch_bounds__(256) void knn_bf16_kernel(
         float d = fmaxf(__builtin_fmaf(-2.f, acc[v], qq + rv[e]), 0.f);
         d = base + i < L2 ? d : Lim<float>::inf();
         dv[v] = d;
-        mask |= (d < ld[KC - 1] ? 1u : 0u) << v;
+        pc += d < thr ? 1 : 0;
       }
     }
-    while (mask) {  // candidates in increasing reference order
-      const int v = __builtin_ctz(mask);
-      mask &= mask - 1;
-      const float d = kb_select16(dv, v);
-      const int id = base + 8 * (v >> 2) + 4 * h + (v & 3);
-      // sorted insertion (no-op when d >= the last entry)
-      bool c[KC];
+    if (__ballot(nq_ + pc > KB_QCAP) != 0) drain();  // keep every queue within capacity
 #pragma unroll
-      for (int s = 0; s < KC; ++s) c[s] = d < ld[s];
-#pragma unroll
-      for (int s = KC - 1; s > 0; --s) {
-        ld[s] = c[s - 1] ? ld[s - 1] : (c[s] ? d : ld[s]);
-        li[s] = c[s - 1] ? li[s - 1] : (c[s] ? id : li[s]);
+    for (int v = 0; v < 16; ++v) {
+      if (dv[v] < thr) {  // thr may predate a drain: a stale entry inserts as a no-op
+        sm.q.d[w][nq_][lane] = dv[v];
+        sm.q.i[w][nq_][lane] = base + 8 * (v >> 2) + 4 * h + (v & 3);
+        ++nq_;
       }
-      ld[0] = c[0] ? d : ld[0];
-      li[0] = c[0] ? id : li[0];
     }
   }
+  drain();
+  __syncthreads();  // the queues' LDS becomes the lists'
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
-    s_ld[j][2 * w + h][s] = ld[s];
-    s_li[j][2 * w + h][s] = li[s];
+    sm.l.d[j][2 * w + h][s] = ld[s];
+    sm.l.i[j][2 * w + h][s] = li[s];
   }
   __syncthreads();
 
@@ -186,8 +207,8 @@ __global__ __launch_bounds__(256) void knn_bf16_kernel(
 #pragma unroll
         for (int L = 0; L < 2 * KB_WAVES; ++L) {
           const int p = ptr[L];
-          const float d = p < KC ? s_ld[j][L][p] : Lim<float>::inf();
-          const int i = p < KC ? s_li[j][L][p] : 0x7fffffff;
+          const float d = p < KC ? sm.l.d[j][L][p] : Lim<float>::inf();
+          const int i = p < KC ? sm.l.i[j][L][p] : 0x7fffffff;
           if (d < bd || (d == bd && i < bi)) {
             bd = d;
             bi = i;
