@@ -41,7 +41,6 @@ constexpr int FPS_THREADS = 1024;
 constexpr int FPS_WAVES = FPS_THREADS / 64;
 constexpr int FPS_GRID = 16;  // Morton grid per axis (4096 cells)
 constexpr int FPS_CELLS = FPS_GRID * FPS_GRID * FPS_GRID;
-constexpr uint32_t FPS_INVALID = 0x80000000u;
 
 // candidate/value type: float holds every binary16 and binary32 value exactly
 template <typename T> struct FpsV { typedef float type; };
@@ -67,11 +66,12 @@ template <> struct FpsConst<half_t> {
   __device__ static float tiny() { return 1e-3f; }
 };
 
-// One sorted point: coordinates and meta = rank | FPS_INVALID-if-skipped,
+// One sorted point: coordinates and key = ~rank for a point that takes part,
+// 0 for one that does not (its running minimum is then held at 0),
 // loaded as a single 16-byte access for float.
 template <typename T> struct FpsRec {
   T x, y, z;
-  uint32_t meta;
+  uint32_t key;
 };
 
 struct FpsLayout {
@@ -117,10 +117,13 @@ struct CandD {
 template <typename T> struct FpsCand { typedef CandF type; };
 template <> struct FpsCand<double> { typedef CandD type; };
 
-__device__ __forceinline__ CandF cand_make(float v, uint32_t r, CandF*) {
-  return {((uint64_t)__float_as_uint(v) << 32) | (uint64_t)(0xffffffffu - r)};
+// key = ~rank, or 0 for "no candidate" (whose value is then +0)
+__device__ __forceinline__ CandF cand_make(float v, uint32_t key, CandF*) {
+  return {((uint64_t)__float_as_uint(v) << 32) | (uint64_t)key};
 }
-__device__ __forceinline__ CandD cand_make(double v, uint32_t r, CandD*) { return {v, r}; }
+__device__ __forceinline__ CandD cand_make(double v, uint32_t key, CandD*) {
+  return key ? CandD{v, ~key} : CandD{-1.0, 0xffffffffu};
+}
 __device__ __forceinline__ CandF cand_none(CandF*) { return {0}; }
 __device__ __forceinline__ CandD cand_none(CandD*) { return {-1.0, 0xffffffffu}; }
 __device__ __forceinline__ bool cand_gt(CandF a, CandF b) { return a.k > b.k; }
@@ -152,6 +155,13 @@ __device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
   v = dpp_umax<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
+// first lane whose candidate equals c (c is wave-uniform and held by a lane)
+template <typename C>
+__device__ __forceinline__ int lane_of(C mine, C c) {
+  const uint64_t hit = __ballot(cand_eq(mine, c));
+  return hit ? __builtin_ctzll(hit) : 0;
+}
+
 // Best candidate of the whole wave: the largest value word, then the largest
 // rank word among the lanes holding that value.
 __device__ __forceinline__ CandF wave_best(CandF c) {
@@ -168,6 +178,26 @@ __device__ __forceinline__ CandD wave_best(CandD c) {
   }
   return c;
 }
+// Best candidate of the wave and the (first) lane holding it.  The rank
+// pass only runs when several lanes share the largest value.
+__device__ __forceinline__ CandF wave_best_at(CandF c, int& wl) {
+  const uint32_t hi = (uint32_t)(c.k >> 32);
+  const uint32_t mh = wave_umax(hi);
+  const uint64_t eq = __ballot(hi == mh);
+  if (__builtin_popcountll(eq) == 1) {
+    wl = __builtin_ctzll(eq);
+    return {((uint64_t)mh << 32) | (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)c.k, wl)};
+  }
+  const uint32_t ml = wave_umax(hi == mh ? (uint32_t)c.k : 0u);
+  const CandF b = {((uint64_t)mh << 32) | ml};
+  wl = lane_of(c, b);
+  return b;
+}
+__device__ __forceinline__ CandD wave_best_at(CandD c, int& wl) {
+  const CandD b = wave_best(c);
+  wl = lane_of(c, b);
+  return b;
+}
 __device__ __forceinline__ CandD row0_best(CandD c) {
 #pragma unroll
   for (int m = 8; m >= 1; m >>= 1) {
@@ -177,6 +207,9 @@ __device__ __forceinline__ CandD row0_best(CandD c) {
   return {__shfl(c.v, 0, 64), (uint32_t)__shfl((int)c.r, 0, 64)};
 }
 
+__device__ __forceinline__ float vmax(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ double vmax(double a, double b) { return fmax(a, b); }
+
 __device__ __forceinline__ float bcast(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
@@ -185,12 +218,6 @@ __device__ __forceinline__ half_t bcast(half_t v, int lane) {
   return (half_t)bcast((float)v, lane);  // exact round trip
 }
 
-// first lane whose candidate equals c (c is wave-uniform and held by a lane)
-template <typename C>
-__device__ __forceinline__ int lane_of(C mine, C c) {
-  const uint64_t hit = __ballot(cand_eq(mine, c));
-  return hit ? __builtin_ctzll(hit) : 0;
-}
 
 template <typename T>
 __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ pts, int N, int m,
@@ -310,11 +337,11 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     const uint32_t t = (uint32_t)(k & (bs - 1));
     const uint32_t rev = bs_bits ? (__builtin_bitreverse32(t) >> (32 - bs_bits)) : 0u;
     const uint32_t rank = rev * (uint32_t)per + (uint32_t)(k / bs);
-    recs[pos] = FpsRec<T>{x, y, z, rank | (valid ? 0u : FPS_INVALID)};
-    ts[pos] = init;
+    recs[pos] = FpsRec<T>{x, y, z, valid ? ~rank : 0u};
+    ts[pos] = valid ? init : (T)0;
   }
   for (int64_t k = N + tid; k < L.np; k += FPS_THREADS) {
-    recs[k] = FpsRec<T>{(T)0, (T)0, (T)0, FPS_INVALID};
+    recs[k] = FpsRec<T>{(T)0, (T)0, (T)0, 0u};
     ts[k] = (T)0;
   }
   __syncthreads();
@@ -338,8 +365,8 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     for (int i = 0; i < s_sz; ++i) {
       const int pos = sb * s_sz + i;
       const FpsRec<T> rc = recs[pos];
-      const uint32_t mt = rc.meta;
-      if (mt & FPS_INVALID) continue;
+      const uint32_t mt = rc.key;
+      if (mt == 0) continue;
       const T x = rc.x, y = rc.y, z = rc.z;
       blo[0] = x < blo[0] ? (V)x : blo[0];
       blo[1] = y < blo[1] ? (V)y : blo[1];
@@ -357,82 +384,96 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     }
   }
   // the wave's best bucket (uniform)
-  C wbest = wave_best(bbest);
-  int wlane = lane_of(bbest, wbest);
+  int wlane;
+  C wbest = wave_best_at(bbest, wlane);
   T wx = bcast(bx, wlane), wy = bcast(by, wlane), wz = bcast(bz, wlane);
 
   // ---- 4. the sampling loop ----
   T ox = P[0], oy = P[1], oz = P[2];
   if (tid == 0) out[0] = 0;
-  const V margin = (V)FpsConst<T>::margin();
+  int rk = 0;  // wave 0: lane j mod 64 holds the rank of sample j
+  // A bucket is visited only when the squared distance from the new sample to
+  // its box is at most reach = max(best * (1 + 2 margin), tiny); beyond it the
+  // sample is provably farther from every point in the bucket than that
+  // point's running minimum (best bounds them all; the margin dwarfs the
+  // rounding of both sides).  A bucket without participating points has
+  // reach -1 and is never visited.
+  const V grow = (V)1 + (V)2 * (V)FpsConst<T>::margin();
   const V tiny = (V)FpsConst<T>::tiny();
-  constexpr int BATCH = 4;
+  auto reach_of = [&](C c) -> V { return cand_valid(c) ? vmax((V)cand_val(c) * grow, tiny) : (V)-1; };
+  V reach = reach_of(bbest);
   for (int j = 1; j < m; ++j) {
-    // A bucket can be skipped when the new sample is provably farther from
-    // every point in it than that point's running minimum.
-    bool touch = false;
-    if (cand_valid(bbest)) {
-      const V o3[3] = {(V)ox, (V)oy, (V)oz};
-      V lb2 = (V)0;
+    const V o3[3] = {(V)ox, (V)oy, (V)oz};
+    V lb2 = (V)0;
 #pragma unroll
-      for (int c = 0; c < 3; ++c) {
-        V e = blo[c] - o3[c];
-        const V f = o3[c] - bhi[c];
-        e = e > f ? e : f;
-        e = e > (V)0 ? e : (V)0;
-        lb2 += e * e;
-      }
-      touch = !(lb2 * ((V)1 - margin) > (V)cand_val(bbest) && lb2 > tiny);
+    for (int c = 0; c < 3; ++c) {
+      const V e = vmax(vmax(blo[c] - o3[c], o3[c] - bhi[c]), (V)0);
+      lb2 += e * e;
     }
-    uint64_t tm = __ballot(touch);
+    uint64_t tm = __ballot(lb2 <= reach);
     const bool rereduce = (tm >> wlane) & 1;
-    while (tm) {
-      // up to BATCH touched buckets: their loads are issued together, then
-      // each present bucket is updated and re-reduced
-      int bits[BATCH];
+    // Touched buckets are visited NB at a time: every slot's loads are issued
+    // unconditionally (an empty slot re-reads slot 0's bucket), the NB wave
+    // reductions are independent straight-line code, and the running-minimum
+    // stores come last, so no load or reduction of the batch waits for a store.
+    auto visit = [&](auto nbc) {
+      constexpr int NB = decltype(nbc)::value;
+      int bits[NB];
 #pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
+      for (int u = 0; u < NB; ++u) {
         bits[u] = tm ? __builtin_ctzll(tm) : -1;
         tm &= tm ? tm - 1 : 0;
       }
       for (int p0 = 0; p0 < s_sz; p0 += 64) {
-        FpsRec<T> rc[BATCH];
-        T t[BATCH];
-        int pos[BATCH];
+        int pos[NB];
+        FpsRec<T> rc[NB];
+        T t[NB];
 #pragma unroll
-        for (int u = 0; u < BATCH; ++u) {
-          if (bits[u] >= 0) {
-            pos[u] = (bits[u] * FPS_WAVES + w) * s_sz + p0 + lane;
-            rc[u] = recs[pos[u]];
-            t[u] = ts[pos[u]];
-          }
+        for (int u = 0; u < NB; ++u) {
+          const int bu = bits[u] >= 0 ? bits[u] : bits[0];
+          pos[u] = (bu * FPS_WAVES + w) * s_sz + p0 + lane;
+          rc[u] = recs[pos[u]];
+          t[u] = ts[pos[u]];
         }
+        T t2[NB];
+        C cand[NB];
 #pragma unroll
-        for (int u = 0; u < BATCH; ++u) {
-          if (bits[u] < 0) continue;
-          C cand = cand_none(ctag);
-          if (!(rc[u].meta & FPS_INVALID)) {
-            const T d = sq3((T)(rc[u].x - ox), (T)(rc[u].y - oy), (T)(rc[u].z - oz));  // fps.cu:145
-            const T t2 = d < t[u] ? d : t[u];                                           // fps.cu:146
-            if (t2 != t[u]) ts[pos[u]] = t2;
-            cand = cand_make((V)t2, rc[u].meta, ctag);
-          }
-          const C best = wave_best(cand);
-          const int wl = lane_of(cand, best);
-          const T cx = bcast(rc[u].x, wl), cy = bcast(rc[u].y, wl), cz = bcast(rc[u].z, wl);
+        for (int u = 0; u < NB; ++u) {
+          const T d = sq3((T)(rc[u].x - ox), (T)(rc[u].y - oy), (T)(rc[u].z - oz));  // fps.cu:145
+          t2[u] = d < t[u] ? d : t[u];                                                // fps.cu:146
+          cand[u] = cand_make((V)t2[u], rc[u].key, ctag);
+        }
+        C best[NB];
+        int wl[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) best[u] = wave_best_at(cand[u], wl[u]);
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+          const T cx = bcast(rc[u].x, wl[u]), cy = bcast(rc[u].y, wl[u]), cz = bcast(rc[u].z, wl[u]);
           // passes after the first (buckets larger than 64) keep the max
-          if (lane == bits[u] && (p0 == 0 || cand_gt(best, bbest))) {
-            bbest = best;
+          if (lane == bits[u] && (p0 == 0 || cand_gt(best[u], bbest))) {
+            bbest = best[u];
             bx = cx;
             by = cy;
             bz = cz;
           }
         }
+#pragma unroll
+        for (int u = 0; u < NB; ++u)
+          if (bits[u] >= 0 && t2[u] != t[u]) ts[pos[u]] = t2[u];
       }
+    };
+    if (tm) {
+      while (tm) {
+        const int nt = __builtin_popcountll(tm);
+        if (nt == 1) visit(std::integral_constant<int, 1>{});
+        else if (nt == 2) visit(std::integral_constant<int, 2>{});
+        else visit(std::integral_constant<int, 4>{});
+      }
+      reach = reach_of(bbest);
     }
     if (rereduce) {  // the wave's best bucket changed; otherwise wbest stands
-      wbest = wave_best(bbest);
-      wlane = lane_of(bbest, wbest);
+      wbest = wave_best_at(bbest, wlane);
       wx = bcast(bx, wlane);
       wy = bcast(by, wlane);
       wz = bcast(bz, wlane);
@@ -463,16 +504,25 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
       gw = lane_of(mine.c, g);
     }
     // the rank is decoded to an index after the loop, off the critical path
+    int r;
     if (!cand_valid(g)) {  // nothing participates: the reference's index 0
       ox = P[0];
       oy = P[1];
       oz = P[2];
-      if (tid == 0) out[j] = -1;
+      r = -1;
     } else {
       ox = bcast(mine.x, gw);
       oy = bcast(mine.y, gw);
       oz = bcast(mine.z, gw);
-      if (tid == 0) out[j] = (int64_t)cand_rank(g);
+      r = (int)cand_rank(g);
+    }
+    // wave 0 stores the ranks 64 at a time
+    if (w == 0) {
+      rk = lane == (j & 63) ? r : rk;
+      if ((j & 63) == 63 || j == m - 1) {
+        const int jj = (j & ~63) + lane;
+        if (jj >= 1 && jj <= j) out[jj] = (int64_t)rk;
+      }
     }
   }
   // rank -> point index: rank = bitrev(k mod BS) * per + k / BS
