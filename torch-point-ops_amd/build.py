@@ -45,7 +45,8 @@ HIPCC_FLAGS = [
 ]
 
 # Per-file additions (none at present).
-HIPCC_FILE_FLAGS: dict = {}
+# fps.hip: its one-lane LDS atomic needs no wave-level pre-reduction
+HIPCC_FILE_FLAGS: dict = {"fps.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
 
 
 def _run(cmd, verbose):

@@ -209,6 +209,8 @@ __device__ __forceinline__ CandD row0_best(CandD c) {
 
 __device__ __forceinline__ float vmax(float a, float b) { return fmaxf(a, b); }
 __device__ __forceinline__ double vmax(double a, double b) { return fmax(a, b); }
+__device__ __forceinline__ float vfma(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ double vfma(double a, double b, double c) { return __builtin_fma(a, b, c); }
 
 __device__ __forceinline__ float bcast(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
@@ -386,10 +388,10 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
   // the wave's best bucket (uniform)
   int wlane;
   C wbest = wave_best_at(bbest, wlane);
-  T wx = bcast(bx, wlane), wy = bcast(by, wlane), wz = bcast(bz, wlane);
 
   // ---- 4. the sampling loop ----
-  T ox = P[0], oy = P[1], oz = P[2];
+  const T p0x = P[0], p0y = P[1], p0z = P[2];
+  T ox = p0x, oy = p0y, oz = p0z;
   if (tid == 0) out[0] = 0;
   int rk = 0;  // wave 0: lane j mod 64 holds the rank of sample j
   // A bucket is visited only when the squared distance from the new sample to
@@ -404,12 +406,10 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
   V reach = reach_of(bbest);
   for (int j = 1; j < m; ++j) {
     const V o3[3] = {(V)ox, (V)oy, (V)oz};
-    V lb2 = (V)0;
+    V e[3];
 #pragma unroll
-    for (int c = 0; c < 3; ++c) {
-      const V e = vmax(vmax(blo[c] - o3[c], o3[c] - bhi[c]), (V)0);
-      lb2 += e * e;
-    }
+    for (int c = 0; c < 3; ++c) e[c] = vmax(vmax(blo[c] - o3[c], o3[c] - bhi[c]), (V)0);
+    const V lb2 = vfma(e[2], e[2], vfma(e[1], e[1], e[0] * e[0]));
     uint64_t tm = __ballot(lb2 <= reach);
     const bool rereduce = (tm >> wlane) & 1;
     // Touched buckets are visited NB at a time: every slot's loads are issued
@@ -474,48 +474,41 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     }
     if (rereduce) {  // the wave's best bucket changed; otherwise wbest stands
       wbest = wave_best_at(bbest, wlane);
-      wx = bcast(bx, wlane);
-      wy = bcast(by, wlane);
-      wz = bcast(bz, wlane);
     }
     const int par = j & 1;
     C g;
     int gw;
-    WaveBest mine = {cand_none(ctag), (T)0, (T)0, (T)0};
+    WaveBest mine;
+    // the lane holding the wave's best publishes it from its own registers;
+    // every lane then reads wave (lane mod 16)'s entry
     if constexpr (sizeof(C) == 8) {
       // Packed keys: every wave folds its best into one LDS word with an
       // atomic max; slots rotate over 3 iterations so the reset of the next
       // slot (before this barrier) never races with its readers (before the
       // previous barrier) or its writers (after this barrier).
       if (tid == 0) s_gkey[(j + 1) % 3] = 0;
-      if (lane == 0) {
-        atomicMax(&s_gkey[j % 3], (unsigned long long)wbest.k);
-        s_wb[par][w] = WaveBest{wbest, wx, wy, wz};
+      if (lane == wlane) {
+        atomicMax(&s_gkey[j % 3], (unsigned long long)bbest.k);
+        s_wb[par][w] = WaveBest{bbest, bx, by, bz};
       }
       __syncthreads();
-      if (lane < FPS_WAVES) mine = s_wb[par][lane];  // issued with the key read
+      mine = s_wb[par][lane & (FPS_WAVES - 1)];  // issued with the key read
       g = C{s_gkey[j % 3]};
       gw = lane_of(mine.c, g);
     } else {
-      if (lane == 0) s_wb[par][w] = WaveBest{wbest, wx, wy, wz};
+      if (lane == wlane) s_wb[par][w] = WaveBest{bbest, bx, by, bz};
       __syncthreads();
-      if (lane < FPS_WAVES) mine = s_wb[par][lane];
+      mine = s_wb[par][lane & (FPS_WAVES - 1)];
       g = row0_best(mine.c);
       gw = lane_of(mine.c, g);
     }
-    // the rank is decoded to an index after the loop, off the critical path
-    int r;
-    if (!cand_valid(g)) {  // nothing participates: the reference's index 0
-      ox = P[0];
-      oy = P[1];
-      oz = P[2];
-      r = -1;
-    } else {
-      ox = bcast(mine.x, gw);
-      oy = bcast(mine.y, gw);
-      oz = bcast(mine.z, gw);
-      r = (int)cand_rank(g);
-    }
+    // Nothing participates: the reference's index 0 (rank -1 here).  The
+    // rank is decoded to an index after the loop, off the critical path.
+    const bool gv = cand_valid(g);
+    ox = gv ? bcast(mine.x, gw) : p0x;
+    oy = gv ? bcast(mine.y, gw) : p0y;
+    oz = gv ? bcast(mine.z, gw) : p0z;
+    const int r = gv ? (int)cand_rank(g) : -1;
     // wave 0 stores the ranks 64 at a time
     if (w == 0) {
       rk = lane == (j & 63) ? r : rk;
