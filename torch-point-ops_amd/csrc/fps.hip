@@ -138,6 +138,9 @@ __device__ __forceinline__ float cand_val(CandF a) { return __uint_as_float((uin
 __device__ __forceinline__ double cand_val(CandD a) { return a.v; }
 __device__ __forceinline__ uint32_t cand_rank(CandF a) { return 0xffffffffu - (uint32_t)a.k; }
 __device__ __forceinline__ uint32_t cand_rank(CandD a) { return a.r; }
+// the record key (~rank, 0 for none) of a candidate
+__device__ __forceinline__ uint32_t cand_keyword(CandF a) { return (uint32_t)a.k; }
+__device__ __forceinline__ uint32_t cand_keyword(CandD a) { return ~a.r; }
 
 template <int CTRL, int ROWMASK>
 __device__ __forceinline__ uint32_t dpp_umax(uint32_t v) {
@@ -411,7 +414,7 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     for (int c = 0; c < 3; ++c) e[c] = vmax(vmax(blo[c] - o3[c], o3[c] - bhi[c]), (V)0);
     const V lb2 = vfma(e[2], e[2], vfma(e[1], e[1], e[0] * e[0]));
     uint64_t tm = __ballot(lb2 <= reach);
-    const bool rereduce = (tm >> wlane) & 1;
+    bool rereduce = false;  // the best of the wave's best bucket changed
     // Touched buckets are visited NB at a time: every slot's loads are issued
     // unconditionally (an empty slot re-reads slot 0's bucket), the NB wave
     // reductions are independent straight-line code, and the running-minimum
@@ -443,20 +446,30 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
           t2[u] = d < t[u] ? d : t[u];                                                // fps.cu:146
           cand[u] = cand_make((V)t2[u], rc[u].key, ctag);
         }
-        C best[NB];
-        int wl[NB];
-#pragma unroll
-        for (int u = 0; u < NB; ++u) best[u] = wave_best_at(cand[u], wl[u]);
+        // A bucket's best stays its best unless that point's own running
+        // minimum dropped (the others can only drop too), so the reduction
+        // runs only then (always for buckets larger than 64 points).
+        bool red[NB];
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-          const T cx = bcast(rc[u].x, wl[u]), cy = bcast(rc[u].y, wl[u]), cz = bcast(rc[u].z, wl[u]);
+          const int bu = bits[u] >= 0 ? bits[u] : bits[0];
+          const uint32_t bkey = (uint32_t)__builtin_amdgcn_readlane((int)cand_keyword(bbest), bu);
+          red[u] = bits[u] >= 0 && (s_sz > 64 || __ballot(rc[u].key == bkey && t2[u] != t[u]) != 0);
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+          if (!red[u]) continue;
+          int wl;
+          const C best = wave_best_at(cand[u], wl);
+          const T cx = bcast(rc[u].x, wl), cy = bcast(rc[u].y, wl), cz = bcast(rc[u].z, wl);
           // passes after the first (buckets larger than 64) keep the max
-          if (lane == bits[u] && (p0 == 0 || cand_gt(best[u], bbest))) {
-            bbest = best[u];
+          if (lane == bits[u] && (p0 == 0 || cand_gt(best, bbest))) {
+            bbest = best;
             bx = cx;
             by = cy;
             bz = cz;
           }
+          rereduce |= bits[u] == wlane;
         }
 #pragma unroll
         for (int u = 0; u < NB; ++u)
