@@ -343,13 +343,12 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     const uint32_t rev = bs_bits ? (__builtin_bitreverse32(t) >> (32 - bs_bits)) : 0u;
     const uint32_t rank = rev * (uint32_t)per + (uint32_t)(k / bs);
     recs[pos] = FpsRec<T>{x, y, z, valid ? ~rank : 0u};
-    ts[pos] = valid ? init : (T)0;
   }
-  for (int64_t k = N + tid; k < L.np; k += FPS_THREADS) {
-    recs[k] = FpsRec<T>{(T)0, (T)0, (T)0, 0u};
-    ts[k] = (T)0;
-  }
+  for (int64_t k = N + tid; k < L.np; k += FPS_THREADS) recs[k] = FpsRec<T>{(T)0, (T)0, (T)0, 0u};
   __syncthreads();
+  // running minima in sorted order (coalesced): init, or 0 for a point that
+  // does not take part
+  for (int64_t k = tid; k < L.np; k += FPS_THREADS) ts[k] = recs[k].key ? init : (T)0;
 
   // ---- 3. bucket summaries ----
   // Lane l of wave w owns bucket sb = l * 16 + w: buckets adjacent in Morton
@@ -367,9 +366,14 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     bhi[c] = (V)-__builtin_inf();
   }
   if (sb < nb) {
-    for (int i = 0; i < s_sz; ++i) {
-      const int pos = sb * s_sz + i;
-      const FpsRec<T> rc = recs[pos];
+    constexpr int U = 8;  // records in flight per step
+    for (int i0 = 0; i0 < s_sz; i0 += U) {
+    FpsRec<T> rcu[U];
+#pragma unroll
+    for (int e = 0; e < U; ++e) rcu[e] = recs[sb * s_sz + i0 + e];
+#pragma unroll
+    for (int e = 0; e < U; ++e) {
+      const FpsRec<T> rc = rcu[e];
       const uint32_t mt = rc.key;
       if (mt == 0) continue;
       const T x = rc.x, y = rc.y, z = rc.z;
@@ -386,6 +390,7 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
         by = y;
         bz = z;
       }
+    }
     }
   }
   // the wave's best bucket (uniform)
