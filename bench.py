@@ -5,10 +5,12 @@
 Headline: one step = Chamfer forward + backward
 (ChamferDistance('mean') and its gradient) at B=32, N=M=8192, float32, inputs
 resident in HBM.  value = directed pair-distances per second (2*B*N*M per
-step) in G/s.  The roofline object covers the dominant kernel (the Chamfer
-forward kernel, timed with HIP events on the stream it runs on, inside the
-timed region): 9 FLOP per directed pair against the 157.3 TFLOP/s FP32
-vector peak.  The CPU baseline is the reference's CPU formulation of Chamfer
+step) in G/s.  The roofline object covers the dominant kernels, the Chamfer
+forward (grid sort + exact grid search, timed together with HIP events on
+the stream they run on, inside the timed region): 9 FLOP per directed pair
+of the brute-force algorithm against the 157.3 TFLOP/s FP32 peak, next to
+the pairs the search actually evaluated; its traffic comes from the
+FETCH_SIZE/WRITE_SIZE runs summarised in profiles/.  The CPU baseline is the reference's CPU formulation of Chamfer
 (tests/test_chamfer.py:11-25 of the reference: broadcast, square, sum, min,
 plus autograd backward), chunked, on a bounded sample, on the host's cores.
 
@@ -349,7 +351,7 @@ def main():
     executed = FLOP_PER_PAIR * ch["pairs_evaluated"] / ch["grid_fwd_sec"] / 1e12
     dense = FLOP_PER_PAIR * ch["pairs"] / ch["dense_fwd_sec"] / 1e12
     traffic = None
-    tfile = os.path.join(REPO, "profiles", "chamfer_fwd_c2_traffic.json")
+    tfile = os.path.join(REPO, "profiles", "chamfer_grid_fwd_c2_traffic.json")
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
 
@@ -370,7 +372,8 @@ def main():
                                "ChamferDistance('mean') (BASELINE.json configs[1])",
                    "global_batch": ch["B"], "points": [ch["N"], ch["M"]],
                    "pairs_per_step": ch["pairs"], "parallelism": "single GPU"},
-        "roofline": {"bound": "valu",
+        "roofline": {"bound": "mfma",
+                     "compute_unit": "VALU (fp32 vector ALU; 157.3 TFLOP/s is MI355X's fp32 peak)",
                      "kernel": "chamfer_grid_sort_kernel + chamfer_grid_search_kernel",
                      "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
