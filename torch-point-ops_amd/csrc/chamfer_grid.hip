@@ -312,19 +312,8 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     for (int a = 0; a < 3; ++a) rmax = max(rmax, max(ci[a], ga[a] - 1 - ci[a]));
     float bd = Lim<float>::inf();
     int bi = 0x7fffffff;
-    // evaluate every point of cell cc unless its box is farther than bd
-    auto visit = [&](int cx, int cy, int cz) {
-      const int cc[3] = {cx, cy, cz};
-      float gap[3];
-#pragma unroll
-      for (int a = 0; a < 3; ++a) {
-        const float clo = (ga[a] > 1 ? glo[a] + (float)cc[a] * cs[a] : glo[a]) - eps[a];
-        const float chi = (ga[a] > 1 ? glo[a] + (float)(cc[a] + 1) * cs[a] : ghi[a]) + eps[a];
-        gap[a] = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
-      }
-      if (sq3(gap[0], gap[1], gap[2]) * (1.f - 0x1p-20f) > bd) return;
-      const uint32_t code = cg_code(cx, cy, cz);
-      const int j0 = cstart[code], j1 = cstart[code + 1];
+    // evaluate every point of sorted positions [j0, j1)
+    auto scan = [&](int j0, int j1) {
       for (int j = j0; j < j1; j += CG_UNROLL) {
         // CG_UNROLL loads in flight; positions past the cell repeat its last
         // point, whose second evaluation cannot change the result
@@ -342,6 +331,20 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
         }
       }
       examined += j1 - j0;
+    };
+    // evaluate every point of cell cc unless its box is farther than bd
+    auto visit = [&](int cx, int cy, int cz) {
+      const int cc[3] = {cx, cy, cz};
+      float gap[3];
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        const float clo = (ga[a] > 1 ? glo[a] + (float)cc[a] * cs[a] : glo[a]) - eps[a];
+        const float chi = (ga[a] > 1 ? glo[a] + (float)(cc[a] + 1) * cs[a] : ghi[a]) + eps[a];
+        gap[a] = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
+      }
+      if (sq3(gap[0], gap[1], gap[2]) * (1.f - 0x1p-20f) > bd) return;
+      const uint32_t code = cg_code(cx, cy, cz);
+      scan(cstart[code], cstart[code + 1]);
     };
     // phase 1: Chebyshev rings around the query's cell until a point is found
     int rdone = -1;
@@ -364,7 +367,11 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     }
     // phase 2: the box of cells within the best distance (cell assignment is
     // monotone in each coordinate, so the box holds every point within it);
-    // cells of the rings already walked are skipped
+    // cells of the rings already walked are skipped.  The gap to a cell is
+    // accumulated per axis as the loops descend, so a slab or row whose
+    // partial lower bound already exceeds the best distance is skipped whole
+    // (the bound only grows with more axes; any summation order rounds by a
+    // few u, well inside the 2^-20 margin).
     int blo[3], bhi[3];
     const float rad = __builtin_sqrtf(bd) * (1.f + 0x1p-19f);
 #pragma unroll
@@ -373,13 +380,32 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
       blo[a] = ga[a] > 1 ? cg_axis_cell(qv[a] - ra, glo[a], gs[a]) : 0;
       bhi[a] = ga[a] > 1 ? cg_axis_cell(qv[a] + ra, glo[a], gs[a]) : 0;
     }
-    for (int cz = blo[2]; cz <= bhi[2]; ++cz)
-      for (int cy = blo[1]; cy <= bhi[1]; ++cy)
+    auto gap2 = [&](int a, int c) {
+      const float clo = (ga[a] > 1 ? glo[a] + (float)c * cs[a] : glo[a]) - eps[a];
+      const float chi = (ga[a] > 1 ? glo[a] + (float)(c + 1) * cs[a] : ghi[a]) + eps[a];
+      const float g = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
+      return g * g;
+    };
+    constexpr float keep = 1.f - 0x1p-20f;
+    for (int cz = blo[2]; cz <= bhi[2]; ++cz) {
+      const float gz = gap2(2, cz);
+      if (gz * keep > bd) continue;
+      const uint32_t kz = cg_spread((uint32_t)cz) << 2;
+      const int dz = abs(cz - ci[2]);
+      for (int cy = blo[1]; cy <= bhi[1]; ++cy) {
+        const float gzy = gz + gap2(1, cy);
+        if (gzy * keep > bd) continue;
+        const uint32_t kzy = kz | (cg_spread((uint32_t)cy) << 1);
+        const int dzy = max(dz, abs(cy - ci[1]));
         for (int cx = blo[0]; cx <= bhi[0]; ++cx) {
-          const int cheb = max(abs(cx - ci[0]), max(abs(cy - ci[1]), abs(cz - ci[2])));
-          if (cheb <= rdone) continue;
-          visit(cx, cy, cz);
+          if (max(dzy, abs(cx - ci[0])) <= rdone) continue;
+          if ((gzy + gap2(0, cx)) * keep > bd) continue;
+          const uint32_t code = kzy | cg_spread((uint32_t)cx);
+          const int j0 = cstart[code], j1 = cstart[code + 1];
+          scan(j0, j1);
         }
+      }
+    }
     dout[oq] = bd;
     iout[oq] = bi;
   }
