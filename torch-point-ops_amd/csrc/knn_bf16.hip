@@ -76,7 +76,9 @@ __device__ __forceinline__ void kb_insert(float (&ld)[KC], int (&li)[KC], float 
   li[0] = c[0] ? id : li[0];
 }
 
-template <int KS, int KC>
+// KS k-steps of 16 dims; HALF: D % 16 == 8, so the upper half of the last
+// step lies past D (its operands are zero)
+template <int KS, bool HALF, int KC>
 __global__ __launch_bounds__(256) void knn_bf16_kernel(
     const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb,
@@ -95,6 +97,8 @@ __global__ __launch_bounds__(256) void knn_bf16_kernel(
     Queues q;
     Lists l;
   } sm;
+  // s_bound[w][j]: wave w's bound for query j (see below)
+  __shared__ float s_bound[KB_WAVES][KB_Q];
 
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const int n = lb / nqb, qb = lb - n * nqb;
@@ -125,6 +129,27 @@ __global__ __launch_bounds__(256) void knn_bf16_kernel(
     ld[s] = Lim<float>::inf();
     li[s] = 0x7fffffff;
   }
+  // Shared bound.  The 8 lists of a query (2 lanes x 4 waves) hold disjoint
+  // references, so if each has at least c = ceil(K / 8) entries, 8c >= K of
+  // them are <= the largest of the 8 lists' c-th entries: that value bounds
+  // the query's K-th distance, and a candidate above it can never be among
+  // the K nearest.  One strictly above is dropped; equality is kept so that
+  // the (distance, index) order of ties is unaffected.  Lists only improve,
+  // so an older published value is still a valid bound.
+  if (lane < KB_Q) s_bound[w][lane] = Lim<float>::inf();
+  __syncthreads();
+  const int cth = (K + 7) / 8 - 1;  // 0..3
+  float sb = Lim<float>::inf();
+  auto refresh_bound = [&]() {
+    const float own = cth == 0 ? ld[0] : (cth == 1 ? ld[1] : (cth == 2 ? ld[2] : ld[3]));
+    const float pair = fmaxf(own, __shfl_xor(own, 32));
+    if (h == 0) __hip_atomic_store(&s_bound[w][j], pair, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    float b = pair;
+#pragma unroll
+    for (int v = 0; v < KB_WAVES; ++v)
+      if (v != w) b = fmaxf(b, __hip_atomic_load(&s_bound[v][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    sb = b;
+  };
   int nq_ = 0;  // queued candidates of this lane
   // insert the queue in order: each pass a lane first skips (cheaply) the
   // entries no longer below its list's last one, then inserts its next entry,
@@ -143,19 +168,36 @@ __global__ __launch_bounds__(256) void knn_bf16_kernel(
   };
 
   const int ntiles = (L2 + KB_T - 1) / KB_T;
-  for (int t = w; t < ntiles; t += KB_WAVES) {
-    const int base = t * KB_T;
-    const __bf16* __restrict__ ra = rb + (size_t)min(base + j, L2 - 1) * D;
-    f16v_t acc = {};
+  // Row operand of tile t for this lane: reference base + j, dims 16s + 8h ..
+  // + 7.  Loads are unconditional (row clamped into [0, L2), a half past D
+  // re-reads the step's lower half and is zeroed at use), so they all issue
+  // together; each tile's loads are made one tile ahead.
+  bf8_t an[KS];
+  auto load_rows = [&](int t) {
+    const int r = min(t * KB_T + j, L2 - 1);
+    const __bf16* __restrict__ ra = rb + (size_t)max(r, 0) * D;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const int d0 = 16 * s + 8 * h;
-      const bf8_t a = d0 < D ? *reinterpret_cast<const bf8_t*>(ra + d0) : bf8_t{};
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], acc, 0, 0, 0);
+      const int d0 = (HALF && s == KS - 1) ? 16 * s : 16 * s + 8 * h;
+      an[s] = *reinterpret_cast<const bf8_t*>(ra + d0);
     }
+  };
+  if (w < ntiles) load_rows(w);
+  for (int t = w; t < ntiles; t += KB_WAVES) {
+    const int base = t * KB_T;
+    bf8_t a[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) a[s] = an[s];
+    if constexpr (HALF) a[KS - 1] = h ? bf8_t{} : a[KS - 1];
+    load_rows(t + KB_WAVES);  // the wave's next tile, in flight during this one
+    f16v_t acc = {};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq[s], acc, 0, 0, 0);
+    if ((t & (4 * KB_WAVES - 1)) == w) refresh_bound();  // every 4th tile of the wave
     float dv[16];
     int pc = 0;
-    const float thr = ld[KC - 1];
+    // below the own list's last entry and not above the shared bound
+    const float thr = fminf(ld[KC - 1], sb < Lim<float>::inf() ? __uint_as_float(__float_as_uint(sb) + 1u) : sb);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const float4 r4 = *reinterpret_cast<const float4*>(rr + base + 8 * g + 4 * h);
@@ -233,30 +275,31 @@ bool knn_bf16_supported(int64_t D, int64_t K, int norm) {
   return norm == 2 && D % 8 == 0 && D >= 8 && D <= 128 && K >= 1 && K <= 32;
 }
 
-template <int KS, int KC>
+template <int KS, bool HALF, int KC>
 static void kb_launch(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
                       int N, int P1, int P2, int D, int K, const float* qn, const float* rn,
                       int64_t* idxs, void* dists, hipStream_t s) {
   const int nqb = (P1 + KB_Q - 1) / KB_Q;
-  hipLaunchKernelGGL((knn_bf16_kernel<KS, KC>), dim3(N * nqb), dim3(256), 0, s,
+  hipLaunchKernelGGL((knn_bf16_kernel<KS, HALF, KC>), dim3(N * nqb), dim3(256), 0, s,
                      (const __bf16*)p1, (const __bf16*)p2, l1, l2, P1, P2, D, K, nqb, qn, rn, idxs,
                      (__bf16*)dists);
 }
 
 template <int KC>
-static void kb_dispatch_ks(int ks, const void* p1, const void* p2, const int64_t* l1,
-                           const int64_t* l2, int N, int P1, int P2, int D, int K, const float* qn,
+static void kb_dispatch_ks(int D, const void* p1, const void* p2, const int64_t* l1,
+                           const int64_t* l2, int N, int P1, int P2, int K, const float* qn,
                            const float* rn, int64_t* idxs, void* dists, hipStream_t s) {
-  switch (ks) {
-    case 1: kb_launch<1, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
-    case 2: kb_launch<2, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
-    case 3: kb_launch<3, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
-    case 4: kb_launch<4, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
-    case 5: kb_launch<5, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
-    case 6: kb_launch<6, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
-    case 7: kb_launch<7, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
-    default: kb_launch<8, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+  // D % 8 == 0, 8 <= D <= 128: D / 8 = 2 KS - HALF
+#define KB_CASE(DD, KS_, HALF_) \
+  case DD: kb_launch<KS_, HALF_, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
+  switch (D) {
+    KB_CASE(8, 1, true) KB_CASE(16, 1, false) KB_CASE(24, 2, true) KB_CASE(32, 2, false)
+    KB_CASE(40, 3, true) KB_CASE(48, 3, false) KB_CASE(56, 4, true) KB_CASE(64, 4, false)
+    KB_CASE(72, 5, true) KB_CASE(80, 5, false) KB_CASE(88, 6, true) KB_CASE(96, 6, false)
+    KB_CASE(104, 7, true) KB_CASE(112, 7, false) KB_CASE(120, 8, true)
+    default: kb_launch<8, false, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s); break;
   }
+#undef KB_CASE
 }
 
 void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
@@ -271,9 +314,8 @@ void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const in
   if (r2 > 0)
     hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)std::min<int64_t>((r2 + 255) / 256, 65536)),
                        dim3(256), 0, s, (const __bf16*)p2, r2, kb_pad(P2), (int64_t)P2, D, rn);
-  const int ks = (D + 15) / 16;
-  if (K <= 16) kb_dispatch_ks<16>(ks, p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s);
-  else kb_dispatch_ks<32>(ks, p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, idxs, dists, s);
+  if (K <= 16) kb_dispatch_ks<16>(D, p1, p2, l1, l2, N, P1, P2, K, qn, rn, idxs, dists, s);
+  else kb_dispatch_ks<32>(D, p1, p2, l1, l2, N, P1, P2, K, qn, rn, idxs, dists, s);
 }
 
 }  // namespace tpo
