@@ -73,7 +73,10 @@ def test_argument_errors_are_reported(lib):
     lib.tpo_knn_workspace_size.argtypes = [ctypes.c_int, I, I, I, I, I, ctypes.c_int]
     lib.tpo_knn_workspace_size.restype = I
     assert lib.tpo_knn_workspace_size(0, 8, 16384, 16384, 3, 16, 2) == 8 * 16384 * 4
-    assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 128, 32, 2) == 4 * (4096 + 65536) * 4
+    # bf16: squared norms (float per point), then a partial list of K (d, index)
+    # pairs per query and reference slice (config 5 runs 8 slices)
+    assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 128, 32, 2) == \
+        4 * (4096 + 65536) * 4 + 4 * 4096 * 8 * 32 * 8
     assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 128, 32, 1) == 0  # no bf16 L1 kernel
     assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 130, 32, 2) == 0  # D % 8 != 0
     assert lib.tpo_knn_fwd(3, None, None, None, None, 1, 4, 4, 3, 2, 2, -1, None, None, None,

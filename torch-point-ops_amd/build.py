@@ -44,9 +44,10 @@ HIPCC_FLAGS = [
     f"-I{INCLUDE}",
 ]
 
-# Per-file additions (none at present).
-# fps.hip: its one-lane LDS atomic needs no wave-level pre-reduction
-HIPCC_FILE_FLAGS: dict = {"fps.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
+# fps.hip: its one-lane LDS atomic needs no wave-level pre-reduction.
+# knn_bf16.hip: MFMA results in VGPRs, read by the VALU without AGPR copies.
+HIPCC_FILE_FLAGS: dict = {"fps.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+                          "knn_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd, verbose):

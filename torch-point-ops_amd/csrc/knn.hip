@@ -30,7 +30,7 @@
 
 namespace tpo {
 // knn_bf16.hip
-int64_t knn_bf16_workspace(int64_t N, int64_t P1, int64_t P2);
+int64_t knn_bf16_workspace(int64_t N, int64_t P1, int64_t P2, int64_t K);
 bool knn_bf16_supported(int64_t D, int64_t K, int norm);
 void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
                      int P1, int P2, int D, int K, int64_t* idxs, void* dists, void* ws,
@@ -588,7 +588,7 @@ using namespace tpo;
 extern "C" int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int64_t P2,
                                           int64_t D, int64_t K, int norm) {
   if (N < 0 || P1 < 0 || P2 < 0 || D < 1 || K < 0) return -1;
-  if (dtype == TPO_BF16) return knn_bf16_supported(D, K, norm) ? knn_bf16_workspace(N, P1, P2) : 0;
+  if (dtype == TPO_BF16) return knn_bf16_supported(D, K, norm) ? knn_bf16_workspace(N, P1, P2, K) : 0;
   return ((N * P1 * 4 + 255) / 256) * 256;
 }
 
@@ -611,7 +611,7 @@ extern "C" int tpo_knn_fwd(int dtype, const void* p1, const void* p2, const int6
     if (N == 0 || P1 == 0) return TPO_OK;
     if (((uintptr_t)p1 | (uintptr_t)p2) & 15)
       return set_error(TPO_ERR_ARG, "tpo_knn_fwd: bfloat16 points must be 16-byte aligned");
-    const int64_t need = knn_bf16_workspace(N, P1, P2);
+    const int64_t need = knn_bf16_workspace(N, P1, P2, K);
     if (!workspace || workspace_bytes < need)
       return set_error(TPO_ERR_WORKSPACE, "tpo_knn_fwd: workspace of %lld bytes < %lld",
                        (long long)workspace_bytes, (long long)need);
