@@ -260,10 +260,17 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
     const int64_t* __restrict__ len2, const int32_t* __restrict__ order, int P1, int P2, int D,
     int K, int nqb, int pad_sentinel, int sorted2, int64_t* __restrict__ idxs,
     T* __restrict__ dists) {
+  // float D=3: reference points reach the lanes through a wave-private LDS
+  // block (each lane stages one, every lane reads them back as broadcasts),
+  // so the whole wave takes part in every chunk; lanes without a query run
+  // along with a dummy one and an empty candidate threshold
+  constexpr bool STAGED = DT == 3 && sizeof(T) == 4;
+  __shared__ float4 s_ref[STAGED ? 4 : 1][64];
   const int n = blockIdx.x / nqb;
   const int i = (blockIdx.x - n * nqb) * 256 + threadIdx.x;  // position in processing order
-  if (i >= P1) return;
-  const int q = order ? order[(size_t)n * P1 + i] : i;  // query row handled by this lane
+  const bool in_range = i < P1;
+  if (!STAGED && !in_range) return;
+  const int q = in_range ? (order ? order[(size_t)n * P1 + i] : i) : 0;  // query row of this lane
   int64_t l1 = len1[n], l2 = len2[n];
   l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
   l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
@@ -271,13 +278,14 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
   const size_t row = (size_t)n * P1 + q;
   int64_t* __restrict__ io = idxs + row * K;
   T* __restrict__ dout = dists + row * K;
-  if (q >= l1) {  // never written by the reference: its zeros
+  const bool act = in_range && q < l1;
+  if (in_range && !act) {  // never written by the reference: its zeros
     for (int s = 0; s < K; ++s) {
       io[s] = 0;
       dout[s] = (T)0;
     }
-    return;
   }
+  if (!STAGED && !act) return;
   const int Dd = DT > 0 ? DT : D;
   const T* __restrict__ qp = p1 + row * Dd;
   const T* __restrict__ rp = p2 + (size_t)n * P2 * Dd;
@@ -333,13 +341,43 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
       T thr;
       int ms;
       first_max<T, KC>(sd, K, thr, ms);
+      if (!act) thr = -Lim<T>::inf();  // a lane without a query has no candidates
+      // STAGED: references j0 .. j0 + 63 of a 64-reference stage sit in
+      // s_ref[wave]; each lane's next one is loaded a stage ahead
+      const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+      float pf[3] = {0.f, 0.f, 0.f};
+      auto prefetch = [&](int jb) {
+        if constexpr (STAGED) {
+          const T* __restrict__ r = rp + (size_t)min(jb + ln, L2 - 1) * 3;
+          pf[0] = (float)r[0];
+          pf[1] = (float)r[1];
+          pf[2] = (float)r[2];
+        }
+      };
+      prefetch(K);
       for (int j0 = K; j0 < L2; j0 += KNN_CHUNK) {
         const int cn = min(KNN_CHUNK, L2 - j0);
+        const int ph = (j0 - K) & 63;  // position of the chunk in its stage
+        if constexpr (STAGED) {
+          if (ph == 0) {  // the wave's previous reads of s_ref[wv] precede this write
+            s_ref[wv][ln] = make_float4(pf[0], pf[1], pf[2], 0.f);
+            __builtin_amdgcn_wave_barrier();
+            prefetch(j0 + 64);
+          }
+        }
         // distances of the chunk stay in registers; bit (cn-1-c) of mask
         // flags reference j0+c as a candidate against the current maximum
         T dch[KNN_CHUNK];
         uint32_t mask = 0;
-        if (cn == KNN_CHUNK) {
+        if (STAGED && cn == KNN_CHUNK) {
+#pragma unroll
+          for (int c = 0; c < KNN_CHUNK; ++c) {
+            const float4 r4 = s_ref[STAGED ? wv : 0][ph + c];
+            const T rv[3] = {(T)r4.x, (T)r4.y, (T)r4.z};
+            dch[c] = knn_dist<T, DT, NORM>(qr, qp, rv, D);
+            mask = push_lt(mask, dch[c], thr);
+          }
+        } else if (cn == KNN_CHUNK) {
 #pragma unroll
           for (int c = 0; c < KNN_CHUNK; ++c) {
             const T* __restrict__ r = rp + (size_t)(j0 + c) * Dd;
@@ -381,6 +419,7 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
       }
     }
   }
+  if (!act) return;
   const int64_t pad_i = pad_sentinel ? -1 : 0;
   const T pad_d = pad_sentinel ? Lim<T>::inf() : (T)0;
 #pragma unroll
