@@ -482,6 +482,8 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
       }
     };
     if (tm) {
+      // the visiting waves set the barrier's arrival: let them issue first
+      __builtin_amdgcn_s_setprio(3);
       while (tm) {
         const int nt = __builtin_popcountll(tm);
         if (nt == 1) visit(std::integral_constant<int, 1>{});
@@ -489,6 +491,7 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
         else visit(std::integral_constant<int, 4>{});
       }
       reach = reach_of(bbest);
+      __builtin_amdgcn_s_setprio(0);
     }
     if (rereduce) {  // the wave's best bucket changed; otherwise wbest stands
       wbest = wave_best_at(bbest, wlane);
