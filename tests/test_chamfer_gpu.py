@@ -355,6 +355,19 @@ def test_gradients_vs_torch_reference(tpo, dev, B, N, M):
     assert torch.allclose(ga, ra, atol=1e-4) and torch.allclose(gb, rb, atol=1e-4)
 
 
+@pytest.mark.parametrize("which", [1, 2])
+def test_gradient_through_one_output(tpo, dev, which):
+    # the other distance output (and both index outputs) get no gradient
+    g = torch.Generator().manual_seed(40 + which)
+    p1 = torch.randn(2, 37, 3, generator=g).to(dev).requires_grad_(True)
+    p2 = torch.randn(2, 29, 3, generator=g).to(dev).requires_grad_(True)
+    d1, d2 = tpo.chamfer_distance(p1, p2)
+    ga, gb = torch.autograd.grad((d1 if which == 1 else d2).sum(), (p1, p2))
+    r1, r2 = torch_reference(p1, p2)
+    ra, rb = torch.autograd.grad((r1 if which == 1 else r2).sum(), (p1, p2))
+    assert torch.allclose(ga, ra, atol=1e-4) and torch.allclose(gb, rb, atol=1e-4)
+
+
 def test_gradcheck_float64(tpo, dev):
     g = torch.Generator().manual_seed(5)
     p1 = torch.randn(1, 4, 3, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)

@@ -10,8 +10,16 @@ from .. import _C  # noqa: F401
 
 
 def _chamfer_backward(ctx, grad_dist1, grad_dist2, grad_idx1, grad_idx2):
-    # index outputs carry no gradient (reference chamfer/__init__.py:6-11)
+    # index outputs carry no gradient (reference chamfer/__init__.py:6-11);
+    # gradients are not materialised, so an unused distance output arrives
+    # as None and counts as zeros
     xyz1, xyz2, idx1, idx2 = ctx.saved_tensors
+    if grad_dist1 is None and grad_dist2 is None:
+        return None, None
+    if grad_dist1 is None:
+        grad_dist1 = torch.zeros(idx1.shape, dtype=xyz1.dtype, device=xyz1.device)
+    if grad_dist2 is None:
+        grad_dist2 = torch.zeros(idx2.shape, dtype=xyz2.dtype, device=xyz2.device)
     return torch.ops.torch_point_ops_chamfer.chamfer_backward(
         xyz1, xyz2, idx1, idx2, grad_dist1, grad_dist2
     )
@@ -21,6 +29,7 @@ def _chamfer_setup_context(ctx, inputs, output):
     xyz1, xyz2 = inputs
     _d1, _d2, idx1, idx2 = output
     ctx.save_for_backward(xyz1, xyz2, idx1, idx2)
+    ctx.set_materialize_grads(False)  # no zero tensors for the index outputs
 
 
 torch.library.register_autograd(

@@ -11,6 +11,8 @@ from .. import _C  # noqa: F401
 
 def _knn_backward(ctx, grad_idxs, grad_dists):
     p1, p2, lengths1, lengths2, idxs = ctx.saved_tensors
+    if grad_dists is None:  # gradients are not materialised: the index output has none
+        return None, None, None, None, None, None, None
     grad_p1, grad_p2 = torch.ops.torch_point_ops_knn.knn_backward(
         p1, p2, lengths1, lengths2, idxs, ctx.norm, grad_dists
     )
@@ -23,6 +25,7 @@ def _knn_setup_context(ctx, inputs, output):
     idxs, _dists = output
     ctx.save_for_backward(p1, p2, lengths1, lengths2, idxs)
     ctx.norm = norm
+    ctx.set_materialize_grads(False)  # no zero tensor for the index output
 
 
 torch.library.register_autograd(
