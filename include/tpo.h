@@ -92,6 +92,37 @@ int tpo_chamfer_bwd(int dtype, const void* xyz1, const void* xyz2,
                     void* grad_xyz1, void* grad_xyz2, void* stream);
 
 /*
+ * Chamfer loss: ChamferDistance(reduction="mean" / "sum")
+ * (torch_point_ops/chamfer/chamfer.py:18-24) in one forward and one
+ * backward call.  No single counterpart in the reference, which reduces
+ * chamfer_forward's distances with torch.mean / torch.sum; these entry points
+ * fuse that reduction into the forward and the reduction's gradient into the
+ * backward.
+ *   loss (one element of `dtype`): mean != 0: mean(dist1) + mean(dist2)
+ *     (NaN when a cloud is empty, like torch.mean); mean == 0: sum + sum.
+ *     The sums are taken in a fixed order, so the loss is deterministic; it
+ *     matches torch's reduction of tpo_chamfer_fwd's distances to rounding.
+ *   idx1, idx2 as tpo_chamfer_fwd (the backward needs them); the distances
+ *   themselves are not stored.
+ *   workspace (required): tpo_chamfer_loss_workspace_size() bytes, 256-byte
+ *   aligned, contents need not be initialised.
+ * tpo_chamfer_loss_bwd: grad_loss is ONE device element of `dtype`; the
+ *   gradients equal tpo_chamfer_bwd's with grad_dist = grad_loss / numel
+ *   (mean, multiplied by the reciprocal as torch's MeanBackward does) or
+ *   grad_loss (sum) for every point.
+ */
+int64_t tpo_chamfer_loss_workspace_size(int dtype, int64_t B, int64_t N, int64_t M);
+int tpo_chamfer_loss_fwd(int dtype, const void* xyz1, const void* xyz2,
+                         int64_t B, int64_t N, int64_t M, int mean, void* loss,
+                         int32_t* idx1, int32_t* idx2,
+                         void* workspace, int64_t workspace_bytes, void* stream);
+int tpo_chamfer_loss_bwd(int dtype, const void* xyz1, const void* xyz2,
+                         const int32_t* idx1, const int32_t* idx2,
+                         const void* grad_loss, int mean,
+                         int64_t B, int64_t N, int64_t M,
+                         void* grad_xyz1, void* grad_xyz2, void* stream);
+
+/*
  * KNN forward.  Replaces knn_cuda_forward
  * (torch_point_ops/knn/csrc/cuda/knn.cu:295-398),
  * torch_point_ops_knn::knn_forward (knn.cpp:168-169).

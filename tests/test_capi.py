@@ -68,6 +68,25 @@ def test_argument_errors_are_reported(lib):
     assert lib.tpo_chamfer_workspace_size(0, 2, 100, 8192) == 0    # too small to prune
     assert lib.tpo_chamfer_workspace_size(1, 32, 8192, 8192) == 0  # float only
     assert lib.tpo_chamfer_workspace_size(0, -1, 3, 3) == -1
+    # fused module loss: the forward's workspace (grid search or none), both
+    # distance arrays, 2 x 256 chunk sums (doubles); 256-byte regions
+    lib.tpo_chamfer_loss_workspace_size.argtypes = [ctypes.c_int, I, I, I]
+    lib.tpo_chamfer_loss_workspace_size.restype = I
+    assert lib.tpo_chamfer_loss_workspace_size(0, 32, 8192, 8192) == \
+        lib.tpo_chamfer_workspace_size(0, 32, 8192, 8192) + 2 * 32 * 8192 * 4 + 4096
+    # double: dist1 1600 -> 1792 bytes (256-byte regions), dist2 1024, chunk sums 4096
+    assert lib.tpo_chamfer_loss_workspace_size(1, 2, 100, 64) == 1792 + 1024 + 4096
+    assert lib.tpo_chamfer_loss_workspace_size(9, 2, 100, 64) == -1
+    lib.tpo_chamfer_loss_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, ctypes.c_int, P, P, P, P,
+                                         I, P]
+    fake = ctypes.c_void_p(4096)  # never dereferenced: the calls fail their checks first
+    assert lib.tpo_chamfer_loss_fwd(0, fake, fake, 2, 8, 8, 1, None, fake, fake, fake, 1 << 20,
+                                    None) == -1  # no loss output
+    assert lib.tpo_chamfer_loss_fwd(0, fake, fake, 2, 8, 8, 1, fake, fake, fake, None, 0,
+                                    None) == -4  # no workspace
+    assert b"workspace" in lib.tpo_last_error()
+    assert lib.tpo_chamfer_loss_fwd(5, fake, fake, 2, 8, 8, 1, fake, fake, fake, fake, 1 << 20,
+                                    None) == -2  # dtype
     lib.tpo_chamfer_pairs_evaluated.argtypes = [ctypes.c_int, P, I, I, I, P, P]
     assert lib.tpo_chamfer_pairs_evaluated(0, None, 2, 4096, 4096, None, None) == -1
     lib.tpo_knn_workspace_size.argtypes = [ctypes.c_int, I, I, I, I, I, ctypes.c_int]

@@ -368,6 +368,52 @@ def test_gradient_through_one_output(tpo, dev, which):
     assert torch.allclose(ga, ra, atol=1e-4) and torch.allclose(gb, rb, atol=1e-4)
 
 
+@pytest.mark.parametrize("red", ["mean", "sum"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
+@pytest.mark.parametrize("shape", [(2, 37, 29), (3, 3000, 2500), (1, 0, 5), (0, 4, 4)])
+def test_module_loss_matches_unfused_reduction(tpo, dev, red, dtype, shape):
+    # ChamferDistance(reduction) reduces inside the kernels; the reference
+    # module reduces chamfer_forward's distances with torch (chamfer.py:18-24)
+    B, N, M = shape
+    g = torch.Generator().manual_seed(50 + N)
+    p1 = torch.randn(B, N, 3, generator=g).to(dev, dtype)
+    p2 = (torch.randn(B, M, 3, generator=g) * 1.5).to(dev, dtype)
+    a, b = p1.clone().requires_grad_(True), p2.clone().requires_grad_(True)
+    loss = tpo.ChamferDistance(red)(a, b)
+    d1, d2 = tpo.chamfer_distance(p1, p2)
+    ref = d1.mean() + d2.mean() if red == "mean" else d1.sum() + d2.sum()
+    assert loss.dtype == dtype and loss.shape == ()
+    rtol = {torch.float32: 1e-5, torch.float64: 1e-12, torch.float16: 2e-3}[dtype]
+    assert torch.allclose(loss, ref, rtol=rtol, atol=0, equal_nan=True), (loss, ref)
+    assert torch.equal(loss, tpo.ChamferDistance(red)(p1, p2)) or torch.isnan(loss)
+    if B * (N + M) == 0:
+        return
+    ga, gb = torch.autograd.grad(loss, (a, b))
+    a2, b2 = p1.clone().requires_grad_(True), p2.clone().requires_grad_(True)
+    e1, e2 = tpo.chamfer_distance(a2, b2)
+    r = e1.mean() + e2.mean() if red == "mean" else e1.sum() + e2.sum()
+    ra, rb = torch.autograd.grad(r, (a2, b2))
+    # same per-point gradient, same kernel: equal up to the order of atomic sums
+    gtol = 1e-2 if dtype == torch.float16 else 1e-6
+    for got, want in ((ga, ra), (gb, rb)):
+        assert got.shape == want.shape
+        if want.numel() == 0:
+            continue
+        scale = max(want.abs().max().item(), 1e-30)
+        assert (got - want).abs().max().item() <= gtol * scale
+
+
+def test_module_loss_at_headline_size(tpo, dev):
+    # many search workgroups on every XCD feed the last-workgroup reduction
+    p1, p2 = (t.to(dev) for t in workloads.chamfer_c2(B=8))
+    loss = tpo.ChamferDistance("mean")(p1, p2)
+    d1, d2 = tpo.chamfer_distance(p1, p2)
+    e1 = d1.double().mean() + d2.double().mean()
+    assert abs(loss.item() - e1.item()) <= 1e-5 * abs(e1.item())
+    for _ in range(3):
+        assert torch.equal(loss, tpo.ChamferDistance("mean")(p1, p2))
+
+
 def test_gradcheck_float64(tpo, dev):
     g = torch.Generator().manual_seed(5)
     p1 = torch.randn(1, 4, 3, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
@@ -390,6 +436,10 @@ def test_opcheck_and_compile(tpo, dev):
     p2 = torch.randn(1, 3, 3, generator=g).to(dev)
     opcheck(torch.ops.torch_point_ops_chamfer.chamfer_forward.default, (p1, p2),
             raise_exception=True)
+    for mean in (True, False):
+        opcheck(torch.ops.torch_point_ops_chamfer.chamfer_loss_forward.default,
+                (p1.clone().requires_grad_(True), p2.clone().requires_grad_(True), mean),
+                raise_exception=True)
     model = tpo.ChamferDistance().to(dev)
     a = torch.randn(1, 64, 3, generator=g).to(dev)
     b = torch.randn(1, 128, 3, generator=g).to(dev)

@@ -387,14 +387,30 @@ __global__ __launch_bounds__(256) void chamfer_fwd_filter_kernel(
 }
 
 // ---------------------------------------------------------------- backward
+// Upstream gradient of one cloud's distances: one value per point, or (the
+// loss entry points) the loss gradient spread over every point the way
+// torch's autograd does it for the module's reduction -- MeanBackward
+// multiplies by 1 / numel in the accumulation type, SumBackward copies.
+template <typename T>
+struct PointGrad {
+  const T* __restrict__ p;  // per point, or the single loss gradient
+  int64_t count;            // 0: per point; > 0: mean over count points; < 0: sum
+  __device__ __forceinline__ bool uniform() const { return count != 0; }
+  __device__ __forceinline__ T spread() const {  // the per-point value (uniform only)
+    using A = typename std::conditional<sizeof(T) == 8, double, float>::type;
+    return count > 0 ? (T)((A)p[0] * ((A)1 / (A)count)) : p[0];
+  }
+};
+
 // Pass 1: grad_q[i] = g (q_i - r_idx[i]) with g = 2 grad_dist[i] (in dtype);
 // every element of both outputs is written here.
 template <typename T>
 __global__ __launch_bounds__(256) void chamfer_bwd_direct_kernel(
     const T* __restrict__ xyz1, const T* __restrict__ xyz2, const int32_t* __restrict__ idx1,
-    const int32_t* __restrict__ idx2, const T* __restrict__ gd1, const T* __restrict__ gd2,
-    int64_t B, int64_t N, int64_t M, T* __restrict__ g1, T* __restrict__ g2) {
+    const int32_t* __restrict__ idx2, PointGrad<T> gd1, PointGrad<T> gd2, int64_t B, int64_t N,
+    int64_t M, T* __restrict__ g1, T* __restrict__ g2) {
   const int64_t n1 = B * N, total = n1 + B * M;
+  const T u1 = gd1.uniform() ? gd1.spread() : (T)0, u2 = gd2.uniform() ? gd2.spread() : (T)0;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
     const bool dir = t >= n1;
@@ -407,7 +423,8 @@ __global__ __launch_bounds__(256) void chamfer_bwd_direct_kernel(
     T* go = dir ? g2 : g1;
     T cx = (T)0, cy = (T)0, cz = (T)0;
     if (j2 >= 0 && j2 < nr) {
-      const T g = (T)((dir ? gd2 : gd1)[u] * (T)2);
+      const PointGrad<T> gd = dir ? gd2 : gd1;
+      const T g = (T)((gd.uniform() ? (dir ? u2 : u1) : gd.p[u]) * (T)2);
       const int64_t ro = (b * nr + j2) * 3;
       cx = (T)(g * (T)(q[3 * u] - r[ro]));
       cy = (T)(g * (T)(q[3 * u + 1] - r[ro + 1]));
@@ -423,9 +440,10 @@ __global__ __launch_bounds__(256) void chamfer_bwd_direct_kernel(
 template <typename T>
 __global__ __launch_bounds__(256) void chamfer_bwd_scatter_kernel(
     const T* __restrict__ xyz1, const T* __restrict__ xyz2, const int32_t* __restrict__ idx1,
-    const int32_t* __restrict__ idx2, const T* __restrict__ gd1, const T* __restrict__ gd2,
-    int64_t B, int64_t N, int64_t M, T* __restrict__ g1, T* __restrict__ g2) {
+    const int32_t* __restrict__ idx2, PointGrad<T> gd1, PointGrad<T> gd2, int64_t B, int64_t N,
+    int64_t M, T* __restrict__ g1, T* __restrict__ g2) {
   const int64_t n1 = B * N, total = n1 + B * M;
+  const T u1 = gd1.uniform() ? gd1.spread() : (T)0, u2 = gd2.uniform() ? gd2.spread() : (T)0;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
     const bool dir = t >= n1;
@@ -437,7 +455,8 @@ __global__ __launch_bounds__(256) void chamfer_bwd_scatter_kernel(
     const int64_t j2 = (dir ? idx2 : idx1)[u];
     if (j2 < 0 || j2 >= nr) continue;
     T* gr = dir ? g1 : g2;
-    const T g = (T)((dir ? gd2 : gd1)[u] * (T)2);
+    const PointGrad<T> gd = dir ? gd2 : gd1;
+    const T g = (T)((gd.uniform() ? (dir ? u2 : u1) : gd.p[u]) * (T)2);
     const int64_t ro = (b * nr + j2) * 3;
     atomic_add(gr + ro, (T)(-(T)(g * (T)(q[3 * u] - r[ro]))));
     atomic_add(gr + ro + 1, (T)(-(T)(g * (T)(q[3 * u + 1] - r[ro + 1]))));
@@ -455,8 +474,8 @@ constexpr int CH_BWD_MAX_SLICES = 16;   // beyond this the 2-pass path is cheape
 template <typename T>
 __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
     const T* __restrict__ xyz1, const T* __restrict__ xyz2, const int32_t* __restrict__ idx1,
-    const int32_t* __restrict__ idx2, const T* __restrict__ gd1, const T* __restrict__ gd2, int N,
-    int M, int S, T* __restrict__ g1, T* __restrict__ g2) {
+    const int32_t* __restrict__ idx2, PointGrad<T> gd1, PointGrad<T> gd2, int N, int M, int S,
+    T* __restrict__ g1, T* __restrict__ g2) {
   extern __shared__ float acc[];
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const int sl = lb % S;
@@ -469,8 +488,11 @@ __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
   const T* __restrict__ oth = (c ? xyz1 : xyz2) + (size_t)b * n_oth * 3;
   const int32_t* __restrict__ idx_own = (c ? idx2 : idx1) + (size_t)b * n_own;
   const int32_t* __restrict__ idx_oth = (c ? idx1 : idx2) + (size_t)b * n_oth;
-  const T* __restrict__ gd_own = (c ? gd2 : gd1) + (size_t)b * n_own;
-  const T* __restrict__ gd_oth = (c ? gd1 : gd2) + (size_t)b * n_oth;
+  const PointGrad<T> pg_own = c ? gd2 : gd1, pg_oth = c ? gd1 : gd2;
+  const bool uni_own = pg_own.uniform(), uni_oth = pg_oth.uniform();
+  const T u_own = uni_own ? pg_own.spread() : (T)0, u_oth = uni_oth ? pg_oth.spread() : (T)0;
+  const T* __restrict__ gd_own = pg_own.p + (uni_own ? 0 : (size_t)b * n_own);
+  const T* __restrict__ gd_oth = pg_oth.p + (uni_oth ? 0 : (size_t)b * n_oth);
   T* __restrict__ out = (c ? g2 : g1) + (size_t)b * n_own * 3;
 
   for (int i = threadIdx.x; i < 3 * (hi - lo); i += 256) acc[i] = 0.f;
@@ -480,7 +502,7 @@ __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
   for (int j = threadIdx.x; j < n_oth; j += 256) {
     const int i = idx_oth[j];
     if (i < lo || i >= hi) continue;
-    const T g = (T)(gd_oth[j] * (T)2);
+    const T g = (T)((uni_oth ? u_oth : gd_oth[j]) * (T)2);
 #pragma unroll
     for (int k = 0; k < 3; ++k)
       atomicAdd(&acc[3 * (i - lo) + k], -(float)(T)(g * (T)(oth[3 * j + k] - own[3 * i + k])));
@@ -490,7 +512,7 @@ __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
   for (int i = lo + threadIdx.x; i < hi; i += 256) {
     const int j2 = idx_own[i];
     const bool ok = j2 >= 0 && j2 < n_oth;
-    const T g = (T)(gd_own[i] * (T)2);
+    const T g = (T)((uni_own ? u_own : gd_own[i]) * (T)2);
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
       const T d = ok ? (T)(g * (T)(own[3 * i + k] - oth[3 * j2 + k])) : (T)0;
@@ -541,9 +563,11 @@ static void fwd_dispatch(const void* x1, const void* x2, int B, int N, int M, vo
 template <typename T>
 static void bwd_dispatch(const void* x1, const void* x2, const int32_t* i1, const int32_t* i2,
                          const void* gd1, const void* gd2, int64_t B, int64_t N, int64_t M,
-                         void* g1, void* g2, hipStream_t s) {
+                         void* g1, void* g2, hipStream_t s, int64_t count1 = 0,
+                         int64_t count2 = 0) {
   const int64_t total = B * (N + M);
   if (total == 0) return;
+  const PointGrad<T> pg1{(const T*)gd1, count1}, pg2{(const T*)gd2, count2};
   if (sizeof(T) <= 4) {
     // slices: enough for one cloud's slice to fit LDS and for ~512 workgroups
     const int64_t nmax = std::max(N, M);
@@ -554,17 +578,115 @@ static void bwd_dispatch(const void* x1, const void* x2, const int32_t* i1, cons
       const int64_t span = (nmax + S - 1) / S;
       hipLaunchKernelGGL(chamfer_bwd_fused_kernel<T>, dim3((unsigned)(2 * B * S)), dim3(256),
                          (size_t)(3 * span * sizeof(float)), s, (const T*)x1, (const T*)x2, i1, i2,
-                         (const T*)gd1, (const T*)gd2, (int)N, (int)M, (int)S, (T*)g1, (T*)g2);
+                         pg1, pg2, (int)N, (int)M, (int)S, (T*)g1, (T*)g2);
       return;
     }
   }
   const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
   hipLaunchKernelGGL(chamfer_bwd_direct_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s,
-                     (const T*)x1, (const T*)x2, i1, i2, (const T*)gd1, (const T*)gd2, B, N, M,
-                     (T*)g1, (T*)g2);
+                     (const T*)x1, (const T*)x2, i1, i2, pg1, pg2, B, N, M, (T*)g1, (T*)g2);
   hipLaunchKernelGGL(chamfer_bwd_scatter_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s,
-                     (const T*)x1, (const T*)x2, i1, i2, (const T*)gd1, (const T*)gd2, B, N, M,
-                     (T*)g1, (T*)g2);
+                     (const T*)x1, (const T*)x2, i1, i2, pg1, pg2, B, N, M, (T*)g1, (T*)g2);
+}
+
+// ------------------------------------------------------------------- loss
+// The module's reduction (tpo_chamfer_loss_fwd): the forward stores both
+// distance arrays in the workspace, chamfer_loss_part_kernel sums fixed
+// chunks of them in original point order and chamfer_loss_final_kernel adds
+// the chunk sums in a fixed order, so the loss does not depend on how the
+// forward scheduled its queries.  (A reduction inside the grid search, one
+// sum per wave, would follow the search's query order, which the sort's
+// arrival-order ranks make nondeterministic; and publishing those sums to a
+// last workgroup needs a device-scope release per workgroup, an L2 writeback
+// that evicts the reference points the other workgroups are reading.)
+constexpr int CH_LOSS_PARTS = 256;       // chunks per array, at most
+constexpr int64_t CH_LOSS_CHUNK = 2048;  // elements per chunk, at least
+
+static int64_t loss_parts(int64_t n) {
+  return std::min<int64_t>((n + CH_LOSS_CHUNK - 1) / CH_LOSS_CHUNK, CH_LOSS_PARTS);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void chamfer_loss_part_kernel(const T* __restrict__ d1,
+                                                                const T* __restrict__ d2,
+                                                                int64_t n1, int64_t n2, int p1,
+                                                                int p2, double* __restrict__ part) {
+  using A = typename std::conditional<sizeof(T) == 8, double, float>::type;
+  __shared__ A s_red[4];
+  const int k = blockIdx.x;
+  const bool second = k >= p1;
+  const T* d = second ? d2 : d1;
+  const int64_t n = second ? n2 : n1;
+  const int np = second ? p2 : p1, kk = second ? k - p1 : k;
+  const int64_t chunk = (n + np - 1) / np;
+  const int64_t lo = kk * chunk < n ? kk * chunk : n, hi = lo + chunk < n ? lo + chunk : n;
+  A a = (A)0;
+#pragma unroll 8
+  for (int64_t i = lo + threadIdx.x; i < hi; i += 256) a += (A)d[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = a;
+  __syncthreads();
+  if (threadIdx.x == 0) part[k] = (double)(((s_red[0] + s_red[1]) + s_red[2]) + s_red[3]);
+}
+
+// Loss from the chunk sums: parts [0, p1) sum dist1, [p1, p1 + p2) dist2.
+// Thread 0 writes, as torch.mean / torch.sum of each array followed by
+// their sum (chamfer.py:20-23; torch's mean scales the accumulated sum by
+// 1 / numel in the accumulation type, and an empty array's mean is NaN):
+//   mean: (T)(S1 * (1 / count1)) + (T)(S2 * (1 / count2))
+//   sum:  (T)S1 + (T)S2
+template <typename T>
+__global__ __launch_bounds__(64) void chamfer_loss_final_kernel(const double* __restrict__ part,
+                                                                int p1, int p2, int mean,
+                                                                int64_t count1, int64_t count2,
+                                                                T* __restrict__ loss) {
+  using A = typename std::conditional<sizeof(T) == 8, double, float>::type;
+  A a1 = (A)0, a2 = (A)0;
+  for (int k = threadIdx.x; k < p1; k += 64) a1 += (A)part[k];
+  for (int k = threadIdx.x; k < p2; k += 64) a2 += (A)part[p1 + k];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    a1 += __shfl_xor(a1, o);
+    a2 += __shfl_xor(a2, o);
+  }
+  if (threadIdx.x == 0) {
+    if (mean) {
+      a1 *= (A)1 / (A)count1;
+      a2 *= (A)1 / (A)count2;
+    }
+    loss[0] = (T)((A)(T)a1 + (A)(T)a2);
+  }
+}
+
+// Workspace of tpo_chamfer_loss_fwd: [forward workspace][dist1][dist2][chunk sums].
+struct LossLayout {
+  int64_t fwd, d1, d2, part, total;
+};
+
+static LossLayout loss_layout(int64_t fwd_bytes, int64_t esize, int64_t B, int64_t N, int64_t M) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  LossLayout L;
+  L.fwd = 0;
+  L.d1 = up(fwd_bytes);
+  L.d2 = L.d1 + up(B * N * esize);
+  L.part = L.d2 + up(B * M * esize);
+  L.total = L.part + up(2 * CH_LOSS_PARTS * 8);
+  return L;
+}
+
+template <typename T>
+static void loss_reduce(const LossLayout& L, char* ws, int64_t B, int64_t N, int64_t M, int mean,
+                        void* loss, hipStream_t s) {
+  const T* d1 = (const T*)(ws + L.d1);
+  const T* d2 = (const T*)(ws + L.d2);
+  double* part = (double*)(ws + L.part);
+  const int p1 = (int)loss_parts(B * N), p2 = (int)loss_parts(B * M);
+  if (p1 + p2 > 0)
+    hipLaunchKernelGGL(chamfer_loss_part_kernel<T>, dim3(p1 + p2), dim3(256), 0, s, d1, d2, B * N,
+                       B * M, p1, p2, part);
+  hipLaunchKernelGGL(chamfer_loss_final_kernel<T>, dim3(1), dim3(64), 0, s, part, p1, p2, mean,
+                     B * N, B * M, (T*)loss);
 }
 
 }  // namespace tpo
@@ -634,4 +756,76 @@ extern "C" int tpo_chamfer_bwd(int dtype, const void* xyz1, const void* xyz2,
     default: return set_error(TPO_ERR_DTYPE, "tpo_chamfer_bwd: unsupported dtype %d", dtype);
   }
   return check_launch("tpo_chamfer_bwd");
+}
+
+static int64_t esize_of(int dtype) {
+  return dtype == TPO_F32 ? 4 : dtype == TPO_F64 ? 8 : dtype == TPO_F16 ? 2 : -1;
+}
+
+static LossLayout loss_layout_for(int dtype, int64_t B, int64_t N, int64_t M) {
+  const int64_t fwd = prune_applies(dtype, B, N, M) ? chamfer_prune_workspace(B, N, M) : 0;
+  return loss_layout(fwd, esize_of(dtype), B, N, M);
+}
+
+extern "C" int64_t tpo_chamfer_loss_workspace_size(int dtype, int64_t B, int64_t N, int64_t M) {
+  if (B < 0 || N < 0 || M < 0 || esize_of(dtype) < 0) return -1;
+  return loss_layout_for(dtype, B, N, M).total;
+}
+
+extern "C" int tpo_chamfer_loss_fwd(int dtype, const void* xyz1, const void* xyz2, int64_t B,
+                                    int64_t N, int64_t M, int mean, void* loss, int32_t* idx1,
+                                    int32_t* idx2, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
+  if (B < 0 || N < 0 || M < 0 || N >= (1 << 28) || M >= (1 << 28) ||
+      B * (N + M) >= ((int64_t)1 << 31))
+    return set_error(TPO_ERR_ARG, "tpo_chamfer_loss_fwd: bad sizes B=%lld N=%lld M=%lld",
+                     (long long)B, (long long)N, (long long)M);
+  if (!loss || (B > 0 && ((N > 0 && (!xyz1 || !idx1)) || (M > 0 && (!xyz2 || !idx2)))))
+    return set_error(TPO_ERR_ARG, "tpo_chamfer_loss_fwd: null pointer");
+  if (esize_of(dtype) < 0)
+    return set_error(TPO_ERR_DTYPE, "tpo_chamfer_loss_fwd: unsupported dtype %d", dtype);
+  const LossLayout L = loss_layout_for(dtype, B, N, M);
+  if (!workspace || workspace_bytes < L.total)
+    return set_error(TPO_ERR_WORKSPACE, "tpo_chamfer_loss_fwd: workspace of %lld bytes < %lld",
+                     (long long)(workspace ? workspace_bytes : 0), (long long)L.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)workspace;
+  void* d1 = w + L.d1;
+  void* d2 = w + L.d2;
+  if (B > 0 && N + M > 0) {
+    if (prune_applies(dtype, B, N, M))
+      launch_chamfer_fwd_prune(xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2, w + L.fwd,
+                               s);
+    else if (dtype == TPO_F32)
+      fwd_dispatch<float>(xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2, s);
+    else if (dtype == TPO_F64)
+      fwd_dispatch<double>(xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2, s);
+    else
+      fwd_dispatch<half_t>(xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2, s);
+  }
+  switch (dtype) {
+    case TPO_F32: loss_reduce<float>(L, w, B, N, M, mean != 0, loss, s); break;
+    case TPO_F64: loss_reduce<double>(L, w, B, N, M, mean != 0, loss, s); break;
+    case TPO_F16: loss_reduce<half_t>(L, w, B, N, M, mean != 0, loss, s); break;
+  }
+  return check_launch("tpo_chamfer_loss_fwd");
+}
+
+extern "C" int tpo_chamfer_loss_bwd(int dtype, const void* xyz1, const void* xyz2,
+                                    const int32_t* idx1, const int32_t* idx2,
+                                    const void* grad_loss, int mean, int64_t B, int64_t N,
+                                    int64_t M, void* gxyz1, void* gxyz2, void* stream) {
+  if (B < 0 || N < 0 || M < 0 || B * (N + M) >= ((int64_t)1 << 40))
+    return set_error(TPO_ERR_ARG, "tpo_chamfer_loss_bwd: bad sizes");
+  if (B == 0 || (N == 0 && M == 0)) return TPO_OK;
+  if (!grad_loss) return set_error(TPO_ERR_ARG, "tpo_chamfer_loss_bwd: null grad_loss");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t c1 = mean ? B * N : -1, c2 = mean ? B * M : -1;
+  switch (dtype) {
+    case TPO_F32: bwd_dispatch<float>(xyz1, xyz2, idx1, idx2, grad_loss, grad_loss, B, N, M, gxyz1, gxyz2, s, c1, c2); break;
+    case TPO_F64: bwd_dispatch<double>(xyz1, xyz2, idx1, idx2, grad_loss, grad_loss, B, N, M, gxyz1, gxyz2, s, c1, c2); break;
+    case TPO_F16: bwd_dispatch<half_t>(xyz1, xyz2, idx1, idx2, grad_loss, grad_loss, B, N, M, gxyz1, gxyz2, s, c1, c2); break;
+    default: return set_error(TPO_ERR_DTYPE, "tpo_chamfer_loss_bwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("tpo_chamfer_loss_bwd");
 }

@@ -104,6 +104,58 @@ std::tuple<at::Tensor, at::Tensor> chamfer_backward_hip(
   return {g1, g2};
 }
 
+// ChamferDistance(reduction="mean" / "sum") fused: loss and the indices the
+// backward needs (chamfer.py:18-24 reduces chamfer_forward's distances).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> chamfer_loss_forward_hip(
+    const at::Tensor& xyz1_in, const at::Tensor& xyz2_in, bool mean) {
+  check_hip(xyz1_in, "xyz1");
+  check_hip(xyz2_in, "xyz2");
+  TORCH_CHECK(xyz1_in.dim() == 3 && xyz2_in.dim() == 3 && xyz1_in.size(2) == 3 &&
+                  xyz2_in.size(2) == 3,
+              "chamfer_loss_forward expects (B,N,3) and (B,M,3) tensors");
+  TORCH_CHECK(xyz1_in.size(0) == xyz2_in.size(0), "batch sizes differ");
+  TORCH_CHECK(xyz1_in.scalar_type() == xyz2_in.scalar_type(), "dtypes differ");
+  TORCH_CHECK(xyz1_in.device() == xyz2_in.device(), "xyz1 and xyz2 must be on the same device");
+  c10::OptionalDeviceGuard guard(xyz1_in.device());
+  const at::Tensor xyz1 = xyz1_in.contiguous(), xyz2 = xyz2_in.contiguous();
+  const int64_t B = xyz1.size(0), N = xyz1.size(1), M = xyz2.size(1);
+  const int dt = dtype_code(xyz1, "chamfer_loss_forward");
+  at::Tensor loss = at::empty({}, xyz1.options());
+  at::Tensor idx1 = at::empty({B, N}, xyz1.options().dtype(at::kInt));
+  at::Tensor idx2 = at::empty({B, M}, xyz1.options().dtype(at::kInt));
+  const int64_t ws_bytes = tpo_chamfer_loss_workspace_size(dt, B, N, M);
+  TORCH_CHECK(ws_bytes >= 0, "chamfer_loss_forward: bad sizes");
+  at::Tensor ws = at::empty({std::max<int64_t>(ws_bytes, 1)}, xyz1.options().dtype(at::kByte));
+  check_rc(tpo_chamfer_loss_fwd(dt, xyz1.data_ptr(), xyz2.data_ptr(), B, N, M, mean ? 1 : 0,
+                                loss.data_ptr(), idx1.data_ptr<int32_t>(),
+                                idx2.data_ptr<int32_t>(), ws.data_ptr(), ws_bytes,
+                                stream_of(xyz1)),
+           "chamfer_loss_forward");
+  return {loss, idx1, idx2};
+}
+
+std::tuple<at::Tensor, at::Tensor> chamfer_loss_backward_hip(
+    const at::Tensor& xyz1_in, const at::Tensor& xyz2_in, const at::Tensor& idx1_in,
+    const at::Tensor& idx2_in, const at::Tensor& grad_loss_in, bool mean) {
+  check_hip(xyz1_in, "xyz1");
+  c10::OptionalDeviceGuard guard(xyz1_in.device());
+  const at::Tensor xyz1 = xyz1_in.contiguous(), xyz2 = xyz2_in.contiguous();
+  const int64_t B = xyz1.size(0), N = xyz1.size(1), M = xyz2.size(1);
+  TORCH_CHECK(idx1_in.scalar_type() == at::kInt && idx2_in.scalar_type() == at::kInt,
+              "chamfer_loss_backward expects int32 indices");
+  TORCH_CHECK(idx1_in.numel() == B * N && idx2_in.numel() == B * M, "index shapes differ");
+  TORCH_CHECK(grad_loss_in.numel() == 1, "chamfer_loss_backward expects a scalar gradient");
+  const at::Tensor idx1 = idx1_in.contiguous(), idx2 = idx2_in.contiguous();
+  const at::Tensor gl = grad_loss_in.to(xyz1.device(), xyz1.scalar_type()).contiguous();
+  const int dt = dtype_code(xyz1, "chamfer_loss_backward");
+  at::Tensor g1 = at::empty_like(xyz1), g2 = at::empty_like(xyz2);
+  check_rc(tpo_chamfer_loss_bwd(dt, xyz1.data_ptr(), xyz2.data_ptr(), idx1.data_ptr<int32_t>(),
+                                idx2.data_ptr<int32_t>(), gl.data_ptr(), mean ? 1 : 0, B, N, M,
+                                g1.data_ptr(), g2.data_ptr(), stream_of(xyz1)),
+           "chamfer_loss_backward");
+  return {g1, g2};
+}
+
 // chamfer.cpp:21-31: the reference has no CPU kernel.
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> chamfer_forward_cpu(
     const at::Tensor&, const at::Tensor&) {
@@ -112,6 +164,15 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> chamfer_forward_cpu(
 std::tuple<at::Tensor, at::Tensor> chamfer_backward_cpu(const at::Tensor&, const at::Tensor&,
                                                         const at::Tensor&, const at::Tensor&,
                                                         const at::Tensor&, const at::Tensor&) {
+  TORCH_CHECK(false, "chamfer_backward is not implemented for CPU");
+}
+std::tuple<at::Tensor, at::Tensor, at::Tensor> chamfer_loss_forward_cpu(const at::Tensor&,
+                                                                        const at::Tensor&, bool) {
+  TORCH_CHECK(false, "chamfer_forward is not implemented for CPU");
+}
+std::tuple<at::Tensor, at::Tensor> chamfer_loss_backward_cpu(const at::Tensor&, const at::Tensor&,
+                                                             const at::Tensor&, const at::Tensor&,
+                                                             const at::Tensor&, bool) {
   TORCH_CHECK(false, "chamfer_backward is not implemented for CPU");
 }
 
@@ -299,14 +360,22 @@ TORCH_LIBRARY(torch_point_ops_chamfer, m) {
   m.def("chamfer_forward(Tensor xyz1, Tensor xyz2) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("chamfer_backward(Tensor xyz1, Tensor xyz2, Tensor idx1, Tensor idx2, "
         "Tensor grad_dist1, Tensor grad_dist2) -> (Tensor, Tensor)");
+  // the module's reduction fused into the kernels (no reference schema)
+  m.def("chamfer_loss_forward(Tensor xyz1, Tensor xyz2, bool mean) -> (Tensor, Tensor, Tensor)");
+  m.def("chamfer_loss_backward(Tensor xyz1, Tensor xyz2, Tensor idx1, Tensor idx2, "
+        "Tensor grad_loss, bool mean) -> (Tensor, Tensor)");
 }
 TORCH_LIBRARY_IMPL(torch_point_ops_chamfer, CPU, m) {
   m.impl("chamfer_forward", &chamfer_forward_cpu);
   m.impl("chamfer_backward", &chamfer_backward_cpu);
+  m.impl("chamfer_loss_forward", &chamfer_loss_forward_cpu);
+  m.impl("chamfer_loss_backward", &chamfer_loss_backward_cpu);
 }
 TORCH_LIBRARY_IMPL(torch_point_ops_chamfer, CUDA, m) {
   m.impl("chamfer_forward", &chamfer_forward_hip);
   m.impl("chamfer_backward", &chamfer_backward_hip);
+  m.impl("chamfer_loss_forward", &chamfer_loss_forward_hip);
+  m.impl("chamfer_loss_backward", &chamfer_loss_backward_hip);
 }
 
 TORCH_LIBRARY(torch_point_ops_knn, m) {

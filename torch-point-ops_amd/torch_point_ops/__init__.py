@@ -10,7 +10,7 @@ import torch  # noqa: F401  (loads libc10 / libtorch before the extension)
 
 from . import _C  # noqa: F401  (registers the torch.ops schemas and HIP kernels)
 
-from .chamfer import ChamferDistance, chamfer_distance
+from .chamfer import ChamferDistance, chamfer_distance, chamfer_loss
 from .emd import EarthMoverDistance, emd, earth_movers_distance
 from .knn import KNearestNeighbors, knn_points, knn_gather
 from .fps import (
@@ -26,6 +26,7 @@ from .fps import (
 __all__ = [
     "ChamferDistance",
     "chamfer_distance",
+    "chamfer_loss",
     "EarthMoverDistance",
     "emd",
     "earth_movers_distance",

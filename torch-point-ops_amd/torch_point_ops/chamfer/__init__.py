@@ -57,6 +57,57 @@ def _chamfer_backward_fake(xyz1, xyz2, idx1, idx2, grad_dist1, grad_dist2):
     return torch.empty_like(xyz1), torch.empty_like(xyz2)
 
 
+def _chamfer_loss_backward(ctx, grad_loss, grad_idx1, grad_idx2):
+    if grad_loss is None:
+        return None, None, None
+    xyz1, xyz2, idx1, idx2 = ctx.saved_tensors
+    g1, g2 = torch.ops.torch_point_ops_chamfer.chamfer_loss_backward(
+        xyz1, xyz2, idx1, idx2, grad_loss, ctx.mean
+    )
+    return g1, g2, None
+
+
+def _chamfer_loss_setup_context(ctx, inputs, output):
+    xyz1, xyz2, mean = inputs
+    _loss, idx1, idx2 = output
+    ctx.save_for_backward(xyz1, xyz2, idx1, idx2)
+    ctx.mean = mean
+    ctx.set_materialize_grads(False)
+
+
+torch.library.register_autograd(
+    "torch_point_ops_chamfer::chamfer_loss_forward",
+    _chamfer_loss_backward,
+    setup_context=_chamfer_loss_setup_context,
+)
+
+
+@torch.library.register_fake("torch_point_ops_chamfer::chamfer_loss_forward")
+def _chamfer_loss_forward_fake(xyz1, xyz2, mean):
+    b, n, m = xyz1.shape[0], xyz1.shape[1], xyz2.shape[1]
+    return (
+        torch.empty((), dtype=xyz1.dtype, device=xyz1.device),
+        torch.empty(b, n, dtype=torch.int32, device=xyz1.device),
+        torch.empty(b, m, dtype=torch.int32, device=xyz1.device),
+    )
+
+
+@torch.library.register_fake("torch_point_ops_chamfer::chamfer_loss_backward")
+def _chamfer_loss_backward_fake(xyz1, xyz2, idx1, idx2, grad_loss, mean):
+    return torch.empty_like(xyz1), torch.empty_like(xyz2)
+
+
+def chamfer_loss(xyz1: torch.Tensor, xyz2: torch.Tensor, mean: bool = True) -> torch.Tensor:
+    """mean(dist1) + mean(dist2) (or the sums) of chamfer_distance(xyz1, xyz2),
+    reduced inside the forward kernels; the backward spreads the loss gradient
+    over the points inside the backward kernel.  Deterministic; equal to the
+    unfused reduction up to the order of the float sums."""
+    loss, _i1, _i2 = torch.ops.torch_point_ops_chamfer.chamfer_loss_forward(
+        xyz1.contiguous(), xyz2.contiguous(), mean
+    )
+    return loss
+
+
 def chamfer_distance(xyz1: torch.Tensor, xyz2: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Squared distance from every point to its nearest neighbour in the other cloud.
 

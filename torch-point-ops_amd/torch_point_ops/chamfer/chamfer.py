@@ -1,7 +1,7 @@
 """ChamferDistance module (reference: torch_point_ops/chamfer/chamfer.py:5-26)."""
 import torch
 
-from . import chamfer_distance
+from . import chamfer_distance, chamfer_loss
 
 _REDUCTIONS = ("mean", "sum", None, "none")
 
@@ -10,7 +10,8 @@ class ChamferDistance(torch.nn.Module):
     """Chamfer distance between two point clouds with an optional reduction.
 
     reduction: "mean" -> mean(dist1) + mean(dist2); "sum" -> sum(dist1) + sum(dist2);
-    None / "none" -> the tuple (dist1, dist2).
+    None / "none" -> the tuple (dist1, dist2).  The two reductions run inside
+    the Chamfer kernels (chamfer_loss) instead of as separate torch reductions.
     """
 
     def __init__(self, reduction="mean"):
@@ -22,9 +23,6 @@ class ChamferDistance(torch.nn.Module):
         self.reduction = reduction
 
     def forward(self, xyz1, xyz2):
-        dist1, dist2 = chamfer_distance(xyz1, xyz2)
-        if self.reduction == "mean":
-            return dist1.mean() + dist2.mean()
-        if self.reduction == "sum":
-            return dist1.sum() + dist2.sum()
-        return dist1, dist2
+        if self.reduction in ("mean", "sum"):
+            return chamfer_loss(xyz1, xyz2, self.reduction == "mean")
+        return chamfer_distance(xyz1, xyz2)
