@@ -69,13 +69,14 @@ def test_argument_errors_are_reported(lib):
     assert lib.tpo_chamfer_workspace_size(1, 32, 8192, 8192) == 0  # float only
     assert lib.tpo_chamfer_workspace_size(0, -1, 3, 3) == -1
     # fused module loss: the forward's workspace (grid search or none), both
-    # distance arrays, 2 x 256 chunk sums (doubles); 256-byte regions
+    # distance arrays, 2 x 256 chunk sums (doubles), a workgroup counter;
+    # 256-byte regions
     lib.tpo_chamfer_loss_workspace_size.argtypes = [ctypes.c_int, I, I, I]
     lib.tpo_chamfer_loss_workspace_size.restype = I
     assert lib.tpo_chamfer_loss_workspace_size(0, 32, 8192, 8192) == \
-        lib.tpo_chamfer_workspace_size(0, 32, 8192, 8192) + 2 * 32 * 8192 * 4 + 4096
+        lib.tpo_chamfer_workspace_size(0, 32, 8192, 8192) + 2 * 32 * 8192 * 4 + 4096 + 256
     # double: dist1 1600 -> 1792 bytes (256-byte regions), dist2 1024, chunk sums 4096
-    assert lib.tpo_chamfer_loss_workspace_size(1, 2, 100, 64) == 1792 + 1024 + 4096
+    assert lib.tpo_chamfer_loss_workspace_size(1, 2, 100, 64) == 1792 + 1024 + 4096 + 256
     assert lib.tpo_chamfer_loss_workspace_size(9, 2, 100, 64) == -1
     lib.tpo_chamfer_loss_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, ctypes.c_int, P, P, P, P,
                                          I, P]

@@ -465,18 +465,22 @@ __global__ __launch_bounds__(256) void chamfer_bwd_scatter_kernel(
 }
 
 // One workgroup per (batch, cloud, slice of that cloud's points): the slice's
-// gradient rows live in LDS; the workgroup scans the other cloud's nearest
-// indices and accumulates, with LDS atomics, the terms that land in its
-// slice; then it adds its points' direct terms and writes each element once.
-constexpr int CH_BWD_SLICE_MAX = 4096;  // points per slice (48 KiB of LDS)
+// gradient rows and coordinates live in LDS; the workgroup scans the other
+// cloud's nearest indices and accumulates, with LDS atomics, the terms that
+// land in its slice; then it adds its points' direct terms and writes each
+// element once.  The scan's loads do not depend on the indices (VEC: four
+// consecutive points per lane, one 16-byte index load and three 16-byte
+// coordinate loads), so they are all in flight together; only the LDS
+// atomics are conditional.
+constexpr int CH_BWD_SLICE_MAX = 4096;  // points per slice (96 KiB of LDS)
 constexpr int CH_BWD_MAX_SLICES = 16;   // beyond this the 2-pass path is cheaper
 
-template <typename T>
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
     const T* __restrict__ xyz1, const T* __restrict__ xyz2, const int32_t* __restrict__ idx1,
     const int32_t* __restrict__ idx2, PointGrad<T> gd1, PointGrad<T> gd2, int N, int M, int S,
     T* __restrict__ g1, T* __restrict__ g2) {
-  extern __shared__ float acc[];
+  extern __shared__ float sm[];
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const int sl = lb % S;
   const int c = (lb / S) & 1;  // 0: gradient of cloud 1, 1: of cloud 2
@@ -484,6 +488,8 @@ __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
   const int n_own = c ? M : N, n_oth = c ? N : M;
   const int span = (n_own + S - 1) / S;
   const int lo = min(n_own, sl * span), hi = min(n_own, lo + span);
+  float* __restrict__ acc = sm;                 // 3 * span
+  float* __restrict__ s_own = sm + 3 * span;    // the slice's coordinates
   const T* __restrict__ own = (c ? xyz2 : xyz1) + (size_t)b * n_own * 3;
   const T* __restrict__ oth = (c ? xyz1 : xyz2) + (size_t)b * n_oth * 3;
   const int32_t* __restrict__ idx_own = (c ? idx2 : idx1) + (size_t)b * n_own;
@@ -495,28 +501,54 @@ __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
   const T* __restrict__ gd_oth = pg_oth.p + (uni_oth ? 0 : (size_t)b * n_oth);
   T* __restrict__ out = (c ? g2 : g1) + (size_t)b * n_own * 3;
 
-  for (int i = threadIdx.x; i < 3 * (hi - lo); i += 256) acc[i] = 0.f;
+  for (int t = threadIdx.x; t < 3 * (hi - lo); t += 256) {
+    acc[t] = 0.f;
+    s_own[t] = (float)own[3 * lo + t];
+  }
   __syncthreads();
-  // other cloud's points j whose nearest point i is in [lo, hi)
+  // other cloud's point j whose nearest point i is in [lo, hi)
   // (chamfer.cu:229-231 of the other direction): acc[i] += -(g_j (r_j - q_i))
-  for (int j = threadIdx.x; j < n_oth; j += 256) {
-    const int i = idx_oth[j];
-    if (i < lo || i >= hi) continue;
-    const T g = (T)((uni_oth ? u_oth : gd_oth[j]) * (T)2);
-#pragma unroll
-    for (int k = 0; k < 3; ++k)
-      atomicAdd(&acc[3 * (i - lo) + k], -(float)(T)(g * (T)(oth[3 * j + k] - own[3 * i + k])));
+  auto scatter = [&](int j, int i, T rx, T ry, T rz, T gj) {
+    if (i < lo || i >= hi) return;
+    const T g = (T)(gj * (T)2);
+    const int a = 3 * (i - lo);
+    atomicAdd(&acc[a], -(float)(T)(g * (T)(rx - (T)s_own[a])));
+    atomicAdd(&acc[a + 1], -(float)(T)(g * (T)(ry - (T)s_own[a + 1])));
+    atomicAdd(&acc[a + 2], -(float)(T)(g * (T)(rz - (T)s_own[a + 2])));
+  };
+  if constexpr (VEC) {  // float, n_oth % 4 == 0, 16-byte aligned rows
+    const int4* __restrict__ iv = reinterpret_cast<const int4*>(idx_oth);
+    const float4* __restrict__ rv = reinterpret_cast<const float4*>(oth);
+    const float4* __restrict__ gv = reinterpret_cast<const float4*>(gd_oth);
+#pragma unroll 2
+    for (int q = threadIdx.x; q < n_oth / 4; q += 256) {
+      const int4 ii = iv[q];
+      const float4 r0 = rv[3 * q], r1 = rv[3 * q + 1], r2 = rv[3 * q + 2];
+      float4 gg = make_float4(u_oth, u_oth, u_oth, u_oth);
+      if (!uni_oth) gg = gv[q];
+      scatter(4 * q, ii.x, r0.x, r0.y, r0.z, gg.x);
+      scatter(4 * q + 1, ii.y, r0.w, r1.x, r1.y, gg.y);
+      scatter(4 * q + 2, ii.z, r1.z, r1.w, r2.x, gg.z);
+      scatter(4 * q + 3, ii.w, r2.y, r2.z, r2.w, gg.w);
+    }
+  } else {
+#pragma unroll 4
+    for (int j = threadIdx.x; j < n_oth; j += 256)
+      scatter(j, idx_oth[j], oth[3 * j], oth[3 * j + 1], oth[3 * j + 2],
+              uni_oth ? u_oth : gd_oth[j]);
   }
   __syncthreads();
   // direct term of the slice's points (chamfer.cu:226-228)
   for (int i = lo + threadIdx.x; i < hi; i += 256) {
     const int j2 = idx_own[i];
     const bool ok = j2 >= 0 && j2 < n_oth;
+    const int jj = ok ? j2 : 0;
     const T g = (T)((uni_own ? u_own : gd_own[i]) * (T)2);
+    const int a = 3 * (i - lo);
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-      const T d = ok ? (T)(g * (T)(own[3 * i + k] - oth[3 * j2 + k])) : (T)0;
-      out[3 * i + k] = (T)(acc[3 * (i - lo) + k] + (float)d);
+      const T d = ok ? (T)(g * (T)((T)s_own[a + k] - oth[3 * jj + k])) : (T)0;
+      out[3 * i + k] = (T)(acc[a + k] + (float)d);
     }
   }
 }
@@ -576,9 +608,22 @@ static void bwd_dispatch(const void* x1, const void* x2, const int32_t* i1, cons
     S = std::max(S, std::min({want, std::max<int64_t>(1, nmax / 512), (int64_t)CH_BWD_MAX_SLICES}));
     if (S <= CH_BWD_MAX_SLICES && 2 * B * S < (1 << 30)) {
       const int64_t span = (nmax + S - 1) / S;
-      hipLaunchKernelGGL(chamfer_bwd_fused_kernel<T>, dim3((unsigned)(2 * B * S)), dim3(256),
-                         (size_t)(3 * span * sizeof(float)), s, (const T*)x1, (const T*)x2, i1, i2,
-                         pg1, pg2, (int)N, (int)M, (int)S, (T*)g1, (T*)g2);
+      const size_t lds = (size_t)(6 * span * sizeof(float));
+      auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+      const bool vec = sizeof(T) == 4 && N % 4 == 0 && M % 4 == 0 && al16(x1) && al16(x2) &&
+                       al16(i1) && al16(i2) && (count1 != 0 || al16(gd1)) &&
+                       (count2 != 0 || al16(gd2));
+      if constexpr (sizeof(T) == 4) {
+        if (vec) {
+          hipLaunchKernelGGL((chamfer_bwd_fused_kernel<T, true>), dim3((unsigned)(2 * B * S)),
+                             dim3(256), lds, s, (const T*)x1, (const T*)x2, i1, i2, pg1, pg2,
+                             (int)N, (int)M, (int)S, (T*)g1, (T*)g2);
+          return;
+        }
+      }
+      hipLaunchKernelGGL((chamfer_bwd_fused_kernel<T, false>), dim3((unsigned)(2 * B * S)),
+                         dim3(256), lds, s, (const T*)x1, (const T*)x2, i1, i2, pg1, pg2, (int)N,
+                         (int)M, (int)S, (T*)g1, (T*)g2);
       return;
     }
   }
@@ -591,28 +636,59 @@ static void bwd_dispatch(const void* x1, const void* x2, const int32_t* i1, cons
 
 // ------------------------------------------------------------------- loss
 // The module's reduction (tpo_chamfer_loss_fwd): the forward stores both
-// distance arrays in the workspace, chamfer_loss_part_kernel sums fixed
-// chunks of them in original point order and chamfer_loss_final_kernel adds
-// the chunk sums in a fixed order, so the loss does not depend on how the
+// distance arrays in the workspace and chamfer_loss_part_kernel sums fixed
+// chunks of them in original point order; the chunk sums are then added in
+// a fixed order, by the last part workgroup to finish (LAST: the grid path,
+// whose sort kernel zeroes the workgroup counter) or by
+// chamfer_loss_final_kernel.  The loss therefore does not depend on how the
 // forward scheduled its queries.  (A reduction inside the grid search, one
 // sum per wave, would follow the search's query order, which the sort's
-// arrival-order ranks make nondeterministic; and publishing those sums to a
-// last workgroup needs a device-scope release per workgroup, an L2 writeback
-// that evicts the reference points the other workgroups are reading.)
+// arrival-order ranks make nondeterministic; and a device-scope release per
+// search workgroup is an L2 writeback that evicts the reference points the
+// other workgroups are reading.)
 constexpr int CH_LOSS_PARTS = 256;       // chunks per array, at most
-constexpr int64_t CH_LOSS_CHUNK = 2048;  // elements per chunk, at least
+constexpr int64_t CH_LOSS_CHUNK = 4096;  // elements per chunk, at least
 
 static int64_t loss_parts(int64_t n) {
   return std::min<int64_t>((n + CH_LOSS_CHUNK - 1) / CH_LOSS_CHUNK, CH_LOSS_PARTS);
 }
 
+// Loss from the chunk sums, by one wave: parts [0, p1) sum dist1,
+// [p1, p1 + p2) dist2.  Lane 0 writes, as torch.mean / torch.sum of each
+// array followed by their sum (chamfer.py:20-23; torch's mean scales the
+// accumulated sum by 1 / numel in the accumulation type, and an empty
+// array's mean is NaN):
+//   mean: (T)(S1 * (1 / count1)) + (T)(S2 * (1 / count2))
+//   sum:  (T)S1 + (T)S2
 template <typename T>
-__global__ __launch_bounds__(256) void chamfer_loss_part_kernel(const T* __restrict__ d1,
-                                                                const T* __restrict__ d2,
-                                                                int64_t n1, int64_t n2, int p1,
-                                                                int p2, double* __restrict__ part) {
+__device__ void chamfer_loss_finish(const double* part, int p1, int p2, int mean, int64_t count1,
+                                    int64_t count2, T* loss) {
+  using A = typename std::conditional<sizeof(T) == 8, double, float>::type;
+  const int lane = threadIdx.x & 63;
+  A a1 = (A)0, a2 = (A)0;
+  for (int k = lane; k < p1; k += 64) a1 += (A)part[k];
+  for (int k = lane; k < p2; k += 64) a2 += (A)part[p1 + k];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    a1 += __shfl_xor(a1, o);
+    a2 += __shfl_xor(a2, o);
+  }
+  if (lane == 0) {
+    if (mean) {
+      a1 *= (A)1 / (A)count1;
+      a2 *= (A)1 / (A)count2;
+    }
+    loss[0] = (T)((A)(T)a1 + (A)(T)a2);
+  }
+}
+
+template <typename T, bool LAST>
+__global__ __launch_bounds__(256) void chamfer_loss_part_kernel(
+    const T* __restrict__ d1, const T* __restrict__ d2, int64_t n1, int64_t n2, int p1, int p2,
+    double* __restrict__ part, uint32_t* __restrict__ done, int mean, T* __restrict__ loss) {
   using A = typename std::conditional<sizeof(T) == 8, double, float>::type;
   __shared__ A s_red[4];
+  __shared__ int s_last;
   const int k = blockIdx.x;
   const bool second = k >= p1;
   const T* d = second ? d2 : d1;
@@ -628,40 +704,33 @@ __global__ __launch_bounds__(256) void chamfer_loss_part_kernel(const T* __restr
   if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = a;
   __syncthreads();
   if (threadIdx.x == 0) part[k] = (double)(((s_red[0] + s_red[1]) + s_red[2]) + s_red[3]);
+  if constexpr (LAST) {
+    // publish the chunk sum (device-scope release), count the workgroup;
+    // the last one acquires every chunk sum and finishes the loss
+    if (threadIdx.x == 0) {
+      __threadfence();
+      s_last = atomicAdd(done, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (s_last && threadIdx.x < 64) {
+      __threadfence();
+      chamfer_loss_finish<T>(part, p1, p2, mean, n1, n2, loss);
+    }
+  }
 }
 
-// Loss from the chunk sums: parts [0, p1) sum dist1, [p1, p1 + p2) dist2.
-// Thread 0 writes, as torch.mean / torch.sum of each array followed by
-// their sum (chamfer.py:20-23; torch's mean scales the accumulated sum by
-// 1 / numel in the accumulation type, and an empty array's mean is NaN):
-//   mean: (T)(S1 * (1 / count1)) + (T)(S2 * (1 / count2))
-//   sum:  (T)S1 + (T)S2
 template <typename T>
 __global__ __launch_bounds__(64) void chamfer_loss_final_kernel(const double* __restrict__ part,
                                                                 int p1, int p2, int mean,
                                                                 int64_t count1, int64_t count2,
                                                                 T* __restrict__ loss) {
-  using A = typename std::conditional<sizeof(T) == 8, double, float>::type;
-  A a1 = (A)0, a2 = (A)0;
-  for (int k = threadIdx.x; k < p1; k += 64) a1 += (A)part[k];
-  for (int k = threadIdx.x; k < p2; k += 64) a2 += (A)part[p1 + k];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    a1 += __shfl_xor(a1, o);
-    a2 += __shfl_xor(a2, o);
-  }
-  if (threadIdx.x == 0) {
-    if (mean) {
-      a1 *= (A)1 / (A)count1;
-      a2 *= (A)1 / (A)count2;
-    }
-    loss[0] = (T)((A)(T)a1 + (A)(T)a2);
-  }
+  chamfer_loss_finish<T>(part, p1, p2, mean, count1, count2, loss);
 }
 
-// Workspace of tpo_chamfer_loss_fwd: [forward workspace][dist1][dist2][chunk sums].
+// Workspace of tpo_chamfer_loss_fwd:
+// [forward workspace][dist1][dist2][chunk sums][workgroup counter].
 struct LossLayout {
-  int64_t fwd, d1, d2, part, total;
+  int64_t fwd, d1, d2, part, done, total;
 };
 
 static LossLayout loss_layout(int64_t fwd_bytes, int64_t esize, int64_t B, int64_t N, int64_t M) {
@@ -671,20 +740,29 @@ static LossLayout loss_layout(int64_t fwd_bytes, int64_t esize, int64_t B, int64
   L.d1 = up(fwd_bytes);
   L.d2 = L.d1 + up(B * N * esize);
   L.part = L.d2 + up(B * M * esize);
-  L.total = L.part + up(2 * CH_LOSS_PARTS * 8);
+  L.done = L.part + up(2 * CH_LOSS_PARTS * 8);
+  L.total = L.done + 256;
   return L;
 }
 
+// counter_zeroed: the forward's sort kernel has set the counter to 0, so the
+// part kernel can finish the loss itself (one launch instead of two).
 template <typename T>
 static void loss_reduce(const LossLayout& L, char* ws, int64_t B, int64_t N, int64_t M, int mean,
-                        void* loss, hipStream_t s) {
+                        void* loss, bool counter_zeroed, hipStream_t s) {
   const T* d1 = (const T*)(ws + L.d1);
   const T* d2 = (const T*)(ws + L.d2);
   double* part = (double*)(ws + L.part);
+  uint32_t* done = (uint32_t*)(ws + L.done);
   const int p1 = (int)loss_parts(B * N), p2 = (int)loss_parts(B * M);
+  if (counter_zeroed && p1 + p2 > 0) {
+    hipLaunchKernelGGL((chamfer_loss_part_kernel<T, true>), dim3(p1 + p2), dim3(256), 0, s, d1,
+                       d2, B * N, B * M, p1, p2, part, done, mean, (T*)loss);
+    return;
+  }
   if (p1 + p2 > 0)
-    hipLaunchKernelGGL(chamfer_loss_part_kernel<T>, dim3(p1 + p2), dim3(256), 0, s, d1, d2, B * N,
-                       B * M, p1, p2, part);
+    hipLaunchKernelGGL((chamfer_loss_part_kernel<T, false>), dim3(p1 + p2), dim3(256), 0, s, d1,
+                       d2, B * N, B * M, p1, p2, part, done, mean, (T*)loss);
   hipLaunchKernelGGL(chamfer_loss_final_kernel<T>, dim3(1), dim3(64), 0, s, part, p1, p2, mean,
                      B * N, B * M, (T*)loss);
 }
@@ -792,10 +870,11 @@ extern "C" int tpo_chamfer_loss_fwd(int dtype, const void* xyz1, const void* xyz
   char* w = (char*)workspace;
   void* d1 = w + L.d1;
   void* d2 = w + L.d2;
+  const bool grid = B > 0 && N + M > 0 && prune_applies(dtype, B, N, M);
   if (B > 0 && N + M > 0) {
-    if (prune_applies(dtype, B, N, M))
+    if (grid)
       launch_chamfer_fwd_prune(xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2, w + L.fwd,
-                               s);
+                               s, (uint32_t*)(w + L.done));
     else if (dtype == TPO_F32)
       fwd_dispatch<float>(xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2, s);
     else if (dtype == TPO_F64)
@@ -804,9 +883,9 @@ extern "C" int tpo_chamfer_loss_fwd(int dtype, const void* xyz1, const void* xyz
       fwd_dispatch<half_t>(xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2, s);
   }
   switch (dtype) {
-    case TPO_F32: loss_reduce<float>(L, w, B, N, M, mean != 0, loss, s); break;
-    case TPO_F64: loss_reduce<double>(L, w, B, N, M, mean != 0, loss, s); break;
-    case TPO_F16: loss_reduce<half_t>(L, w, B, N, M, mean != 0, loss, s); break;
+    case TPO_F32: loss_reduce<float>(L, w, B, N, M, mean != 0, loss, grid, s); break;
+    case TPO_F64: loss_reduce<double>(L, w, B, N, M, mean != 0, loss, grid, s); break;
+    case TPO_F16: loss_reduce<half_t>(L, w, B, N, M, mean != 0, loss, grid, s); break;
   }
   return check_launch("tpo_chamfer_loss_fwd");
 }

@@ -104,7 +104,7 @@ __device__ __forceinline__ int cg_hidx(uint32_t code) { return (int)(code + (cod
 template <int PPT>
 __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     const float* __restrict__ xyz1, const float* __restrict__ xyz2, int N, int M,
-    char* __restrict__ ws, CgLayout L) {
+    char* __restrict__ ws, CgLayout L, uint32_t* __restrict__ zero) {
   __shared__ uint32_t cnt[CG_CELLS + CG_CELLS / 32];
   __shared__ float red[6][16];
   __shared__ uint32_t part[16];
@@ -112,6 +112,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   const int c = blockIdx.x & 1, b = blockIdx.x >> 1;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int n = c ? M : N;
+  if (zero && blockIdx.x == 0 && tid == 0) *zero = 0u;
   const int64_t PN = cg_pad(N), PM = cg_pad(M);
   const int64_t base = (int64_t)b * (PN + PM) + (c ? PN : 0);
   const float* __restrict__ P = (c ? xyz2 : xyz1) + (size_t)b * n * 3;
@@ -310,8 +311,11 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     int rmax = 0;
 #pragma unroll
     for (int a = 0; a < 3; ++a) rmax = max(rmax, max(ci[a], ga[a] - 1 - ci[a]));
-    float bd = Lim<float>::inf();
-    int bi = 0x7fffffff;
+    // best (distance, index) as one key: distances here are finite and >= 0,
+    // so their bits order like the values, and the index breaks ties
+    uint64_t bkey = ((uint64_t)0x7f800000u << 32) | 0x7fffffffu;
+    auto bdist = [&]() { return __uint_as_float((uint32_t)(bkey >> 32)); };
+    const char* __restrict__ rsb = reinterpret_cast<const char*>(rs);
     // evaluate every point of sorted positions [j0, j1)
     auto scan = [&](int j0, int j1) {
       for (int j = j0; j < j1; j += CG_UNROLL) {
@@ -319,15 +323,13 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
         // point, whose second evaluation cannot change the result
         float4 p[CG_UNROLL];
 #pragma unroll
-        for (int u = 0; u < CG_UNROLL; ++u) p[u] = rs[min(j + u, j1 - 1)];
+        for (int u = 0; u < CG_UNROLL; ++u)
+          p[u] = *reinterpret_cast<const float4*>(rsb + (uint32_t)min(j + u, j1 - 1) * 16u);
 #pragma unroll
         for (int u = 0; u < CG_UNROLL; ++u) {
           const float d = sq3((float)(p[u].x - q.x), (float)(p[u].y - q.y), (float)(p[u].z - q.z));
-          const int oi = __float_as_int(p[u].w);
-          // branch-free (d, index) minimum
-          const bool take = (d < bd) | ((d == bd) & (oi < bi));
-          bd = take ? d : bd;
-          bi = take ? oi : bi;
+          const uint64_t key = ((uint64_t)__float_as_uint(d) << 32) | __float_as_uint(p[u].w);
+          bkey = key < bkey ? key : bkey;
         }
       }
       examined += j1 - j0;
@@ -342,13 +344,13 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
         const float chi = (ga[a] > 1 ? glo[a] + (float)(cc[a] + 1) * cs[a] : ghi[a]) + eps[a];
         gap[a] = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
       }
-      if (sq3(gap[0], gap[1], gap[2]) * (1.f - 0x1p-20f) > bd) return;
+      if (sq3(gap[0], gap[1], gap[2]) * (1.f - 0x1p-20f) > bdist()) return;
       const uint32_t code = cg_code(cx, cy, cz);
       scan(cstart[code], cstart[code + 1]);
     };
     // phase 1: Chebyshev rings around the query's cell until a point is found
     int rdone = -1;
-    for (int r = 0; r <= rmax && bd == Lim<float>::inf(); ++r) {
+    for (int r = 0; r <= rmax && bdist() == Lim<float>::inf(); ++r) {
       const int z0 = max(-r, -ci[2]), z1 = min(r, ga[2] - 1 - ci[2]);
       const int y0 = max(-r, -ci[1]), y1 = min(r, ga[1] - 1 - ci[1]);
       const int x0 = max(-r, -ci[0]), x1 = min(r, ga[0] - 1 - ci[0]);
@@ -373,6 +375,7 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     // (the bound only grows with more axes; any summation order rounds by a
     // few u, well inside the 2^-20 margin).
     int blo[3], bhi[3];
+    const float bd = bdist();
     const float rad = __builtin_sqrtf(bd) * (1.f + 0x1p-19f);
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
@@ -389,25 +392,25 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     constexpr float keep = 1.f - 0x1p-20f;
     for (int cz = blo[2]; cz <= bhi[2]; ++cz) {
       const float gz = gap2(2, cz);
-      if (gz * keep > bd) continue;
+      if (gz * keep > bdist()) continue;
       const uint32_t kz = cg_spread((uint32_t)cz) << 2;
       const int dz = abs(cz - ci[2]);
       for (int cy = blo[1]; cy <= bhi[1]; ++cy) {
         const float gzy = gz + gap2(1, cy);
-        if (gzy * keep > bd) continue;
+        if (gzy * keep > bdist()) continue;
         const uint32_t kzy = kz | (cg_spread((uint32_t)cy) << 1);
         const int dzy = max(dz, abs(cy - ci[1]));
         for (int cx = blo[0]; cx <= bhi[0]; ++cx) {
           if (max(dzy, abs(cx - ci[0])) <= rdone) continue;
-          if ((gzy + gap2(0, cx)) * keep > bd) continue;
+          if ((gzy + gap2(0, cx)) * keep > bdist()) continue;
           const uint32_t code = kzy | cg_spread((uint32_t)cx);
           const int j0 = cstart[code], j1 = cstart[code + 1];
           scan(j0, j1);
         }
       }
     }
-    dout[oq] = bd;
-    iout[oq] = bi;
+    dout[oq] = bdist();
+    iout[oq] = (int)(uint32_t)bkey;
   }
   {  // points evaluated by this wave
     int e = examined;
@@ -453,14 +456,15 @@ int64_t chamfer_prune_workspace(int64_t B, int64_t N, int64_t M) {
 }
 
 void launch_chamfer_fwd_prune(const void* x1, const void* x2, int B, int N, int M, void* d1,
-                              void* d2, int32_t* i1, int32_t* i2, void* ws, hipStream_t s) {
+                              void* d2, int32_t* i1, int32_t* i2, void* ws, hipStream_t s,
+                              uint32_t* zero) {
   const CgLayout L = cg_layout(B, N, M);
   if (std::max(N, M) <= 1024 * 8)
     hipLaunchKernelGGL(chamfer_grid_sort_kernel<8>, dim3(2 * B), dim3(1024), 0, s,
-                       (const float*)x1, (const float*)x2, N, M, (char*)ws, L);
+                       (const float*)x1, (const float*)x2, N, M, (char*)ws, L, zero);
   else
     hipLaunchKernelGGL(chamfer_grid_sort_kernel<0>, dim3(2 * B), dim3(1024), 0, s,
-                       (const float*)x1, (const float*)x2, N, M, (char*)ws, L);
+                       (const float*)x1, (const float*)x2, N, M, (char*)ws, L, zero);
   const int nqb1 = (N + CG_WG - 1) / CG_WG, nqb2 = (M + CG_WG - 1) / CG_WG;
   hipLaunchKernelGGL((chamfer_grid_search_kernel<CG_WG>), dim3(B * (nqb1 + nqb2)), dim3(CG_WG), 0,
                      s, (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2, (const char*)ws,
