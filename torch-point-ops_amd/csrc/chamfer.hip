@@ -474,9 +474,11 @@ __global__ __launch_bounds__(256) void chamfer_bwd_scatter_kernel(
 // atomics are conditional.
 constexpr int CH_BWD_SLICE_MAX = 4096;  // points per slice (96 KiB of LDS)
 constexpr int CH_BWD_MAX_SLICES = 16;   // beyond this the 2-pass path is cheaper
+constexpr int CH_BWD_THREADS = 512;     // threads per workgroup
+constexpr int CH_BWD_PF = 2;            // own points per thread prefetched for the direct term
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
+__global__ __launch_bounds__(CH_BWD_THREADS) void chamfer_bwd_fused_kernel(
     const T* __restrict__ xyz1, const T* __restrict__ xyz2, const int32_t* __restrict__ idx1,
     const int32_t* __restrict__ idx2, PointGrad<T> gd1, PointGrad<T> gd2, int N, int M, int S,
     T* __restrict__ g1, T* __restrict__ g2) {
@@ -501,7 +503,21 @@ __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
   const T* __restrict__ gd_oth = pg_oth.p + (uni_oth ? 0 : (size_t)b * n_oth);
   T* __restrict__ out = (c ? g2 : g1) + (size_t)b * n_own * 3;
 
-  for (int t = threadIdx.x; t < 3 * (hi - lo); t += 256) {
+  // direct-term inputs of the first CH_BWD_PF points per thread, fetched
+  // now so their latency hides behind the staging and the scan
+  int pj[CH_BWD_PF];
+  T pg[CH_BWD_PF], po[CH_BWD_PF][3];
+#pragma unroll
+  for (int u = 0; u < CH_BWD_PF; ++u) {
+    const int i = lo + (int)threadIdx.x + CH_BWD_THREADS * u;
+    const int j2 = i < hi ? idx_own[i] : -1;
+    const bool ok = j2 >= 0 && j2 < n_oth;
+    pj[u] = ok ? j2 : -1;
+    pg[u] = i < hi ? (T)((uni_own ? u_own : gd_own[i]) * (T)2) : (T)0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) po[u][k] = ok ? oth[3 * j2 + k] : (T)0;
+  }
+  for (int t = threadIdx.x; t < 3 * (hi - lo); t += CH_BWD_THREADS) {
     acc[t] = 0.f;
     s_own[t] = (float)own[3 * lo + t];
   }
@@ -521,7 +537,7 @@ __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
     const float4* __restrict__ rv = reinterpret_cast<const float4*>(oth);
     const float4* __restrict__ gv = reinterpret_cast<const float4*>(gd_oth);
 #pragma unroll 2
-    for (int q = threadIdx.x; q < n_oth / 4; q += 256) {
+    for (int q = threadIdx.x; q < n_oth / 4; q += CH_BWD_THREADS) {
       const int4 ii = iv[q];
       const float4 r0 = rv[3 * q], r1 = rv[3 * q + 1], r2 = rv[3 * q + 2];
       float4 gg = make_float4(u_oth, u_oth, u_oth, u_oth);
@@ -533,13 +549,25 @@ __global__ __launch_bounds__(256) void chamfer_bwd_fused_kernel(
     }
   } else {
 #pragma unroll 4
-    for (int j = threadIdx.x; j < n_oth; j += 256)
+    for (int j = threadIdx.x; j < n_oth; j += CH_BWD_THREADS)
       scatter(j, idx_oth[j], oth[3 * j], oth[3 * j + 1], oth[3 * j + 2],
               uni_oth ? u_oth : gd_oth[j]);
   }
   __syncthreads();
   // direct term of the slice's points (chamfer.cu:226-228)
-  for (int i = lo + threadIdx.x; i < hi; i += 256) {
+#pragma unroll
+  for (int u = 0; u < CH_BWD_PF; ++u) {
+    const int i = lo + (int)threadIdx.x + CH_BWD_THREADS * u;
+    if (i >= hi) break;
+    const int a = 3 * (i - lo);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const T d = pj[u] >= 0 ? (T)(pg[u] * (T)((T)s_own[a + k] - po[u][k])) : (T)0;
+      out[3 * i + k] = (T)(acc[a + k] + (float)d);
+    }
+  }
+  for (int i = lo + (int)threadIdx.x + CH_BWD_THREADS * CH_BWD_PF; i < hi;
+       i += CH_BWD_THREADS) {
     const int j2 = idx_own[i];
     const bool ok = j2 >= 0 && j2 < n_oth;
     const int jj = ok ? j2 : 0;
@@ -616,13 +644,15 @@ static void bwd_dispatch(const void* x1, const void* x2, const int32_t* i1, cons
       if constexpr (sizeof(T) == 4) {
         if (vec) {
           hipLaunchKernelGGL((chamfer_bwd_fused_kernel<T, true>), dim3((unsigned)(2 * B * S)),
-                             dim3(256), lds, s, (const T*)x1, (const T*)x2, i1, i2, pg1, pg2,
+                             dim3(CH_BWD_THREADS), lds, s, (const T*)x1, (const T*)x2, i1, i2,
+                             pg1, pg2,
                              (int)N, (int)M, (int)S, (T*)g1, (T*)g2);
           return;
         }
       }
       hipLaunchKernelGGL((chamfer_bwd_fused_kernel<T, false>), dim3((unsigned)(2 * B * S)),
-                         dim3(256), lds, s, (const T*)x1, (const T*)x2, i1, i2, pg1, pg2, (int)N,
+                         dim3(CH_BWD_THREADS), lds, s, (const T*)x1, (const T*)x2, i1, i2, pg1,
+                         pg2, (int)N,
                          (int)M, (int)S, (T*)g1, (T*)g2);
       return;
     }

@@ -10,7 +10,9 @@
 // 2. chamfer_grid_search_kernel: one lane per query, queries taken in the
 //    sorted (Morton) order of their own cloud so a wave's lanes search nearby
 //    cells.  A lane walks Chebyshev rings of cells around its query's cell
-//    until it has a candidate, then visits the box of cells that can hold a
+//    until it has a candidate (ring 1 nearest cells first, its edge and
+//    corner groups skipped whole when a lower bound of their gaps exceeds
+//    the best distance), then visits the box of cells that can hold a
 //    point within the best distance found (cell assignment is monotone in
 //    each coordinate, and the box is widened by 2^-19 relative plus the
 //    rounding of its bounds), evaluating every point of a visited cell with
@@ -26,6 +28,8 @@
 //    and every query of a reference cloud holding such a coordinate, are
 //    scanned over the whole reference cloud in original order by chunk_scan
 //    (the reference's NaN rule included).
+// The best (distance, index) pair is one 64-bit key: distances here are
+// finite and non-negative, so their bits order like their values.
 // Results are identical to the reference's; the work depends on the data
 // (clustered and spread clouds need a few dozen points per query, a cloud
 // squeezed into one cell degrades to a full scan).  Each wave records the
@@ -40,6 +44,7 @@ namespace tpo {
 
 constexpr int CG_GRID = 32;  // cells per axis
 constexpr int CG_CELLS = CG_GRID * CG_GRID * CG_GRID;
+constexpr int CG_CSTRIDE = CG_CELLS + 4;  // cell-start ints per cloud (16-byte rows)
 constexpr int CG_WG = 256;    // queries per search workgroup
 constexpr int CG_UNROLL = 2;  // points of a cell loaded together
 
@@ -49,7 +54,7 @@ __host__ __device__ inline int64_t cg_pad(int64_t n) { return (n + 63) & ~(int64
 struct CgLayout {
   int64_t hdr;     // 2B x 16 floats: lo[3], hi[3], cells per unit[3], cell size[3], bad
   int64_t pts;     // float4 per padded point: sorted (x, y, z, original index bits)
-  int64_t cstart;  // (CG_CELLS + 1) int32 per cloud: first sorted position of a cell
+  int64_t cstart;  // CG_CSTRIDE int32 per cloud: first sorted position of a cell, then n
   int64_t rank;    // int32 per point: rank within its cell (sort scratch)
   int64_t stats;   // int32 per search wave: points evaluated
   int64_t total;
@@ -70,7 +75,7 @@ static CgLayout cg_layout(int64_t B, int64_t N, int64_t M) {
   L.pts = o;
   o = cg_align(o + B * P * 16);
   L.cstart = o;
-  o = cg_align(o + 2 * B * (CG_CELLS + 1) * 4);
+  o = cg_align(o + 2 * B * CG_CSTRIDE * 4);
   L.rank = o;
   o = cg_align(o + B * P * 4);
   L.stats = o;
@@ -105,7 +110,9 @@ template <int PPT>
 __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     const float* __restrict__ xyz1, const float* __restrict__ xyz2, int N, int M,
     char* __restrict__ ws, CgLayout L, uint32_t* __restrict__ zero) {
-  __shared__ uint32_t cnt[CG_CELLS + CG_CELLS / 32];
+  // cell counts, then (PPT > 0) the sorted points staged for a coalesced write
+  __shared__ __align__(16) uint32_t cnt[CG_CELLS + CG_CELLS / 32];
+  static_assert(sizeof(cnt) >= 1024 * 8 * sizeof(float4), "staging area");
   __shared__ float red[6][16];
   __shared__ uint32_t part[16];
   __shared__ uint32_t s_bad;
@@ -119,7 +126,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   float* __restrict__ hdr = reinterpret_cast<float*>(ws + L.hdr) + (size_t)blockIdx.x * 16;
   float4* __restrict__ pts = reinterpret_cast<float4*>(ws + L.pts) + base;
   int32_t* __restrict__ cstart =
-      reinterpret_cast<int32_t*>(ws + L.cstart) + (size_t)blockIdx.x * (CG_CELLS + 1);
+      reinterpret_cast<int32_t*>(ws + L.cstart) + (size_t)blockIdx.x * CG_CSTRIDE;
   int32_t* __restrict__ rank = reinterpret_cast<int32_t*>(ws + L.rank) + base;
 
   constexpr int R = PPT > 0 ? PPT : 1;
@@ -176,7 +183,8 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
       red[a][w] = lo[a];
       red[3 + a][w] = hi[a];
     }
-  for (int k = tid; k < CG_CELLS + CG_CELLS / 32; k += 1024) cnt[k] = 0;
+  for (int k = tid; k < (CG_CELLS + CG_CELLS / 32) / 4; k += 1024)
+    reinterpret_cast<uint4*>(cnt)[k] = make_uint4(0u, 0u, 0u, 0u);
   __syncthreads();
   if (big >= CH_BIG) atomicOr(&s_bad, 1u);
   float glo[3], ghi[3], gs[3];
@@ -197,15 +205,20 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     return cg_code(cg_axis_cell(x, glo[0], gs[0]), cg_axis_cell(y, glo[1], gs[1]),
                    cg_axis_cell(z, glo[2], gs[2]));
   };
-  uint32_t rk[R];
+  uint32_t rk[R], hx[R];  // PPT > 0: rank within the cell, histogram slot of the cell
   for (int i = 0; i < iters; ++i) {
     const int k = tid + 1024 * i;
     if (k >= n) break;
     float x, y, z;
     point(i, k, x, y, z);
-    const uint32_t r = atomicAdd(&cnt[cg_hidx(code_of(x, y, z))], 1u);
-    if constexpr (PPT > 0) rk[i] = r;
-    else rank[k] = (int32_t)r;
+    const int h = cg_hidx(code_of(x, y, z));
+    const uint32_t r = atomicAdd(&cnt[h], 1u);
+    if constexpr (PPT > 0) {
+      rk[i] = r;
+      hx[i] = (uint32_t)h;
+    } else {
+      rank[k] = (int32_t)r;
+    }
   }
   __syncthreads();
   {  // exclusive scan of the cell counts, CPT consecutive cells per thread
@@ -234,17 +247,42 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     if (tid == 1023) cstart[CG_CELLS] = (int32_t)run;
   }
   __syncthreads();
-  for (int k = tid; k < CG_CELLS; k += 1024) cstart[k] = (int32_t)cnt[cg_hidx(k)];  // coalesced
-  for (int i = 0; i < iters; ++i) {
-    const int k = tid + 1024 * i;
-    if (k >= n) break;
-    float x, y, z;
-    point(i, k, x, y, z);
-    const uint32_t r = PPT > 0 ? rk[i] : (uint32_t)rank[k];
-    pts[cnt[cg_hidx(code_of(x, y, z))] + r] = make_float4(x, y, z, __int_as_float(k));
+  for (int k = tid; k < CG_CELLS / 4; k += 1024) {  // coalesced, 4 cells per store
+    const int c0 = cg_hidx(4 * k);  // the 4 cells share one padded run of 32
+    reinterpret_cast<int4*>(cstart)[k] =
+        make_int4((int)cnt[c0], (int)cnt[c0 + 1], (int)cnt[c0 + 2], (int)cnt[c0 + 3]);
   }
-  for (int pos = n + tid; pos < cg_pad(n); pos += 1024)
-    pts[pos] = make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
+  if constexpr (PPT > 0) {
+    // sorted positions into registers; once every read of the counts is done
+    // the points are placed in LDS and written out in order, coalesced
+    uint32_t at[R];
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int k = tid + 1024 * i;
+      at[i] = k < n ? cnt[hx[i]] + rk[i] : 0u;
+    }
+    __syncthreads();
+    float4* __restrict__ stage = reinterpret_cast<float4*>(cnt);
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int k = tid + 1024 * i;
+      if (k < n) stage[at[i]] = make_float4(px[i], py[i], pz[i], __int_as_float(k));
+    }
+    __syncthreads();
+    for (int pos = tid; pos < cg_pad(n); pos += 1024)
+      pts[pos] = pos < n ? stage[pos] : make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
+  } else {
+    for (int i = 0; i < iters; ++i) {
+      const int k = tid + 1024 * i;
+      if (k >= n) break;
+      float x, y, z;
+      point(i, k, x, y, z);
+      pts[cnt[cg_hidx(code_of(x, y, z))] + (uint32_t)rank[k]] =
+          make_float4(x, y, z, __int_as_float(k));
+    }
+    for (int pos = n + tid; pos < cg_pad(n); pos += 1024)
+      pts[pos] = make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
+  }
   if (tid == 0) {
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
@@ -279,7 +317,7 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
   const float4* __restrict__ qs = reinterpret_cast<const float4*>(ws + L.pts) + base_q;
   const float4* __restrict__ rs = reinterpret_cast<const float4*>(ws + L.pts) + base_r;
   const int32_t* __restrict__ cstart =
-      reinterpret_cast<const int32_t*>(ws + L.cstart) + (size_t)(2 * b + cr) * (CG_CELLS + 1);
+      reinterpret_cast<const int32_t*>(ws + L.cstart) + (size_t)(2 * b + cr) * CG_CSTRIDE;
   const float* __restrict__ h = reinterpret_cast<const float*>(ws + L.hdr) + (2 * b + cr) * 16;
   const float* __restrict__ rp = (dir ? xyz1 : xyz2) + (size_t)b * nr * 3;  // original order
   const float* __restrict__ qp = (dir ? xyz2 : xyz1) + (size_t)b * nq * 3;
@@ -349,8 +387,54 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
       scan(cstart[code], cstart[code + 1]);
     };
     // phase 1: Chebyshev rings around the query's cell until a point is found
-    int rdone = -1;
-    for (int r = 0; r <= rmax && bdist() == Lim<float>::inf(); ++r) {
+    visit(ci[0], ci[1], ci[2]);
+    int rdone = 0;
+    if (bdist() == Lim<float>::inf() && rmax >= 1) {
+      // ring 1, nearest cells first: the six face neighbours (the nearer face
+      // of each axis first), then the 12 edge and 8 corner neighbours, each
+      // group skipped whole when a lower bound of its cells' gaps (the same
+      // per-axis gaps visit computes, combined monotonically) already exceeds
+      // the best distance
+      float gn[3];
+      int sn[3];
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        // gap to the neighbour below (its upper bound) and above (its lower bound)
+        const float gm = ci[a] > 0 ? fmaxf(qv[a] - (glo[a] + (float)ci[a] * cs[a] + eps[a]), 0.f)
+                                   : __builtin_inff();
+        const float gp = ci[a] < ga[a] - 1
+                             ? fmaxf((glo[a] + (float)(ci[a] + 1) * cs[a] - eps[a]) - qv[a], 0.f)
+                             : __builtin_inff();
+        sn[a] = gm <= gp ? -1 : 1;
+        gn[a] = fminf(gm, gp);
+      }
+      auto inb = [&](int a, int d) { return ci[a] + d >= 0 && ci[a] + d < ga[a]; };
+      auto cell = [&](int dx, int dy, int dz) {
+        if (inb(0, dx) && inb(1, dy) && inb(2, dz)) visit(ci[0] + dx, ci[1] + dy, ci[2] + dz);
+      };
+      cell(sn[0], 0, 0);
+      cell(0, sn[1], 0);
+      cell(0, 0, sn[2]);
+      cell(-sn[0], 0, 0);
+      cell(0, -sn[1], 0);
+      cell(0, 0, -sn[2]);
+      constexpr float keep1 = 1.f - 0x1p-20f;
+      const float ge = fminf(fminf(sq3(gn[0], gn[1], 0.f), sq3(gn[0], 0.f, gn[2])),
+                             sq3(0.f, gn[1], gn[2]));
+      if (!(ge * keep1 > bdist())) {
+        for (int e = 0; e < 12; ++e) {  // (a, b) axis pair with signs
+          const int pr = e >> 2, sa = (e & 1) ? 1 : -1, sb = (e & 2) ? 1 : -1;
+          const int dx = pr == 2 ? 0 : sa, dy = pr == 0 ? sb : (pr == 1 ? 0 : sa);
+          const int dz = pr == 0 ? 0 : sb;
+          cell(dx, dy, dz);
+        }
+        if (!(sq3(gn[0], gn[1], gn[2]) * keep1 > bdist()))
+          for (int c = 0; c < 8; ++c)
+            cell((c & 1) ? 1 : -1, (c & 2) ? 1 : -1, (c & 4) ? 1 : -1);
+      }
+      rdone = 1;
+    }
+    for (int r = 2; r <= rmax && bdist() == Lim<float>::inf(); ++r) {
       const int z0 = max(-r, -ci[2]), z1 = min(r, ga[2] - 1 - ci[2]);
       const int y0 = max(-r, -ci[1]), y1 = min(r, ga[1] - 1 - ci[1]);
       const int x0 = max(-r, -ci[0]), x1 = min(r, ga[0] - 1 - ci[0]);
