@@ -16,8 +16,10 @@ FETCH_SIZE/WRITE_SIZE runs summarised in profiles/.  The CPU baseline is the ref
 plus autograd backward), chunked, on a bounded sample, on the host's cores.
 
 Secondary lines (other BASELINE configs, reported under "secondary"):
-knn_points c3, FPS c4 (ms), gather_points c4 fwd/bwd (GB/s), each with a
-bounded CPU baseline of the reference CPU kernels' restatement (oracle/).
+Chamfer c2 in float16, knn_points c3, knn_points c5 (bfloat16, matrix
+cores), FPS c4 (ms), gather_points c4 fwd/bwd (GB/s); the KNN and FPS lines
+carry a bounded CPU baseline of the reference CPU kernels' restatement
+(oracle/).
 
 Prints exactly one JSON line.
 """
@@ -163,6 +165,19 @@ def chamfer_forward_paths(torch, p1, p2, reps):
     torch.cuda.synchronize()
     res["pairs_evaluated"] = int(pairs.item())
     return res
+
+
+def bench_chamfer_fp16(tpo, torch, steps):
+    """Config 2's float16 variant: ChamferDistance('mean') forward + backward."""
+    import workloads
+
+    p1, p2 = workloads.chamfer_c2(dtype=torch.float16)
+    dev = torch.device("cuda:0")
+    a = p1.to(dev).requires_grad_(True)
+    b = p2.to(dev).requires_grad_(True)
+    model = tpo.ChamferDistance("mean")
+    sec = time_steps(lambda: torch.autograd.grad(model(a, b), (a, b)), steps, 2, torch)
+    return dict(pairs=2 * a.shape[0] * a.shape[1] * b.shape[1], sec=sec)
 
 
 def bench_knn(tpo, torch, steps):
@@ -413,6 +428,13 @@ def main():
         sec = {"chamfer_dense_c2": {
             "kernel": "chamfer_fwd_filter_kernel<8,16>", "fwd_ms": round(ch["dense_fwd_sec"] * 1e3, 4),
             "achieved_tflops": round(dense, 3), "frac_fp32_peak": round(dense / FP32_PEAK_TFLOPS, 4)}}
+        log("[bench] chamfer c2 fp16")
+        h = bench_chamfer_fp16(tpo, torch, max(3, args.steps // 4))
+        sec["chamfer_c2_fp16"] = {"ms_per_step": round(h["sec"] * 1e3, 4),
+                                  "G_pair_dists_per_s": round(h["pairs"] / h["sec"] / 1e9, 2),
+                                  "note": "fwd+bwd of ChamferDistance('mean'), float16 inputs, "
+                                          "half arithmetic (exact grid search with half "
+                                          "rounding margins)"}
         log("[bench] knn c3")
         kn = bench_knn(tpo, torch, max(3, args.steps // 4))
         sec["knn_c3"] = {"G_pair_dists_per_s_kernel": round(kn["pairs"] / kn["sec_kernel"] / 1e9, 2),

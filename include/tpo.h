@@ -56,10 +56,10 @@ int tpo_abi_version(void);
  *   point of the other cloud; idx1 (B,N), idx2 (B,M) int32: the FIRST index
  *   attaining it.  An empty other cloud gives dist 0, idx 0.
  *   workspace (optional, tpo_chamfer_workspace_size() bytes, 256-byte
- *   aligned; size 0 means none is used): with it, float clouds of at least
- *   2048 points each are searched with exact spatial pruning, which is much
- *   faster on clustered or spread-out data; results are identical with or
- *   without it.
+ *   aligned; size 0 means none is used): with it, float and half clouds of
+ *   at least 2048 points each are searched with exact spatial pruning, which
+ *   is much faster on clustered or spread-out data; results are identical
+ *   with or without it.
  */
 int64_t tpo_chamfer_workspace_size(int dtype, int64_t B, int64_t N, int64_t M);
 int tpo_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2,

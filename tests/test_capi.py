@@ -66,7 +66,9 @@ def test_argument_errors_are_reported(lib):
     lib.tpo_chamfer_workspace_size.restype = I
     assert lib.tpo_chamfer_workspace_size(0, 32, 8192, 8192) > 32 * 16384 * 20
     assert lib.tpo_chamfer_workspace_size(0, 2, 100, 8192) == 0    # too small to prune
-    assert lib.tpo_chamfer_workspace_size(1, 32, 8192, 8192) == 0  # float only
+    assert lib.tpo_chamfer_workspace_size(1, 32, 8192, 8192) == 0  # no pruned double path
+    assert lib.tpo_chamfer_workspace_size(2, 32, 8192, 8192) == \
+        lib.tpo_chamfer_workspace_size(0, 32, 8192, 8192)  # half: same float4 layout
     assert lib.tpo_chamfer_workspace_size(0, -1, 3, 3) == -1
     # fused module loss: the forward's workspace (grid search or none), both
     # distance arrays, 2 x 256 chunk sums (doubles), a workgroup counter;

@@ -253,6 +253,15 @@ def _pruned_case(kind, g):
         p2[0, 77] = 2.0 ** 62
         p1[1, 5, 1] = -1e30
         return p1, p2
+    if kind == "half_subnormal":  # squared differences below half's normal range
+        return (torch.randn(2, 2500, 3, generator=g) * 3e-3,
+                torch.randn(2, 2300, 3, generator=g) * 3e-3)
+    if kind == "half_overflow":  # far pairs overflow to inf in half; near ones do not
+        return (torch.randn(2, 2400, 3, generator=g) * 150,
+                torch.randn(2, 2600, 3, generator=g) * 150)
+    if kind == "half_all_inf":  # every distance inf in half: ties everywhere
+        return (torch.rand(1, 2100, 3, generator=g) + 300.0,
+                torch.rand(1, 2200, 3, generator=g) - 300.0)
     if kind == "nonfinite":
         p1, p2 = torch.randn(3, 2100, 3, generator=g), torch.randn(3, 2600, 3, generator=g)
         p2[0, 1000, 0] = float("nan")   # reference cloud with a NaN: every query re-scanned
@@ -265,14 +274,25 @@ def _pruned_case(kind, g):
 @pytest.mark.parametrize("kind", ["uniform", "blobs", "flat", "single_point", "apart",
                                   "duplicates", "lattice", "line", "tiny", "offset", "huge",
                                   "nonfinite"])
-def test_pruned_forward_vs_oracle(tpo, O, dev, kind):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_pruned_forward_vs_oracle(tpo, O, dev, kind, dtype):
     g = torch.Generator().manual_seed(len(kind))
     p1, p2 = _pruned_case(kind, g)
     assert min(p1.shape[1], p2.shape[1]) >= 2048
-    check_vs_oracle(O, dev, p1.float(), p2.float())
+    check_vs_oracle(O, dev, p1.to(dtype), p2.to(dtype))
 
 
-def test_pruned_equals_dense_and_counts_pairs(tpo, dev):
+@pytest.mark.parametrize("kind", ["half_subnormal", "half_overflow", "half_all_inf"])
+def test_pruned_half_rounding_cases_vs_oracle(tpo, O, dev, kind):
+    # the half search prunes with margins for half rounding, subnormal
+    # intermediates and overflow to inf
+    g = torch.Generator().manual_seed(len(kind))
+    p1, p2 = _pruned_case(kind, g)
+    check_vs_oracle(O, dev, p1.half(), p2.half())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_pruned_equals_dense_and_counts_pairs(tpo, dev, dtype):
     import ctypes
     from torch_point_ops import _native
 
@@ -282,16 +302,19 @@ def test_pruned_equals_dense_and_counts_pairs(tpo, dev):
     lib.tpo_chamfer_workspace_size.argtypes = [ctypes.c_int, I, I, I]
     lib.tpo_chamfer_workspace_size.restype = I
     lib.tpo_chamfer_pairs_evaluated.argtypes = [ctypes.c_int, P, I, I, I, P, P]
-    p1, p2 = (t.to(dev) for t in workloads.chamfer_c2())
+    p1, p2 = (t.to(dev) for t in workloads.chamfer_c2(dtype=dtype))
+    code = 0 if dtype == torch.float32 else 2
     B, N, M = p1.shape[0], p1.shape[1], p2.shape[1]
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     outs = []
-    ws = torch.empty(lib.tpo_chamfer_workspace_size(0, B, N, M), dtype=torch.uint8, device=dev)
+    ws = torch.empty(lib.tpo_chamfer_workspace_size(code, B, N, M), dtype=torch.uint8,
+                     device=dev)
     for w in (None, ws):
-        d1, d2 = torch.empty(B, N, device=dev), torch.empty(B, M, device=dev)
+        d1 = torch.empty(B, N, device=dev, dtype=dtype)
+        d2 = torch.empty(B, M, device=dev, dtype=dtype)
         i1 = torch.empty(B, N, dtype=torch.int32, device=dev)
         i2 = torch.empty(B, M, dtype=torch.int32, device=dev)
-        rc = lib.tpo_chamfer_fwd(0, p1.data_ptr(), p2.data_ptr(), B, N, M, d1.data_ptr(),
+        rc = lib.tpo_chamfer_fwd(code, p1.data_ptr(), p2.data_ptr(), B, N, M, d1.data_ptr(),
                                  d2.data_ptr(), i1.data_ptr(), i2.data_ptr(),
                                  None if w is None else w.data_ptr(),
                                  0 if w is None else w.numel(), stream)
@@ -300,7 +323,7 @@ def test_pruned_equals_dense_and_counts_pairs(tpo, dev):
     for a, b in zip(*outs):
         assert torch.equal(a, b)
     pairs = torch.zeros(1, dtype=torch.int64, device=dev)
-    assert lib.tpo_chamfer_pairs_evaluated(0, ws.data_ptr(), B, N, M, pairs.data_ptr(),
+    assert lib.tpo_chamfer_pairs_evaluated(code, ws.data_ptr(), B, N, M, pairs.data_ptr(),
                                            stream) == 0
     n = int(pairs.item())
     assert 0 < n < 2 * B * N * M

@@ -802,7 +802,8 @@ static void loss_reduce(const LossLayout& L, char* ws, int64_t B, int64_t N, int
 using namespace tpo;
 
 static bool prune_applies(int dtype, int64_t B, int64_t N, int64_t M) {
-  return dtype == TPO_F32 && B > 0 && N >= CH_PRUNE_MIN && M >= CH_PRUNE_MIN;
+  return (dtype == TPO_F32 || dtype == TPO_F16) && B > 0 && N >= CH_PRUNE_MIN &&
+         M >= CH_PRUNE_MIN;
 }
 
 extern "C" int64_t tpo_chamfer_workspace_size(int dtype, int64_t B, int64_t N, int64_t M) {
@@ -827,8 +828,8 @@ extern "C" int tpo_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2, in
     if (workspace_bytes < need)
       return set_error(TPO_ERR_WORKSPACE, "tpo_chamfer_fwd: workspace of %lld bytes < %lld",
                        (long long)workspace_bytes, (long long)need);
-    launch_chamfer_fwd_prune(xyz1, xyz2, (int)B, (int)N, (int)M, dist1, dist2, idx1, idx2,
-                             workspace, s);
+    launch_chamfer_fwd_prune(dtype, xyz1, xyz2, (int)B, (int)N, (int)M, dist1, dist2, idx1,
+                             idx2, workspace, s);
     return check_launch("tpo_chamfer_fwd");
   }
   switch (dtype) {
@@ -903,8 +904,8 @@ extern "C" int tpo_chamfer_loss_fwd(int dtype, const void* xyz1, const void* xyz
   const bool grid = B > 0 && N + M > 0 && prune_applies(dtype, B, N, M);
   if (B > 0 && N + M > 0) {
     if (grid)
-      launch_chamfer_fwd_prune(xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2, w + L.fwd,
-                               s, (uint32_t*)(w + L.done));
+      launch_chamfer_fwd_prune(dtype, xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2,
+                               w + L.fwd, s, (uint32_t*)(w + L.done));
     else if (dtype == TPO_F32)
       fwd_dispatch<float>(xyz1, xyz2, (int)B, (int)N, (int)M, d1, d2, idx1, idx2, s);
     else if (dtype == TPO_F64)

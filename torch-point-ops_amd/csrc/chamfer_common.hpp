@@ -116,14 +116,14 @@ __device__ __forceinline__ void merge_chunks(const T* sd, const int* si, T& d, i
   }
 }
 
-// Exact grid-search float forward (chamfer_grid.hip).
+// Exact grid-search forward for float and half clouds (chamfer_grid.hip).
 constexpr int CH_PRUNE_MIN = 2048;  // both clouds at least this large
 int64_t chamfer_prune_workspace(int64_t B, int64_t N, int64_t M);
-// `zero` (optional): a device word the sort kernel sets to 0 before the
-// search runs (the loss reduction's workgroup counter).
-void launch_chamfer_fwd_prune(const void* x1, const void* x2, int B, int N, int M, void* d1,
-                              void* d2, int32_t* i1, int32_t* i2, void* ws, hipStream_t s,
-                              uint32_t* zero = nullptr);
+// dtype: TPO_F32 or TPO_F16.  `zero` (optional): a device word the sort
+// kernel sets to 0 before the search runs (the loss reduction's counter).
+void launch_chamfer_fwd_prune(int dtype, const void* x1, const void* x2, int B, int N, int M,
+                              void* d1, void* d2, int32_t* i1, int32_t* i2, void* ws,
+                              hipStream_t s, uint32_t* zero = nullptr);
 void launch_chamfer_prune_stats(const void* ws, int64_t B, int64_t N, int64_t M, int64_t* out,
                                 hipStream_t s);
 

@@ -1,6 +1,9 @@
-// chamfer_grid.hip -- Chamfer forward for float clouds by exact grid search
-// (replaces chamfer_dist_kernel, chamfer.cu:36-167, when the caller provides
-// a workspace and both clouds have at least CH_PRUNE_MIN points).
+// chamfer_grid.hip -- Chamfer forward for float and half clouds by exact grid
+// search (replaces chamfer_dist_kernel, chamfer.cu:36-167, when the caller
+// provides a workspace and both clouds have at least CH_PRUNE_MIN points).
+// Half coordinates are held as float copies (exact) for the grid; distances
+// are computed in half as the reference does, and the pruning margins cover
+// half rounding (CgMargin).
 //
 // 1. chamfer_grid_sort_kernel, one workgroup per (batch, cloud): the cloud's
 //    bounding box, a counting sort of its points into a 32^3 grid of cells
@@ -104,11 +107,45 @@ __device__ __forceinline__ uint32_t cg_code(int cx, int cy, int cz) {
 // per-thread runs of 32 consecutive cells fall in different LDS banks.
 __device__ __forceinline__ int cg_hidx(uint32_t code) { return (int)(code + (code >> 5)); }
 
+// The reference's squared distance (chamfer.cu:64-67) in the input type T,
+// from the float copies of T coordinates the workspace holds (exact); the
+// result is returned as float (exact).
+template <typename T>
+__device__ __forceinline__ float cg_dist(const float4& p, const float4& q);
+template <>
+__device__ __forceinline__ float cg_dist<float>(const float4& p, const float4& q) {
+  return sq3((float)(p.x - q.x), (float)(p.y - q.y), (float)(p.z - q.z));
+}
+template <>
+__device__ __forceinline__ float cg_dist<half_t>(const float4& p, const float4& q) {
+  return (float)sq3((half_t)((half_t)p.x - (half_t)q.x), (half_t)((half_t)p.y - (half_t)q.y),
+                    (half_t)((half_t)p.z - (half_t)q.z));
+}
+
+// Pruning margins: a cell whose float lower bound g2 of the exact squared
+// distance satisfies g2 * lb - abs > best holds no point whose computed
+// distance is <= best, and every point with computed distance <= best lies
+// within sqrt((best + abs) * inv) of the query.  float: the computed
+// distance is within 5u (u = 2^-24) of the exact one, far inside the 2^-20
+// factor.  half: six roundings of relative error <= 2^-11 each, plus the
+// absolute error of subnormal intermediates (< 2^-22 in all), so lb is
+// below (1 - 2^-20)(1 - 2^-11)^6, inv above (1 - 2^-11)^-6 and abs 2^-20.
+template <typename T>
+struct CgMargin;
+template <>
+struct CgMargin<float> {
+  static constexpr float lb = 1.f - 0x1p-20f, abs = 0.f, inv = 1.f;
+};
+template <>
+struct CgMargin<half_t> {
+  static constexpr float lb = 0.997f, abs = 0x1p-20f, inv = 1.003f;
+};
+
 // PPT > 0: every thread keeps its (at most PPT) points in registers across the
 // passes (n <= 1024 * PPT); PPT == 0: the passes reload from memory.
-template <int PPT>
+template <typename TI, int PPT>
 __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
-    const float* __restrict__ xyz1, const float* __restrict__ xyz2, int N, int M,
+    const TI* __restrict__ xyz1, const TI* __restrict__ xyz2, int N, int M,
     char* __restrict__ ws, CgLayout L, uint32_t* __restrict__ zero) {
   // cell counts, then (PPT > 0) the sorted points staged for a coalesced write
   __shared__ __align__(16) uint32_t cnt[CG_CELLS + CG_CELLS / 32];
@@ -122,7 +159,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   if (zero && blockIdx.x == 0 && tid == 0) *zero = 0u;
   const int64_t PN = cg_pad(N), PM = cg_pad(M);
   const int64_t base = (int64_t)b * (PN + PM) + (c ? PN : 0);
-  const float* __restrict__ P = (c ? xyz2 : xyz1) + (size_t)b * n * 3;
+  const TI* __restrict__ P = (c ? xyz2 : xyz1) + (size_t)b * n * 3;
   float* __restrict__ hdr = reinterpret_cast<float*>(ws + L.hdr) + (size_t)blockIdx.x * 16;
   float4* __restrict__ pts = reinterpret_cast<float4*>(ws + L.pts) + base;
   int32_t* __restrict__ cstart =
@@ -135,9 +172,9 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const int k = min(tid + 1024 * i, n - 1);  // duplicates of the last point: harmless below
-      px[i] = P[3 * k];
-      py[i] = P[3 * k + 1];
-      pz[i] = P[3 * k + 2];
+      px[i] = (float)P[3 * k];
+      py[i] = (float)P[3 * k + 1];
+      pz[i] = (float)P[3 * k + 2];
     }
   }
   auto point = [&](int i, int k, float& x, float& y, float& z) {
@@ -146,9 +183,9 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
       y = py[i];
       z = pz[i];
     } else {
-      x = P[3 * k];
-      y = P[3 * k + 1];
-      z = P[3 * k + 2];
+      x = (float)P[3 * k];
+      y = (float)P[3 * k + 1];
+      z = (float)P[3 * k + 2];
     }
   };
   const int iters = PPT > 0 ? PPT : (n + 1023) / 1024;
@@ -295,11 +332,12 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   }
 }
 
-template <int WG>
+template <typename T, int WG>
 __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
-    const float* __restrict__ xyz1, const float* __restrict__ xyz2, int B, int N, int M,
-    int nqb1, int nqb2, const char* __restrict__ ws, CgLayout L, float* __restrict__ dist1,
-    float* __restrict__ dist2, int32_t* __restrict__ idx1, int32_t* __restrict__ idx2) {
+    const T* __restrict__ xyz1, const T* __restrict__ xyz2, int B, int N, int M, int nqb1,
+    int nqb2, const char* __restrict__ ws, CgLayout L, T* __restrict__ dist1,
+    T* __restrict__ dist2, int32_t* __restrict__ idx1, int32_t* __restrict__ idx2) {
+  using Mg = CgMargin<T>;
   const int bid = xcd_logical_block(blockIdx.x, gridDim.x);
   int lb = bid;
   const int g1 = B * nqb1;
@@ -319,9 +357,9 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
   const int32_t* __restrict__ cstart =
       reinterpret_cast<const int32_t*>(ws + L.cstart) + (size_t)(2 * b + cr) * CG_CSTRIDE;
   const float* __restrict__ h = reinterpret_cast<const float*>(ws + L.hdr) + (2 * b + cr) * 16;
-  const float* __restrict__ rp = (dir ? xyz1 : xyz2) + (size_t)b * nr * 3;  // original order
-  const float* __restrict__ qp = (dir ? xyz2 : xyz1) + (size_t)b * nq * 3;
-  float* __restrict__ dout = (dir ? dist2 : dist1) + (size_t)b * nq;
+  const T* __restrict__ rp = (dir ? xyz1 : xyz2) + (size_t)b * nr * 3;  // original order
+  const T* __restrict__ qp = (dir ? xyz2 : xyz1) + (size_t)b * nq * 3;
+  T* __restrict__ dout = (dir ? dist2 : dist1) + (size_t)b * nq;
   int32_t* __restrict__ iout = (dir ? idx2 : idx1) + (size_t)b * nq;
 
   const int lane = lane_id(), w = wave_id();
@@ -365,7 +403,7 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
           p[u] = *reinterpret_cast<const float4*>(rsb + (uint32_t)min(j + u, j1 - 1) * 16u);
 #pragma unroll
         for (int u = 0; u < CG_UNROLL; ++u) {
-          const float d = sq3((float)(p[u].x - q.x), (float)(p[u].y - q.y), (float)(p[u].z - q.z));
+          const float d = cg_dist<T>(p[u], q);
           const uint64_t key = ((uint64_t)__float_as_uint(d) << 32) | __float_as_uint(p[u].w);
           bkey = key < bkey ? key : bkey;
         }
@@ -382,7 +420,7 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
         const float chi = (ga[a] > 1 ? glo[a] + (float)(cc[a] + 1) * cs[a] : ghi[a]) + eps[a];
         gap[a] = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
       }
-      if (sq3(gap[0], gap[1], gap[2]) * (1.f - 0x1p-20f) > bdist()) return;
+      if (sq3(gap[0], gap[1], gap[2]) * Mg::lb - Mg::abs > bdist()) return;
       const uint32_t code = cg_code(cx, cy, cz);
       scan(cstart[code], cstart[code + 1]);
     };
@@ -418,17 +456,16 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
       cell(-sn[0], 0, 0);
       cell(0, -sn[1], 0);
       cell(0, 0, -sn[2]);
-      constexpr float keep1 = 1.f - 0x1p-20f;
       const float ge = fminf(fminf(sq3(gn[0], gn[1], 0.f), sq3(gn[0], 0.f, gn[2])),
                              sq3(0.f, gn[1], gn[2]));
-      if (!(ge * keep1 > bdist())) {
+      if (!(ge * Mg::lb - Mg::abs > bdist())) {
         for (int e = 0; e < 12; ++e) {  // (a, b) axis pair with signs
           const int pr = e >> 2, sa = (e & 1) ? 1 : -1, sb = (e & 2) ? 1 : -1;
           const int dx = pr == 2 ? 0 : sa, dy = pr == 0 ? sb : (pr == 1 ? 0 : sa);
           const int dz = pr == 0 ? 0 : sb;
           cell(dx, dy, dz);
         }
-        if (!(sq3(gn[0], gn[1], gn[2]) * keep1 > bdist()))
+        if (!(sq3(gn[0], gn[1], gn[2]) * Mg::lb - Mg::abs > bdist()))
           for (int c = 0; c < 8; ++c)
             cell((c & 1) ? 1 : -1, (c & 2) ? 1 : -1, (c & 4) ? 1 : -1);
       }
@@ -460,7 +497,7 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     // few u, well inside the 2^-20 margin).
     int blo[3], bhi[3];
     const float bd = bdist();
-    const float rad = __builtin_sqrtf(bd) * (1.f + 0x1p-19f);
+    const float rad = __builtin_sqrtf((bd + Mg::abs) * Mg::inv) * (1.f + 0x1p-19f);
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
       const float ra = rad + eps[a] + 0x1p-20f * __builtin_fabsf(qv[a]);
@@ -473,27 +510,26 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
       const float g = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
       return g * g;
     };
-    constexpr float keep = 1.f - 0x1p-20f;
     for (int cz = blo[2]; cz <= bhi[2]; ++cz) {
       const float gz = gap2(2, cz);
-      if (gz * keep > bdist()) continue;
+      if (gz * Mg::lb - Mg::abs > bdist()) continue;
       const uint32_t kz = cg_spread((uint32_t)cz) << 2;
       const int dz = abs(cz - ci[2]);
       for (int cy = blo[1]; cy <= bhi[1]; ++cy) {
         const float gzy = gz + gap2(1, cy);
-        if (gzy * keep > bdist()) continue;
+        if (gzy * Mg::lb - Mg::abs > bdist()) continue;
         const uint32_t kzy = kz | (cg_spread((uint32_t)cy) << 1);
         const int dzy = max(dz, abs(cy - ci[1]));
         for (int cx = blo[0]; cx <= bhi[0]; ++cx) {
           if (max(dzy, abs(cx - ci[0])) <= rdone) continue;
-          if ((gzy + gap2(0, cx)) * keep > bdist()) continue;
+          if ((gzy + gap2(0, cx)) * Mg::lb - Mg::abs > bdist()) continue;
           const uint32_t code = kzy | cg_spread((uint32_t)cx);
           const int j0 = cstart[code], j1 = cstart[code + 1];
           scan(j0, j1);
         }
       }
     }
-    dout[oq] = bdist();
+    dout[oq] = (T)bdist();
     iout[oq] = (int)(uint32_t)bkey;
   }
   {  // points evaluated by this wave
@@ -509,11 +545,11 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     const int l = __builtin_ctzll(fb);
     fb &= fb - 1;
     const int o = __shfl(oq, l);
-    float md;
+    T md;
     int mi;
     chunk_scan(qp[3 * o], qp[3 * o + 1], qp[3 * o + 2], rp, 0, nr, lane, md, mi);
     if (mi == 0x7fffffff) {  // no reference counts: cannot happen with nr > 0
-      md = 0.f;
+      md = (T)0;
       mi = 0;
     }
     if (lane == 0) {
@@ -539,20 +575,29 @@ int64_t chamfer_prune_workspace(int64_t B, int64_t N, int64_t M) {
   return cg_layout(B, N, M).total;
 }
 
-void launch_chamfer_fwd_prune(const void* x1, const void* x2, int B, int N, int M, void* d1,
-                              void* d2, int32_t* i1, int32_t* i2, void* ws, hipStream_t s,
-                              uint32_t* zero) {
+template <typename T>
+static void launch_prune(const void* x1, const void* x2, int B, int N, int M, void* d1, void* d2,
+                         int32_t* i1, int32_t* i2, void* ws, hipStream_t s, uint32_t* zero) {
   const CgLayout L = cg_layout(B, N, M);
   if (std::max(N, M) <= 1024 * 8)
-    hipLaunchKernelGGL(chamfer_grid_sort_kernel<8>, dim3(2 * B), dim3(1024), 0, s,
-                       (const float*)x1, (const float*)x2, N, M, (char*)ws, L, zero);
+    hipLaunchKernelGGL((chamfer_grid_sort_kernel<T, 8>), dim3(2 * B), dim3(1024), 0, s,
+                       (const T*)x1, (const T*)x2, N, M, (char*)ws, L, zero);
   else
-    hipLaunchKernelGGL(chamfer_grid_sort_kernel<0>, dim3(2 * B), dim3(1024), 0, s,
-                       (const float*)x1, (const float*)x2, N, M, (char*)ws, L, zero);
+    hipLaunchKernelGGL((chamfer_grid_sort_kernel<T, 0>), dim3(2 * B), dim3(1024), 0, s,
+                       (const T*)x1, (const T*)x2, N, M, (char*)ws, L, zero);
   const int nqb1 = (N + CG_WG - 1) / CG_WG, nqb2 = (M + CG_WG - 1) / CG_WG;
-  hipLaunchKernelGGL((chamfer_grid_search_kernel<CG_WG>), dim3(B * (nqb1 + nqb2)), dim3(CG_WG), 0,
-                     s, (const float*)x1, (const float*)x2, B, N, M, nqb1, nqb2, (const char*)ws,
-                     L, (float*)d1, (float*)d2, i1, i2);
+  hipLaunchKernelGGL((chamfer_grid_search_kernel<T, CG_WG>), dim3(B * (nqb1 + nqb2)),
+                     dim3(CG_WG), 0, s, (const T*)x1, (const T*)x2, B, N, M, nqb1, nqb2,
+                     (const char*)ws, L, (T*)d1, (T*)d2, i1, i2);
+}
+
+void launch_chamfer_fwd_prune(int dtype, const void* x1, const void* x2, int B, int N, int M,
+                              void* d1, void* d2, int32_t* i1, int32_t* i2, void* ws,
+                              hipStream_t s, uint32_t* zero) {
+  if (dtype == TPO_F16)
+    launch_prune<half_t>(x1, x2, B, N, M, d1, d2, i1, i2, ws, s, zero);
+  else
+    launch_prune<float>(x1, x2, B, N, M, d1, d2, i1, i2, ws, s, zero);
 }
 
 void launch_chamfer_prune_stats(const void* ws, int64_t B, int64_t N, int64_t M, int64_t* out,
