@@ -401,8 +401,9 @@ def main():
                    "pairs_per_step": ch["pairs"], "parallelism": "single GPU"},
         "roofline": {"bound": "mfma",
                      "compute_unit": "VALU (fp32 vector ALU; 157.3 TFLOP/s is MI355X's fp32 peak)",
-                     "kernel": "chamfer_grid_sort_kernel + chamfer_grid_search_kernel<256> "
-                               "(+ chamfer_loss_part/final_kernel: the module's fused mean)",
+                     "kernel": "chamfer_grid_sort_kernel<float,8> + chamfer_grid_search_kernel"
+                               "<float,256> + chamfer_loss_part_kernel<float,true> (the "
+                               "module's fused mean)",
                      "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
                      "traffic": traffic, "fwd_ms": round(ch["loss_fwd_sec"] * 1e3, 4),
