@@ -154,6 +154,23 @@ int tpo_knn_fwd(int dtype, const void* p1, const void* p2,
                 void* stream);
 
 /*
+ * KNN forward with the rows sorted the way knn_points(return_sorted=True)
+ * returns them (torch_point_ops/knn/__init__.py:111-131: torch's sort of
+ * each row after the forward, slots past lengths2 keyed +inf, then zeroed).
+ * No single counterpart in the reference: the forward and the module's sort
+ * in one launch.  F32/F64/F16 with 2 <= K <= 32 only; arguments and padding
+ * as tpo_knn_fwd.  Each row is sorted by replaying torch's 32-wide bitonic
+ * network, so equal distances come out in the same order as torch.sort
+ * puts them.
+ */
+int tpo_knn_fwd_sorted(int dtype, const void* p1, const void* p2,
+                       const int64_t* lengths1, const int64_t* lengths2,
+                       int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,
+                       int norm, int version, int64_t* idxs, void* dists,
+                       int* version_out, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
+/*
  * KNN backward.  Replaces knn_cuda_backward (knn.cu:469-534),
  * torch_point_ops_knn::knn_backward (knn.cpp:170-171).
  *   idxs / grad_dists (N,P1,K); grad_p1 (N,P1,D), grad_p2 (N,P2,D) `dtype`.

@@ -102,6 +102,77 @@ def test_config3_subset_exact_and_full_properties(tpo, O, dev):
         assert torch.allclose(at, sd[n, :a].double(), rtol=1e-6, atol=1e-9)
 
 
+def _module_sort(idxs, dists, lengths2, K):
+    # knn_points' sort after the forward (reference knn/__init__.py:111-131)
+    if lengths2.min() < K:
+        mask = lengths2[:, None] <= torch.arange(K, device=dists.device)[None]
+        mask = mask[:, None].expand(-1, dists.shape[1], -1)
+        keyed = dists.clone()
+        keyed[mask] = torch.tensor(float("inf"), dtype=dists.dtype, device=dists.device)
+        ds, order = keyed.sort(dim=2)
+        ds[mask] = torch.tensor(0, dtype=dists.dtype, device=dists.device)
+    else:
+        ds, order = dists.sort(dim=2)
+    return idxs.gather(2, order), ds
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
+@pytest.mark.parametrize("K", [2, 3, 5, 8, 16, 17, 32])
+@pytest.mark.parametrize("case", ["lattice", "ragged", "nonfinite", "highd"])
+def test_sorted_rows_in_kernel_match_torch_sort(tpo, dev, dtype, K, case):
+    # knn_points(return_sorted=True) sorts inside the kernel by replaying
+    # torch's network: rows, ties and padding must equal the forward
+    # followed by the reference module's torch sort
+    g = torch.Generator().manual_seed(K * 7 + len(case))
+    D = 3
+    if case == "lattice":  # integer points: many exactly equal distances
+        p1 = torch.randint(0, 4, (2, 300, 3), generator=g).float()
+        p2 = torch.randint(0, 4, (2, 200, 3), generator=g).float()
+        l1, l2 = torch.tensor([300, 250]), torch.tensor([200, 120])
+    elif case == "ragged":  # one cloud with fewer points than K
+        p1 = torch.randn(3, 200, 3, generator=g)
+        p2 = torch.randn(3, 150, 3, generator=g).round(decimals=1)
+        l1, l2 = torch.tensor([200, 180, 7]), torch.tensor([150, max(1, K // 2), 40])
+    elif case == "nonfinite":
+        p1 = torch.randn(2, 100, 3, generator=g)
+        p2 = torch.randn(2, 120, 3, generator=g)
+        p2[0, 3, 1] = float("inf")
+        p2[1, 5:9, 0] = float("nan")
+        p1[1, 2, 2] = float("inf")
+        l1, l2 = torch.tensor([100, 100]), torch.tensor([120, 120])
+    else:
+        D = 5
+        p1 = torch.randint(0, 3, (2, 150, D), generator=g).float()
+        p2 = torch.randint(0, 3, (2, 180, D), generator=g).float()
+        l1, l2 = torch.tensor([150, 90]), torch.tensor([180, 100])
+    a, b = p1.to(dev, dtype), p2.to(dev, dtype)
+    la, lb = l1.to(dev), l2.to(dev)
+    for version in (-1, 0, 1, 2, 3):
+        for norm in (1, 2):
+            si, sd = tpo.knn_points(a, b, la, lb, norm=norm, K=K, version=version)
+            ri, rd = torch.ops.torch_point_ops_knn.knn_forward(a, b, la, lb, norm, K, version)
+            ei, ed = _module_sort(ri, rd, lb, K)
+            assert torch.equal(si, ei), (version, norm)
+            assert torch.equal(sd.isnan(), ed.isnan())
+            assert torch.equal(torch.nan_to_num(sd), torch.nan_to_num(ed)), (version, norm)
+
+
+def test_sorted_rows_config3_and_gradient(tpo, dev):
+    p1, p2, l1, l2 = (t.to(dev) for t in workloads.knn_c3())
+    si, sd = tpo.knn_points(p1, p2, l1, l2, K=16)
+    ri, rd = torch.ops.torch_point_ops_knn.knn_forward(p1, p2, l1, l2, 2, 16, -1)
+    ei, ed = _module_sort(ri, rd, l2, 16)
+    assert torch.equal(si, ei) and torch.equal(sd, ed)
+    a = p1[:2, :500].clone().requires_grad_(True)
+    b = p2[:2, :700].clone().requires_grad_(True)
+    la = torch.tensor([500, 300], device=dev)
+    lb = torch.tensor([700, 10], device=dev)
+    ga, gb = torch.autograd.grad(tpo.knn_points(a, b, la, lb, K=16)[1].square().sum(), (a, b))
+    ri, rd = torch.ops.torch_point_ops_knn.knn_forward(a, b, la, lb, 2, 16, -1)
+    ra, rb = torch.autograd.grad(_module_sort(ri, rd, lb, 16)[1].square().sum(), (a, b))
+    assert torch.allclose(ga, ra, rtol=1e-5, atol=1e-6) and torch.allclose(gb, rb, rtol=1e-5, atol=1e-6)
+
+
 def test_knn_points_sorted_and_gather(tpo, O, dev):
     g = torch.Generator().manual_seed(22)
     p1 = torch.randn(3, 40, 3, generator=g)
@@ -214,6 +285,9 @@ def test_module_opcheck_compile_precision(tpo, dev):
     assert nn.shape == (2, 8, 3, 3)
     l = torch.tensor([3], device=dev)
     opcheck(torch.ops.torch_point_ops_knn.knn_forward.default,
+            (p1[:1, :3].contiguous(), p2[:1, :3].contiguous(), l, l, 2, 2, -1),
+            raise_exception=True)
+    opcheck(torch.ops.torch_point_ops_knn.knn_forward_sorted.default,
             (p1[:1, :3].contiguous(), p2[:1, :3].contiguous(), l, l, 2, 2, -1),
             raise_exception=True)
     m = tpo.KNearestNeighbors(K=3).to(dev)

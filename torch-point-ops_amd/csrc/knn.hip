@@ -254,12 +254,61 @@ __global__ __launch_bounds__(1024) void knn_order_kernel(const T* __restrict__ p
   for (int k = L1 + tid; k < P1; k += 1024) out[k] = k;  // rows past lengths1 keep their place
 }
 
-template <typename T, int DT, int NORM, int KC>
+// knn_points(return_sorted=True) sorts each row with torch's sort along the
+// last dim (knn/__init__.py:111-131).  For rows of at most 32 entries torch
+// runs a 32-wide bitonic network (entries past the row invalid, sorting last)
+// whose compare-exchange swaps unless the first key is valid and strictly
+// less (NaN counts as largest) -- so ties come out in the network's order, not
+// a stable one.  This replays that network on a lane's row in registers.
+// Only the first KC positions can hold valid entries: KC is a power of two,
+// every exchange within blocks of at most KC positions stays inside one
+// block, and an exchange across position KC (a valid entry against an
+// invalid one) runs in ascending direction, which never moves the entry up.
+template <typename T>
+__device__ __forceinline__ bool knn_isnan(T x) {
+  return x != x;
+}
+template <typename T, int KC>
+__device__ __forceinline__ void knn_sort_row(T (&d)[KC], int (&ix)[KC], uint32_t valid) {
+  auto cas = [&](int a, int b, bool up) {  // branch-free compare-exchange
+    const bool va = (valid >> a) & 1u, vb = (valid >> b) & 1u;
+    const bool lt = !knn_isnan(d[a]) && (knn_isnan(d[b]) || d[a] < d[b]);
+    const bool x = ((lt && va) || !vb) == up;
+    const T da = d[a], db = d[b];
+    const int ia = ix[a], ib = ix[b];
+    d[a] = x ? db : da;
+    d[b] = x ? da : db;
+    ix[a] = x ? ib : ia;
+    ix[b] = x ? ia : ib;
+    valid ^= (x && va != vb) ? (1u << a) | (1u << b) : 0u;
+  };
+#pragma unroll
+  for (int size = 2; size < 32; size *= 2)
+#pragma unroll
+    for (int stride = size / 2; stride > 0; stride /= 2)
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int a = 2 * t - (t & (stride - 1));
+        if (a + stride < KC) cas(a, a + stride, (t & (size / 2)) != 0);
+      }
+#pragma unroll
+  for (int stride = 16; stride > 0; stride /= 2)
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int a = 2 * t - (t & (stride - 1));
+      if (a + stride < KC) cas(a, a + stride, false);
+    }
+}
+
+// mode bit 0: RegisterMinK<2> (version 3, K = 2); bit 1 (= SORT): rows
+// sorted as knn_points(return_sorted=True) returns them (knn_sort_row).
+template <typename T, int DT, int NORM, int KC, bool SORT>
 __global__ __launch_bounds__(256) void knn_fwd_kernel(
     const T* __restrict__ p1, const T* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, const int32_t* __restrict__ order, int P1, int P2, int D,
-    int K, int nqb, int pad_sentinel, int sorted2, int64_t* __restrict__ idxs,
+    int K, int nqb, int pad_sentinel, int mode, int64_t* __restrict__ idxs,
     T* __restrict__ dists) {
+  const int sorted2 = mode & 1;
   // float D=3: reference points reach the lanes through a wave-private LDS
   // block (each lane stages one, every lane reads them back as broadcasts),
   // so the whole wave takes part in every chunk; lanes without a query run
@@ -422,6 +471,26 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
   if (!act) return;
   const int64_t pad_i = pad_sentinel ? -1 : 0;
   const T pad_d = pad_sentinel ? Lim<T>::inf() : (T)0;
+  if constexpr (SORT) {
+    // the module's sort: slots past the reference count key as +inf, sort
+    // last and read 0 afterwards (knn/__init__.py:111-131)
+#pragma unroll
+    for (int s = 0; s < KC; ++s) {
+      if (s >= size) {
+        sd[s] = Lim<T>::inf();
+        si[s] = (int)pad_i;
+      }
+    }
+    knn_sort_row<T, KC>(sd, si, K >= 32 ? 0xffffffffu : (1u << K) - 1u);
+#pragma unroll
+    for (int s = 0; s < KC; ++s) {
+      if (s < K) {
+        io[s] = (int64_t)si[s];
+        dout[s] = s < size ? sd[s] : (T)0;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
     if (s < K) {
@@ -538,9 +607,14 @@ void launch_fwd_kc(const void* p1, const void* p2, const int64_t* l1, const int6
                    const int32_t* order, int N, int P1, int P2, int D, int K, int pad,
                    int sorted2, int64_t* idxs, void* dists, hipStream_t s) {
   const int nqb = (P1 + 255) / 256;
-  hipLaunchKernelGGL((knn_fwd_kernel<T, DT, NORM, KC>), dim3(N * nqb), dim3(256), 0, s,
-                     (const T*)p1, (const T*)p2, l1, l2, order, P1, P2, D, K, nqb, pad, sorted2,
-                     idxs, (T*)dists);
+  if (sorted2 & 2)
+    hipLaunchKernelGGL((knn_fwd_kernel<T, DT, NORM, KC, true>), dim3(N * nqb), dim3(256), 0, s,
+                       (const T*)p1, (const T*)p2, l1, l2, order, P1, P2, D, K, nqb, pad, sorted2,
+                       idxs, (T*)dists);
+  else
+    hipLaunchKernelGGL((knn_fwd_kernel<T, DT, NORM, KC, false>), dim3(N * nqb), dim3(256), 0, s,
+                       (const T*)p1, (const T*)p2, l1, l2, order, P1, P2, D, K, nqb, pad, sorted2,
+                       idxs, (T*)dists);
 }
 
 template <typename T, int DT, int NORM>
@@ -631,11 +705,11 @@ extern "C" int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int6
   return ((N * P1 * 4 + 255) / 256) * 256;
 }
 
-extern "C" int tpo_knn_fwd(int dtype, const void* p1, const void* p2, const int64_t* lengths1,
-                           const int64_t* lengths2, int64_t N, int64_t P1, int64_t P2, int64_t D,
-                           int64_t K, int norm, int version, int64_t* idxs, void* dists,
-                           int* version_out, void* workspace, int64_t workspace_bytes,
-                           void* stream) {
+static int knn_fwd_impl(int dtype, const void* p1, const void* p2, const int64_t* lengths1,
+                        const int64_t* lengths2, int64_t N, int64_t P1, int64_t P2, int64_t D,
+                        int64_t K, int norm, int version, int64_t* idxs, void* dists,
+                        int* version_out, void* workspace, int64_t workspace_bytes, void* stream,
+                        bool sort_rows) {
   if (N < 0 || P1 < 0 || P2 < 0 || D < 1 || K < 0 || N >= (1 << 20) || P1 >= (1 << 30) ||
       P2 >= (1 << 30) || D >= (1 << 20) || K >= (1 << 20))
     return set_error(TPO_ERR_ARG, "tpo_knn_fwd: bad sizes");
@@ -663,7 +737,7 @@ extern "C" int tpo_knn_fwd(int dtype, const void* p1, const void* p2, const int6
   if (version_out) *version_out = v;
   if (N == 0 || P1 == 0 || K == 0) return TPO_OK;
   const int pad = v <= 1;
-  const int sorted2 = (v == 3 && K == 2);
+  const int sorted2 = (v == 3 && K == 2) | (sort_rows ? 2 : 0);  // the kernel's mode bits
   // the query ordering is an optimisation: without workspace, keep row order
   int32_t* order = (workspace && workspace_bytes >= N * P1 * 4) ? (int32_t*)workspace : nullptr;
   hipStream_t s = (hipStream_t)stream;
@@ -674,6 +748,29 @@ extern "C" int tpo_knn_fwd(int dtype, const void* p1, const void* p2, const int6
     default: return set_error(TPO_ERR_DTYPE, "tpo_knn_fwd: unsupported dtype %d", dtype);
   }
   return check_launch("tpo_knn_fwd");
+}
+
+extern "C" int tpo_knn_fwd(int dtype, const void* p1, const void* p2, const int64_t* lengths1,
+                           const int64_t* lengths2, int64_t N, int64_t P1, int64_t P2, int64_t D,
+                           int64_t K, int norm, int version, int64_t* idxs, void* dists,
+                           int* version_out, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
+  return knn_fwd_impl(dtype, p1, p2, lengths1, lengths2, N, P1, P2, D, K, norm, version, idxs,
+                      dists, version_out, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int tpo_knn_fwd_sorted(int dtype, const void* p1, const void* p2,
+                                  const int64_t* lengths1, const int64_t* lengths2, int64_t N,
+                                  int64_t P1, int64_t P2, int64_t D, int64_t K, int norm,
+                                  int version, int64_t* idxs, void* dists, int* version_out,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  if (dtype != TPO_F32 && dtype != TPO_F64 && dtype != TPO_F16)
+    return set_error(TPO_ERR_DTYPE, "tpo_knn_fwd_sorted: unsupported dtype %d", dtype);
+  if (K < 2 || K > 32)
+    return set_error(TPO_ERR_ARG, "tpo_knn_fwd_sorted: needs 2 <= K <= 32 (got %lld)",
+                     (long long)K);
+  return knn_fwd_impl(dtype, p1, p2, lengths1, lengths2, N, P1, P2, D, K, norm, version, idxs,
+                      dists, version_out, workspace, workspace_bytes, stream, true);
 }
 
 extern "C" int tpo_knn_bwd(int dtype, const void* p1, const void* p2, const int64_t* lengths1,

@@ -234,6 +234,48 @@ std::tuple<at::Tensor, at::Tensor> knn_forward_hip(const at::Tensor& p1_in,
   return {idxs, dists};
 }
 
+// knn_points(return_sorted=True) in one launch: the forward with each row
+// sorted as the module's torch sort leaves it (knn/__init__.py:111-131).
+// float/double/half with 2 <= K <= 32; the module keeps its own sort otherwise.
+std::tuple<at::Tensor, at::Tensor> knn_forward_sorted_hip(const at::Tensor& p1_in,
+                                                          const at::Tensor& p2_in,
+                                                          const at::Tensor& lengths1_in,
+                                                          const at::Tensor& lengths2_in,
+                                                          int64_t norm, int64_t K,
+                                                          int64_t version) {
+  TORCH_CHECK(p1_in.device() == p2_in.device(), "p1 and p2 must be on the same device");
+  TORCH_CHECK(p1_in.device() == lengths1_in.device(),
+              "p1 and lengths1 must be on the same device");
+  TORCH_CHECK(p1_in.device() == lengths2_in.device(),
+              "p1 and lengths2 must be on the same device");
+  check_hip(p1_in, "p1");
+  c10::OptionalDeviceGuard guard(p1_in.device());
+  TORCH_CHECK(p1_in.dim() == 3 && p2_in.dim() == 3, "knn_forward_sorted expects (N,P,D) tensors");
+  const int64_t N = p1_in.size(0), P1 = p1_in.size(1), P2 = p2_in.size(1), D = p1_in.size(2);
+  TORCH_CHECK((norm == 1) || (norm == 2), "Norm must be 1 or 2.");
+  TORCH_CHECK(p2_in.size(2) == D, "Point sets must have the same last dimension");
+  TORCH_CHECK(K >= 2 && K <= 32, "knn_forward_sorted needs 2 <= K <= 32");
+  auto idxs = at::empty({N, P1, K}, lengths1_in.options().dtype(at::kLong));
+  auto dists = at::empty({N, P1, K}, p1_in.options());
+  if (idxs.numel() == 0) return {idxs, dists};
+  TORCH_CHECK(p2_in.size(0) == N && lengths1_in.numel() == N && lengths2_in.numel() == N,
+              "batch sizes differ");
+  TORCH_CHECK(p1_in.scalar_type() == p2_in.scalar_type(), "p1 and p2 dtypes differ");
+  TORCH_CHECK(lengths1_in.scalar_type() == at::kLong && lengths2_in.scalar_type() == at::kLong,
+              "lengths must be int64");
+  const at::Tensor l1 = lengths1_in.contiguous(), l2 = lengths2_in.contiguous();
+  const at::Tensor p1 = p1_in.contiguous(), p2 = p2_in.contiguous();
+  const int dt = dtype_code(p1, "knn_forward_sorted");
+  const int64_t ws = tpo_knn_workspace_size(dt, N, P1, P2, D, K, (int)norm);
+  at::Tensor work = at::empty({ws > 0 ? ws : 1}, p1.options().dtype(at::kByte));
+  check_rc(tpo_knn_fwd_sorted(dt, p1.data_ptr(), p2.data_ptr(), l1.data_ptr<int64_t>(),
+                              l2.data_ptr<int64_t>(), N, P1, P2, D, K, (int)norm, (int)version,
+                              idxs.data_ptr<int64_t>(), dists.data_ptr(), nullptr,
+                              work.data_ptr(), ws, stream_of(p1)),
+           "knn_forward_sorted");
+  return {idxs, dists};
+}
+
 std::tuple<at::Tensor, at::Tensor> knn_backward_hip(const at::Tensor& p1_in,
                                                     const at::Tensor& p2_in,
                                                     const at::Tensor& lengths1_in,
@@ -383,9 +425,13 @@ TORCH_LIBRARY(torch_point_ops_knn, m) {
         "int norm, int K, int version) -> (Tensor, Tensor)");
   m.def("knn_backward(Tensor p1, Tensor p2, Tensor lengths1, Tensor lengths2, "
         "Tensor idxs, int norm, Tensor grad_dists) -> (Tensor, Tensor)");
+  // the forward and knn_points' sort in one launch (no reference schema)
+  m.def("knn_forward_sorted(Tensor p1, Tensor p2, Tensor lengths1, Tensor lengths2, "
+        "int norm, int K, int version) -> (Tensor, Tensor)");
 }
 TORCH_LIBRARY_IMPL(torch_point_ops_knn, CUDA, m) {
   m.impl("knn_forward", &knn_forward_hip);
+  m.impl("knn_forward_sorted", &knn_forward_sorted_hip);
   m.impl("knn_backward", &knn_backward_hip);
 }
 

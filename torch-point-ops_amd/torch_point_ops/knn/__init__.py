@@ -31,6 +31,10 @@ def _knn_setup_context(ctx, inputs, output):
 torch.library.register_autograd(
     "torch_point_ops_knn::knn_forward", _knn_backward, setup_context=_knn_setup_context
 )
+# the sorted forward's rows are a permutation of knn_forward's: same gradient
+torch.library.register_autograd(
+    "torch_point_ops_knn::knn_forward_sorted", _knn_backward, setup_context=_knn_setup_context
+)
 
 
 @torch.library.register_fake("torch_point_ops_knn::knn_forward")
@@ -40,6 +44,15 @@ def _knn_forward_fake(p1, p2, lengths1, lengths2, norm, K, version):
         torch.empty(n, p, K, device=p1.device, dtype=torch.int64),
         torch.empty(n, p, K, device=p1.device, dtype=p1.dtype),
     )
+
+
+@torch.library.register_fake("torch_point_ops_knn::knn_forward_sorted")
+def _knn_forward_sorted_fake(p1, p2, lengths1, lengths2, norm, K, version):
+    return _knn_forward_fake(p1, p2, lengths1, lengths2, norm, K, version)
+
+
+# dtypes whose sorted rows come straight from the kernel (2 <= K <= 32)
+_SORTED_IN_KERNEL = (torch.float32, torch.float64, torch.float16)
 
 
 @torch.library.register_fake("torch_point_ops_knn::knn_backward")
@@ -80,6 +93,13 @@ def knn_points(
         lengths1 = torch.full((N,), P1, dtype=torch.int64, device=p1.device)
     if lengths2 is None:
         lengths2 = torch.full((N,), P2, dtype=torch.int64, device=p1.device)
+
+    if return_sorted and 2 <= K <= 32 and p1.dtype in _SORTED_IN_KERNEL and p1.is_cuda:
+        # the kernel replays the sort below (torch's network, ties included)
+        return torch.ops.torch_point_ops_knn.knn_forward_sorted(
+            p1.contiguous(), p2.contiguous(), lengths1.contiguous(), lengths2.contiguous(),
+            norm, K, version,
+        )
 
     idxs, dists = torch.ops.torch_point_ops_knn.knn_forward(
         p1.contiguous(), p2.contiguous(), lengths1.contiguous(), lengths2.contiguous(),
