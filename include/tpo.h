@@ -171,6 +171,18 @@ int tpo_knn_fwd_sorted(int dtype, const void* p1, const void* p2,
                        void* stream);
 
 /*
+ * knn_gather forward.  Replaces the expand + gather + mask of
+ * knn_gather (torch_point_ops/knn/__init__.py:136-183), which the reference
+ * runs as torch ops.
+ *   x (N,M,U), idx (N,L,K) int64, lengths (N) int64 valid counts of x;
+ *   out (N,L,K,U) of `dtype` (F32/F64/F16/BF16): out[n,l,k] = x[n, idx[n,l,k]]
+ *   for k < lengths[n], else 0 (and 0 for an index outside [0, M)).
+ */
+int tpo_knn_gather(int dtype, const void* x, const int64_t* idx,
+                   const int64_t* lengths, int64_t N, int64_t M, int64_t L, int64_t K,
+                   int64_t U, void* out, void* stream);
+
+/*
  * KNN backward.  Replaces knn_cuda_backward (knn.cu:469-534),
  * torch_point_ops_knn::knn_backward (knn.cpp:170-171).
  *   idxs / grad_dists (N,P1,K); grad_p1 (N,P1,D), grad_p2 (N,P2,D) `dtype`.

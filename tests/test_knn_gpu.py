@@ -173,6 +173,39 @@ def test_sorted_rows_config3_and_gradient(tpo, dev):
     assert torch.allclose(ga, ra, rtol=1e-5, atol=1e-6) and torch.allclose(gb, rb, rtol=1e-5, atol=1e-6)
 
 
+def _torch_knn_gather(x, idx, lengths):
+    # the reference's knn_gather as torch ops (knn/__init__.py:136-183)
+    N, M, U = x.shape
+    K = idx.shape[2]
+    out = x[:, :, None].expand(-1, -1, K, -1).gather(1, idx[..., None].expand(-1, -1, -1, U))
+    if lengths.min() < K:
+        pad = lengths[:, None] <= torch.arange(K, device=x.device)[None]
+        pad = pad[:, None].expand(-1, idx.shape[1], -1)[..., None].expand(-1, -1, -1, U)
+        out[pad] = torch.tensor(0, dtype=x.dtype, device=x.device)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("U", [1, 3, 7])
+def test_knn_gather_kernel_matches_torch_ops(tpo, dev, dtype, U):
+    g = torch.Generator().manual_seed(U)
+    N, M, L, K = 3, 50, 40, 6
+    x = torch.randn(N, M, U, generator=g).to(dev, dtype)
+    idx = torch.randint(0, M, (N, L, K), generator=g).to(dev)
+    lengths = torch.tensor([M, 4, 1], device=dev)
+    got = tpo.knn_gather(x, idx, lengths)
+    assert torch.equal(got, _torch_knn_gather(x, idx, lengths))
+    full = torch.full((N,), M, device=dev)
+    assert torch.equal(tpo.knn_gather(x, idx), _torch_knn_gather(x, idx, full))
+    if dtype in (torch.float32, torch.float64):
+        a = x.clone().requires_grad_(True)
+        b = x.clone().requires_grad_(True)
+        w = torch.randn(N, L, K, U, generator=g).to(dev, dtype)
+        (ga,) = torch.autograd.grad((tpo.knn_gather(a, idx, lengths) * w).sum(), (a,))
+        (gb,) = torch.autograd.grad((_torch_knn_gather(b, idx, lengths) * w).sum(), (b,))
+        assert torch.allclose(ga, gb, rtol=1e-6, atol=1e-6)
+
+
 def test_knn_points_sorted_and_gather(tpo, O, dev):
     g = torch.Generator().manual_seed(22)
     p1 = torch.randn(3, 40, 3, generator=g)
@@ -289,6 +322,10 @@ def test_module_opcheck_compile_precision(tpo, dev):
             raise_exception=True)
     opcheck(torch.ops.torch_point_ops_knn.knn_forward_sorted.default,
             (p1[:1, :3].contiguous(), p2[:1, :3].contiguous(), l, l, 2, 2, -1),
+            raise_exception=True)
+    opcheck(torch.ops.torch_point_ops_knn.knn_gather.default,
+            (p2.clone().requires_grad_(True), torch.randint(0, 10, (2, 8, 3), device=dev),
+             torch.tensor([10, 2], device=dev)),
             raise_exception=True)
     m = tpo.KNearestNeighbors(K=3).to(dev)
     e, c = m(p1[:1], p2[:1]), torch.compile(m)(p1[:1], p2[:1])

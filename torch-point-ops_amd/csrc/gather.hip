@@ -15,6 +15,10 @@
 // value equals the reference's 0 + g exactly.
 // Indices outside [0, N) are ignored (forward writes 0); the reference reads
 // out of bounds there.
+// knn_gather (replaces the expand + gather + mask of knn/__init__.py:136-183):
+// one thread per (cloud, query, neighbour) copies the neighbour's U values,
+// or zeros for slots at or past lengths[n] (the reference's mask, without
+// its host-side lengths.min() test).
 #include "tpo_common.hpp"
 
 #pragma clang fp contract(off)
@@ -117,6 +121,26 @@ __global__ __launch_bounds__(256) void gather_bwd_dup_kernel(const T* __restrict
   }
 }
 
+// E: an unsigned type of the element's size (the values are only copied)
+template <typename E>
+__global__ __launch_bounds__(256) void knn_gather_kernel(const E* __restrict__ x,
+                                                         const int64_t* __restrict__ idx,
+                                                         const int64_t* __restrict__ lengths,
+                                                         int64_t N, int64_t M, int64_t L,
+                                                         int64_t K, int64_t U,
+                                                         E* __restrict__ out) {
+  const int64_t total = N * L * K;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = t / (L * K), k = t % K;
+    const int64_t j = idx[t];
+    const bool ok = k < lengths[n] && j >= 0 && j < M;
+    const E* __restrict__ src = x + (n * M + (ok ? j : 0)) * U;
+    E* __restrict__ dst = out + t * U;
+    for (int64_t u = 0; u < U; ++u) dst[u] = ok ? src[u] : (E)0;
+  }
+}
+
 static unsigned grid_for(int64_t n) {
   int64_t g = (n + 255) / 256;
   if (g > 1 << 20) g = 1 << 20;
@@ -197,4 +221,32 @@ extern "C" int tpo_gather_bwd(int dtype, const void* grad_out, const int64_t* id
     default: return set_error(TPO_ERR_DTYPE, "tpo_gather_bwd: unsupported dtype %d", dtype);
   }
   return check_launch("tpo_gather_bwd");
+}
+
+extern "C" int tpo_knn_gather(int dtype, const void* x, const int64_t* idx,
+                              const int64_t* lengths, int64_t N, int64_t M, int64_t L, int64_t K,
+                              int64_t U, void* out, void* stream) {
+  if (N < 0 || M < 0 || L < 0 || K < 0 || U < 0)
+    return set_error(TPO_ERR_ARG, "tpo_knn_gather: negative size");
+  if (N == 0 || L == 0 || K == 0 || U == 0) return TPO_OK;
+  if (M == 0) return set_error(TPO_ERR_ARG, "tpo_knn_gather: x has no points");
+  hipStream_t s = (hipStream_t)stream;
+  const unsigned g = grid_for(N * L * K);
+  switch (dtype) {
+    case TPO_F32:
+      hipLaunchKernelGGL(knn_gather_kernel<uint32_t>, dim3(g), dim3(256), 0, s,
+                         (const uint32_t*)x, idx, lengths, N, M, L, K, U, (uint32_t*)out);
+      break;
+    case TPO_F64:
+      hipLaunchKernelGGL(knn_gather_kernel<uint64_t>, dim3(g), dim3(256), 0, s,
+                         (const uint64_t*)x, idx, lengths, N, M, L, K, U, (uint64_t*)out);
+      break;
+    case TPO_F16:
+    case TPO_BF16:
+      hipLaunchKernelGGL(knn_gather_kernel<uint16_t>, dim3(g), dim3(256), 0, s,
+                         (const uint16_t*)x, idx, lengths, N, M, L, K, U, (uint16_t*)out);
+      break;
+    default: return set_error(TPO_ERR_DTYPE, "tpo_knn_gather: unsupported dtype %d", dtype);
+  }
+  return check_launch("tpo_knn_gather");
 }

@@ -276,6 +276,39 @@ std::tuple<at::Tensor, at::Tensor> knn_forward_sorted_hip(const at::Tensor& p1_i
   return {idxs, dists};
 }
 
+// knn_gather's expand + gather + mask (knn/__init__.py:136-183) in one launch
+at::Tensor knn_gather_hip(const at::Tensor& x_in, const at::Tensor& idx_in,
+                          const at::Tensor& lengths_in) {
+  check_hip(x_in, "x");
+  c10::OptionalDeviceGuard guard(x_in.device());
+  TORCH_CHECK(x_in.dim() == 3 && idx_in.dim() == 3, "knn_gather expects (N,M,U) and (N,L,K)");
+  const int64_t N = x_in.size(0), M = x_in.size(1), U = x_in.size(2);
+  const int64_t L = idx_in.size(1), K = idx_in.size(2);
+  TORCH_CHECK(idx_in.size(0) == N, "x and idx must have same batch dimension.");
+  TORCH_CHECK(idx_in.scalar_type() == at::kLong && lengths_in.scalar_type() == at::kLong,
+              "idx and lengths must be int64");
+  TORCH_CHECK(lengths_in.numel() == N, "lengths must have one entry per cloud");
+  TORCH_CHECK(x_in.device() == idx_in.device() && x_in.device() == lengths_in.device(),
+              "x, idx and lengths must be on the same device");
+  const at::Tensor x = x_in.contiguous(), idx = idx_in.contiguous();
+  const at::Tensor lengths = lengths_in.contiguous();
+  at::Tensor out = at::empty({N, L, K, U}, x.options());
+  int dt;
+  switch (x.scalar_type()) {
+    case at::kFloat: dt = TPO_F32; break;
+    case at::kDouble: dt = TPO_F64; break;
+    case at::kHalf: dt = TPO_F16; break;
+    case at::kBFloat16: dt = TPO_BF16; break;
+    default: TORCH_CHECK(false, "knn_gather not implemented for '", x.scalar_type(), "'");
+  }
+  TORCH_CHECK(M > 0 || out.numel() == 0, "knn_gather: x has no points");
+  check_rc(tpo_knn_gather(dt, x.data_ptr(), idx.data_ptr<int64_t>(),
+                          lengths.data_ptr<int64_t>(), N, M, L, K, U, out.data_ptr(),
+                          stream_of(x)),
+           "knn_gather");
+  return out;
+}
+
 std::tuple<at::Tensor, at::Tensor> knn_backward_hip(const at::Tensor& p1_in,
                                                     const at::Tensor& p2_in,
                                                     const at::Tensor& lengths1_in,
@@ -428,10 +461,12 @@ TORCH_LIBRARY(torch_point_ops_knn, m) {
   // the forward and knn_points' sort in one launch (no reference schema)
   m.def("knn_forward_sorted(Tensor p1, Tensor p2, Tensor lengths1, Tensor lengths2, "
         "int norm, int K, int version) -> (Tensor, Tensor)");
+  m.def("knn_gather(Tensor x, Tensor idx, Tensor lengths) -> Tensor");
 }
 TORCH_LIBRARY_IMPL(torch_point_ops_knn, CUDA, m) {
   m.impl("knn_forward", &knn_forward_hip);
   m.impl("knn_forward_sorted", &knn_forward_sorted_hip);
+  m.impl("knn_gather", &knn_gather_hip);
   m.impl("knn_backward", &knn_backward_hip);
 }
 

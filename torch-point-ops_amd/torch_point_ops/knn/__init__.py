@@ -55,6 +55,36 @@ def _knn_forward_sorted_fake(p1, p2, lengths1, lengths2, norm, K, version):
 _SORTED_IN_KERNEL = (torch.float32, torch.float64, torch.float16)
 
 
+def _knn_gather_backward(ctx, grad_out):
+    # gather's gradient: scatter-add the rows back (the masked slots carry none)
+    idx, lengths = ctx.saved_tensors
+    if grad_out is None or not ctx.needs_input_grad[0]:
+        return None, None, None
+    N, L, K, U = grad_out.shape
+    keep = (torch.arange(K, device=idx.device)[None] < lengths[:, None])[:, None, :, None]
+    g = (grad_out * keep).reshape(N, L * K, U)
+    j = idx.clamp(0, ctx.M - 1).reshape(N, L * K, 1).expand(-1, -1, U)
+    grad_x = torch.zeros(N, ctx.M, U, dtype=grad_out.dtype, device=grad_out.device)
+    return grad_x.scatter_add_(1, j, g), None, None
+
+
+def _knn_gather_setup_context(ctx, inputs, output):
+    x, idx, lengths = inputs
+    ctx.save_for_backward(idx, lengths)
+    ctx.M = x.shape[1]
+
+
+torch.library.register_autograd(
+    "torch_point_ops_knn::knn_gather", _knn_gather_backward,
+    setup_context=_knn_gather_setup_context,
+)
+
+
+@torch.library.register_fake("torch_point_ops_knn::knn_gather")
+def _knn_gather_fake(x, idx, lengths):
+    return x.new_empty(idx.shape[0], idx.shape[1], idx.shape[2], x.shape[2])
+
+
 @torch.library.register_fake("torch_point_ops_knn::knn_backward")
 def _knn_backward_fake(p1, p2, lengths1, lengths2, idxs, norm, grad_dists):
     return torch.empty_like(p1), torch.empty_like(p2)
@@ -138,6 +168,9 @@ def knn_gather(x: torch.Tensor, idx: torch.Tensor, lengths: torch.Tensor = None)
         raise ValueError("x and idx must have same batch dimension.")
     if lengths is None:
         lengths = torch.full((N,), M, dtype=torch.int64, device=x.device)
+    if x.is_cuda and M > 0:
+        # one kernel for the gather and the mask below (no host-side test)
+        return torch.ops.torch_point_ops_knn.knn_gather(x, idx, lengths.to(torch.int64))
     expanded = idx[:, :, :, None].expand(-1, -1, -1, U)
     out = x[:, :, None].expand(-1, -1, K, -1).gather(1, expanded)
     if lengths.min() < K:
