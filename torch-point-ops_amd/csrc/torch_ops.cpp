@@ -16,6 +16,7 @@
 
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <c10/core/DeviceGuard.h>
+#include <torch/csrc/autograd/custom_function.h>
 
 #include <tuple>
 
@@ -154,6 +155,51 @@ std::tuple<at::Tensor, at::Tensor> chamfer_loss_backward_hip(
                                 g1.data_ptr(), g2.data_ptr(), stream_of(xyz1)),
            "chamfer_loss_backward");
   return {g1, g2};
+}
+
+// Autograd of the fused module loss, in C++: the step's backward runs no
+// Python (the module's gradient is the hot path of ChamferDistance training).
+// Index outputs are non-differentiable and their gradients not materialised.
+class ChamferLossFunction : public torch::autograd::Function<ChamferLossFunction> {
+ public:
+  static torch::autograd::variable_list forward(torch::autograd::AutogradContext* ctx,
+                                                const at::Tensor& xyz1, const at::Tensor& xyz2,
+                                                bool mean) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torch_point_ops_chamfer::chamfer_loss_forward", "")
+                         .typed<std::tuple<at::Tensor, at::Tensor, at::Tensor>(
+                             const at::Tensor&, const at::Tensor&, bool)>();
+    at::Tensor loss, idx1, idx2;
+    {
+      at::AutoDispatchBelowADInplaceOrView below;
+      std::tie(loss, idx1, idx2) = op.call(xyz1, xyz2, mean);
+    }
+    ctx->save_for_backward({xyz1, xyz2, idx1, idx2});
+    ctx->saved_data["mean"] = mean;
+    ctx->mark_non_differentiable({idx1, idx2});
+    ctx->set_materialize_grads(false);
+    return {loss, idx1, idx2};
+  }
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torch_point_ops_chamfer::chamfer_loss_backward", "")
+                         .typed<std::tuple<at::Tensor, at::Tensor>(
+                             const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                             const at::Tensor&, const at::Tensor&, bool)>();
+    if (!grads[0].defined()) return {at::Tensor(), at::Tensor(), at::Tensor()};
+    const auto saved = ctx->get_saved_variables();
+    at::Tensor g1, g2;
+    std::tie(g1, g2) = op.call(saved[0], saved[1], saved[2], saved[3], grads[0],
+                               ctx->saved_data["mean"].toBool());
+    return {g1, g2, at::Tensor()};
+  }
+};
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> chamfer_loss_forward_autograd(
+    const at::Tensor& xyz1, const at::Tensor& xyz2, bool mean) {
+  auto out = ChamferLossFunction::apply(xyz1, xyz2, mean);
+  return {out[0], out[1], out[2]};
 }
 
 // chamfer.cpp:21-31: the reference has no CPU kernel.
@@ -445,6 +491,9 @@ TORCH_LIBRARY_IMPL(torch_point_ops_chamfer, CPU, m) {
   m.impl("chamfer_backward", &chamfer_backward_cpu);
   m.impl("chamfer_loss_forward", &chamfer_loss_forward_cpu);
   m.impl("chamfer_loss_backward", &chamfer_loss_backward_cpu);
+}
+TORCH_LIBRARY_IMPL(torch_point_ops_chamfer, Autograd, m) {
+  m.impl("chamfer_loss_forward", &chamfer_loss_forward_autograd);
 }
 TORCH_LIBRARY_IMPL(torch_point_ops_chamfer, CUDA, m) {
   m.impl("chamfer_forward", &chamfer_forward_hip);

@@ -57,29 +57,8 @@ def _chamfer_backward_fake(xyz1, xyz2, idx1, idx2, grad_dist1, grad_dist2):
     return torch.empty_like(xyz1), torch.empty_like(xyz2)
 
 
-def _chamfer_loss_backward(ctx, grad_loss, grad_idx1, grad_idx2):
-    if grad_loss is None:
-        return None, None, None
-    xyz1, xyz2, idx1, idx2 = ctx.saved_tensors
-    g1, g2 = torch.ops.torch_point_ops_chamfer.chamfer_loss_backward(
-        xyz1, xyz2, idx1, idx2, grad_loss, ctx.mean
-    )
-    return g1, g2, None
-
-
-def _chamfer_loss_setup_context(ctx, inputs, output):
-    xyz1, xyz2, mean = inputs
-    _loss, idx1, idx2 = output
-    ctx.save_for_backward(xyz1, xyz2, idx1, idx2)
-    ctx.mean = mean
-    ctx.set_materialize_grads(False)
-
-
-torch.library.register_autograd(
-    "torch_point_ops_chamfer::chamfer_loss_forward",
-    _chamfer_loss_backward,
-    setup_context=_chamfer_loss_setup_context,
-)
+# chamfer_loss_forward's autograd is registered in C++ (torch_ops.cpp,
+# ChamferLossFunction): the training step's backward runs no Python.
 
 
 @torch.library.register_fake("torch_point_ops_chamfer::chamfer_loss_forward")
