@@ -33,12 +33,52 @@ def test_schemas_match_reference(tpo):
         assert s.split("::", 1)[-1] == schema
 
 
+def test_fused_ops_schemas_and_fake_kernels(tpo):
+    # the extra ops behind ChamferDistance's reduction and knn_points' sort
+    # and gather: schemas, and FakeTensor shapes (what torch.compile traces)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    ops = torch.ops
+    want = {
+        ops.torch_point_ops_chamfer.chamfer_loss_forward:
+            "chamfer_loss_forward(Tensor xyz1, Tensor xyz2, bool mean) -> (Tensor, Tensor, Tensor)",
+        ops.torch_point_ops_chamfer.chamfer_loss_backward:
+            "chamfer_loss_backward(Tensor xyz1, Tensor xyz2, Tensor idx1, Tensor idx2, "
+            "Tensor grad_loss, bool mean) -> (Tensor, Tensor)",
+        ops.torch_point_ops_knn.knn_forward_sorted:
+            "knn_forward_sorted(Tensor p1, Tensor p2, Tensor lengths1, Tensor lengths2, "
+            "int norm, int K, int version) -> (Tensor, Tensor)",
+        ops.torch_point_ops_knn.knn_gather:
+            "knn_gather(Tensor x, Tensor idx, Tensor lengths) -> Tensor",
+    }
+    for op, schema in want.items():
+        assert str(op.default._schema).split("::", 1)[-1] == schema
+    with FakeTensorMode():
+        a, b = torch.empty(2, 7, 3), torch.empty(2, 5, 3)
+        loss, i1, i2 = ops.torch_point_ops_chamfer.chamfer_loss_forward(a, b, True)
+        assert loss.shape == () and i1.shape == (2, 7) and i2.shape == (2, 5)
+        assert i1.dtype == torch.int32
+        l1 = torch.empty(2, dtype=torch.int64)
+        idx, d = ops.torch_point_ops_knn.knn_forward_sorted(a, b, l1, l1, 2, 4, -1)
+        assert idx.shape == (2, 7, 4) and idx.dtype == torch.int64 and d.dtype == a.dtype
+        nn = ops.torch_point_ops_knn.knn_gather(b, idx, l1)
+        assert nn.shape == (2, 7, 4, 3)
+
+
+def test_chamfer_loss_cpu_not_implemented(tpo):
+    a = torch.zeros(1, 2, 3, requires_grad=True)
+    for red in ("mean", "sum"):
+        with pytest.raises(RuntimeError, match="not implemented for CPU"):
+            tpo.ChamferDistance(red)(a, torch.zeros(1, 2, 3))
+
+
 def test_public_names(tpo):
     for name in ("ChamferDistance", "chamfer_distance", "KNearestNeighbors", "knn_points",
                  "knn_gather", "FarthestPointSampling", "furthest_point_sampling",
                  "gather_points", "farthest_point_sample_and_gather",
                  "QuickFarthestPointSampling", "quick_furthest_point_sampling",
                  "quick_farthest_point_sample_and_gather", "EarthMoverDistance", "emd",
+                 "chamfer_loss",
                  "earth_movers_distance"):
         assert hasattr(tpo, name)
     from torch_point_ops.fps import FPSFunction, PointGatherer, fps_function  # noqa: F401
