@@ -1,6 +1,6 @@
 /*
  * tpo.h -- C ABI of libtpo_hip.so, the MI355X (gfx950) kernels behind the
- * torch_point_ops operators chamfer / knn / fps / gather_points.
+ * torch_point_ops operators chamfer / knn / fps / gather_points / emd.
  *
  * Conventions for every entry point:
  *   - all pointers are device pointers (hipMalloc / torch CUDA-device tensors)
@@ -232,6 +232,33 @@ int tpo_gather_bwd(int dtype, const void* grad_out, const int64_t* idx,
                    int64_t B, int64_t C, int64_t N, int64_t M,
                    void* grad_points, void* workspace, int64_t workspace_bytes,
                    void* stream);
+
+/*
+ * Earth mover's distance (approximate matching).
+ *
+ * tpo_emd_fwd replaces emd_cuda_forward (emd.cu:305-347: approxmatch
+ * emd.cu:18-183 + matchcost emd.cu:187-230), the CUDA kernel of
+ * torch_point_ops_emd::emd_forward (emd.cpp:32).
+ *   xyz1 (B,n,3), xyz2 (B,m,3) -> cost (B) (the matching cost before the
+ *   Python wrapper's division by n) and match (B,m,n).  F32/F64/F16.
+ *   n == 0 or m == 0: cost = 0 and match is empty (emd.cu:313-318).
+ *   Deterministic; within a tolerance of the reference (its exponential is
+ *   CUDA's, this one is ROCm's, and the sums run in another order).
+ * tpo_emd_bwd replaces emd_cuda_backward (emd.cu:349-389: matchcostgrad1
+ * emd.cu:234-257 + matchcostgrad2 emd.cu:261-303), the kernel of
+ * torch_point_ops_emd::emd_backward (emd.cpp:33).
+ *   grad_cost (B), match (B,m,n) -> grad_xyz1 (B,n,3), grad_xyz2 (B,m,3).
+ * Both take a workspace of tpo_emd_workspace_size(dtype, B, n, m) bytes,
+ * 256-byte aligned (0 bytes when B, n or m is 0).  B < 65536; n, m < 2^30.
+ */
+int64_t tpo_emd_workspace_size(int dtype, int64_t B, int64_t n, int64_t m);
+int tpo_emd_fwd(int dtype, const void* xyz1, const void* xyz2, int64_t B,
+                int64_t n, int64_t m, void* cost, void* match,
+                void* workspace, int64_t workspace_bytes, void* stream);
+int tpo_emd_bwd(int dtype, const void* grad_cost, const void* xyz1,
+                const void* xyz2, const void* match, int64_t B, int64_t n,
+                int64_t m, void* grad_xyz1, void* grad_xyz2,
+                void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -51,6 +51,8 @@ def lib():
             "tpo_ref_fps_rank": [I64, I64],
             "tpo_ref_gather_fwd": [ctypes.c_int, P, P, I64, I64, I64, I64, P],
             "tpo_ref_gather_bwd": [ctypes.c_int, P, P, I64, I64, I64, I64, P, ctypes.c_int],
+            "tpo_ref_emd_fwd": [ctypes.c_int, P, P, I64, I64, I64, P, P],
+            "tpo_ref_emd_bwd": [ctypes.c_int, P, P, P, P, I64, I64, I64, P, P],
             "tpo_ref_f32_to_f16_array": [P, P, I64],
             "tpo_ref_f16_to_f32_array": [P, P, I64],
             "tpo_cpu_knn_fwd_f32": [P, P, P, P, I64, I64, I64, I64, I64, ctypes.c_int, P, P,
@@ -250,3 +252,29 @@ def cpu_gather_bwd_f32(grad_out, idx, n):
     _check(lib().tpo_cpu_gather_bwd_f32(_p(grad_out), _p(idx), B, C, n, M, _p(out)),
            "cpu_gather_bwd")
     return out
+
+
+def emd_fwd(xyz1, xyz2):
+    """emd.cu:18-230 -> (cost[B] before the division by n, match[B, m, n])."""
+    xyz1, xyz2 = _c(xyz1), _c(xyz2)
+    assert xyz1.dtype == xyz2.dtype
+    B, n, _ = xyz1.shape
+    m = xyz2.shape[1]
+    cost = np.empty((B,), xyz1.dtype)
+    match = np.zeros((B, m, n), xyz1.dtype)
+    _check(lib().tpo_ref_emd_fwd(_dt(xyz1), _p(xyz1), _p(xyz2), B, n, m, _p(cost), _p(match)),
+           "emd_fwd")
+    return cost, match
+
+
+def emd_bwd(grad_cost, xyz1, xyz2, match):
+    """emd.cu:234-303 -> (grad_xyz1, grad_xyz2)."""
+    xyz1, xyz2 = _c(xyz1), _c(xyz2)
+    grad_cost, match = _c(grad_cost, xyz1.dtype), _c(match, xyz1.dtype)
+    B, n, _ = xyz1.shape
+    m = xyz2.shape[1]
+    g1 = np.empty_like(xyz1)
+    g2 = np.empty_like(xyz2)
+    _check(lib().tpo_ref_emd_bwd(_dt(xyz1), _p(grad_cost), _p(xyz1), _p(xyz2), _p(match), B, n,
+                                 m, _p(g1), _p(g2)), "emd_bwd")
+    return g1, g2

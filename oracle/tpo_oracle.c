@@ -701,6 +701,171 @@ int tpo_ref_gather_bwd(int dtype, const void* grad_out, const int64_t* idx, int6
 }
 
 /* ------------------------------------------------------------------ */
+/* Earth mover's distance                                              */
+/* ------------------------------------------------------------------ */
+
+/* emd.cu computes in at::opmath_type (float for float32 and float16, double
+   for float64); every opmath operation below rounds to it.  The remain,
+   ratio and match arrays are scalar_t, so float16 stores round to binary16
+   (om_st).  Contractions follow the same rule as the distances above:
+   a*a + b*b + c*c -> fma(c,c, fma(a,a, b*b)) and s += e*w -> fma(e,w,s). */
+INLINE int om64(int dt) { return dt == TPO_REF_F64; }
+INLINE double om_add(int dt, double a, double b) { return om64(dt) ? a + b : (double)((float)a + (float)b); }
+INLINE double om_sub(int dt, double a, double b) { return om64(dt) ? a - b : (double)((float)a - (float)b); }
+INLINE double om_mul(int dt, double a, double b) { return om64(dt) ? a * b : (double)((float)a * (float)b); }
+INLINE double om_div(int dt, double a, double b) { return om64(dt) ? a / b : (double)((float)a / (float)b); }
+INLINE double om_fma(int dt, double a, double b, double c) {
+  return om64(dt) ? fma(a, b, c) : (double)fmaf((float)a, (float)b, (float)c);
+}
+INLINE double om_exp(int dt, double x) { return om64(dt) ? exp(x) : (double)expf((float)x); }
+INLINE double om_st(int dt, double v) { return dt == TPO_REF_F16 ? rh((float)v) : v; }
+/* fminf/fmaxf are float functions: emd.cu:134,136,178 pass them opmath
+   values, so a float64 argument is narrowed to float there. */
+INLINE double om_fminf(double a, float b) { return (double)fminf((float)a, b); }
+INLINE double om_fmaxf(float a, double b) { return (double)fmaxf(a, (float)b); }
+
+/* (x2-x1)^2 + (y2-y1)^2 + (z2-z1)^2, emd.cu:72,120,164,212 */
+INLINE double emd_sq(int dt, const double* p1, const double* p2) {
+  const double a = om_sub(dt, p2[0], p1[0]), b = om_sub(dt, p2[1], p1[1]),
+               c = om_sub(dt, p2[2], p1[2]);
+  return om_fma(dt, c, c, om_fma(dt, a, a, om_mul(dt, b, b)));
+}
+/* exp(level * d), with the float16 clamp of emd.cu:77-80 */
+INLINE double emd_e(int dt, double level, const double* p1, const double* p2) {
+  double d = om_mul(dt, level, emd_sq(dt, p1, p2));
+  if (dt == TPO_REF_F16) d = d < -20.0 ? -20.0 : (d > 20.0 ? 20.0 : d);
+  return om_exp(dt, d);
+}
+
+/* One cloud of approxmatch (emd.cu:18-183) followed by matchcost
+   (emd.cu:187-230).  The reference's 1024-point staging tiles do not change
+   any summation order, so the loops run straight over the points. */
+static void emd_fwd_one(int dt, const void* xyz1, const void* xyz2, int64_t b, int64_t n,
+                        int64_t m, void* cost, void* match_out) {
+  double* X1 = (double*)malloc(sizeof(double) * (size_t)(3 * n + 3 * m + 3 * (n + m) + n * m));
+  double* X2 = X1 + 3 * n;
+  double* remL = X2 + 3 * m;
+  double* remR = remL + n;
+  double* ratL = remR + m;
+  double* ratR = ratL + n;
+  double* match = ratR + m;
+  for (int64_t i = 0; i < 3 * n; ++i) X1[i] = ld(dt, xyz1, b * n * 3 + i);
+  for (int64_t i = 0; i < 3 * m; ++i) X2[i] = ld(dt, xyz2, b * m * 3 + i);
+  /* emd.cu:55,89: static_cast<opmath_t>(1e-9f), or 1e-4f for float16 */
+  const double eps = dt == TPO_REF_F16 ? (double)1e-4f : (double)1e-9f;
+  /* emd.cu:21-28: float(n)/m, stored as scalar_t */
+  double multiL = 1.0, multiR = 1.0;
+  if (n >= m) multiR = om_st(dt, (double)((float)n / (float)m));
+  else multiL = om_st(dt, (double)((float)m / (float)n));
+  for (int64_t i = 0; i < n * m; ++i) match[i] = 0.0;
+  for (int64_t k = 0; k < n; ++k) remL[k] = multiL;
+  for (int64_t l = 0; l < m; ++l) remR[l] = multiR;
+  for (int j = 7; j >= -2; --j) {
+    const double level = j == -2 ? 0.0 : -pow(4.0, j);  /* emd.cu:40-43, exact in float */
+    for (int64_t k = 0; k < n; ++k) {                   /* emd.cu:47-96 */
+      double suml = eps;
+      for (int64_t l = 0; l < m; ++l)
+        suml = om_fma(dt, emd_e(dt, level, X1 + 3 * k, X2 + 3 * l), remR[l], suml);
+      ratL[k] = om_st(dt, om_div(dt, remL[k], om_add(dt, suml, eps)));
+    }
+    for (int64_t l = 0; l < m; ++l) {                   /* emd.cu:98-138 */
+      double sumr = 0.0;
+      for (int64_t k = 0; k < n; ++k)
+        sumr = om_fma(dt, emd_e(dt, level, X1 + 3 * k, X2 + 3 * l), ratL[k], sumr);
+      sumr = om_mul(dt, sumr, remR[l]);
+      const double cons = om_fminf(om_div(dt, remR[l], om_add(dt, sumr, eps)), 1.0f);
+      ratR[l] = om_st(dt, om_mul(dt, cons, remR[l]));
+      remR[l] = om_st(dt, om_fmaxf(0.0f, om_sub(dt, remR[l], sumr)));
+    }
+    for (int64_t k = 0; k < n; ++k) {                   /* emd.cu:140-179 */
+      const double rl = ratL[k];
+      double suml = 0.0;
+      for (int64_t l = 0; l < m; ++l) {
+        const double w =
+            om_mul(dt, om_mul(dt, emd_e(dt, level, X1 + 3 * k, X2 + 3 * l), rl), ratR[l]);
+        match[l * n + k] = om_st(dt, om_add(dt, match[l * n + k], om_st(dt, w)));
+        suml = om_add(dt, suml, w);
+      }
+      remL[k] = om_st(dt, om_fmaxf(0.0f, om_sub(dt, remL[k], suml)));
+    }
+  }
+  /* matchcost: thread t of 512 sums its columns k = t, t+512, ... over l in
+     order, then the block's tree (emd.cu:193-227) */
+  double part[512];
+  for (int t = 0; t < 512; ++t) {
+    double s = 0.0;
+    for (int64_t k = t; k < n; k += 512)
+      for (int64_t l = 0; l < m; ++l)
+        s = om_fma(dt, emd_sq(dt, X1 + 3 * k, X2 + 3 * l), match[l * n + k], s);
+    part[t] = s;
+  }
+  for (int st2 = 1; st2 < 512; st2 <<= 1)
+    for (int t = 0; t + st2 < 512; t += 2 * st2) part[t] = om_add(dt, part[t], part[t + st2]);
+  st(dt, cost, b, om_st(dt, part[0]));
+  for (int64_t i = 0; i < n * m; ++i) st(dt, match_out, b * n * m + i, match[i]);
+  free(X1);
+}
+
+int tpo_ref_emd_fwd(int dtype, const void* xyz1, const void* xyz2, int64_t B, int64_t n,
+                    int64_t m, void* cost, void* match) {
+  if (dtype != TPO_REF_F32 && dtype != TPO_REF_F64 && dtype != TPO_REF_F16) return -2;
+  if (B < 0 || n < 0 || m < 0) return -1;
+  if (n == 0 || m == 0) { /* emd.cu:313-318 */
+    for (int64_t b = 0; b < B; ++b) st(dtype, cost, b, 0.0);
+    return 0;
+  }
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t b = 0; b < B; ++b) emd_fwd_one(dtype, xyz1, xyz2, b, n, m, cost, match);
+  return 0;
+}
+
+/* matchcostgrad1 (emd.cu:234-257) and matchcostgrad2 (emd.cu:261-303) */
+int tpo_ref_emd_bwd(int dtype, const void* grad_cost, const void* xyz1, const void* xyz2,
+                    const void* match, int64_t B, int64_t n, int64_t m, void* grad1,
+                    void* grad2) {
+  const int dt = dtype;
+  if (dt != TPO_REF_F32 && dt != TPO_REF_F64 && dt != TPO_REF_F16) return -2;
+  if (B < 0 || n < 0 || m < 0) return -1;
+  if (n == 0 || m == 0) {
+    for (int64_t i = 0; i < B * n * 3; ++i) st(dt, grad1, i, 0.0);
+    for (int64_t i = 0; i < B * m * 3; ++i) st(dt, grad2, i, 0.0);
+    return 0;
+  }
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t b = 0; b < B; ++b) {
+    const double g = ld(dt, grad_cost, b);
+    for (int64_t l = 0; l < n; ++l) {
+      double p1[3], acc[3] = {0.0, 0.0, 0.0};
+      for (int c = 0; c < 3; ++c) p1[c] = ld(dt, xyz1, (b * n + l) * 3 + c);
+      for (int64_t k = 0; k < m; ++k) {
+        const double d = om_mul(dt, ld(dt, match, b * n * m + k * n + l), 2.0);
+        for (int c = 0; c < 3; ++c)
+          acc[c] = om_fma(dt, om_sub(dt, p1[c], ld(dt, xyz2, (b * m + k) * 3 + c)), d, acc[c]);
+      }
+      for (int c = 0; c < 3; ++c) st(dt, grad1, (b * n + l) * 3 + c, om_st(dt, om_mul(dt, acc[c], g)));
+    }
+    for (int64_t k = 0; k < m; ++k) {
+      double p2[3], part[256][3];
+      for (int c = 0; c < 3; ++c) p2[c] = ld(dt, xyz2, (b * m + k) * 3 + c);
+      for (int t = 0; t < 256; ++t) {
+        double s[3] = {0.0, 0.0, 0.0};
+        for (int64_t jj = t; jj < n; jj += 256) {
+          const double d = om_mul(dt, ld(dt, match, b * n * m + k * n + jj), 2.0);
+          for (int c = 0; c < 3; ++c)
+            s[c] = om_fma(dt, om_sub(dt, p2[c], ld(dt, xyz1, (b * n + jj) * 3 + c)), d, s[c]);
+        }
+        for (int c = 0; c < 3; ++c) part[t][c] = s[c];
+      }
+      for (int st2 = 1; st2 < 256; st2 <<= 1)
+        for (int t = 0; t + st2 < 256; t += 2 * st2)
+          for (int c = 0; c < 3; ++c) part[t][c] = om_add(dt, part[t][c], part[t + st2][c]);
+      for (int c = 0; c < 3; ++c) st(dt, grad2, (b * m + k) * 3 + c, om_st(dt, om_mul(dt, part[0][c], g)));
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* Reference CPU kernels (timed CPU baseline)                          */
 /* ------------------------------------------------------------------ */
 

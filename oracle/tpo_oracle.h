@@ -85,6 +85,19 @@ int tpo_ref_gather_bwd(int dtype, const void* grad_out, const int64_t* idx,
                        int64_t B, int64_t C, int64_t N, int64_t M,
                        void* grad_pts, int accum_f64);
 
+/* Earth mover's distance (approximate matching): emd.cu:18-303.
+   Forward writes cost[B] (the raw matchcost, before the module's division
+   by n) and match[B][m][n]; backward writes grad_xyz1[B][n][3] and
+   grad_xyz2[B][m][3] from grad_cost[B] and match.  float16 runs in float with
+   half storage of the remain/ratio/match arrays, as the reference does.  The
+   exponentials come from the C library (exp/expf): parity with the reference
+   is within a tolerance, not bit-exact. */
+int tpo_ref_emd_fwd(int dtype, const void* xyz1, const void* xyz2, int64_t B,
+                    int64_t n, int64_t m, void* cost, void* match);
+int tpo_ref_emd_bwd(int dtype, const void* grad_cost, const void* xyz1,
+                    const void* xyz2, const void* match, int64_t B, int64_t n,
+                    int64_t m, void* grad1, void* grad2);
+
 /* Reference CPU kernels (timed baseline only): knn.cpp:30-164, fps.cpp:18-141.
    float32 only.  nthreads > 1 splits the outer (cloud x query / cloud) loop
    over OpenMP threads; 1 reproduces the reference's single-threaded loops. */

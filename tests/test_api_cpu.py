@@ -27,6 +27,12 @@ def test_schemas_match_reference(tpo):
             "gather_points_backward(Tensor grad_out, Tensor idx, int n) -> Tensor",
         ops.torch_point_ops_quick_fps.quick_fps_forward:
             "quick_fps_forward(Tensor points, int nsamples, int kd_depth=4) -> Tensor",
+        # emd.cpp:32-33
+        ops.torch_point_ops_emd.emd_forward:
+            "emd_forward(Tensor xyz1, Tensor xyz2) -> (Tensor, Tensor)",
+        ops.torch_point_ops_emd.emd_backward:
+            "emd_backward(Tensor grad_cost, Tensor xyz1, Tensor xyz2, Tensor match) -> "
+            "(Tensor, Tensor)",
     }
     for op, schema in want.items():
         s = str(op.default._schema)
@@ -90,6 +96,19 @@ def test_chamfer_cpu_not_implemented(tpo):
         tpo.chamfer_distance(torch.zeros(1, 2, 3), torch.zeros(1, 2, 3))
 
 
+def test_emd_cpu_not_implemented(tpo):
+    # emd.cpp:19-28
+    with pytest.raises(RuntimeError, match="emd_forward is not implemented for CPU"):
+        tpo.earth_movers_distance(torch.zeros(1, 2, 3), torch.zeros(1, 2, 3))
+    with pytest.raises(RuntimeError, match="emd_backward is not implemented for CPU"):
+        torch.ops.torch_point_ops_emd.emd_backward(torch.zeros(1), torch.zeros(1, 2, 3),
+                                                   torch.zeros(1, 2, 3), torch.zeros(1, 2, 2))
+    assert tpo.emd is tpo.earth_movers_distance
+    from torch_point_ops.emd.emd import EarthMoverDistance
+
+    assert EarthMoverDistance is tpo.EarthMoverDistance
+
+
 def test_validation_errors(tpo):
     p = torch.zeros(1, 10, 3)
     with pytest.raises(ValueError):
@@ -122,8 +141,6 @@ def test_validation_errors(tpo):
         tpo.ChamferDistance(reduction="max")
     with pytest.raises(ValueError):
         tpo.FarthestPointSampling(0)
-    with pytest.raises(NotImplementedError):
-        tpo.emd(p, p)
 
 
 def test_fake_kernels(tpo):
@@ -143,3 +160,7 @@ def test_fake_kernels(tpo):
         assert g.shape == (2, 6, 3)
         gb = torch.ops.torch_point_ops_fps.gather_points_backward(g, s, 7)
         assert gb.shape == (2, 6, 7)
+        cost, match = torch.ops.torch_point_ops_emd.emd_forward(a, b)
+        assert cost.shape == (2,) and match.shape == (2, 7, 5) and match.dtype == a.dtype
+        g1, g2 = torch.ops.torch_point_ops_emd.emd_backward(cost, a, b, match)
+        assert g1.shape == a.shape and g2.shape == b.shape

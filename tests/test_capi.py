@@ -31,7 +31,8 @@ def test_header_declares_the_boundary():
     for must in ("tpo_chamfer_fwd", "tpo_chamfer_bwd", "tpo_chamfer_workspace_size",
                  "tpo_chamfer_pairs_evaluated", "tpo_knn_fwd", "tpo_knn_bwd",
                  "tpo_fps_fwd", "tpo_fps_workspace_size", "tpo_gather_fwd", "tpo_gather_bwd",
-                 "tpo_gather_bwd_workspace_size", "tpo_last_error", "tpo_abi_version"):
+                 "tpo_gather_bwd_workspace_size", "tpo_emd_fwd", "tpo_emd_bwd",
+                 "tpo_emd_workspace_size", "tpo_last_error", "tpo_abi_version"):
         assert must in names
 
 
@@ -106,3 +107,28 @@ def test_argument_errors_are_reported(lib):
     lib.tpo_gather_bwd_workspace_size.argtypes = [I, I]
     lib.tpo_gather_bwd_workspace_size.restype = I
     assert lib.tpo_gather_bwd_workspace_size(16, 65536) == 16 * 65536 * 4
+
+
+def test_emd_sizes_and_errors(lib):
+    P, I = ctypes.c_void_p, ctypes.c_int64
+    lib.tpo_emd_workspace_size.argtypes = [ctypes.c_int, I, I, I]
+    lib.tpo_emd_workspace_size.restype = I
+    # float/half: p1, p2 (4 floats a point), remain, 10 levels of ratios,
+    # 8 x 64 cost partials and 16 chunks of grad_xyz1 partials per cloud
+    B, n, m = 16, 2048, 2048
+    expect = 4 * B * (n * 4 + m * 4 + n + m + 10 * n + 10 * m + 8 * 64 + 16 * n * 3)
+    assert lib.tpo_emd_workspace_size(0, B, n, m) == expect
+    assert lib.tpo_emd_workspace_size(2, B, n, m) == expect
+    assert lib.tpo_emd_workspace_size(1, B, n, m) == 2 * expect
+    assert lib.tpo_emd_workspace_size(0, 2, 0, 5) == 0
+    assert lib.tpo_emd_workspace_size(3, 1, 4, 4) == -1  # bfloat16: not an EMD dtype
+    lib.tpo_emd_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, P, P, P, I, P]
+    assert lib.tpo_emd_fwd(0, None, None, 1, -1, 4, None, None, None, 0, None) == -1
+    assert b"bad sizes" in lib.tpo_last_error()
+    assert lib.tpo_emd_fwd(3, None, None, 1, 4, 4, None, None, None, 0, None) == -2
+    assert lib.tpo_emd_fwd(0, None, None, 1, 4, 4, None, None, None, 0, None) == -4
+    assert b"workspace" in lib.tpo_last_error()
+    lib.tpo_emd_bwd.argtypes = [ctypes.c_int, P, P, P, P, I, I, I, P, P, P, I, P]
+    assert lib.tpo_emd_bwd(0, None, None, None, None, 1, 4, 4, None, None, None, 0, None) == -4
+    assert lib.tpo_emd_bwd(0, None, None, None, None, 70000, 4, 4, None, None, None, 0,
+                           None) == -1

@@ -1,0 +1,550 @@
+// emd.hip -- earth mover's distance (approximate matching) for gfx950.
+//
+// Replaces approxmatch, matchcost, matchcostgrad1 and matchcostgrad2
+// (emd.cu:18-303).  The algorithm is the reference's: mass multiL on every
+// xyz1 point and multiR on every xyz2 point (emd.cu:21-28), then ten levels
+// j = 7 .. -2 with level = -4^j (0 for the last, emd.cu:39-43), each of
+// three passes over all n*m pairs with e(k,l) = exp(level * |p2_l - p1_k|^2)
+// (the argument clamped to [-20, 20] for float16, emd.cu:77-80):
+//   pass 1  ratioL[k] = remainL[k] / (1e-9 + sum_l e * remainR[l] + 1e-9)
+//   pass 2  sumr = remainR[l] * sum_k e * ratioL[k];
+//           ratioR[l] = min(remainR[l] / (sumr + 1e-9), 1) * remainR[l];
+//           remainR[l] = max(0, remainR[l] - sumr)
+//   pass 3  w = e * ratioL[k] * ratioR[l];  match[l][k] += w;
+//           remainL[k] = max(0, remainL[k] - sum_l w)
+// (1e-4 instead of 1e-9 for float16), then cost = sum d(k,l) * match[l][k].
+// Arithmetic is at::opmath_type (float for float and half, double for
+// double); remain/ratio/match values are rounded to the storage dtype as the
+// reference stores them, and the reference's fminf/fmaxf narrow a double
+// argument to float (emd.cu:134,136,178), which is kept.
+//
+// Design for MI355X (the reference runs one 512-thread block per cloud):
+//   * each pass is a grid-wide sweep: a 256-thread workgroup owns 64 points
+//     (one per lane) and its four waves each sum over a quarter of the other
+//     cloud, read with wave-uniform (scalar) loads, combined in fixed order;
+//   * pass 3 of level j and pass 1 of level j-1 need the same inputs, so they
+//     share one sweep (two exponentials per pair): 21 dependent sweeps;
+//   * match is not accumulated in HBM level by level: the per-level ratioL
+//     and ratioR are kept, and one final pass forms
+//     match[l][k] = sum_j e_j(k,l) * ratioL_j[k] * ratioR_j[l] in level order
+//     (each addition rounded as the reference's +=), writes it once and fuses
+//     matchcost's sum of d * match into the same pass;
+//   * every sum has a fixed order, so results are deterministic.
+// The summation orders differ from the reference's sequential loops and the
+// exponential is ROCm's, so parity is to a tolerance, not bit-exact.
+#include "tpo_common.hpp"
+
+#include <type_traits>
+
+namespace tpo {
+namespace {
+
+constexpr int EMD_LEVELS = 10;       // j = 7 .. -2
+constexpr int EMD_THREADS = 256;     // 4 waves
+constexpr int EMD_MATCH_ROWS = 32;   // match rows per workgroup of the final pass
+constexpr int EMD_G1_ROWS = 128;     // match rows per grad_xyz1 partial
+
+template <typename T> struct EmdV { typedef float type; };
+template <> struct EmdV<double> { typedef double type; };
+
+// level of step t = 7 - j (emd.cu:40-43)
+template <typename V>
+__device__ __forceinline__ V emd_level(int t) {
+  return t < 8 ? -(V)(1 << (14 - 2 * t)) : (t == 8 ? (V)-0.25 : (V)0);
+}
+// epsilon of emd.cu:55,89,133: static_cast<opmath_t>(1e-9f), 1e-4f for half
+template <typename T, typename V>
+__device__ __forceinline__ V emd_eps() {
+  return std::is_same<T, half_t>::value ? (V)1e-4f : (V)1e-9f;
+}
+// an opmath value stored as scalar_t and read back
+template <typename T, typename V>
+__device__ __forceinline__ V emd_st(V v) {
+  if constexpr (std::is_same<T, half_t>::value) return (V)(half_t)v;
+  return v;
+}
+__device__ __forceinline__ float emd_exp(float x) { return expf(x); }
+__device__ __forceinline__ double emd_exp(double x) { return exp(x); }
+template <typename T, typename V>
+__device__ __forceinline__ V emd_e(V level, V d) {
+  V a = level * d;
+  if constexpr (std::is_same<T, half_t>::value)
+    a = a < (V)-20 ? (V)-20 : (a > (V)20 ? (V)20 : a);
+  return emd_exp(a);
+}
+// fminf(x, 1.0f) / fmaxf(0.0f, x) of emd.cu:134,136,178 (float functions)
+template <typename V>
+__device__ __forceinline__ V emd_min1(V a) { return (V)fminf((float)a, 1.0f); }
+template <typename V>
+__device__ __forceinline__ V emd_max0(V a) { return (V)fmaxf(0.0f, (float)a); }
+__device__ __forceinline__ float emd_fma(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ double emd_fma(double a, double b, double c) { return __builtin_fma(a, b, c); }
+
+template <typename V>
+__device__ __forceinline__ V wave_sum(V v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Workspace, array-major over the clouds (opmath values):
+//   p1[B][n][4], p2[B][m][4]   coordinates (x, y, z, 0)
+//   reml[B][n], remr[B][m]     remaining mass
+//   rl[B][10][n], rr[B][10][m] ratioL / ratioR of every level
+//   cost[B][gy][gx]            matchcost partials of the final pass
+//   g1[B][nchunk][n][3]        grad_xyz1 partials of the backward
+struct EmdLayout {
+  int64_t p1, p2, reml, remr, rl, rr, cost, g1, total;
+  int gx, gy, nchunk;
+};
+template <typename V>
+inline EmdLayout emd_layout(int64_t B, int64_t n, int64_t m) {
+  EmdLayout L;
+  L.gx = (int)((n + EMD_THREADS - 1) / EMD_THREADS);
+  L.gy = (int)((m + EMD_MATCH_ROWS - 1) / EMD_MATCH_ROWS);
+  L.nchunk = (int)((m + EMD_G1_ROWS - 1) / EMD_G1_ROWS);
+  auto al = [](int64_t v) { return (v + 255) / 256 * 256; };
+  const int64_t s = (int64_t)sizeof(V);
+  int64_t o = 0;
+  L.p1 = o; o += al(B * n * 4 * s);
+  L.p2 = o; o += al(B * m * 4 * s);
+  L.reml = o; o += al(B * n * s);
+  L.remr = o; o += al(B * m * s);
+  L.rl = o; o += al(B * EMD_LEVELS * n * s);
+  L.rr = o; o += al(B * EMD_LEVELS * m * s);
+  L.cost = o; o += al(B * (int64_t)L.gx * L.gy * s);
+  L.g1 = o; o += al(B * (int64_t)L.nchunk * n * 3 * s);
+  L.total = o;
+  return L;
+}
+
+// ---------------------------------------------------------------- forward
+
+template <typename T>
+__global__ __launch_bounds__(EMD_THREADS) void emd_prep_kernel(
+    const T* __restrict__ xyz1, const T* __restrict__ xyz2, int n, int m, float mult_l,
+    float mult_r, typename EmdV<T>::type* __restrict__ p1, typename EmdV<T>::type* __restrict__ p2,
+    typename EmdV<T>::type* __restrict__ reml, typename EmdV<T>::type* __restrict__ remr) {
+  typedef typename EmdV<T>::type V;
+  const int64_t b = blockIdx.y;
+  const int i = blockIdx.x * EMD_THREADS + threadIdx.x;
+  if (i < n) {
+    const T* s = xyz1 + (b * n + i) * 3;
+    V* d = p1 + (b * n + i) * 4;
+    d[0] = (V)s[0]; d[1] = (V)s[1]; d[2] = (V)s[2]; d[3] = (V)0;
+    reml[b * n + i] = emd_st<T, V>((V)mult_l);
+  }
+  if (i < m) {
+    const T* s = xyz2 + (b * m + i) * 3;
+    V* d = p2 + (b * m + i) * 4;
+    d[0] = (V)s[0]; d[1] = (V)s[1]; d[2] = (V)s[2]; d[3] = (V)0;
+    remr[b * m + i] = emd_st<T, V>((V)mult_r);
+  }
+}
+
+// Sums over the "other" cloud for one own point per lane; the four waves take
+// a quarter of the other points each.  NS = 1 sums e(la)*wa; NS = 2 also
+// sums e(lb)*wb with the same distances.
+template <typename T, int NS>
+__device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restrict__ other, int cnt,
+                                          typename EmdV<T>::type x, typename EmdV<T>::type y,
+                                          typename EmdV<T>::type z, typename EmdV<T>::type la,
+                                          const typename EmdV<T>::type* __restrict__ wa,
+                                          typename EmdV<T>::type lb,
+                                          const typename EmdV<T>::type* __restrict__ wb,
+                                          typename EmdV<T>::type* sums) {
+  typedef typename EmdV<T>::type V;
+  __shared__ V s_part[NS][EMD_THREADS / 64 - 1][64];
+  const int w = wave_id(), lane = lane_id();
+  const int q0 = (int)((int64_t)cnt * w / 4), q1 = (int)((int64_t)cnt * (w + 1) / 4);
+  V sa = (V)0, sb = (V)0;
+#pragma unroll 4
+  for (int q = q0; q < q1; ++q) {
+    const V d = sq3(other[4 * q] - x, other[4 * q + 1] - y, other[4 * q + 2] - z);
+    sa = emd_fma(emd_e<T>(la, d), wa[q], sa);
+    if constexpr (NS == 2) sb = emd_fma(emd_e<T>(lb, d), wb[q], sb);
+  }
+  if (w > 0) {
+    s_part[0][w - 1][lane] = sa;
+    if constexpr (NS == 2) s_part[NS - 1][w - 1][lane] = sb;
+  }
+  __syncthreads();
+  if (w == 0) {
+    sums[0] = ((sa + s_part[0][0][lane]) + s_part[0][1][lane]) + s_part[0][2][lane];
+    if constexpr (NS == 2)
+      sums[1] = ((sb + s_part[NS - 1][0][lane]) + s_part[NS - 1][1][lane]) + s_part[NS - 1][2][lane];
+  }
+}
+
+// Step s = 0..10 over the xyz1 points: pass 3 of level s-1 (s >= 1), then
+// pass 1 of level s (s <= 9).  MODE 1: pass 1 only; 2: pass 3 only; 3: both.
+template <typename T, int MODE>
+__global__ __launch_bounds__(EMD_THREADS) void emd_rows_kernel(
+    const typename EmdV<T>::type* __restrict__ p1, const typename EmdV<T>::type* __restrict__ p2,
+    const typename EmdV<T>::type* __restrict__ remr, const typename EmdV<T>::type* __restrict__ rr,
+    typename EmdV<T>::type* __restrict__ reml, typename EmdV<T>::type* __restrict__ rl, int n, int m,
+    int s) {
+  typedef typename EmdV<T>::type V;
+  const int64_t b = blockIdx.y;
+  const int lane = lane_id();
+  const int k = blockIdx.x * 64 + lane;
+  V x = (V)0, y = (V)0, z = (V)0;
+  if (k < n) {
+    x = p1[(b * n + k) * 4];
+    y = p1[(b * n + k) * 4 + 1];
+    z = p1[(b * n + k) * 4 + 2];
+  }
+  const V* other = p2 + b * m * 4;
+  const V* w3 = rr + (b * EMD_LEVELS + (s - 1)) * m;  // ratioR of level s-1
+  const V* w1 = remr + b * m;
+  V sums[2];
+  if constexpr (MODE == 1) emd_sweep<T, 1>(other, m, x, y, z, emd_level<V>(s), w1, (V)0, w1, sums);
+  if constexpr (MODE == 2) emd_sweep<T, 1>(other, m, x, y, z, emd_level<V>(s - 1), w3, (V)0, w3, sums);
+  if constexpr (MODE == 3)
+    emd_sweep<T, 2>(other, m, x, y, z, emd_level<V>(s - 1), w3, emd_level<V>(s), w1, sums);
+  if (wave_id() != 0 || k >= n) return;
+  const V eps = emd_eps<T, V>();
+  V rem = reml[b * n + k];
+  if constexpr (MODE != 1) {  // emd.cu:177-178 (sum_l w = ratioL * sum_l e * ratioR)
+    const V ratl = rl[(b * EMD_LEVELS + (s - 1)) * n + k];
+    rem = emd_st<T, V>(emd_max0(rem - ratl * sums[0]));
+    reml[b * n + k] = rem;
+  }
+  if constexpr (MODE != 2) {  // emd.cu:88-95
+    const V suml = eps + sums[MODE == 3 ? 1 : 0];
+    rl[(b * EMD_LEVELS + s) * n + k] = emd_st<T, V>(rem / (suml + eps));
+  }
+}
+
+// Pass 2 of level t over the xyz2 points (emd.cu:98-138).
+template <typename T>
+__global__ __launch_bounds__(EMD_THREADS) void emd_cols_kernel(
+    const typename EmdV<T>::type* __restrict__ p1, const typename EmdV<T>::type* __restrict__ p2,
+    const typename EmdV<T>::type* __restrict__ rl, typename EmdV<T>::type* __restrict__ remr,
+    typename EmdV<T>::type* __restrict__ rr, int n, int m, int t) {
+  typedef typename EmdV<T>::type V;
+  const int64_t b = blockIdx.y;
+  const int lane = lane_id();
+  const int l = blockIdx.x * 64 + lane;
+  V x = (V)0, y = (V)0, z = (V)0;
+  if (l < m) {
+    x = p2[(b * m + l) * 4];
+    y = p2[(b * m + l) * 4 + 1];
+    z = p2[(b * m + l) * 4 + 2];
+  }
+  // d(k,l) takes the differences p2 - p1 as the rows pass does; squaring
+  // makes the sign irrelevant, so the same values result.
+  V sums[2];
+  emd_sweep<T, 1>(p1 + b * n * 4, n, x, y, z, emd_level<V>(t), rl + (b * EMD_LEVELS + t) * n, (V)0,
+                  nullptr, sums);
+  if (wave_id() != 0 || l >= m) return;
+  const V eps = emd_eps<T, V>();
+  const V rem = remr[b * m + l];
+  const V sumr = sums[0] * rem;
+  const V cons = emd_min1(rem / (sumr + eps));
+  rr[(b * EMD_LEVELS + t) * m + l] = emd_st<T, V>(cons * rem);
+  remr[b * m + l] = emd_st<T, V>(emd_max0(rem - sumr));
+}
+
+// match[l][k] over the ten levels, written once, and matchcost's partial sum.
+template <typename T>
+__global__ __launch_bounds__(EMD_THREADS) void emd_match_kernel(
+    const typename EmdV<T>::type* __restrict__ p1, const typename EmdV<T>::type* __restrict__ p2,
+    const typename EmdV<T>::type* __restrict__ rl, const typename EmdV<T>::type* __restrict__ rr,
+    int n, int m, T* __restrict__ match, typename EmdV<T>::type* __restrict__ cpart) {
+  typedef typename EmdV<T>::type V;
+  __shared__ V s_red[EMD_THREADS / 64];
+  const int64_t b = blockIdx.z;
+  const int k = blockIdx.x * EMD_THREADS + threadIdx.x;
+  const bool own = k < n;
+  const int kk = own ? k : n - 1;
+  const V x = p1[(b * n + kk) * 4], y = p1[(b * n + kk) * 4 + 1], z = p1[(b * n + kk) * 4 + 2];
+  V r[EMD_LEVELS];
+#pragma unroll
+  for (int t = 0; t < EMD_LEVELS; ++t) r[t] = rl[(b * EMD_LEVELS + t) * n + kk];
+  const int l0 = blockIdx.y * EMD_MATCH_ROWS;
+  const int l1 = min(m, l0 + EMD_MATCH_ROWS);
+  const V* q = p2 + b * m * 4;
+  const V* rrb = rr + b * EMD_LEVELS * m;
+  V cs = (V)0;
+  for (int l = l0; l < l1; ++l) {
+    const V d = sq3(q[4 * l] - x, q[4 * l + 1] - y, q[4 * l + 2] - z);
+    V mt = (V)0;
+#pragma unroll
+    for (int t = 0; t < EMD_LEVELS; ++t) {
+      const V w = (emd_e<T>(emd_level<V>(t), d) * r[t]) * rrb[t * m + l];  // emd.cu:170
+      mt = emd_st<T, V>(mt + emd_st<T, V>(w));                             // emd.cu:171
+    }
+    if (own) match[(b * m + l) * (int64_t)n + k] = (T)mt;
+    cs = emd_fma(d, mt, cs);  // emd.cu:212-213
+  }
+  cs = own ? cs : (V)0;
+  cs = wave_sum(cs);
+  if (lane_id() == 0) s_red[wave_id()] = cs;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    cpart[(b * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] =
+        ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
+}
+
+// cost[b] = the sum of the cloud's partials, in a fixed order.
+template <typename T>
+__global__ __launch_bounds__(EMD_THREADS) void emd_cost_kernel(
+    const typename EmdV<T>::type* __restrict__ cpart, int parts, T* __restrict__ cost) {
+  typedef typename EmdV<T>::type V;
+  __shared__ V s_red[EMD_THREADS / 64];
+  const int64_t b = blockIdx.x;
+  V s = (V)0;
+  for (int i = threadIdx.x; i < parts; i += EMD_THREADS) s += cpart[b * parts + i];
+  s = wave_sum(s);
+  if (lane_id() == 0) s_red[wave_id()] = s;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    cost[b] = (T)emd_st<T, V>(((s_red[0] + s_red[1]) + s_red[2]) + s_red[3]);
+}
+
+template <typename T>
+__global__ void emd_zero_kernel(T* __restrict__ p, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) p[i] = (T)0;
+}
+
+// ---------------------------------------------------------------- backward
+
+// grad_xyz2[l] = grad_cost * sum_k (p2_l - p1_k) * 2 match[l][k]
+// (emd.cu:261-303): one wave per row of match.
+template <typename T>
+__global__ __launch_bounds__(EMD_THREADS) void emd_grad2_kernel(
+    const T* __restrict__ grad_cost, const T* __restrict__ xyz1, const T* __restrict__ xyz2,
+    const T* __restrict__ match, int n, int m, T* __restrict__ grad2) {
+  typedef typename EmdV<T>::type V;
+  const int64_t b = blockIdx.y;
+  const int l = blockIdx.x * (EMD_THREADS / 64) + wave_id();
+  if (l >= m) return;
+  const V x2 = (V)xyz2[(b * m + l) * 3], y2 = (V)xyz2[(b * m + l) * 3 + 1],
+          z2 = (V)xyz2[(b * m + l) * 3 + 2];
+  const T* row = match + (b * m + l) * (int64_t)n;
+  const T* p = xyz1 + b * n * 3;
+  V ax = (V)0, ay = (V)0, az = (V)0;
+  for (int k = lane_id(); k < n; k += 64) {
+    const V d = (V)row[k] * (V)2;
+    ax = emd_fma(x2 - (V)p[3 * k], d, ax);
+    ay = emd_fma(y2 - (V)p[3 * k + 1], d, ay);
+    az = emd_fma(z2 - (V)p[3 * k + 2], d, az);
+  }
+  ax = wave_sum(ax);
+  ay = wave_sum(ay);
+  az = wave_sum(az);
+  if (lane_id() == 0) {
+    const V g = (V)grad_cost[b];
+    grad2[(b * m + l) * 3] = (T)(ax * g);
+    grad2[(b * m + l) * 3 + 1] = (T)(ay * g);
+    grad2[(b * m + l) * 3 + 2] = (T)(az * g);
+  }
+}
+
+// grad_xyz1 partials over EMD_G1_ROWS rows of match (emd.cu:234-257).
+template <typename T>
+__global__ __launch_bounds__(EMD_THREADS) void emd_grad1_part_kernel(
+    const T* __restrict__ xyz1, const T* __restrict__ xyz2, const T* __restrict__ match, int n,
+    int m, typename EmdV<T>::type* __restrict__ part) {
+  typedef typename EmdV<T>::type V;
+  const int64_t b = blockIdx.z;
+  const int k = blockIdx.x * EMD_THREADS + threadIdx.x;
+  if (k >= n) return;
+  const V x1 = (V)xyz1[(b * n + k) * 3], y1 = (V)xyz1[(b * n + k) * 3 + 1],
+          z1 = (V)xyz1[(b * n + k) * 3 + 2];
+  const int l0 = blockIdx.y * EMD_G1_ROWS, l1 = min(m, l0 + EMD_G1_ROWS);
+  const T* q = xyz2 + b * m * 3;
+  V ax = (V)0, ay = (V)0, az = (V)0;
+#pragma unroll 4
+  for (int l = l0; l < l1; ++l) {
+    const V d = (V)match[(b * m + l) * (int64_t)n + k] * (V)2;
+    ax = emd_fma(x1 - (V)q[3 * l], d, ax);
+    ay = emd_fma(y1 - (V)q[3 * l + 1], d, ay);
+    az = emd_fma(z1 - (V)q[3 * l + 2], d, az);
+  }
+  V* o = part + ((b * gridDim.y + blockIdx.y) * n + k) * 3;
+  o[0] = ax;
+  o[1] = ay;
+  o[2] = az;
+}
+
+template <typename T>
+__global__ __launch_bounds__(EMD_THREADS) void emd_grad1_final_kernel(
+    const T* __restrict__ grad_cost, const typename EmdV<T>::type* __restrict__ part, int n,
+    int nchunk, T* __restrict__ grad1) {
+  typedef typename EmdV<T>::type V;
+  const int64_t b = blockIdx.y;
+  const int k = blockIdx.x * EMD_THREADS + threadIdx.x;
+  if (k >= n) return;
+  V a[3] = {(V)0, (V)0, (V)0};
+  for (int c = 0; c < nchunk; ++c) {
+    const V* o = part + ((b * nchunk + c) * n + k) * 3;
+    a[0] += o[0];
+    a[1] += o[1];
+    a[2] += o[2];
+  }
+  const V g = (V)grad_cost[b];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) grad1[(b * n + k) * 3 + c] = (T)(a[c] * g);
+}
+
+// ---------------------------------------------------------------- host side
+
+template <typename T>
+int emd_fwd_impl(const void* xyz1, const void* xyz2, int64_t B, int64_t n, int64_t m, void* cost,
+                 void* match, char* ws, hipStream_t s) {
+  typedef typename EmdV<T>::type V;
+  const EmdLayout L = emd_layout<V>(B, n, m);
+  V* p1 = (V*)(ws + L.p1);
+  V* p2 = (V*)(ws + L.p2);
+  V* reml = (V*)(ws + L.reml);
+  V* remr = (V*)(ws + L.remr);
+  V* rl = (V*)(ws + L.rl);
+  V* rr = (V*)(ws + L.rr);
+  V* cp = (V*)(ws + L.cost);
+  // emd.cu:21-28: float(n)/m
+  const float mult_l = n >= m ? 1.0f : (float)m / (float)n;
+  const float mult_r = n >= m ? (float)n / (float)m : 1.0f;
+  const int nn = (int)n, mm = (int)m;
+  const unsigned bb = (unsigned)B;
+  hipLaunchKernelGGL(emd_prep_kernel<T>, dim3((unsigned)((std::max(n, m) + 255) / 256), bb),
+                     dim3(EMD_THREADS), 0, s, (const T*)xyz1, (const T*)xyz2, nn, mm, mult_l, mult_r,
+                     p1, p2, reml, remr);
+  const dim3 grow((unsigned)((n + 63) / 64), bb), gcol((unsigned)((m + 63) / 64), bb);
+  for (int st = 0; st <= EMD_LEVELS; ++st) {
+    if (st == 0)
+      hipLaunchKernelGGL((emd_rows_kernel<T, 1>), grow, dim3(EMD_THREADS), 0, s, p1, p2, remr, rr,
+                         reml, rl, nn, mm, st);
+    else if (st == EMD_LEVELS)
+      hipLaunchKernelGGL((emd_rows_kernel<T, 2>), grow, dim3(EMD_THREADS), 0, s, p1, p2, remr, rr,
+                         reml, rl, nn, mm, st);
+    else
+      hipLaunchKernelGGL((emd_rows_kernel<T, 3>), grow, dim3(EMD_THREADS), 0, s, p1, p2, remr, rr,
+                         reml, rl, nn, mm, st);
+    if (st < EMD_LEVELS)
+      hipLaunchKernelGGL(emd_cols_kernel<T>, gcol, dim3(EMD_THREADS), 0, s, p1, p2, rl, remr, rr,
+                         nn, mm, st);
+  }
+  hipLaunchKernelGGL(emd_match_kernel<T>, dim3((unsigned)L.gx, (unsigned)L.gy, bb),
+                     dim3(EMD_THREADS), 0, s, p1, p2, rl, rr, nn, mm, (T*)match, cp);
+  hipLaunchKernelGGL(emd_cost_kernel<T>, dim3(bb), dim3(EMD_THREADS), 0, s, cp, L.gx * L.gy,
+                     (T*)cost);
+  return check_launch("tpo_emd_fwd");
+}
+
+template <typename T>
+int emd_bwd_impl(const void* grad_cost, const void* xyz1, const void* xyz2, const void* match,
+                 int64_t B, int64_t n, int64_t m, void* grad1, void* grad2, char* ws,
+                 hipStream_t s) {
+  typedef typename EmdV<T>::type V;
+  const EmdLayout L = emd_layout<V>(B, n, m);
+  V* part = (V*)(ws + L.g1);
+  const int nn = (int)n, mm = (int)m;
+  const unsigned bb = (unsigned)B;
+  hipLaunchKernelGGL(emd_grad2_kernel<T>, dim3((unsigned)((m + 3) / 4), bb), dim3(EMD_THREADS), 0,
+                     s, (const T*)grad_cost, (const T*)xyz1, (const T*)xyz2, (const T*)match, nn, mm,
+                     (T*)grad2);
+  hipLaunchKernelGGL(emd_grad1_part_kernel<T>, dim3((unsigned)L.gx, (unsigned)L.nchunk, bb),
+                     dim3(EMD_THREADS), 0, s, (const T*)xyz1, (const T*)xyz2, (const T*)match, nn,
+                     mm, part);
+  hipLaunchKernelGGL(emd_grad1_final_kernel<T>, dim3((unsigned)L.gx, bb), dim3(EMD_THREADS), 0, s,
+                     (const T*)grad_cost, part, nn, L.nchunk, (T*)grad1);
+  return check_launch("tpo_emd_bwd");
+}
+
+template <typename T>
+void emd_zero(void* p, int64_t count, hipStream_t s) {
+  if (count <= 0) return;
+  hipLaunchKernelGGL(emd_zero_kernel<T>, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s,
+                     (T*)p, count);
+}
+
+int emd_check_sizes(const char* what, int64_t B, int64_t n, int64_t m) {
+  if (B < 0 || n < 0 || m < 0 || B >= 65536 || n >= ((int64_t)1 << 30) ||
+      m >= ((int64_t)1 << 30) || n * m >= ((int64_t)1 << 40))
+    return set_error(TPO_ERR_ARG, "%s: bad sizes B=%lld n=%lld m=%lld", what, (long long)B,
+                     (long long)n, (long long)m);
+  return TPO_OK;
+}
+
+}  // namespace
+}  // namespace tpo
+
+using namespace tpo;
+
+extern "C" int64_t tpo_emd_workspace_size(int dtype, int64_t B, int64_t n, int64_t m) {
+  if (B < 0 || n < 0 || m < 0) return -1;
+  if (B == 0 || n == 0 || m == 0) return 0;
+  switch (dtype) {
+    case TPO_F32:
+    case TPO_F16: return emd_layout<float>(B, n, m).total;
+    case TPO_F64: return emd_layout<double>(B, n, m).total;
+    default: set_error(TPO_ERR_DTYPE, "tpo_emd_workspace_size: unsupported dtype %d", dtype); return -1;
+  }
+}
+
+extern "C" int tpo_emd_fwd(int dtype, const void* xyz1, const void* xyz2, int64_t B, int64_t n,
+                           int64_t m, void* cost, void* match, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+  if (int rc = emd_check_sizes("tpo_emd_fwd", B, n, m)) return rc;
+  if (dtype != TPO_F32 && dtype != TPO_F64 && dtype != TPO_F16)
+    return set_error(TPO_ERR_DTYPE, "tpo_emd_fwd: unsupported dtype %d", dtype);
+  hipStream_t s = (hipStream_t)stream;
+  if (B == 0) return TPO_OK;
+  if (n == 0 || m == 0) {  // emd.cu:313-318: zero cost, empty match
+    if (dtype == TPO_F64) emd_zero<double>(cost, B, s);
+    else if (dtype == TPO_F32) emd_zero<float>(cost, B, s);
+    else emd_zero<half_t>(cost, B, s);
+    return check_launch("tpo_emd_fwd");
+  }
+  const int64_t need = tpo_emd_workspace_size(dtype, B, n, m);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255))
+    return set_error(TPO_ERR_WORKSPACE, "tpo_emd_fwd: workspace needs %lld bytes (256-aligned)",
+                     (long long)need);
+  switch (dtype) {
+    case TPO_F32: return emd_fwd_impl<float>(xyz1, xyz2, B, n, m, cost, match, (char*)workspace, s);
+    case TPO_F64: return emd_fwd_impl<double>(xyz1, xyz2, B, n, m, cost, match, (char*)workspace, s);
+    default: return emd_fwd_impl<half_t>(xyz1, xyz2, B, n, m, cost, match, (char*)workspace, s);
+  }
+}
+
+extern "C" int tpo_emd_bwd(int dtype, const void* grad_cost, const void* xyz1, const void* xyz2,
+                           const void* match, int64_t B, int64_t n, int64_t m, void* grad_xyz1,
+                           void* grad_xyz2, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
+  if (int rc = emd_check_sizes("tpo_emd_bwd", B, n, m)) return rc;
+  if (dtype != TPO_F32 && dtype != TPO_F64 && dtype != TPO_F16)
+    return set_error(TPO_ERR_DTYPE, "tpo_emd_bwd: unsupported dtype %d", dtype);
+  hipStream_t s = (hipStream_t)stream;
+  if (B == 0) return TPO_OK;
+  if (n == 0 || m == 0) {  // emd.cu:365-369
+    if (dtype == TPO_F64) {
+      emd_zero<double>(grad_xyz1, B * n * 3, s);
+      emd_zero<double>(grad_xyz2, B * m * 3, s);
+    } else if (dtype == TPO_F32) {
+      emd_zero<float>(grad_xyz1, B * n * 3, s);
+      emd_zero<float>(grad_xyz2, B * m * 3, s);
+    } else {
+      emd_zero<half_t>(grad_xyz1, B * n * 3, s);
+      emd_zero<half_t>(grad_xyz2, B * m * 3, s);
+    }
+    return check_launch("tpo_emd_bwd");
+  }
+  const int64_t need = tpo_emd_workspace_size(dtype, B, n, m);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255))
+    return set_error(TPO_ERR_WORKSPACE, "tpo_emd_bwd: workspace needs %lld bytes (256-aligned)",
+                     (long long)need);
+  switch (dtype) {
+    case TPO_F32:
+      return emd_bwd_impl<float>(grad_cost, xyz1, xyz2, match, B, n, m, grad_xyz1, grad_xyz2,
+                                 (char*)workspace, s);
+    case TPO_F64:
+      return emd_bwd_impl<double>(grad_cost, xyz1, xyz2, match, B, n, m, grad_xyz1, grad_xyz2,
+                                  (char*)workspace, s);
+    default:
+      return emd_bwd_impl<half_t>(grad_cost, xyz1, xyz2, match, B, n, m, grad_xyz1, grad_xyz2,
+                                  (char*)workspace, s);
+  }
+}

@@ -5,6 +5,7 @@
 //   torch_point_ops_knn      knn.cpp:166-171
 //   torch_point_ops_fps      fps.cpp:158-162
 //   torch_point_ops_quick_fps fps.cpp:165-167
+//   torch_point_ops_emd      emd.cpp:31-34
 // and implements them for the CUDA dispatch key (HIP tensors on ROCm) by
 // calling the C ABI of libtpo_hip.so on the current HIP stream.  Validation
 // and error texts follow the reference's TORCH_CHECKs.  The shim does the
@@ -475,6 +476,76 @@ at::Tensor gather_points_backward_hip(const at::Tensor& grad_in, const at::Tenso
   return out;
 }
 
+// ---------------------------------------------------------------------- emd
+// emd.cu:11-13: CHECK_CUDA + CHECK_CONTIGUOUS
+void check_emd_input(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
+std::tuple<at::Tensor, at::Tensor> emd_forward_hip(const at::Tensor& xyz1,
+                                                   const at::Tensor& xyz2) {
+  check_emd_input(xyz1, "xyz1");
+  check_emd_input(xyz2, "xyz2");
+  // emd.cu:309-311
+  TORCH_CHECK(xyz1.dim() == 3 && xyz2.dim() == 3, "Input tensors must be 3D");
+  TORCH_CHECK(xyz1.size(0) == xyz2.size(0), "Input tensors must have the same batch size");
+  TORCH_CHECK(xyz1.size(2) == 3 && xyz2.size(2) == 3, "Input tensors must have 3 channels");
+  TORCH_CHECK(xyz1.scalar_type() == xyz2.scalar_type(), "dtypes differ");
+  TORCH_CHECK(xyz1.device() == xyz2.device(), "xyz1 and xyz2 must be on the same device");
+  c10::OptionalDeviceGuard guard(xyz1.device());
+  const int64_t B = xyz1.size(0), n = xyz1.size(1), m = xyz2.size(1);
+  const int dt = dtype_code(xyz1, "emd_forward");
+  at::Tensor cost = at::empty({B}, xyz1.options());
+  at::Tensor match = at::empty({B, m, n}, xyz1.options());
+  const int64_t ws_bytes = tpo_emd_workspace_size(dt, B, n, m);
+  TORCH_CHECK(ws_bytes >= 0, "emd_forward: ", tpo_last_error());
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes}, xyz1.options().dtype(at::kByte));
+  check_rc(tpo_emd_fwd(dt, xyz1.data_ptr(), xyz2.data_ptr(), B, n, m, cost.data_ptr(),
+                       match.data_ptr(), ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+                       stream_of(xyz1)),
+           "emd_forward");
+  return {cost, match};
+}
+
+std::tuple<at::Tensor, at::Tensor> emd_backward_hip(const at::Tensor& grad_cost_in,
+                                                    const at::Tensor& xyz1, const at::Tensor& xyz2,
+                                                    const at::Tensor& match) {
+  TORCH_CHECK(grad_cost_in.is_cuda(), "grad_cost must be a CUDA tensor");
+  check_emd_input(xyz1, "xyz1");
+  check_emd_input(xyz2, "xyz2");
+  check_emd_input(match, "match");
+  TORCH_CHECK(xyz1.dim() == 3 && xyz2.dim() == 3, "Input tensors must be 3D");
+  c10::OptionalDeviceGuard guard(xyz1.device());
+  const int64_t B = xyz1.size(0), n = xyz1.size(1), m = xyz2.size(1);
+  TORCH_CHECK(xyz2.size(0) == B && grad_cost_in.numel() == B, "batch sizes differ");
+  TORCH_CHECK(match.scalar_type() == xyz1.scalar_type() && xyz2.scalar_type() == xyz1.scalar_type(),
+              "dtypes differ");
+  TORCH_CHECK(match.numel() == B * m * n, "match must be (B, m, n)");
+  const int dt = dtype_code(xyz1, "emd_backward");
+  const at::Tensor grad_cost = grad_cost_in.to(xyz1.scalar_type()).contiguous();
+  at::Tensor g1 = at::empty_like(xyz1), g2 = at::empty_like(xyz2);
+  const int64_t ws_bytes = tpo_emd_workspace_size(dt, B, n, m);
+  TORCH_CHECK(ws_bytes >= 0, "emd_backward: ", tpo_last_error());
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes}, xyz1.options().dtype(at::kByte));
+  check_rc(tpo_emd_bwd(dt, grad_cost.data_ptr(), xyz1.data_ptr(), xyz2.data_ptr(), match.data_ptr(),
+                       B, n, m, g1.data_ptr(), g2.data_ptr(), ws_bytes > 0 ? ws.data_ptr() : nullptr,
+                       ws_bytes, stream_of(xyz1)),
+           "emd_backward");
+  return {g1, g2};
+}
+
+// emd.cpp:19-28
+std::tuple<at::Tensor, at::Tensor> emd_forward_cpu(const at::Tensor&, const at::Tensor&) {
+  TORCH_CHECK(false, "emd_forward is not implemented for CPU");
+}
+std::tuple<at::Tensor, at::Tensor> emd_backward_cpu(const at::Tensor&, const at::Tensor&,
+                                                    const at::Tensor&, const at::Tensor&) {
+  TORCH_CHECK(false, "emd_backward is not implemented for CPU");
+}
+
 }  // namespace
 
 TORCH_LIBRARY(torch_point_ops_chamfer, m) {
@@ -535,6 +606,19 @@ TORCH_LIBRARY(torch_point_ops_quick_fps, m) {
 }
 TORCH_LIBRARY_IMPL(torch_point_ops_quick_fps, CUDA, m) {
   m.impl("quick_fps_forward", &quick_fps_forward_hip);
+}
+
+TORCH_LIBRARY(torch_point_ops_emd, m) {
+  m.def("emd_forward(Tensor xyz1, Tensor xyz2) -> (Tensor, Tensor)");
+  m.def("emd_backward(Tensor grad_cost, Tensor xyz1, Tensor xyz2, Tensor match) -> (Tensor, Tensor)");
+}
+TORCH_LIBRARY_IMPL(torch_point_ops_emd, CPU, m) {
+  m.impl("emd_forward", &emd_forward_cpu);
+  m.impl("emd_backward", &emd_backward_cpu);
+}
+TORCH_LIBRARY_IMPL(torch_point_ops_emd, CUDA, m) {
+  m.impl("emd_forward", &emd_forward_hip);
+  m.impl("emd_backward", &emd_backward_hip);
 }
 
 }  // namespace torch_point_ops

@@ -1,20 +1,18 @@
-"""Placeholders for the reference's EMD API (torch_point_ops/emd/emd.py)."""
+"""EarthMoverDistance module (reference: torch_point_ops/emd/emd.py:1-19)."""
 import torch
 
-_MSG = ("earth mover's distance is not part of the MI355X build of torch_point_ops "
-        "(only chamfer, knn, fps and gather_points are)")
-
-
-def earth_movers_distance(xyz1, xyz2, *args, **kwargs):
-    raise NotImplementedError(_MSG)
-
-
-emd = earth_movers_distance
+from . import earth_movers_distance
 
 
 class EarthMoverDistance(torch.nn.Module):
-    def __init__(self, *args, **kwargs):
-        super().__init__()
+    """Mean over the batch of the earth mover's distance of two point clouds."""
 
     def forward(self, xyz1, xyz2):
-        raise NotImplementedError(_MSG)
+        """
+        Args:
+            xyz1 (torch.Tensor): (B, N, 3)
+            xyz2 (torch.Tensor): (B, M, 3)
+        Returns:
+            torch.Tensor: () mean EMD distance
+        """
+        return earth_movers_distance(xyz1, xyz2).mean()
