@@ -114,12 +114,13 @@ def test_emd_sizes_and_errors(lib):
     lib.tpo_emd_workspace_size.argtypes = [ctypes.c_int, I, I, I]
     lib.tpo_emd_workspace_size.restype = I
     # float/half: p1, p2 (4 floats a point), remain, 10 levels of ratios,
-    # 8 x 64 cost partials and 16 chunks of grad_xyz1 partials per cloud
+    # 8 x 64 cost partials and 16 chunks of grad_xyz1 partials per cloud,
+    # plus the int32 point orders
     B, n, m = 16, 2048, 2048
-    expect = 4 * B * (n * 4 + m * 4 + n + m + 10 * n + 10 * m + 8 * 64 + 16 * n * 3)
-    assert lib.tpo_emd_workspace_size(0, B, n, m) == expect
-    assert lib.tpo_emd_workspace_size(2, B, n, m) == expect
-    assert lib.tpo_emd_workspace_size(1, B, n, m) == 2 * expect
+    vals = B * (n * 4 + m * 4 + n + m + 10 * n + 10 * m + 8 * 64 + 16 * n * 3)
+    assert lib.tpo_emd_workspace_size(0, B, n, m) == 4 * vals + 4 * B * (n + m)
+    assert lib.tpo_emd_workspace_size(2, B, n, m) == 4 * vals + 4 * B * (n + m)
+    assert lib.tpo_emd_workspace_size(1, B, n, m) == 8 * vals + 4 * B * (n + m)
     assert lib.tpo_emd_workspace_size(0, 2, 0, 5) == 0
     assert lib.tpo_emd_workspace_size(3, 1, 4, 4) == -1  # bfloat16: not an EMD dtype
     lib.tpo_emd_fwd.argtypes = [ctypes.c_int, P, P, I, I, I, P, P, P, I, P]

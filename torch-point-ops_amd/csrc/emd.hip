@@ -19,9 +19,12 @@
 // argument to float (emd.cu:134,136,178), which is kept.
 //
 // Design for MI355X (the reference runs one 512-thread block per cloud):
-//   * each pass is a grid-wide sweep: a 256-thread workgroup owns 64 points
-//     (one per lane) and its four waves each sum over a quarter of the other
+//   * each pass is a grid-wide sweep: a 512-thread workgroup owns 64 points
+//     (one per lane) and its eight waves each sum over an eighth of the other
 //     cloud, read with wave-uniform (scalar) loads, combined in fixed order;
+//   * exponentials that are +0 in all 64 lanes (arguments below the float
+//     or double underflow, the steep levels on distant points) are skipped
+//     with a wave-uniform branch, which changes no sum;
 //   * pass 3 of level j and pass 1 of level j-1 need the same inputs, so they
 //     share one sweep (two exponentials per pair): 21 dependent sweeps;
 //   * match is not accumulated in HBM level by level: the per-level ratioL
@@ -41,6 +44,7 @@ namespace {
 
 constexpr int EMD_LEVELS = 10;       // j = 7 .. -2
 constexpr int EMD_THREADS = 256;     // 4 waves
+constexpr int EMD_SWEEP_THREADS = 512;  // 8 waves per 64 points of a sweep
 constexpr int EMD_MATCH_ROWS = 32;   // match rows per workgroup of the final pass
 constexpr int EMD_G1_ROWS = 128;     // match rows per grad_xyz1 partial
 
@@ -72,6 +76,21 @@ __device__ __forceinline__ V emd_e(V level, V d) {
     a = a < (V)-20 ? (V)-20 : (a > (V)20 ? (V)20 : a);
   return emd_exp(a);
 }
+// Below these arguments exp() is exactly +0 (float: e^-103.98 is half the
+// smallest denormal; double: e^-745.2), so a term e * w adds exactly nothing
+// to a sum of non-negative terms; float16 clamps its argument at -20.
+template <typename T, typename V>
+__device__ __forceinline__ V emd_zero_below() {
+  return std::is_same<T, double>::value ? (V)-760 : (V)-120;
+}
+// True when exp(level * d) is +0 in every lane of the wave, so the wave can
+// skip the exponential and its products (wave-uniform branch).  A NaN
+// argument is never "below", so NaN still propagates.
+template <typename T, typename V>
+__device__ __forceinline__ bool emd_wave_zero(V level, V d) {
+  if constexpr (std::is_same<T, half_t>::value) return false;
+  return __builtin_amdgcn_ballot_w64(!(level * d < emd_zero_below<T, V>())) == 0;
+}
 // fminf(x, 1.0f) / fmaxf(0.0f, x) of emd.cu:134,136,178 (float functions)
 template <typename V>
 __device__ __forceinline__ V emd_min1(V a) { return (V)fminf((float)a, 1.0f); }
@@ -93,8 +112,9 @@ __device__ __forceinline__ V wave_sum(V v) {
 //   rl[B][10][n], rr[B][10][m] ratioL / ratioR of every level
 //   cost[B][gy][gx]            matchcost partials of the final pass
 //   g1[B][nchunk][n][3]        grad_xyz1 partials of the backward
+//   ord1[B][n], ord2[B][m]     int32: each cloud's points in Morton order
 struct EmdLayout {
-  int64_t p1, p2, reml, remr, rl, rr, cost, g1, total;
+  int64_t p1, p2, reml, remr, rl, rr, cost, g1, ord1, ord2, total;
   int gx, gy, nchunk;
 };
 template <typename V>
@@ -114,6 +134,8 @@ inline EmdLayout emd_layout(int64_t B, int64_t n, int64_t m) {
   L.rr = o; o += al(B * EMD_LEVELS * m * s);
   L.cost = o; o += al(B * (int64_t)L.gx * L.gy * s);
   L.g1 = o; o += al(B * (int64_t)L.nchunk * n * 3 * s);
+  L.ord1 = o; o += al(B * n * 4);
+  L.ord2 = o; o += al(B * m * 4);
   L.total = o;
   return L;
 }
@@ -142,9 +164,122 @@ __global__ __launch_bounds__(EMD_THREADS) void emd_prep_kernel(
   }
 }
 
-// Sums over the "other" cloud for one own point per lane; the four waves take
-// a quarter of the other points each.  NS = 1 sums e(la)*wa; NS = 2 also
-// sums e(lb)*wb with the same distances.
+// The points of one cloud (blockIdx.y: 0 = xyz1, 1 = xyz2) listed by the
+// cell of a 16^3 grid over its bounding box, in Morton order of the cells
+// (counting sort in LDS; the order inside a cell is whatever the atomics
+// give).  A sweep's wave then holds 64 nearby points, so the steep levels'
+// exponentials vanish in all of its lanes at once.  Which wave a point sits
+// in changes no result: its sums run over the other cloud in a fixed order
+// and a skipped term is exactly zero.
+constexpr int EMD_ORDER_THREADS = 1024;
+constexpr int EMD_OGRID = 16;
+constexpr int EMD_OCELLS = EMD_OGRID * EMD_OGRID * EMD_OGRID;
+
+__device__ __forceinline__ uint32_t emd_spread3(uint32_t v) {  // 4 bits -> every third bit
+  v &= 0xf;
+  v = (v | (v << 4)) & 0x0c3;
+  v = (v | (v << 2)) & 0x249;
+  return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(EMD_ORDER_THREADS) void emd_order_kernel(
+    const T* __restrict__ xyz1, const T* __restrict__ xyz2, int n, int m, int* __restrict__ ord1,
+    int* __restrict__ ord2) {
+  __shared__ uint32_t s_cnt[EMD_OCELLS];
+  __shared__ float s_box[6][EMD_ORDER_THREADS / 64];
+  __shared__ uint32_t s_part[EMD_ORDER_THREADS / 64];
+  const int64_t b = blockIdx.x;
+  const bool two = blockIdx.y != 0;
+  const int N = two ? m : n;
+  const T* P = two ? xyz2 + b * m * 3 : xyz1 + b * n * 3;
+  int* ord = two ? ord2 + b * m : ord1 + b * n;
+  const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+  float lo[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
+  float hi[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  for (int k = tid; k < N; k += EMD_ORDER_THREADS) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const float v = (float)P[3 * k + c];
+      lo[c] = fminf(lo[c], v);
+      hi[c] = fmaxf(hi[c], v);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      lo[c] = fminf(lo[c], __shfl_xor(lo[c], o, 64));
+      hi[c] = fmaxf(hi[c], __shfl_xor(hi[c], o, 64));
+    }
+    if (lane == 0) {
+      s_box[c][w] = lo[c];
+      s_box[3 + c][w] = hi[c];
+    }
+  }
+  for (int c = tid; c < EMD_OCELLS; c += EMD_ORDER_THREADS) s_cnt[c] = 0;
+  __syncthreads();
+  float org[3], scl[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    float a = __builtin_inff(), z = -__builtin_inff();
+    for (int v = 0; v < EMD_ORDER_THREADS / 64; ++v) {
+      a = fminf(a, s_box[c][v]);
+      z = fmaxf(z, s_box[3 + c][v]);
+    }
+    const float ext = z - a;
+    org[c] = a;
+    scl[c] = (ext > 0.f && ext < __builtin_inff()) ? (float)EMD_OGRID / ext : 0.f;
+  }
+  auto cell_of = [&](int k) -> uint32_t {
+    uint32_t cc[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const float f = ((float)P[3 * k + c] - org[c]) * scl[c];
+      int i = (f == f) ? (int)f : 0;  // NaN -> cell 0
+      cc[c] = (uint32_t)(i < 0 ? 0 : (i > EMD_OGRID - 1 ? EMD_OGRID - 1 : i));
+    }
+    return emd_spread3(cc[0]) | (emd_spread3(cc[1]) << 1) | (emd_spread3(cc[2]) << 2);
+  };
+  for (int k = tid; k < N; k += EMD_ORDER_THREADS) atomicAdd(&s_cnt[cell_of(k)], 1u);
+  __syncthreads();
+  {  // exclusive scan of the counters, EMD_OCELLS / EMD_ORDER_THREADS per thread
+    constexpr int PER = EMD_OCELLS / EMD_ORDER_THREADS;
+    uint32_t v[PER], sum = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      v[i] = s_cnt[tid * PER + i];
+      sum += v[i];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) s_part[w] = incl;
+    __syncthreads();
+    uint32_t run = incl - sum;
+    for (int v2 = 0; v2 < w; ++v2) run += s_part[v2];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      s_cnt[tid * PER + i] = run;
+      run += v[i];
+    }
+  }
+  __syncthreads();
+  for (int k = tid; k < N; k += EMD_ORDER_THREADS) ord[atomicAdd(&s_cnt[cell_of(k)], 1u)] = k;
+}
+
+// One point of the coordinate arrays (x, y, z, unused), read whole.
+template <typename V>
+struct __attribute__((aligned(4 * sizeof(V)))) EmdPt {
+  V x, y, z, w;
+};
+
+// Sums over the "other" cloud for one own point per lane; the waves of the
+// workgroup take an equal share of the other points each.  NS = 1 sums
+// e(la)*wa; NS = 2 also sums e(lb)*wb with the same distances.
 template <typename T, int NS>
 __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restrict__ other, int cnt,
                                           typename EmdV<T>::type x, typename EmdV<T>::type y,
@@ -154,40 +289,105 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
                                           const typename EmdV<T>::type* __restrict__ wb,
                                           typename EmdV<T>::type* sums) {
   typedef typename EmdV<T>::type V;
-  __shared__ V s_part[NS][EMD_THREADS / 64 - 1][64];
+  constexpr int NW = EMD_SWEEP_THREADS / 64;
+  __shared__ V s_part[NS][NW - 1][64];
   const int w = wave_id(), lane = lane_id();
-  const int q0 = (int)((int64_t)cnt * w / 4), q1 = (int)((int64_t)cnt * (w + 1) / 4);
+  const int q0 = (int)((int64_t)cnt * w / NW), q1 = (int)((int64_t)cnt * (w + 1) / NW);
   V sa = (V)0, sb = (V)0;
-#pragma unroll 4
-  for (int q = q0; q < q1; ++q) {
-    const V d = sq3(other[4 * q] - x, other[4 * q + 1] - y, other[4 * q + 2] - z);
-    sa = emd_fma(emd_e<T>(la, d), wa[q], sa);
-    if constexpr (NS == 2) sb = emd_fma(emd_e<T>(lb, d), wb[q], sb);
+  // The wave stages its share of the other cloud 64 points at a time in its
+  // own slice of LDS: lane i loads point i of the next chunk (vector loads,
+  // issued before the current chunk is processed), then every lane reads the
+  // chunk's points back as broadcasts.  The points are taken in batches of U;
+  // one wave-uniform test per level decides whether any of the batch's
+  // exponentials can be non-zero.  Terms are added in point order, as in a
+  // plain loop.
+  constexpr int C = 64, U = 8;
+  __shared__ EmdPt<V> s_pt[NW][C];  // (x, y, z, wa)
+  __shared__ V s_wb[NS == 2 ? NW : 1][C];
+  const V zb = emd_zero_below<T, V>();
+  const EmdPt<V>* op = (const EmdPt<V>*)other;
+  EmdPt<V> nr;
+  V nb = (V)0;
+  auto fetch = [&](int c0) {
+    const int qq = c0 + lane;
+    if (qq < q1) {
+      const EmdPt<V> g = op[qq];
+      nr = EmdPt<V>{g.x, g.y, g.z, wa[qq]};
+      if constexpr (NS == 2) nb = wb[qq];
+    } else {
+      nr = EmdPt<V>{(V)0, (V)0, (V)0, (V)0};
+    }
+  };
+  auto batch = [&](int base, auto ucnt) {
+    constexpr int UB = decltype(ucnt)::value;
+    EmdPt<V> pt[UB];
+    V pb[UB];
+    V d[UB];
+    bool nza = false, nzb = false;
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      pt[u] = s_pt[w][base + u];
+      if constexpr (NS == 2) pb[u] = s_wb[w][base + u];
+      d[u] = sq3(pt[u].x - x, pt[u].y - y, pt[u].z - z);
+      nza |= !(la * d[u] < zb);  // NaN counts as non-zero
+      if constexpr (NS == 2) nzb |= !(lb * d[u] < zb);
+    }
+    if (std::is_same<T, half_t>::value || __builtin_amdgcn_ballot_w64(nza) != 0) {
+#pragma unroll
+      for (int u = 0; u < UB; ++u) sa = emd_fma(emd_e<T>(la, d[u]), pt[u].w, sa);
+    }
+    if constexpr (NS == 2) {
+      if (std::is_same<T, half_t>::value || __builtin_amdgcn_ballot_w64(nzb) != 0) {
+#pragma unroll
+        for (int u = 0; u < UB; ++u) sb = emd_fma(emd_e<T>(lb, d[u]), pb[u], sb);
+      }
+    }
+  };
+  if (q0 < q1) fetch(q0);
+  for (int c0 = q0; c0 < q1; c0 += C) {
+    // the previous chunk's reads were issued before this write (LDS runs a
+    // wave's operations in order), so one slice per wave suffices
+    s_pt[w][lane] = nr;
+    if constexpr (NS == 2) s_wb[w][lane] = nb;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (c0 + C < q1) fetch(c0 + C);
+    const int cn = min(C, q1 - c0);
+    int u0 = 0;
+    for (; u0 + U <= cn; u0 += U) batch(u0, std::integral_constant<int, U>{});
+    for (; u0 < cn; ++u0) batch(u0, std::integral_constant<int, 1>{});
+    __builtin_amdgcn_wave_barrier();
   }
   if (w > 0) {
     s_part[0][w - 1][lane] = sa;
     if constexpr (NS == 2) s_part[NS - 1][w - 1][lane] = sb;
   }
   __syncthreads();
-  if (w == 0) {
-    sums[0] = ((sa + s_part[0][0][lane]) + s_part[0][1][lane]) + s_part[0][2][lane];
-    if constexpr (NS == 2)
-      sums[1] = ((sb + s_part[NS - 1][0][lane]) + s_part[NS - 1][1][lane]) + s_part[NS - 1][2][lane];
+  if (w == 0) {  // wave 0's sum, then waves 1 .. NW-1 in order
+#pragma unroll
+    for (int v = 0; v < NW - 1; ++v) {
+      sa += s_part[0][v][lane];
+      if constexpr (NS == 2) sb += s_part[NS - 1][v][lane];
+    }
+    sums[0] = sa;
+    if constexpr (NS == 2) sums[1] = sb;
   }
 }
 
 // Step s = 0..10 over the xyz1 points: pass 3 of level s-1 (s >= 1), then
 // pass 1 of level s (s <= 9).  MODE 1: pass 1 only; 2: pass 3 only; 3: both.
 template <typename T, int MODE>
-__global__ __launch_bounds__(EMD_THREADS) void emd_rows_kernel(
+__global__ __launch_bounds__(EMD_SWEEP_THREADS) void emd_rows_kernel(
     const typename EmdV<T>::type* __restrict__ p1, const typename EmdV<T>::type* __restrict__ p2,
     const typename EmdV<T>::type* __restrict__ remr, const typename EmdV<T>::type* __restrict__ rr,
-    typename EmdV<T>::type* __restrict__ reml, typename EmdV<T>::type* __restrict__ rl, int n, int m,
-    int s) {
+    typename EmdV<T>::type* __restrict__ reml, typename EmdV<T>::type* __restrict__ rl,
+    const int* __restrict__ ord1, int n, int m, int s) {
   typedef typename EmdV<T>::type V;
   const int64_t b = blockIdx.y;
   const int lane = lane_id();
-  const int k = blockIdx.x * 64 + lane;
+  const int pos = blockIdx.x * 64 + lane;
+  const int k = pos < n ? ord1[b * n + pos] : n;  // this lane's xyz1 point
   V x = (V)0, y = (V)0, z = (V)0;
   if (k < n) {
     x = p1[(b * n + k) * 4];
@@ -218,14 +418,15 @@ __global__ __launch_bounds__(EMD_THREADS) void emd_rows_kernel(
 
 // Pass 2 of level t over the xyz2 points (emd.cu:98-138).
 template <typename T>
-__global__ __launch_bounds__(EMD_THREADS) void emd_cols_kernel(
+__global__ __launch_bounds__(EMD_SWEEP_THREADS) void emd_cols_kernel(
     const typename EmdV<T>::type* __restrict__ p1, const typename EmdV<T>::type* __restrict__ p2,
     const typename EmdV<T>::type* __restrict__ rl, typename EmdV<T>::type* __restrict__ remr,
-    typename EmdV<T>::type* __restrict__ rr, int n, int m, int t) {
+    typename EmdV<T>::type* __restrict__ rr, const int* __restrict__ ord2, int n, int m, int t) {
   typedef typename EmdV<T>::type V;
   const int64_t b = blockIdx.y;
   const int lane = lane_id();
-  const int l = blockIdx.x * 64 + lane;
+  const int pos = blockIdx.x * 64 + lane;
+  const int l = pos < m ? ord2[b * m + pos] : m;  // this lane's xyz2 point
   V x = (V)0, y = (V)0, z = (V)0;
   if (l < m) {
     x = p2[(b * m + l) * 4];
@@ -272,6 +473,7 @@ __global__ __launch_bounds__(EMD_THREADS) void emd_match_kernel(
     V mt = (V)0;
 #pragma unroll
     for (int t = 0; t < EMD_LEVELS; ++t) {
+      if (emd_wave_zero<T>(emd_level<V>(t), d)) continue;  // w = +0: mt + 0 == mt
       const V w = (emd_e<T>(emd_level<V>(t), d) * r[t]) * rrb[t * m + l];  // emd.cu:170
       mt = emd_st<T, V>(mt + emd_st<T, V>(w));                             // emd.cu:171
     }
@@ -404,6 +606,8 @@ int emd_fwd_impl(const void* xyz1, const void* xyz2, int64_t B, int64_t n, int64
   V* rl = (V*)(ws + L.rl);
   V* rr = (V*)(ws + L.rr);
   V* cp = (V*)(ws + L.cost);
+  int* ord1 = (int*)(ws + L.ord1);
+  int* ord2 = (int*)(ws + L.ord2);
   // emd.cu:21-28: float(n)/m
   const float mult_l = n >= m ? 1.0f : (float)m / (float)n;
   const float mult_r = n >= m ? (float)n / (float)m : 1.0f;
@@ -412,20 +616,22 @@ int emd_fwd_impl(const void* xyz1, const void* xyz2, int64_t B, int64_t n, int64
   hipLaunchKernelGGL(emd_prep_kernel<T>, dim3((unsigned)((std::max(n, m) + 255) / 256), bb),
                      dim3(EMD_THREADS), 0, s, (const T*)xyz1, (const T*)xyz2, nn, mm, mult_l, mult_r,
                      p1, p2, reml, remr);
+  hipLaunchKernelGGL(emd_order_kernel<T>, dim3(bb, 2), dim3(EMD_ORDER_THREADS), 0, s,
+                     (const T*)xyz1, (const T*)xyz2, nn, mm, ord1, ord2);
   const dim3 grow((unsigned)((n + 63) / 64), bb), gcol((unsigned)((m + 63) / 64), bb);
   for (int st = 0; st <= EMD_LEVELS; ++st) {
     if (st == 0)
-      hipLaunchKernelGGL((emd_rows_kernel<T, 1>), grow, dim3(EMD_THREADS), 0, s, p1, p2, remr, rr,
-                         reml, rl, nn, mm, st);
+      hipLaunchKernelGGL((emd_rows_kernel<T, 1>), grow, dim3(EMD_SWEEP_THREADS), 0, s, p1, p2, remr, rr,
+                         reml, rl, ord1, nn, mm, st);
     else if (st == EMD_LEVELS)
-      hipLaunchKernelGGL((emd_rows_kernel<T, 2>), grow, dim3(EMD_THREADS), 0, s, p1, p2, remr, rr,
-                         reml, rl, nn, mm, st);
+      hipLaunchKernelGGL((emd_rows_kernel<T, 2>), grow, dim3(EMD_SWEEP_THREADS), 0, s, p1, p2, remr, rr,
+                         reml, rl, ord1, nn, mm, st);
     else
-      hipLaunchKernelGGL((emd_rows_kernel<T, 3>), grow, dim3(EMD_THREADS), 0, s, p1, p2, remr, rr,
-                         reml, rl, nn, mm, st);
+      hipLaunchKernelGGL((emd_rows_kernel<T, 3>), grow, dim3(EMD_SWEEP_THREADS), 0, s, p1, p2, remr, rr,
+                         reml, rl, ord1, nn, mm, st);
     if (st < EMD_LEVELS)
-      hipLaunchKernelGGL(emd_cols_kernel<T>, gcol, dim3(EMD_THREADS), 0, s, p1, p2, rl, remr, rr,
-                         nn, mm, st);
+      hipLaunchKernelGGL(emd_cols_kernel<T>, gcol, dim3(EMD_SWEEP_THREADS), 0, s, p1, p2, rl, remr, rr,
+                         ord2, nn, mm, st);
   }
   hipLaunchKernelGGL(emd_match_kernel<T>, dim3((unsigned)L.gx, (unsigned)L.gy, bb),
                      dim3(EMD_THREADS), 0, s, p1, p2, rl, rr, nn, mm, (T*)match, cp);
