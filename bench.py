@@ -17,9 +17,10 @@ plus autograd backward), chunked, on a bounded sample, on the host's cores.
 
 Secondary lines (other BASELINE configs, reported under "secondary"):
 Chamfer c2 in float16, knn_points c3, knn_points c5 (bfloat16, matrix
-cores), FPS c4 (ms), gather_points c4 fwd/bwd (GB/s); the KNN and FPS lines
-carry a bounded CPU baseline of the reference CPU kernels' restatement
-(oracle/).
+cores), FPS c4 (ms), gather_points c4 fwd/bwd (GB/s), earth mover's
+distance at B=16, N=M=2048 (ms, against the reference's published RTX 3090
+time); the KNN, FPS and EMD lines carry a bounded CPU baseline of the
+oracle's restatement of the reference kernels (oracle/).
 
 Prints exactly one JSON line.
 """
@@ -37,6 +38,7 @@ sys.path.insert(0, os.path.join(REPO, "torch-point-ops_amd"))
 sys.path.insert(0, REPO)
 
 FP32_PEAK_TFLOPS = 157.3
+EMD_REF_MS = 32.366  # README.md:314, EMD FP32 eager, B16_N2048_M2048, RTX 3090
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense MFMA
 FLOP_PER_PAIR = 9  # 3 sub + 3 mul + 2 add + 1 compare per directed pair
@@ -233,6 +235,25 @@ def bench_fps(tpo, torch, steps):
                 bwd_bytes=B * C * N * 4 + B * C * M * 4 + B * M * 8, idx=idx.cpu(), pts=pts.cpu())
 
 
+def bench_emd(tpo, torch, steps):
+    """earth_movers_distance forward (no grad, as benchmark_flops.py:146-160
+    times it) and EarthMoverDistance forward + backward at B=16, N=M=2048."""
+    import workloads
+
+    a, b = (t.to("cuda:0") for t in workloads.emd_b16())
+
+    def fwd():
+        with torch.no_grad():
+            tpo.earth_movers_distance(a, b)
+
+    sec = time_steps(fwd, steps, 3, torch)
+    ga = a.clone().requires_grad_(True)
+    gb = b.clone().requires_grad_(True)
+    mod = tpo.EarthMoverDistance()
+    sec_fb = time_steps(lambda: torch.autograd.grad(mod(ga, gb), (ga, gb)), steps, 2, torch)
+    return dict(sec=sec, sec_fb=sec_fb, B=a.shape[0], N=a.shape[1], M=b.shape[1])
+
+
 # --------------------------------------------------------------------- CPU
 
 def cpu_chamfer(torch, budget_s=12.0):
@@ -316,6 +337,21 @@ def cpu_fps(O, np, pts, threads):
                        f"(fps.cpp restated)")
 
 
+def cpu_emd(O, threads):
+    """The oracle's restatement of emd.cu's approxmatch + matchcost (the
+    reference has no CPU kernel), one cloud per thread."""
+    import workloads
+
+    a, b = workloads.emd_b16()
+    nc = max(1, min(threads, a.shape[0]))
+    t0 = time.perf_counter()
+    O.emd_fwd(a[:nc].numpy(), b[:nc].numpy())
+    sec = time.perf_counter() - t0
+    return dict(value=round(nc / sec, 3), unit="clouds/s", cores=nc, kind="port",
+                sample=f"{nc} of the 16 clouds (2048 x 2048, float32), one per OpenMP thread, "
+                       f"oracle/tpo_oracle.c restating emd.cu:18-230")
+
+
 # ---------------------------------------------------------------- profiling
 
 def profile_run(tpo, torch, reps=5):
@@ -346,6 +382,18 @@ def profile_run(tpo, torch, reps=5):
     print("profile run done", flush=True)
 
 
+def profile_emd(tpo, torch, reps=5):
+    """EMD forward + backward at B=16, N=M=2048, float32, for rocprofv3."""
+    import workloads
+
+    a, b = (t.to("cuda:0").requires_grad_(True) for t in workloads.emd_b16())
+    mod = tpo.EarthMoverDistance()
+    for _ in range(reps):
+        torch.autograd.grad(mod(a, b), (a, b))
+    torch.cuda.synchronize()
+    print("profile emd done", flush=True)
+
+
 # -------------------------------------------------------------------- main
 
 def main():
@@ -357,6 +405,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-run", action="store_true",
                     help="run the fixed kernel sequence for rocprofv3 and exit")
+    ap.add_argument("--profile-emd", action="store_true",
+                    help="run EMD forward + backward (B=16, N=M=2048) for rocprofv3 and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs on a single MI355X "
@@ -370,6 +420,9 @@ def main():
 
     if args.profile_run:
         profile_run(tpo, torch)
+        return
+    if args.profile_emd:
+        profile_emd(tpo, torch)
         return
     log("[bench] chamfer c2 fwd+bwd")
     ch = bench_chamfer(tpo, torch, args.steps, args.warmup)
@@ -462,8 +515,20 @@ def main():
             "bwd_us": round(fp["gather_bwd_sec"] * 1e6, 2),
             "bwd_GBs": round(fp["bwd_bytes"] / fp["gather_bwd_sec"] / 1e9, 1),
             "bwd_frac_hbm": round(fp["bwd_bytes"] / fp["gather_bwd_sec"] / 1e9 / HBM_PEAK_GBS, 3)}
+        log("[bench] emd b16 n2048")
+        em = bench_emd(tpo, torch, max(3, args.steps // 4))
+        sec["emd_b16_n2048"] = {
+            "ms_fwd": round(em["sec"] * 1e3, 3),
+            "ms_fwd_bwd": round(em["sec_fb"] * 1e3, 3),
+            "clouds_per_s": round(em["B"] / em["sec"], 1),
+            "reference_rtx3090_ms_fwd": EMD_REF_MS,
+            "speedup_vs_reference_rtx3090": round(EMD_REF_MS / (em["sec"] * 1e3), 2),
+            "note": "earth_movers_distance forward under no_grad (the reference benchmark's "
+                    "timing, README.md:314 quotes 32.366 ms eager fp32 on an RTX 3090) and "
+                    "EarthMoverDistance fwd+bwd; float32, torch.randn clouds"}
         if not args.no_cpu:
-            log("[bench] cpu baselines (knn, fps)")
+            log("[bench] cpu baselines (knn, fps, emd)")
+            sec["emd_b16_n2048"]["cpu_baseline"] = cpu_emd(O, threads)
             sec["knn_c3"]["cpu_baseline"] = cpu_knn(O, np, threads)
             sec["fps_c4"]["cpu_baseline"] = cpu_fps(O, np, fp["pts"], threads)
             sec["knn_c5_bf16"]["cpu_baseline"] = cpu_knn_c5(O, np, threads)

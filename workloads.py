@@ -11,6 +11,9 @@ moved to the GPU, so the same seed gives the same bits everywhere.
   c4  FPS B=16, N=65536 -> 4096; 90% uniform [-1,1]^3, 10% in a sigma=0.05
       Gaussian blob; then gather_points of a (16, 64, 65536) N(0,1) feature map
   c5  high-D knn, B=4, 4096 x 65536, D=128, K=32, rows L2-normalised
+  emd earth mover's distance, B=16, N=M=2048, N(0,1)^3: the reference
+      benchmark's generator (benchmark_flops.py:39-49) at the size of its
+      published EMD rows (README.md:275,311-314)
 """
 from __future__ import annotations
 
@@ -86,4 +89,11 @@ def knn_c5(seed: int = 6, B: int = 4, P1: int = 4096, P2: int = 65536, D: int = 
     p2 = torch.randn(B, P2, D, generator=g)
     p1 = p1 / p1.norm(dim=-1, keepdim=True)
     p2 = p2 / p2.norm(dim=-1, keepdim=True)
+    return p1.to(dtype), p2.to(dtype)
+
+
+def emd_b16(seed: int = 7, B: int = 16, N: int = 2048, M: int = 2048, dtype=torch.float32):
+    g = _g(seed)
+    p1 = torch.randn(B, N, 3, generator=g)
+    p2 = torch.randn(B, M, 3, generator=g)
     return p1.to(dtype), p2.to(dtype)
