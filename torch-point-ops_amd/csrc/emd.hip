@@ -67,10 +67,27 @@ __device__ __forceinline__ V emd_st(V v) {
   if constexpr (std::is_same<T, half_t>::value) return (V)(half_t)v;
   return v;
 }
-__device__ __forceinline__ float emd_exp(float x) { return expf(x); }
+// exp(x) of the float paths (x <= 0 here, or NaN): 2^(x log2 e) with
+// x log2 e split as h + l by Cody and Waite's two-term reduction,
+// h = fl(x L1), l = fma(x, L2, fma(x, L1, -h)) where L1 + L2 = log2 e to 48
+// bits; 2^h from the hardware exp2 (v_exp_f32) and 2^l = 1 + l ln2 to within
+// (l ln2)^2 / 2 < 2^-33 since |l| < 2^-16.  Arguments below -150 give +0
+// (the value is below 2^-216); NaN stays NaN.  Results below 2^-126 may
+// flush to 0, far below every term these sums can resolve.
+__device__ __forceinline__ float emd_exp(float x) {
+  x = x < -150.f ? -150.f : x;
+  constexpr float L1 = 1.44269502162933349609375f;  // fl(log2 e)
+  constexpr float L2 = 1.925962989e-8f;             // log2 e - L1
+  const float h = x * L1;
+  const float l = __builtin_fmaf(x, L2, __builtin_fmaf(x, L1, -h));
+  const float r = __builtin_amdgcn_exp2f(h);
+  return __builtin_fmaf(r, l * 0.693147180559945309f, r);
+}
 __device__ __forceinline__ double emd_exp(double x) { return exp(x); }
 template <typename T, typename V>
 __device__ __forceinline__ V emd_e(V level, V d) {
+  // the last level: exp(0 * d) = 1 for finite d, NaN otherwise, = 0 * d + 1
+  if (level == (V)0) return level * d + (V)1;
   V a = level * d;
   if constexpr (std::is_same<T, half_t>::value)
     a = a < (V)-20 ? (V)-20 : (a > (V)20 ? (V)20 : a);
