@@ -249,7 +249,7 @@ int tpo_gather_bwd(int dtype, const void* grad_out, const int64_t* idx,
  * torch_point_ops_emd::emd_backward (emd.cpp:33).
  *   grad_cost (B), match (B,m,n) -> grad_xyz1 (B,n,3), grad_xyz2 (B,m,3).
  * Both take a workspace of tpo_emd_workspace_size(dtype, B, n, m) bytes,
- * 256-byte aligned (0 bytes when B, n or m is 0).  B < 65536; n, m < 2^30.
+ * 256-byte aligned (0 bytes when B, n or m is 0).  B < 2^31; n, m < 2^30.
  */
 int64_t tpo_emd_workspace_size(int dtype, int64_t B, int64_t n, int64_t m);
 int tpo_emd_fwd(int dtype, const void* xyz1, const void* xyz2, int64_t B,

@@ -131,5 +131,5 @@ def test_emd_sizes_and_errors(lib):
     assert b"workspace" in lib.tpo_last_error()
     lib.tpo_emd_bwd.argtypes = [ctypes.c_int, P, P, P, P, I, I, I, P, P, P, I, P]
     assert lib.tpo_emd_bwd(0, None, None, None, None, 1, 4, 4, None, None, None, 0, None) == -4
-    assert lib.tpo_emd_bwd(0, None, None, None, None, 70000, 4, 4, None, None, None, 0,
+    assert lib.tpo_emd_bwd(0, None, None, None, None, 1 << 31, 4, 4, None, None, None, 0,
                            None) == -1

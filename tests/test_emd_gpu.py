@@ -216,3 +216,31 @@ def test_errors(dev):
         torch.ops.torch_point_ops_emd.emd_forward(torch.randn(2, 8, 3, device=dev), p)
     with pytest.raises(RuntimeError, match="not implemented for"):
         torch.ops.torch_point_ops_emd.emd_forward(p.bfloat16(), p.bfloat16())
+
+
+def test_nan_propagates_and_stays_in_its_cloud(O, dev):
+    """A NaN coordinate makes its cloud's cost NaN, as in the reference (its
+    exponentials turn NaN), while the other clouds are unaffected: the
+    kernels' exact skipping of zero exponentials never skips a NaN."""
+    p1, p2 = clouds(2, 40, 30, torch.float32, seed=21)
+    p1[0, 7, 1] = float("nan")
+    cost, match = torch.ops.torch_point_ops_emd.emd_forward(p1.to(dev), p2.to(dev))
+    ec, em = O.emd_fwd(np_(p1), np_(p2))
+    assert np.isnan(ec[0]) and torch.isnan(cost[0])
+    close(np_(match[1]), em[1], *TOL[torch.float32])
+    close(np_(cost[1:]), ec[1:], TOL[torch.float32][0], 0.0, scale=1.0)
+
+
+def test_more_clouds_than_one_launch_holds(O, dev):
+    """B = 65537 > 65535 clouds per launch: the entry points run the clouds
+    in chunks and reuse the workspace."""
+    p1, p2 = clouds(65537, 3, 2, torch.float32, seed=22)
+    cost, match = torch.ops.torch_point_ops_emd.emd_forward(p1.to(dev), p2.to(dev))
+    ec, em = O.emd_fwd(np_(p1), np_(p2))
+    close(np_(match), em, *TOL[torch.float32])
+    close(np_(cost), ec, TOL[torch.float32][0], 1e-6, scale=np.abs(ec).max())
+    gc = torch.rand(65537, generator=torch.Generator().manual_seed(3))
+    g1, g2 = torch.ops.torch_point_ops_emd.emd_backward(gc.to(dev), p1.to(dev), p2.to(dev), match)
+    e1, e2 = O.emd_bwd(np_(gc), np_(p1), np_(p2), np_(match))
+    close(np_(g1), e1, 1e-4, 1e-4, scale=np.abs(e1).max())
+    close(np_(g2), e2, 1e-4, 1e-4, scale=np.abs(e2).max())
