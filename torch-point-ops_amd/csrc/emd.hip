@@ -28,7 +28,7 @@
 //     are listed in Morton order so a wave's 64 points are neighbours;
 //   * the float paths' exp is a two-term Cody-Waite reduction on the
 //     hardware exp2 (at most 1.24 ulp from exp over [-87, 0], measured);
-//     the last level's exp(0 * d) is 0 * d + 1 exactly;
+//     their last level's exp(0 * d) is 0 * d + 1 exactly;
 //   * pass 3 of level j and pass 1 of level j-1 need the same inputs, so they
 //     share one sweep (two exponentials per pair): 21 dependent sweeps;
 //   * match is not accumulated in HBM level by level: the per-level ratioL
@@ -92,7 +92,9 @@ __device__ __forceinline__ double emd_exp(double x) { return exp(x); }
 template <typename T, typename V>
 __device__ __forceinline__ V emd_e(V level, V d) {
   // the last level: exp(0 * d) = 1 for finite d, NaN otherwise, = 0 * d + 1
-  if (level == (V)0) return level * d + (V)1;
+  // (float paths; the double kernels keep their registers for exp)
+  if constexpr (!std::is_same<V, double>::value)
+    if (level == (V)0) return level * d + (V)1;
   V a = level * d;
   if constexpr (std::is_same<T, half_t>::value)
     a = a < (V)-20 ? (V)-20 : (a > (V)20 ? (V)20 : a);
