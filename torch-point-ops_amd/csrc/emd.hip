@@ -419,7 +419,7 @@ __global__ __launch_bounds__(EMD_SWEEP_THREADS) void emd_rows_kernel(
     z = p1[(b * n + k) * 4 + 2];
   }
   const V* other = p2 + b * m * 4;
-  const V* w3 = rr + (b * EMD_LEVELS + (s - 1)) * m;  // ratioR of level s-1
+  const V* w3 = rr + (b * EMD_LEVELS + (s >= 1 ? s - 1 : 0)) * m;  // ratioR of level s-1
   const V* w1 = remr + b * m;
   V sums[2];
   if constexpr (MODE == 1) emd_sweep<T, 1>(other, m, x, y, z, emd_level<V>(s), w1, (V)0, w1, sums);
