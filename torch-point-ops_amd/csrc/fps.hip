@@ -29,7 +29,9 @@
 //      re-reduces their best candidates, reduces over its 64 buckets, and
 //      one barrier later every wave reduces the 16 wave results.
 //   Work per sample drops from N points to the few buckets near the new
-//   sample, while the result is bit-identical to the full sweep.
+//   sample, while the result is bit-identical to the full sweep.  The first
+//   sample (index 0) touches every point; its update is made in the set-up
+//   pass that initialises the running minima, with the same arithmetic.
 #include "tpo_common.hpp"
 
 #pragma clang fp contract(off)
@@ -346,9 +348,15 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
   }
   for (int64_t k = N + tid; k < L.np; k += FPS_THREADS) recs[k] = FpsRec<T>{(T)0, (T)0, (T)0, 0u};
   __syncthreads();
-  // running minima in sorted order (coalesced): init, or 0 for a point that
-  // does not take part
-  for (int64_t k = tid; k < L.np; k += FPS_THREADS) ts[k] = recs[k].key ? init : (T)0;
+  // running minima in sorted order (coalesced), already updated by the first
+  // sample (index 0) exactly as a visit would: min(d, init), or 0 for a point
+  // that does not take part
+  const T p0x = P[0], p0y = P[1], p0z = P[2];
+  for (int64_t k = tid; k < L.np; k += FPS_THREADS) {
+    const FpsRec<T> rc = recs[k];
+    const T d = sq3((T)(rc.x - p0x), (T)(rc.y - p0y), (T)(rc.z - p0z));  // fps.cu:145
+    ts[k] = rc.key ? (d < init ? d : init) : (T)0;                        // fps.cu:146
+  }
 
   // ---- 3. bucket summaries ----
   // Lane l of wave w owns bucket sb = l * 16 + w: buckets adjacent in Morton
@@ -383,7 +391,8 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
       bhi[0] = x > bhi[0] ? (V)x : bhi[0];
       bhi[1] = y > bhi[1] ? (V)y : bhi[1];
       bhi[2] = z > bhi[2] ? (V)z : bhi[2];
-      const C cand = cand_make((V)init, mt, ctag);
+      const T d0 = sq3((T)(x - p0x), (T)(y - p0y), (T)(z - p0z));
+      const C cand = cand_make((V)(d0 < init ? d0 : init), mt, ctag);
       if (cand_gt(cand, bbest)) {
         bbest = cand;
         bx = x;
@@ -398,7 +407,6 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
   C wbest = wave_best_at(bbest, wlane);
 
   // ---- 4. the sampling loop ----
-  const T p0x = P[0], p0y = P[1], p0z = P[2];
   T ox = p0x, oy = p0y, oz = p0z;
   if (tid == 0) out[0] = 0;
   int rk = 0;  // wave 0: lane j mod 64 holds the rank of sample j
@@ -418,7 +426,8 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
 #pragma unroll
     for (int c = 0; c < 3; ++c) e[c] = vmax(vmax(blo[c] - o3[c], o3[c] - bhi[c]), (V)0);
     const V lb2 = vfma(e[2], e[2], vfma(e[1], e[1], e[0] * e[0]));
-    uint64_t tm = __ballot(lb2 <= reach);
+    // the first sample's updates were made while the cloud was set up
+    uint64_t tm = j > 1 ? __ballot(lb2 <= reach) : 0;
     bool rereduce = false;  // the best of the wave's best bucket changed
     // Touched buckets are visited NB at a time: every slot's loads are issued
     // unconditionally (an empty slot re-reads slot 0's bucket), the NB wave
