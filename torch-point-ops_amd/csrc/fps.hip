@@ -495,9 +495,13 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
       __builtin_amdgcn_s_setprio(3);
       while (tm) {
         const int nt = __builtin_popcountll(tm);
+        // rounds of exactly the touched count (an empty slot costs a whole
+        // load and distance pass), 5 at a time beyond that
         if (nt == 1) visit(std::integral_constant<int, 1>{});
         else if (nt == 2) visit(std::integral_constant<int, 2>{});
-        else visit(std::integral_constant<int, 4>{});
+        else if (nt == 3) visit(std::integral_constant<int, 3>{});
+        else if (nt == 4) visit(std::integral_constant<int, 4>{});
+        else visit(std::integral_constant<int, 5>{});
       }
       reach = reach_of(bbest);
       __builtin_amdgcn_s_setprio(0);
