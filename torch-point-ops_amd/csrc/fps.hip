@@ -430,9 +430,10 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     uint64_t tm = j > 1 ? __ballot(lb2 <= reach) : 0;
     bool rereduce = false;  // the best of the wave's best bucket changed
     // Touched buckets are visited NB at a time: every slot's loads are issued
-    // unconditionally (an empty slot re-reads slot 0's bucket), the NB wave
-    // reductions are independent straight-line code, and the running-minimum
-    // stores come last, so no load or reduction of the batch waits for a store.
+    // first (the rounds below never leave a slot empty; an empty slot would
+    // re-read slot 0's bucket), the NB wave reductions are independent
+    // straight-line code, and the running-minimum stores come last, so no load
+    // or reduction of the batch waits for a store.
     auto visit = [&](auto nbc) {
       constexpr int NB = decltype(nbc)::value;
       int bits[NB];
@@ -495,8 +496,8 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
       __builtin_amdgcn_s_setprio(3);
       while (tm) {
         const int nt = __builtin_popcountll(tm);
-        // rounds of exactly the touched count (an empty slot costs a whole
-        // load and distance pass), 5 at a time beyond that
+        // rounds of exactly the touched count (an empty slot would cost a
+        // whole load and distance pass), 5 at a time beyond that
         if (nt == 1) visit(std::integral_constant<int, 1>{});
         else if (nt == 2) visit(std::integral_constant<int, 2>{});
         else if (nt == 3) visit(std::integral_constant<int, 3>{});
