@@ -60,6 +60,8 @@ def test_config4_prefix_exact_and_full_properties(tpo, O, dev, origin_blob):
     sub = [0, 9, 15]
     ref = O.fps(np_(pts[sub]), 192)
     assert np.array_equal(np_(idx[sub, :192]), ref)
+    # one cloud's whole run (4096 samples) against the oracle (~3 s on the CPU)
+    assert np.array_equal(np_(idx[7]), O.fps(np_(pts[[7]]), 4096)[0])
     # full run: start at 0, all distinct, no skipped point selected, and the
     # selected point's distance to the previous samples never increases
     n = idx.cpu()
