@@ -102,6 +102,60 @@ def test_config3_subset_exact_and_full_properties(tpo, O, dev):
         assert torch.allclose(at, sd[n, :a].double(), rtol=1e-6, atol=1e-9)
 
 
+def _long_cloud_inputs(case, g):
+    # long reference clouds (the staged float D=3 sweep over 5000 references,
+    # lengths2 ragged, a cloud with a single query row)
+    N, P1, P2 = 4, 300, 5000
+    if case == "lattice":  # many exactly equal distances
+        p1 = torch.randint(0, 6, (N, P1, 3), generator=g).float()
+        p2 = torch.randint(0, 6, (N, P2, 3), generator=g).float()
+    else:
+        p1 = torch.randn(N, P1, 3, generator=g)
+        p2 = torch.randn(N, P2, 3, generator=g)
+    if case == "nonfinite":
+        p2[0, 3, 1] = float("nan")     # in the fill
+        p2[1, 700, 0] = float("inf")
+        p2[1, 2600:2610, 2] = float("nan")
+        p2[2, 4000, 0] = -float("inf")
+        p1[2, 5, 1] = float("nan")
+        p1[3, 7, 0] = float("inf")
+    if case == "descending":  # every reference closer than all before it: all are inserted
+        r = p2.norm(dim=-1)
+        p2 = torch.gather(p2, 1, r.argsort(dim=1, descending=True)[..., None].expand(-1, -1, 3))
+        p1 = p1 * 1e-3
+    l1 = torch.tensor([P1, 250, 299, 1])
+    l2 = torch.tensor([P2, 1000, 2560, 4321])
+    return p1, p2, l1, l2
+
+
+@pytest.mark.parametrize("case", ["random", "lattice", "nonfinite", "descending"])
+@pytest.mark.parametrize("K,norm,version", [(1, 2, -1), (5, 1, -1), (16, 2, -1), (16, 2, 0),
+                                            (17, 1, 2), (32, 2, -1), (2, 2, 2)])
+def test_long_clouds_forward_bit_exact(tpo, O, dev, case, K, norm, version):
+    g = torch.Generator().manual_seed(K * 31 + norm + len(case))
+    p1, p2, l1, l2 = _long_cloud_inputs(case, g)
+    idx, d = raw(p1, p2, l1, l2, norm, K, version, dev)
+    ei, ed = O.knn_fwd(np_(p1), np_(p2), np_(l1), np_(l2), norm=norm, K=K, version=version)
+    assert_same(np_(idx), ei)
+    assert_same(np_(d), ed)
+
+
+@pytest.mark.parametrize("case", ["random", "lattice", "nonfinite"])
+@pytest.mark.parametrize("K", [2, 8, 16, 32])
+def test_long_clouds_sorted_rows_match_torch_sort(tpo, dev, case, K):
+    g = torch.Generator().manual_seed(K + 7 * len(case))
+    p1, p2, l1, l2 = _long_cloud_inputs(case, g)
+    a, b, la, lb = p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev)
+    for version in (-1, 0, 2):
+        for norm in (1, 2):
+            si, sd = tpo.knn_points(a, b, la, lb, norm=norm, K=K, version=version)
+            ri, rd = torch.ops.torch_point_ops_knn.knn_forward(a, b, la, lb, norm, K, version)
+            ei, ed = _module_sort(ri, rd, lb, K)
+            assert torch.equal(si, ei), (version, norm)
+            assert torch.equal(sd.isnan(), ed.isnan())
+            assert torch.equal(torch.nan_to_num(sd), torch.nan_to_num(ed)), (version, norm)
+
+
 def _module_sort(idxs, dists, lengths2, K):
     # knn_points' sort after the forward (reference knn/__init__.py:111-131)
     if lengths2.min() < K:

@@ -335,6 +335,9 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
     }
   }
   if (!STAGED && !act) return;
+  // rows past lengths1 sit at the end of the processing order: a wave with
+  // no query left has nothing to stage for
+  if (STAGED && __ballot(act) == 0) return;
   const int Dd = DT > 0 ? DT : D;
   const T* __restrict__ qp = p1 + row * Dd;
   const T* __restrict__ rp = p2 + (size_t)n * P2 * Dd;
