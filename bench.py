@@ -300,7 +300,7 @@ def cpu_knn(O, np, threads):
     a = p1[:, :q].numpy()
     ln1 = np.minimum(l1.numpy(), q)
     t0 = time.perf_counter()
-    O.cpu_knn_fwd_f32(a, p2.numpy(), ln1, l2.numpy(), 16, 2, nthreads=threads)
+    O.cpu_knn_fwd(a, p2.numpy(), ln1, l2.numpy(), 16, 2, nthreads=threads)
     sec = time.perf_counter() - t0
     pairs = float((ln1 * l2.numpy()).sum())
     return dict(value=pairs / sec / 1e9, unit="G pair-dists/s", cores=threads, kind="port",
@@ -317,7 +317,7 @@ def cpu_knn_c5(O, np, threads):
     ln1 = np.full(a.shape[0], nq, dtype=np.int64)
     ln2 = np.full(a.shape[0], b.shape[1], dtype=np.int64)
     t0 = time.perf_counter()
-    O.cpu_knn_fwd_f32(a, b, ln1, ln2, 32, 2, nthreads=threads)
+    O.cpu_knn_fwd(a, b, ln1, ln2, 32, 2, nthreads=threads)
     sec = time.perf_counter() - t0
     pairs = float(a.shape[0] * nq * b.shape[1])
     return dict(value=pairs / sec / 1e9, unit="G pair-dists/s", cores=threads, kind="port",
@@ -329,7 +329,7 @@ def cpu_fps(O, np, pts, threads):
     nc = min(threads, pts.shape[0])
     m = 512
     t0 = time.perf_counter()
-    O.cpu_fps_f32(pts[:nc].numpy(), m, nthreads=nc)
+    O.cpu_fps(pts[:nc].numpy(), m, nthreads=nc)
     sec = time.perf_counter() - t0
     upd = nc * pts.shape[1] * (m - 1)
     return dict(value=upd / sec / 1e9, unit="G point-updates/s", cores=nc, kind="port",

@@ -55,11 +55,13 @@ def lib():
             "tpo_ref_emd_bwd": [ctypes.c_int, P, P, P, P, I64, I64, I64, P, P],
             "tpo_ref_f32_to_f16_array": [P, P, I64],
             "tpo_ref_f16_to_f32_array": [P, P, I64],
-            "tpo_cpu_knn_fwd_f32": [P, P, P, P, I64, I64, I64, I64, I64, ctypes.c_int, P, P,
-                                    ctypes.c_int],
-            "tpo_cpu_fps_f32": [P, I64, I64, I64, P, ctypes.c_int],
-            "tpo_cpu_gather_fwd_f32": [P, P, I64, I64, I64, I64, P],
-            "tpo_cpu_gather_bwd_f32": [P, P, I64, I64, I64, I64, P],
+            "tpo_cpu_knn_fwd": [ctypes.c_int, P, P, P, P, I64, I64, I64, I64, I64, ctypes.c_int,
+                                P, P, ctypes.c_int],
+            "tpo_cpu_knn_bwd": [ctypes.c_int, P, P, P, P, P, ctypes.c_int, P, I64, I64, I64, I64,
+                                I64, P, P, ctypes.c_int],
+            "tpo_cpu_fps": [ctypes.c_int, P, I64, I64, I64, P, ctypes.c_int],
+            "tpo_cpu_gather_fwd": [ctypes.c_int, P, P, I64, I64, I64, I64, P],
+            "tpo_cpu_gather_bwd": [ctypes.c_int, P, P, I64, I64, I64, I64, P],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -71,6 +73,7 @@ def lib():
 
 
 def _c(a, dtype=None):
+    a = np.asarray(a)
     a = np.ascontiguousarray(a if dtype is None else a.astype(dtype, copy=False))
     return a
 
@@ -210,46 +213,68 @@ def gather_bwd(grad_out, idx, n, accum_f64=False):
     return out
 
 
-# --- reference CPU kernels (timed baseline) ---------------------------------
+# --- reference CPU kernels (knn.cpp / fps.cpp semantics) --------------------
 
-def cpu_knn_fwd_f32(p1, p2, len1, len2, K, norm=2, nthreads=1):
-    """knn.cpp:30-99 restated (sorted output, padding idx -1)."""
-    p1, p2 = _c(p1, np.float32), _c(p2, np.float32)
+def cpu_knn_fwd(p1, p2, len1, len2, K, norm=2, nthreads=1):
+    """knn.cpp:30-99 restated -> (idxs int64 sorted ascending, padding -1; dists)."""
+    p1, p2 = _c(p1), _c(p2)
+    assert p1.dtype == p2.dtype
     N, P1, D = p1.shape
     P2 = p2.shape[1]
     len1, len2 = _c(len1, np.int64), _c(len2, np.int64)
     idxs = np.empty((N, P1, K), np.int64)
-    dists = np.empty((N, P1, K), np.float32)
-    _check(lib().tpo_cpu_knn_fwd_f32(_p(p1), _p(p2), _p(len1), _p(len2), N, P1, P2, D, K, norm,
-                                     _p(idxs), _p(dists), nthreads), "cpu_knn_fwd")
+    dists = np.empty((N, P1, K), p1.dtype)
+    _check(lib().tpo_cpu_knn_fwd(_dt(p1), _p(p1), _p(p2), _p(len1), _p(len2), N, P1, P2, D, K,
+                                 norm, _p(idxs), _p(dists), nthreads), "cpu_knn_fwd")
     return idxs, dists
 
 
-def cpu_fps_f32(points, nsamples, nthreads=1):
-    """fps.cpp:18-88 restated (CPU semantics)."""
-    points = _c(points, np.float32)
+def cpu_knn_bwd(p1, p2, len1, len2, idxs, norm, grad_dists, nthreads=1):
+    """knn.cpp:104-164 restated -> (grad_p1, grad_p2)."""
+    p1, p2 = _c(p1), _c(p2)
+    N, P1, D = p1.shape
+    P2 = p2.shape[1]
+    K = idxs.shape[2]
+    len1, len2 = _c(len1, np.int64), _c(len2, np.int64)
+    idxs = _c(idxs, np.int64)
+    grad_dists = _c(grad_dists, p1.dtype)
+    g1 = np.empty_like(p1)
+    g2 = np.empty_like(p2)
+    _check(lib().tpo_cpu_knn_bwd(_dt(p1), _p(p1), _p(p2), _p(len1), _p(len2), _p(idxs), norm,
+                                 _p(grad_dists), N, P1, P2, D, K, _p(g1), _p(g2), nthreads),
+           "cpu_knn_bwd")
+    return g1, g2
+
+
+def cpu_fps(points, nsamples, nthreads=1):
+    """fps.cpp:18-88 restated (CPU semantics) -> idx (B, nsamples) int64."""
+    points = _c(points)
     B, N, _ = points.shape
     idx = np.empty((B, nsamples), np.int64)
-    _check(lib().tpo_cpu_fps_f32(_p(points), B, N, nsamples, _p(idx), nthreads), "cpu_fps")
+    _check(lib().tpo_cpu_fps(_dt(points), _p(points), B, N, nsamples, _p(idx), nthreads),
+           "cpu_fps")
     return idx
 
 
-def cpu_gather_fwd_f32(points, idx):
-    points = _c(points, np.float32)
+def cpu_gather_fwd(points, idx):
+    """fps.cpp:91-115 restated -> (B, C, M)."""
+    points = _c(points)
     idx = _c(idx, np.int64)
     B, C, N = points.shape
     M = idx.shape[1]
-    out = np.empty((B, C, M), np.float32)
-    _check(lib().tpo_cpu_gather_fwd_f32(_p(points), _p(idx), B, C, N, M, _p(out)), "cpu_gather")
+    out = np.empty((B, C, M), points.dtype)
+    _check(lib().tpo_cpu_gather_fwd(_dt(points), _p(points), _p(idx), B, C, N, M, _p(out)),
+           "cpu_gather")
     return out
 
 
-def cpu_gather_bwd_f32(grad_out, idx, n):
-    grad_out = _c(grad_out, np.float32)
+def cpu_gather_bwd(grad_out, idx, n):
+    """fps.cpp:118-141 restated -> (B, C, n)."""
+    grad_out = _c(grad_out)
     idx = _c(idx, np.int64)
     B, C, M = grad_out.shape
-    out = np.empty((B, C, n), np.float32)
-    _check(lib().tpo_cpu_gather_bwd_f32(_p(grad_out), _p(idx), B, C, n, M, _p(out)),
+    out = np.empty((B, C, n), grad_out.dtype)
+    _check(lib().tpo_cpu_gather_bwd(_dt(grad_out), _p(grad_out), _p(idx), B, C, n, M, _p(out)),
            "cpu_gather_bwd")
     return out
 

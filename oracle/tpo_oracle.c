@@ -866,16 +866,27 @@ int tpo_ref_emd_bwd(int dtype, const void* grad_cost, const void* xyz1, const vo
 }
 
 /* ------------------------------------------------------------------ */
-/* Reference CPU kernels (timed CPU baseline)                          */
+/* Reference CPU kernels (knn.cpp, fps.cpp)                            */
 /* ------------------------------------------------------------------ */
 
-/* max-heap on (dist, idx) pairs: the order of std::priority_queue over
-   std::tuple<scalar_t,int> in knn.cpp:60 */
+/* These restate the reference's CPU dispatch-key kernels, whose arithmetic
+   differs from the CUDA kernels': the reference builds them with g++ -O3 for
+   plain x86-64 (setup.py:78-81), which has no FMA instruction, so every
+   distance sum rounds after each + and *; float16 uses c10::Half's operators
+   (one rounding per operation).  They are the checker of the product's CPU
+   kernels and the timed CPU baseline.  nthreads > 1 splits independent rows
+   or clouds over OpenMP threads; the result does not depend on it. */
+
+/* std::priority_queue<std::tuple<scalar_t,int>> (knn.cpp:60) is a max-heap
+   under std::tuple's operator<: a < b iff a.d < b.d, or neither distance is
+   less than the other and a.i < b.i. */
 typedef struct {
-  float d;
+  double d;
   int i;
 } knn_item;
-static inline int item_lt(knn_item a, knn_item b) { return a.d < b.d || (a.d == b.d && a.i < b.i); }
+static inline int item_lt(knn_item a, knn_item b) {
+  return a.d < b.d || (!(b.d < a.d) && a.i < b.i);
+}
 static void heap_push(knn_item* h, int* n, knn_item v) {
   int c = (*n)++;
   h[c] = v;
@@ -903,19 +914,23 @@ static void heap_pop(knn_item* h, int* n) {
   }
 }
 
-/* knn.cpp:30-99 for float: idxs preset to -1, dists to 0; per query a heap
-   of the K smallest (dist, idx); results stored ascending (:88-93).
-   dist += diff*diff without contraction (no FMA in the reference's
-   x86-64 -O3 build). */
-int tpo_cpu_knn_fwd_f32(const float* p1, const float* p2, const int64_t* len1,
-                        const int64_t* len2, int64_t N, int64_t P1, int64_t P2, int64_t D,
-                        int64_t K, int norm, int64_t* idxs, float* dists, int nthreads) {
-  if (K < 1 || D < 1) return -1;
+static int64_t clamp_len(int64_t v, int64_t hi) { return v < 0 ? 0 : (v > hi ? hi : v); }
+
+/* knn.cpp:30-99: idxs preset to -1 and dists to 0; for each query q <
+   lengths1 a heap of the K smallest (dist, idx) over p2[0:lengths2]: a
+   reference enters while the heap holds fewer than K, or when its distance
+   is strictly below the top's (then the top is popped); the heap is emptied
+   into the row in ascending order (:82-93).  dist = 0; dist += diff*diff
+   (or |diff|) per coordinate, rounded after each operation.  Lengths are
+   clamped to the cloud sizes (the reference reads past the cloud). */
+static int cpu_knn_fwd_dt(int dt, const void* p1, const void* p2, const int64_t* len1,
+                          const int64_t* len2, int64_t N, int64_t P1, int64_t P2, int64_t D,
+                          int64_t K, int norm, int64_t* idxs, void* dists, int nthreads) {
   for (int64_t i = 0; i < N * P1 * K; ++i) {
     idxs[i] = -1;
-    dists[i] = 0.0f;
+    st(dt, dists, i, 0.0);
   }
-  int64_t total = N * P1;
+  const int64_t total = N * P1;
   int err = 0;
 #ifdef _OPENMP
 #pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1)
@@ -931,17 +946,15 @@ int tpo_cpu_knn_fwd_f32(const float* p1, const float* p2, const int64_t* len1,
     for (int64_t t = 0; t < total; ++t) {
       if (!h) continue;
       const int64_t n = t / P1, q = t % P1;
-      if (q >= len1[n]) continue;
-      const int64_t l2 = len2[n] < P2 ? len2[n] : P2;
+      if (q >= clamp_len(len1[n], P1)) continue;
+      const int64_t l2 = clamp_len(len2[n], P2);
       int hn = 0;
-      const float* qp = p1 + (n * P1 + q) * D;
       for (int64_t r = 0; r < l2; ++r) {
-        const float* rp = p2 + (n * P2 + r) * D;
-        float dist = 0.0f;
+        double dist = 0.0;
         for (int64_t d = 0; d < D; ++d) {
-          float diff = qp[d] - rp[d];
-          if (norm == 1) dist += fabsf(diff);
-          else dist += diff * diff;
+          const double diff =
+              op_sub(dt, ld(dt, p1, (n * P1 + q) * D + d), ld(dt, p2, (n * P2 + r) * D + d));
+          dist = op_add(dt, dist, norm == 1 ? fabs(diff) : op_mul(dt, diff, diff));
         }
         if (hn < K || dist < h[0].d) {
           knn_item it = {dist, (int)r};
@@ -950,8 +963,8 @@ int tpo_cpu_knn_fwd_f32(const float* p1, const float* p2, const int64_t* len1,
         }
       }
       const int64_t o = (n * P1 + q) * K;
-      for (int64_t k = hn - 1; k >= 0; --k) { /* ascending order */
-        dists[o + k] = h[0].d;
+      for (int64_t k = hn - 1; k >= 0; --k) { /* the top is the largest: fill from the back */
+        st(dt, dists, o + k, h[0].d);
         idxs[o + k] = h[0].i;
         heap_pop(h, &hn);
       }
@@ -961,12 +974,90 @@ int tpo_cpu_knn_fwd_f32(const float* p1, const float* p2, const int64_t* len1,
   return err ? -3 : 0;
 }
 
-/* fps.cpp:18-88 for float: FLT_MAX init, already-selected points excluded,
-   points with mag <= 1e-3 skipped for the distance update but still
-   candidates (their min distance stays FLT_MAX), ties to the lowest index. */
-int tpo_cpu_fps_f32(const float* pts, int64_t B, int64_t N, int64_t m, int64_t* idx,
+int tpo_cpu_knn_fwd(int dtype, const void* p1, const void* p2, const int64_t* len1,
+                    const int64_t* len2, int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,
+                    int norm, int64_t* idxs, void* dists, int nthreads) {
+  if (N < 0 || P1 < 0 || P2 < 0 || K < 1 || D < 1 || (norm != 1 && norm != 2)) return -1;
+  switch (dtype) {
+    case TPO_REF_F32: return cpu_knn_fwd_dt(TPO_REF_F32, p1, p2, len1, len2, N, P1, P2, D, K, norm, idxs, dists, nthreads);
+    case TPO_REF_F64: return cpu_knn_fwd_dt(TPO_REF_F64, p1, p2, len1, len2, N, P1, P2, D, K, norm, idxs, dists, nthreads);
+    case TPO_REF_F16: return cpu_knn_fwd_dt(TPO_REF_F16, p1, p2, len1, len2, N, P1, P2, D, K, norm, idxs, dists, nthreads);
+    default: return -2;
+  }
+}
+
+/* knn.cpp:104-164: gradients start at zero; for each cloud, rows q <
+   lengths1, slots k < min(lengths2, K) whose index is not -1, coordinates
+   d in order:
+     norm 1: sign = p1 > p2 ? 1 : -1 (-1 on equality, :150), diff = g*sign;
+     norm 2: diff = 2.0*g*(p1 - p2), the product taken in double (2.0 is a
+             double literal) and rounded once to the dtype when stored;
+   grad_p1[q] += diff, grad_p2[idx] -= diff, in this loop order (sequential:
+   the sums are order-dependent).  Indices outside [0, P2) other than -1
+   are skipped (the reference would access out of bounds).  Threads split
+   the clouds. */
+static int cpu_knn_bwd_dt(int dt, const void* p1, const void* p2, const int64_t* len1,
+                          const int64_t* len2, const int64_t* idxs, int norm, const void* gdist,
+                          int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K, void* gp1,
+                          void* gp2, int nthreads) {
+  for (int64_t i = 0; i < N * P1 * D; ++i) st(dt, gp1, i, 0.0);
+  for (int64_t i = 0; i < N * P2 * D; ++i) st(dt, gp2, i, 0.0);
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(dynamic, 1)
+#else
+  (void)nthreads;
+#endif
+  for (int64_t n = 0; n < N; ++n) {
+    const int64_t l1 = clamp_len(len1[n], P1);
+    int64_t l2 = len2[n] < K ? len2[n] : K;
+    for (int64_t q = 0; q < l1; ++q)
+      for (int64_t k = 0; k < l2; ++k) {
+        const int64_t r = idxs[(n * P1 + q) * K + k];
+        if (r == -1 || r < 0 || r >= P2) continue;
+        const double g = ld(dt, gdist, (n * P1 + q) * K + k);
+        for (int64_t d = 0; d < D; ++d) {
+          const int64_t i1 = (n * P1 + q) * D + d, i2 = (n * P2 + r) * D + d;
+          const double v1 = ld(dt, p1, i1), v2 = ld(dt, p2, i2);
+          double diff;
+          if (norm == 1) diff = op_mul(dt, g, v1 > v2 ? 1.0 : -1.0);
+          else diff = rnd(dt, (2.0 * g) * op_sub(dt, v1, v2));
+          st(dt, gp1, i1, op_add(dt, ld(dt, gp1, i1), diff));
+          st(dt, gp2, i2, op_sub(dt, ld(dt, gp2, i2), diff));
+        }
+      }
+  }
+  return 0;
+}
+
+int tpo_cpu_knn_bwd(int dtype, const void* p1, const void* p2, const int64_t* len1,
+                    const int64_t* len2, const int64_t* idxs, int norm, const void* grad_dists,
+                    int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K, void* gp1, void* gp2,
                     int nthreads) {
-  if (N < 1 || m < 1 || m > N) return -1;
+  if (N < 0 || P1 < 0 || P2 < 0 || K < 0 || D < 1 || (norm != 1 && norm != 2)) return -1;
+  switch (dtype) {
+    case TPO_REF_F32: return cpu_knn_bwd_dt(TPO_REF_F32, p1, p2, len1, len2, idxs, norm, grad_dists, N, P1, P2, D, K, gp1, gp2, nthreads);
+    case TPO_REF_F64: return cpu_knn_bwd_dt(TPO_REF_F64, p1, p2, len1, len2, idxs, norm, grad_dists, N, P1, P2, D, K, gp1, gp2, nthreads);
+    case TPO_REF_F16: return cpu_knn_bwd_dt(TPO_REF_F16, p1, p2, len1, len2, idxs, norm, grad_dists, N, P1, P2, D, K, gp1, gp2, nthreads);
+    default: return -2;
+  }
+}
+
+/* x*x + y*y + z*z of fps.cpp:57,64 without contraction: ((x*x + y*y) + z*z). */
+INLINE double cpu_sq3(int dt, double x, double y, double z) {
+  return op_add(dt, op_add(dt, op_mul(dt, x, x), op_mul(dt, y, y)), op_mul(dt, z, z));
+}
+
+/* fps.cpp:18-88 (the CPU semantics, unlike fps.cu's): min distances start at
+   numeric_limits<scalar_t>::max(); index 0 first; each iteration updates the
+   unselected points whose |p|^2 is not <= scalar_t(1e-3) with
+   min(min_dist, dist) (std::min keeps the old value unless the new one is
+   strictly smaller), then picks the first unselected point with the
+   strictly greatest min distance (start -1, index 0 when none). */
+static int cpu_fps_dt(int dt, const void* pts, int64_t B, int64_t N, int64_t m, int64_t* idx,
+                      int nthreads) {
+  const double big = dt == TPO_REF_F64 ? 1.7976931348623157e308
+                                       : (dt == TPO_REF_F16 ? 65504.0 : 3.4028234663852886e38);
+  const double thr = dt == TPO_REF_F64 ? 1e-3 : (dt == TPO_REF_F16 ? rh(1e-3f) : (double)1e-3f);
   int err = 0;
 #ifdef _OPENMP
 #pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(dynamic, 1)
@@ -974,7 +1065,7 @@ int tpo_cpu_fps_f32(const float* pts, int64_t B, int64_t N, int64_t m, int64_t* 
   (void)nthreads;
 #endif
   for (int64_t b = 0; b < B; ++b) {
-    float* md = (float*)malloc((size_t)N * sizeof(float));
+    double* md = (double*)malloc((size_t)N * sizeof(double));
     unsigned char* sel = (unsigned char*)calloc((size_t)N, 1);
     if (!md || !sel) {
       err = 1;
@@ -982,23 +1073,23 @@ int tpo_cpu_fps_f32(const float* pts, int64_t B, int64_t N, int64_t m, int64_t* 
       free(sel);
       continue;
     }
-    const float* p = pts + b * N * 3;
-    for (int64_t k = 0; k < N; ++k) md[k] = 3.402823466e+38f;
+    const int64_t base = b * N * 3;
+    for (int64_t k = 0; k < N; ++k) md[k] = big;
     int64_t cur = 0;
     idx[b * m] = 0;
     sel[0] = 1;
     for (int64_t i = 1; i < m; ++i) {
-      const float cx = p[3 * cur], cy = p[3 * cur + 1], cz = p[3 * cur + 2];
+      const double cx = ld(dt, pts, base + 3 * cur), cy = ld(dt, pts, base + 3 * cur + 1),
+                   cz = ld(dt, pts, base + 3 * cur + 2);
       for (int64_t j = 0; j < N; ++j) {
         if (sel[j]) continue;
-        const float x = p[3 * j], y = p[3 * j + 1], z = p[3 * j + 2];
-        const float mag = x * x + y * y + z * z;
-        if (mag <= 1e-3f) continue;
-        const float dx = x - cx, dy = y - cy, dz = z - cz;
-        const float dist = dx * dx + dy * dy + dz * dz;
-        md[j] = md[j] < dist ? md[j] : dist;
+        const double x = ld(dt, pts, base + 3 * j), y = ld(dt, pts, base + 3 * j + 1),
+                     z = ld(dt, pts, base + 3 * j + 2);
+        if (cpu_sq3(dt, x, y, z) <= thr) continue;
+        const double dist = cpu_sq3(dt, op_sub(dt, x, cx), op_sub(dt, y, cy), op_sub(dt, z, cz));
+        md[j] = dist < md[j] ? dist : md[j];
       }
-      float best = -1.0f;
+      double best = -1.0;
       int64_t bi = 0;
       for (int64_t j = 0; j < N; ++j)
         if (!sel[j] && md[j] > best) {
@@ -1015,22 +1106,45 @@ int tpo_cpu_fps_f32(const float* pts, int64_t B, int64_t N, int64_t m, int64_t* 
   return err ? -3 : 0;
 }
 
-/* fps.cpp:91-115 */
-int tpo_cpu_gather_fwd_f32(const float* pts, const int64_t* idx, int64_t B, int64_t C,
-                           int64_t N, int64_t M, float* out) {
+int tpo_cpu_fps(int dtype, const void* pts, int64_t B, int64_t N, int64_t m, int64_t* idx,
+                int nthreads) {
+  if (B < 0 || N < 1 || m < 1 || m > N) return -1;
+  switch (dtype) {
+    case TPO_REF_F32: return cpu_fps_dt(TPO_REF_F32, pts, B, N, m, idx, nthreads);
+    case TPO_REF_F64: return cpu_fps_dt(TPO_REF_F64, pts, B, N, m, idx, nthreads);
+    case TPO_REF_F16: return cpu_fps_dt(TPO_REF_F16, pts, B, N, m, idx, nthreads);
+    default: return -2;
+  }
+}
+
+/* fps.cpp:91-115: out[b,c,j] = pts[b,c,idx[b,j]]; an index outside [0, N)
+   gives 0 here (the reference reads out of bounds). */
+int tpo_cpu_gather_fwd(int dtype, const void* pts, const int64_t* idx, int64_t B, int64_t C,
+                       int64_t N, int64_t M, void* out) {
+  if (dtype < TPO_REF_F32 || dtype > TPO_REF_F16) return -2;
   for (int64_t b = 0; b < B; ++b)
     for (int64_t c = 0; c < C; ++c)
-      for (int64_t j = 0; j < M; ++j) out[(b * C + c) * M + j] = pts[(b * C + c) * N + idx[b * M + j]];
+      for (int64_t j = 0; j < M; ++j) {
+        const int64_t a = idx[b * M + j];
+        st(dtype, out, (b * C + c) * M + j, (a < 0 || a >= N) ? 0.0 : ld(dtype, pts, (b * C + c) * N + a));
+      }
   return 0;
 }
 
-/* fps.cpp:118-141 */
-int tpo_cpu_gather_bwd_f32(const float* grad_out, const int64_t* idx, int64_t B, int64_t C,
-                           int64_t N, int64_t M, float* grad_pts) {
-  memset(grad_pts, 0, (size_t)(B * C * N) * sizeof(float));
+/* fps.cpp:118-141: zeros, then grad_pts[b,c,idx[b,j]] += grad_out[b,c,j] in
+   (b, c, j) order, rounded to the dtype at every addition; indices outside
+   [0, N) are skipped. */
+int tpo_cpu_gather_bwd(int dtype, const void* grad_out, const int64_t* idx, int64_t B, int64_t C,
+                       int64_t N, int64_t M, void* grad_pts) {
+  if (dtype < TPO_REF_F32 || dtype > TPO_REF_F16) return -2;
+  for (int64_t i = 0; i < B * C * N; ++i) st(dtype, grad_pts, i, 0.0);
   for (int64_t b = 0; b < B; ++b)
     for (int64_t c = 0; c < C; ++c)
-      for (int64_t j = 0; j < M; ++j)
-        grad_pts[(b * C + c) * N + idx[b * M + j]] += grad_out[(b * C + c) * M + j];
+      for (int64_t j = 0; j < M; ++j) {
+        const int64_t a = idx[b * M + j];
+        if (a < 0 || a >= N) continue;
+        const int64_t o = (b * C + c) * N + a;
+        st(dtype, grad_pts, o, op_add(dtype, ld(dtype, grad_pts, o), ld(dtype, grad_out, (b * C + c) * M + j)));
+      }
   return 0;
 }

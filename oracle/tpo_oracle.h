@@ -98,20 +98,28 @@ int tpo_ref_emd_bwd(int dtype, const void* grad_cost, const void* xyz1,
                     const void* xyz2, const void* match, int64_t B, int64_t n,
                     int64_t m, void* grad1, void* grad2);
 
-/* Reference CPU kernels (timed baseline only): knn.cpp:30-164, fps.cpp:18-141.
-   float32 only.  nthreads > 1 splits the outer (cloud x query / cloud) loop
-   over OpenMP threads; 1 reproduces the reference's single-threaded loops. */
-int tpo_cpu_knn_fwd_f32(const float* p1, const float* p2,
-                        const int64_t* len1, const int64_t* len2,
-                        int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,
-                        int norm, int64_t* idxs, float* dists, int nthreads);
-int tpo_cpu_fps_f32(const float* pts, int64_t B, int64_t N, int64_t m,
-                    int64_t* idx, int nthreads);
-int tpo_cpu_gather_fwd_f32(const float* pts, const int64_t* idx, int64_t B,
-                           int64_t C, int64_t N, int64_t M, float* out);
-int tpo_cpu_gather_bwd_f32(const float* grad_out, const int64_t* idx,
-                           int64_t B, int64_t C, int64_t N, int64_t M,
-                           float* grad_pts);
+/* Reference CPU kernels: knn.cpp:30-164, fps.cpp:18-141 (the CPU dispatch
+   key's semantics: no FMA contraction, knn idx padding -1, FPS with
+   FLT_MAX-style initial distances and selected-point exclusion).  They check
+   the product's CPU kernels and are the timed CPU baseline.  dtype 0/1/2.
+   nthreads > 1 splits independent rows (knn forward) or clouds (knn
+   backward, fps) over OpenMP threads; results do not depend on it. */
+int tpo_cpu_knn_fwd(int dtype, const void* p1, const void* p2,
+                    const int64_t* len1, const int64_t* len2,
+                    int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,
+                    int norm, int64_t* idxs, void* dists, int nthreads);
+int tpo_cpu_knn_bwd(int dtype, const void* p1, const void* p2,
+                    const int64_t* len1, const int64_t* len2,
+                    const int64_t* idxs, int norm, const void* grad_dists,
+                    int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,
+                    void* gp1, void* gp2, int nthreads);
+int tpo_cpu_fps(int dtype, const void* pts, int64_t B, int64_t N, int64_t m,
+                int64_t* idx, int nthreads);
+int tpo_cpu_gather_fwd(int dtype, const void* pts, const int64_t* idx, int64_t B,
+                       int64_t C, int64_t N, int64_t M, void* out);
+int tpo_cpu_gather_bwd(int dtype, const void* grad_out, const int64_t* idx,
+                       int64_t B, int64_t C, int64_t N, int64_t M,
+                       void* grad_pts);
 
 #ifdef __cplusplus
 }

@@ -280,21 +280,145 @@ def test_knn_backward_closed_form(O):
         np.testing.assert_allclose(g2, e2, rtol=1e-5, atol=1e-6)
 
 
-def test_knn_cpu_baseline_restatement(O):
-    """knn.cpp semantics: ascending (dist, idx), padding -1, rows sorted."""
+def np_knn_cpu(p1, p2, l1, l2, K, norm):
+    """knn.cpp:30-99 written with numpy elementwise operators in the input
+    dtype (IEEE, no contraction; numpy's float16 operators round each result
+    like c10::Half) and a lexicographic (distance, index) selection instead of
+    a heap."""
+    dt = p1.dtype
+    N, P1, D = p1.shape
+    idx = np.full((N, P1, K), -1, np.int64)
+    dist = np.zeros((N, P1, K), dt)
+    for n in range(N):
+        for q in range(l1[n]):
+            acc = np.zeros(l2[n], dt)
+            for d in range(D):
+                diff = (p1[n, q, d] - p2[n, :l2[n], d]).astype(dt)
+                acc = (acc + (np.abs(diff) if norm == 1 else (diff * diff).astype(dt))).astype(dt)
+            order = np.lexsort((np.arange(l2[n]), acc))[:K]
+            idx[n, q, :len(order)] = order
+            dist[n, q, :len(order)] = acc[order]
+    return idx, dist
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.float16])
+@pytest.mark.parametrize("norm", [1, 2])
+def test_knn_cpu_restatement_vs_numpy(O, dt, norm):
+    """knn.cpp semantics: ascending (dist, idx), ties to the lower index,
+    padding -1 / 0, rows past lengths1 untouched; bit-exact in every dtype."""
     r = rng(12)
-    p1 = r.standard_normal((2, 20, 3)).astype(np.float32)
-    p2 = r.standard_normal((2, 50, 3)).astype(np.float32)
-    l1, l2 = np.array([20, 10]), np.array([50, 3])
-    idx, d = O.cpu_knn_fwd_f32(p1, p2, l1, l2, K=5)
-    full = ((p1[:, :, None, :].astype(np.float64) - p2[:, None, :, :]) ** 2).sum(-1)
-    for n in range(2):
-        ref = np.argsort(full[n, :, :l2[n]], axis=1, kind="stable")[:, :5]
-        k = min(5, l2[n])
-        assert np.array_equal(idx[n, :l1[n], :k], ref[:l1[n], :k])
-        assert (idx[n, :l1[n], k:] == -1).all() and (idx[n, l1[n]:] == -1).all()
-    i8, d8 = O.cpu_knn_fwd_f32(p1, p2, l1, l2, K=5, nthreads=4)
-    assert np.array_equal(i8, idx) and np.array_equal(d8, d)
+    p1 = r.standard_normal((3, 20, 3)).astype(dt)
+    p2 = r.standard_normal((3, 50, 3)).astype(dt)
+    # lattice points: many exactly equal distances
+    p1[2] = r.integers(-2, 3, (20, 3)).astype(dt)
+    p2[2] = r.integers(-2, 3, (50, 3)).astype(dt)
+    l1, l2 = np.array([20, 10, 20]), np.array([50, 3, 50])
+    for K in (1, 5, 12):
+        idx, d = O.cpu_knn_fwd(p1, p2, l1, l2, K=K, norm=norm)
+        ei, ed = np_knn_cpu(p1, p2, l1, l2, K, norm)
+        assert np.array_equal(idx, ei)
+        assert np.array_equal(d.view(np.uint8), ed.view(np.uint8))
+        i8, d8 = O.cpu_knn_fwd(p1, p2, l1, l2, K=K, norm=norm, nthreads=4)
+        assert np.array_equal(i8, idx) and np.array_equal(d8.view(np.uint8), d.view(np.uint8))
+    # D = 5 (not 3): the loop over coordinates is general
+    q = r.standard_normal((1, 7, 5)).astype(dt)
+    s = r.standard_normal((1, 9, 5)).astype(dt)
+    idx, d = O.cpu_knn_fwd(q, s, [7], [9], K=4, norm=norm)
+    ei, ed = np_knn_cpu(q, s, [7], [9], 4, norm)
+    assert np.array_equal(idx, ei) and np.array_equal(d.view(np.uint8), ed.view(np.uint8))
+
+
+def test_knn_cpu_known_values(O):
+    # reference tests/test_knn.py:187-218 and :251-285 on the CPU path
+    p1 = np.array([[[0.0, 0, 0], [1.0, 0, 0]]], np.float32)
+    p2 = np.array([[[0.0, 0, 0], [0.5, 0, 0], [2.0, 0, 0]]], np.float32)
+    idx, d = O.cpu_knn_fwd(p1, p2, [2], [3], K=2)
+    assert idx.tolist() == [[[0, 1], [1, 0]]] and d.tolist() == [[[0.0, 0.25], [0.25, 1.0]]]
+    q = np.zeros((1, 1, 3), np.float32)
+    s = np.array([[[1.0, 1, 1], [2.0, 0, 0]]], np.float32)
+    assert O.cpu_knn_fwd(q, s, [1], [2], K=2, norm=1)[1].tolist() == [[[2.0, 3.0]]]
+    assert O.cpu_knn_fwd(q, s, [1], [2], K=2, norm=2)[1].tolist() == [[[3.0, 4.0]]]
+    # the non-contracted float sum differs from the fma order of the GPU path:
+    # exact rational arithmetic, one rounding per operation
+    r = rng(40)
+    for _ in range(200):
+        a = r.standard_normal((1, 1, 3)).astype(np.float32)
+        b = r.standard_normal((1, 1, 3)).astype(np.float32)
+        _, d = O.cpu_knn_fwd(a, b, [1], [1], K=1)
+        df = [exact.f32_sub(a[0, 0, c], b[0, 0, c]) for c in range(3)]
+        sq = [exact.f32_mul(x, x) for x in df]
+        e = exact.round_f32(exact.Fraction(float(exact.round_f32(
+            exact.Fraction(float(sq[0])) + exact.Fraction(float(sq[1]))))) + exact.Fraction(float(sq[2])))
+        assert d[0, 0, 0].view(np.uint32) == e.view(np.uint32)
+
+
+@pytest.mark.parametrize("norm", [1, 2])
+def test_knn_cpu_backward_finite_difference(O, norm):
+    """Gradient of sum(g * dist) over the listed neighbours, float64, central
+    differences; rows past lengths1, slots past min(lengths2, K) and -1
+    padding contribute nothing (knn.cpp:135-143)."""
+    r = rng(41)
+    p1 = r.standard_normal((2, 6, 3))
+    p2 = r.standard_normal((2, 9, 3))
+    l1, l2 = np.array([6, 4]), np.array([9, 2])
+    K = 3
+    idx, _ = O.cpu_knn_fwd(p1, p2, l1, l2, K=K, norm=norm)
+    g = r.random((2, 6, K))
+    g1, g2 = O.cpu_knn_bwd(p1, p2, l1, l2, idx, norm, g)
+
+    def loss(a, b):
+        s = 0.0
+        for n in range(2):
+            for i in range(l1[n]):
+                for k in range(min(l2[n], K)):
+                    j = idx[n, i, k]
+                    if j < 0:
+                        continue
+                    v = a[n, i] - b[n, j]
+                    s += g[n, i, k] * (np.abs(v).sum() if norm == 1 else (v * v).sum())
+        return s
+
+    h = 1e-6
+    for arr, grad in ((p1, g1), (p2, g2)):
+        for pos in itertools.product(range(2), range(arr.shape[1]), range(3)):
+            old = arr[pos]
+            arr[pos] = old + h
+            up = loss(p1, p2)
+            arr[pos] = old - h
+            dn = loss(p1, p2)
+            arr[pos] = old
+            assert abs((up - dn) / (2 * h) - grad[pos]) < 1e-6
+    assert (g1[1, 4:] == 0).all()
+    # norm 1 on equal coordinates: sign -1 (knn.cpp:150), unlike the GPU path's 0
+    a = np.array([[[1.0, 2.0, 3.0]]], np.float32)
+    b = np.array([[[1.0, 0.0, 5.0]]], np.float32)
+    i1, _ = O.cpu_knn_fwd(a, b, [1], [1], K=1, norm=1)
+    c1, c2 = O.cpu_knn_bwd(a, b, [1], [1], i1, 1, np.array([[[0.5]]], np.float32))
+    assert c1.tolist() == [[[-0.5, 0.5, -0.5]]] and c2.tolist() == [[[0.5, -0.5, 0.5]]]
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+def test_knn_cpu_backward_accumulation_order(O, dt):
+    """Sequential (row, slot) accumulation in the dtype, one rounding per
+    addition: every query shares neighbours, so the order shows in the bits."""
+    r = rng(42)
+    p1 = r.standard_normal((1, 40, 3)).astype(dt)
+    p2 = r.standard_normal((1, 4, 3)).astype(dt)
+    idx, _ = O.cpu_knn_fwd(p1, p2, [40], [4], K=3)
+    g = r.random((1, 40, 3)).astype(dt)
+    g1, g2 = O.cpu_knn_bwd(p1, p2, [40], [4], idx, 2, g)
+    e1 = np.zeros_like(p1)
+    e2 = np.zeros_like(p2)
+    for i in range(40):
+        for k in range(3):
+            j = idx[0, i, k]
+            for d in range(3):
+                sub = (p1[0, i, d] - p2[0, j, d]).astype(dt)
+                t = dt(np.float32(np.float64(2.0) * np.float64(g[0, i, k]) * np.float64(sub)))
+                e1[0, i, d] = dt(e1[0, i, d] + t)
+                e2[0, j, d] = dt(e2[0, j, d] - t)
+    assert np.array_equal(g1.view(np.uint8), e1.view(np.uint8))
+    assert np.array_equal(g2.view(np.uint8), e2.view(np.uint8))
 
 
 # ---------------------------------------------------------------------- fps
@@ -371,17 +495,46 @@ def test_fps_brute_force(O):
     assert O.fps(pts.astype(np.float16), 10)[0, 0] == 0
 
 
-def test_fps_cpu_baseline_restatement(O):
-    """fps.cpp semantics (the reference tests' reference_fps_cpu loop)."""
+def np_fps_cpu(pts, m):
+    """fps.cpp:18-88 with numpy scalar operators in the input dtype."""
+    dt = pts.dtype.type
+    n = pts.shape[0]
+    md = np.full(n, np.finfo(dt).max, dt)
+    sel = np.zeros(n, bool)
+    x, y, z = pts[:, 0], pts[:, 1], pts[:, 2]
+    skip = ((x * x + y * y).astype(dt) + z * z).astype(dt) <= dt(np.float32(1e-3))
+    out = [0]
+    sel[0] = True
+    for _ in range(1, m):
+        c = pts[out[-1]]
+        dx, dy, dz = (x - c[0]).astype(dt), (y - c[1]).astype(dt), (z - c[2]).astype(dt)
+        dist = ((dx * dx + dy * dy).astype(dt) + dz * dz).astype(dt)
+        upd = ~sel & ~skip & (dist < md)
+        md = np.where(upd, dist, md)
+        cand = np.where(sel, dt(-1), md)
+        best = int(np.argmax(cand))  # first index of the maximum
+        out.append(best if cand[best] > -1 else 0)
+        sel[out[-1]] = True
+    return out
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.float16])
+def test_fps_cpu_restatement(O, dt):
+    """fps.cpp semantics (max-value start, selected points excluded,
+    degenerate points first, first index on ties), every dtype."""
     r = rng(16)
-    pts = r.standard_normal((3, 50, 3)).astype(np.float32)
-    idx = O.cpu_fps_f32(pts, 12)
+    pts = r.standard_normal((3, 50, 3)).astype(dt)
+    pts[1] = r.integers(-1, 2, (50, 3)).astype(dt)  # lattice: exact ties
+    pts[2, 7] = 0.0
+    pts[2, 9] = dt(0.01)
+    idx = O.cpu_fps(pts, 12)
     for b in range(3):
-        assert idx[b].tolist() == fps_f64(pts[b].astype(np.float64), 12)
-    assert np.array_equal(O.cpu_fps_f32(pts, 12, nthreads=3), idx)
-    # CPU semantics select degenerate points first (FLT_MAX distance)
-    pts[0, 7] = 0.0
-    assert O.cpu_fps_f32(pts, 3)[0, 1] == 7
+        assert idx[b].tolist() == np_fps_cpu(pts[b], 12)
+    assert np.array_equal(O.cpu_fps(pts, 12, nthreads=3), idx)
+    # CPU semantics select degenerate points first (their distance stays max)
+    assert idx[2, 1] == 7 and idx[2, 2] == 9
+    if dt == np.float32:  # no degenerate points, no ties: both semantics agree
+        assert idx[0].tolist() == fps_f64(pts[0].astype(np.float64), 12)
 
 
 # ------------------------------------------------------------------- gather
@@ -398,8 +551,17 @@ def test_gather_closed_form(O):
     for b in range(2):
         np.add.at(e[b].T, idx[b], go[b].T.astype(np.float64))
     np.testing.assert_allclose(gp, e, rtol=1e-6, atol=1e-6)
-    assert np.array_equal(O.cpu_gather_fwd_f32(pts, idx), out)
-    np.testing.assert_allclose(O.cpu_gather_bwd_f32(go, idx, 20), e, rtol=1e-6, atol=1e-6)
+    assert np.array_equal(O.cpu_gather_fwd(pts, idx), out)
+    np.testing.assert_allclose(O.cpu_gather_bwd(go, idx, 20), e, rtol=1e-6, atol=1e-6)
+    # CPU kernel order (fps.cpp:130-136): sequential additions in the dtype
+    for dt in (np.float16, np.float32):
+        g = go.astype(dt)
+        want = np.zeros((2, 6, 20), dt)
+        for b in range(2):
+            for c in range(6):
+                for j in range(8):
+                    want[b, c, idx[b, j]] = dt(want[b, c, idx[b, j]] + g[b, c, j])
+        assert np.array_equal(O.cpu_gather_bwd(g, idx, 20).view(np.uint8), want.view(np.uint8))
     with pytest.raises(ValueError):
         O.gather_fwd(pts, np.full((2, 8), 20))
 

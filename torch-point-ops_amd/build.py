@@ -82,22 +82,37 @@ def build_hip_lib(jobs: int = 8, verbose: bool = False) -> str:
     return out
 
 
-def build_torch_shim(verbose: bool = False) -> str:
+SHIM_SOURCES = ["torch_ops.cpp", "cpu_ops.cpp"]
+
+
+def build_torch_shim(jobs: int = 8, verbose: bool = False) -> str:
     import torch
     from torch.utils import cpp_extension as ce
 
     inc = ce.include_paths("cuda") + [INCLUDE, sysconfig.get_paths()["include"]]
     libdirs = ce.library_paths("cuda")
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    out = os.path.join(PKG, "_C.so")
-    tmp = out + ".tmp"
-    cmd = [
-        "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+    os.makedirs(BUILD, exist_ok=True)
+    cflags = [
+        "g++", "-O3", "-std=c++17", "-fPIC",
+        # the CPU kernels round after every + and *, as the reference's
+        # plain x86-64 build does; at::parallel_for needs OpenMP
+        "-ffp-contract=off", "-fopenmp",
         "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
         "-DTORCH_EXTENSION_NAME=_C", "-Wno-deprecated-declarations",
         *[f"-I{p}" for p in inc],
-        os.path.join(CSRC, "torch_ops.cpp"),
-        "-o", tmp,
+    ]
+    objs, cmds = [], []
+    for src in SHIM_SOURCES:
+        obj = os.path.join(BUILD, src.replace(".cpp", ".o"))
+        objs.append(obj)
+        cmds.append([*cflags, "-c", os.path.join(CSRC, src), "-o", obj])
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(cmds)))) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    out = os.path.join(PKG, "_C.so")
+    tmp = out + ".tmp"
+    cmd = [
+        "g++", "-shared", "-fopenmp", *objs, "-o", tmp,
         *[f"-L{p}" for p in libdirs],
         f"-L{PKG}", "-ltpo_hip",
         "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch",
@@ -110,7 +125,7 @@ def build_torch_shim(verbose: bool = False) -> str:
 
 def build(jobs: int = 8, verbose: bool = False) -> None:
     build_hip_lib(jobs, verbose)
-    build_torch_shim(verbose)
+    build_torch_shim(jobs, verbose)
 
 
 if __name__ == "__main__":
