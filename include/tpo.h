@@ -14,8 +14,9 @@
  *     returns a thread-local description of the last failure;
  *   - dtype is one of TPO_F32, TPO_F64, TPO_F16 (IEEE binary16), TPO_BF16
  *     (only where stated).
- * The functions keep no global mutable state and may be called from any
- * thread.
+ * The functions keep no global mutable state (apart from
+ * tpo_chamfer_fwd_noalloc's static device scratch and its per-device address
+ * cache) and may be called from any thread.
  */
 #ifndef TPO_H
 #define TPO_H
@@ -66,6 +67,25 @@ int tpo_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2,
                     int64_t B, int64_t N, int64_t M,
                     void* dist1, void* dist2, int32_t* idx1, int32_t* idx2,
                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Chamfer forward that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory or pass a workspace
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as tpo_chamfer_fwd, bit for bit;
+ * the grid-search workspace is a static device array of
+ * tpo_chamfer_noalloc_max_workspace() bytes (32 MiB) that every GPU the
+ * library runs on holds until the process ends.  Sizes whose workspace
+ * (tpo_chamfer_workspace_size) exceeds it are rejected with
+ * TPO_ERR_WORKSPACE (B=32, N=M=8192 needs about 19 MB).  All calls on one
+ * device share that array: calls that overlap on one GPU (other streams or
+ * threads) race; calls ordered on one stream do not.
+ */
+int64_t tpo_chamfer_noalloc_max_workspace(void);
+int tpo_chamfer_fwd_noalloc(int dtype, const void* xyz1, const void* xyz2,
+                            int64_t B, int64_t N, int64_t M,
+                            void* dist1, void* dist2, int32_t* idx1, int32_t* idx2,
+                            void* stream);
 
 /*
  * Diagnostic, no counterpart in the reference: after a tpo_chamfer_fwd call

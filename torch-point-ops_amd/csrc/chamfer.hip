@@ -30,6 +30,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "chamfer_common.hpp"
 #include "tpo_common.hpp"
@@ -839,6 +840,68 @@ extern "C" int tpo_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2, in
     default: return set_error(TPO_ERR_DTYPE, "tpo_chamfer_fwd: unsupported dtype %d", dtype);
   }
   return check_launch("tpo_chamfer_fwd");
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward.  The grid-search workspace lives in a file-scope
+// device array: every GPU the library runs on holds its own copy (allocated
+// when the code object is loaded on that device) until the process ends.
+// Host code never passes `scratch` itself (in host code the name is a
+// stand-in, not a device address): each device's address is looked up once
+// with hipGetSymbolAddress and kept per device.  Every call on a device
+// shares its array, so calls that overlap on one GPU (different streams, or
+// threads) race; calls in one stream are ordered.  Nothing in it needs to
+// start at zero: the sort kernel writes every region the search reads.
+static constexpr int64_t kNoAllocScratchBytes = (int64_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+}  // namespace
+
+static int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(TPO_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(TPO_ERR_ARG, "tpo_chamfer_fwd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(TPO_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TPO_OK;
+}
+
+extern "C" int64_t tpo_chamfer_noalloc_max_workspace(void) { return kNoAllocScratchBytes; }
+
+extern "C" int tpo_chamfer_fwd_noalloc(int dtype, const void* xyz1, const void* xyz2, int64_t B,
+                                       int64_t N, int64_t M, void* dist1, void* dist2,
+                                       int32_t* idx1, int32_t* idx2, void* stream) {
+  const int64_t need = tpo_chamfer_workspace_size(dtype, B, N, M);
+  if (need < 0)
+    return set_error(TPO_ERR_ARG, "tpo_chamfer_fwd_noalloc: bad sizes B=%lld N=%lld M=%lld",
+                     (long long)B, (long long)N, (long long)M);
+  if (need > kNoAllocScratchBytes)
+    return set_error(TPO_ERR_WORKSPACE,
+                     "tpo_chamfer_fwd_noalloc: B=%lld N=%lld M=%lld needs %lld bytes of grid "
+                     "workspace, more than the %lld-byte static scratch (use tpo_chamfer_fwd "
+                     "with a caller-provided workspace)",
+                     (long long)B, (long long)N, (long long)M, (long long)need,
+                     (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = noalloc_scratch(&ws);
+    if (rc != TPO_OK) return rc;
+  }
+  return tpo_chamfer_fwd(dtype, xyz1, xyz2, B, N, M, dist1, dist2, idx1, idx2, ws, need, stream);
 }
 
 extern "C" int tpo_chamfer_pairs_evaluated(int dtype, const void* workspace, int64_t B,
