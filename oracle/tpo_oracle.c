@@ -197,6 +197,10 @@ INLINE double sq3(int dt, double x, double y, double z) {
 INLINE void chamfer_dir(int dt, const void* q, const void* r, int64_t B,
                         int64_t n, int64_t m, void* dist, int32_t* idx) {
   const int64_t tile = 512;
+  /* every (cloud, query) is independent: threads change nothing but speed */
+#ifdef _OPENMP
+#pragma omp parallel for collapse(2) schedule(dynamic, 64)
+#endif
   for (int64_t b = 0; b < B; ++b) {
     for (int64_t j = 0; j < n; ++j) {
       const int64_t qi = (b * n + j) * 3;
@@ -416,18 +420,25 @@ static int knn_fwd_dt(int dt, const void* p1, const void* p2, const int64_t* len
     idxs[i] = 0;
     st(dt, dists, i, 0.0);
   }
-  double* sd = (double*)malloc((size_t)(K > 0 ? K : 1) * sizeof(double));
-  int64_t* si = (int64_t*)malloc((size_t)(K > 0 ? K : 1) * sizeof(int64_t));
-  if (!sd || !si) {
-    free(sd);
-    free(si);
-    return -3;
-  }
-  for (int64_t n = 0; n < N; ++n) {
-    int64_t l1 = len1[n], l2 = len2[n];
-    if (l1 > P1) l1 = P1; /* the reference reads past the cloud here */
-    if (l2 > P2) l2 = P2;
-    for (int64_t q = 0; q < l1; ++q) {
+  int err = 0;
+  /* every query row is independent: threads change nothing but speed */
+#ifdef _OPENMP
+#pragma omp parallel
+#endif
+  {
+    double* sd = (double*)malloc((size_t)(K > 0 ? K : 1) * sizeof(double));
+    int64_t* si = (int64_t*)malloc((size_t)(K > 0 ? K : 1) * sizeof(int64_t));
+    if (!sd || !si) err = 1;
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 16)
+#endif
+    for (int64_t t = 0; t < N * P1; ++t) {
+      if (!sd || !si) continue;
+      const int64_t n = t / P1, q = t % P1;
+      int64_t l1 = len1[n], l2 = len2[n];
+      if (l1 > P1) l1 = P1; /* the reference reads past the cloud here */
+      if (l2 > P2) l2 = P2;
+      if (q >= l1) continue;
       int64_t size = 0;
       for (int64_t s = 0; s < K; ++s) {
         sd[s] = INFINITY; /* NumericLimits::inf(), mink.cuh:83-86 */
@@ -448,10 +459,10 @@ static int knn_fwd_dt(int dt, const void* p1, const void* p2, const int64_t* len
         st(dt, dists, o + s, sd[s]);
       }
     }
+    free(sd);
+    free(si);
   }
-  free(sd);
-  free(si);
-  return 0;
+  return err ? -3 : 0;
 }
 
 int tpo_ref_knn_fwd(int dtype, const void* p1, const void* p2, const int64_t* len1,
@@ -571,21 +582,27 @@ int64_t tpo_ref_fps_rank(int64_t k, int64_t n) {
    temp starts at 1e10 (1e4 for fp16) (fps.cu:291-292). */
 static int fps_dt(int dt, const void* pts, int64_t B, int64_t N, int64_t m, int64_t* idx) {
   const int bs = tpo_ref_fps_block_size(N);
-  double* temp = (double*)malloc((size_t)(N > 0 ? N : 1) * sizeof(double));
-  double* mag = (double*)malloc((size_t)(N > 0 ? N : 1) * sizeof(double));
-  double* dv = (double*)malloc((size_t)bs * sizeof(double));
-  int64_t* di = (int64_t*)malloc((size_t)bs * sizeof(int64_t));
-  if (!temp || !mag || !dv || !di) {
-    free(temp);
-    free(mag);
-    free(dv);
-    free(di);
-    return -3;
-  }
   /* scalar_t(1e-3): the double literal converts to float, then to the dtype */
   const double thr = (dt == TPO_REF_F64) ? 1e-3 : (dt == TPO_REF_F16 ? rh(1e-3f) : (double)1e-3f);
   const double init = (dt == TPO_REF_F16) ? 1e4 : 1e10;
+  int err = 0;
+  /* clouds are independent: threads change nothing but speed */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
   for (int64_t b = 0; b < B; ++b) {
+    double* temp = (double*)malloc((size_t)(N > 0 ? N : 1) * sizeof(double));
+    double* mag = (double*)malloc((size_t)(N > 0 ? N : 1) * sizeof(double));
+    double* dv = (double*)malloc((size_t)bs * sizeof(double));
+    int64_t* di = (int64_t*)malloc((size_t)bs * sizeof(int64_t));
+    if (!temp || !mag || !dv || !di) {
+      err = 1;
+      free(temp);
+      free(mag);
+      free(dv);
+      free(di);
+      continue;
+    }
     const int64_t base = b * N * 3;
     for (int64_t k = 0; k < N; ++k) {
       temp[k] = init;
@@ -626,12 +643,12 @@ static int fps_dt(int dt, const void* pts, int64_t B, int64_t N, int64_t m, int6
       old = di[0];
       idx[b * m + j] = old;
     }
+    free(temp);
+    free(mag);
+    free(dv);
+    free(di);
   }
-  free(temp);
-  free(mag);
-  free(dv);
-  free(di);
-  return 0;
+  return err ? -3 : 0;
 }
 
 int tpo_ref_fps(int dtype, const void* pts, int64_t B, int64_t N, int64_t m, int64_t* idx) {

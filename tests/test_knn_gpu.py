@@ -78,30 +78,6 @@ def test_quantised_ties_bit_exact(tpo, O, dev):
         assert_same(np_(d), ed)
 
 
-def test_config3_subset_exact_and_full_properties(tpo, O, dev):
-    p1, p2, l1, l2 = workloads.knn_c3()
-    idx, d = raw(p1, p2, l1, l2, 2, 16, -1, dev)
-    for n in (0, 7):
-        sel = slice(0, 256)
-        ln1 = torch.tensor([min(256, int(l1[n]))])
-        ei, ed = O.knn_fwd(np_(p1[n:n + 1, sel]), np_(p2[n:n + 1]), np_(ln1), np_(l2[n:n + 1]),
-                           norm=2, K=16)
-        assert_same(np_(idx[n:n + 1, sel]), ei)
-        assert_same(np_(d[n:n + 1, sel]), ed)
-    # full size: rows past lengths1 zero, indices inside lengths2, sorted
-    # distances match a float64 recomputation at the returned indices
-    si, sd = tpo.knn_points(p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev), K=16)
-    for n in range(p1.shape[0]):
-        a, b = int(l1[n]), int(l2[n])
-        assert (idx[n, a:] == 0).all() and (d[n, a:] == 0).all()
-        assert int(si[n, :a].min()) >= 0 and int(si[n, :a].max()) < b
-        assert bool((sd[n, :a, 1:] >= sd[n, :a, :-1]).all())
-        q = p1[n, :a].to(dev, torch.float64)
-        r = p2[n].to(dev, torch.float64)
-        at = ((r[si[n, :a]] - q[:, None]) ** 2).sum(-1)
-        assert torch.allclose(at, sd[n, :a].double(), rtol=1e-6, atol=1e-9)
-
-
 def _long_cloud_inputs(case, g):
     # long reference clouds (the staged float D=3 sweep over 5000 references,
     # lengths2 ragged, a cloud with a single query row)

@@ -40,6 +40,7 @@
 #include <algorithm>
 
 #include "chamfer_common.hpp"
+#include "chamfer_dense.hpp"
 
 #pragma clang fp contract(off)
 
@@ -50,12 +51,14 @@ constexpr int CG_CELLS = CG_GRID * CG_GRID * CG_GRID;
 constexpr int CG_CSTRIDE = CG_CELLS + 4;  // cell-start ints per cloud (16-byte rows)
 constexpr int CG_WG = 256;    // queries per search workgroup
 constexpr int CG_UNROLL = 2;  // points of a cell loaded together
+constexpr int CG_OCC = 2;     // mean own-cell occupancy the search resolution aims at
 
 __host__ __device__ inline int64_t cg_pad(int64_t n) { return (n + 63) & ~(int64_t)63; }
 
 // Byte offsets of the workspace regions (all 256-byte aligned).
 struct CgLayout {
-  int64_t hdr;     // 2B x 16 floats: lo[3], hi[3], cells per unit[3], cell size[3], bad
+  int64_t hdr;     // 2B x 16 floats: lo[3], hi[3], cells per unit[3], cell size[3] (32^3),
+                   // bad, degenerate, level (search cells are 2^level of them per axis)
   int64_t pts;     // float4 per padded point: sorted (x, y, z, original index bits)
   int64_t cstart;  // CG_CSTRIDE int32 per cloud: first sorted position of a cell, then n
   int64_t rank;    // int32 per point: rank within its cell (sort scratch)
@@ -94,9 +97,9 @@ __device__ __forceinline__ uint32_t cg_spread(uint32_t v) {  // 5 bits -> every 
   return v;
 }
 
-__device__ __forceinline__ int cg_axis_cell(float p, float lo, float sc) {
+__device__ __forceinline__ int cg_axis_cell(float p, float lo, float sc, int g = CG_GRID) {
   const float f = (p - lo) * sc;
-  return is_nan(f) ? 0 : (int)fminf(fmaxf(f, 0.f), (float)(CG_GRID - 1));
+  return is_nan(f) ? 0 : (int)fminf(fmaxf(f, 0.f), (float)(g - 1));
 }
 
 __device__ __forceinline__ uint32_t cg_code(int cx, int cy, int cz) {
@@ -153,6 +156,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   __shared__ float red[6][16];
   __shared__ uint32_t part[16];
   __shared__ uint32_t s_bad;
+  __shared__ float s_sq[3][16];  // per wave: sum of count^2 over the cells of 32^3, 16^3, 8^3
   const int c = blockIdx.x & 1, b = blockIdx.x >> 1;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int n = c ? M : N;
@@ -266,6 +270,35 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
       v[i] = cnt[cg_hidx(tid * CPT + i)];
       sum += v[i];
     }
+    {
+      // sums of count^2 over the cells of 32^3, 16^3 and 8^3 (Morton order
+      // nests them: 8 consecutive cells form a 16^3 cell, this thread's 32
+      // and its neighbour's an 8^3 cell), in float, reduced in a fixed order
+      float sq0 = 0.f, sq1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < CPT; i += 8) {
+        uint32_t c8 = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          sq0 = __builtin_fmaf((float)v[i + k], (float)v[i + k], sq0);
+          c8 += v[i + k];
+        }
+        sq1 = __builtin_fmaf((float)c8, (float)c8, sq1);
+      }
+      const float c64 = (float)(sum + (uint32_t)__shfl_xor((int)sum, 1));
+      float sq2 = (lane & 1) ? 0.f : c64 * c64;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        sq0 += __shfl_xor(sq0, o);
+        sq1 += __shfl_xor(sq1, o);
+        sq2 += __shfl_xor(sq2, o);
+      }
+      if (lane == 0) {
+        s_sq[0][w] = sq0;
+        s_sq[1][w] = sq1;
+        s_sq[2][w] = sq2;
+      }
+    }
     uint32_t incl = sum;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -329,15 +362,43 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
       hdr[9 + a] = gs[a] > 0.f ? (ghi[a] - glo[a]) / (float)CG_GRID : 0.f;
     }
     hdr[12] = __uint_as_float(s_bad);
+    // sum(count^2) / n is the mean number of points in a point's own cell.
+    // The search uses the finest of 32^3, 16^3, 8^3 whose mean is at least
+    // CG_OCC (sparse clouds get coarser cells, so a query's 3x3x3
+    // neighbourhood usually holds its nearest point).  A grid whose finest
+    // mean exceeds max(256, n / 32) is degenerate: the dense kernels are
+    // cheaper.  The sums are added in a fixed order, so the choices are
+    // deterministic.
+    float sq[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      sq[k] = 0.f;
+      for (int v2 = 0; v2 < 16; ++v2) sq[k] += s_sq[k][v2];
+    }
+    const float nn = (float)n;
+    const uint32_t level = sq[0] >= CG_OCC * nn ? 0u : (sq[1] >= CG_OCC * nn ? 1u : 2u);
+    hdr[13] = __uint_as_float(n > 0 && sq[0] > (float)max(256, n / 32) * nn ? 1u : 0u);
+    hdr[14] = __uint_as_float(level);
   }
 }
 
+// A lane walks cells one by one; a box of more cells than about nr / 64
+// costs more to walk than the whole cloud costs the wave to scan together,
+// so such lanes (and lanes with no point in their cell's 3x3x3
+// neighbourhood) are answered by a wave-wide scan instead.
+constexpr int CG_BOX_MIN = 128;  // cells a lane may always walk
+__host__ __device__ inline int cg_box_max(int nr) { return max(CG_BOX_MIN, nr >> 6); }
+
 template <typename T, int WG>
-__global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
+__global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
     const T* __restrict__ xyz1, const T* __restrict__ xyz2, int B, int N, int M, int nqb1,
     int nqb2, const char* __restrict__ ws, CgLayout L, T* __restrict__ dist1,
     T* __restrict__ dist2, int32_t* __restrict__ idx1, int32_t* __restrict__ idx2) {
   using Mg = CgMargin<T>;
+  static_assert(WG == 64 * CH_WAVES, "a search workgroup is one 256-query dense block");
+  // LDS: the dense block's arrays (degenerate grids only)
+  __shared__ __align__(16) char s_mem[sizeof(float4) * CH_WAVES * 64 +
+                                      (sizeof(T) + sizeof(int)) * CH_WAVES * WG];
   const int bid = xcd_logical_block(blockIdx.x, gridDim.x);
   int lb = bid;
   const int g1 = B * nqb1;
@@ -361,8 +422,30 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
   const T* __restrict__ qp = (dir ? xyz2 : xyz1) + (size_t)b * nq * 3;
   T* __restrict__ dout = (dir ? dist2 : dist1) + (size_t)b * nq;
   int32_t* __restrict__ iout = (dir ? idx2 : idx1) + (size_t)b * nq;
+  int32_t* __restrict__ stats = reinterpret_cast<int32_t*>(const_cast<char*>(ws) + L.stats);
 
   const int lane = lane_id(), w = wave_id();
+  if (__float_as_uint(h[13]) != 0u) {
+    // a degenerate reference grid: this workgroup's 256 queries (in original
+    // order) are answered by the dense block (every pair evaluated)
+    auto& s_ref = *reinterpret_cast<float4(*)[CH_WAVES][64]>(s_mem);
+    char* tail = s_mem + sizeof(float4) * CH_WAVES * 64;
+    if constexpr (sizeof(T) == 4) {  // two 128-query blocks (keeps the registers low)
+      auto& s_d = *reinterpret_cast<T(*)[CH_WAVES][128]>(tail);
+      auto& s_i = *reinterpret_cast<int(*)[CH_WAVES][128]>(tail + sizeof(T) * CH_WAVES * 128);
+      for (int k = 0; k < WG / 128; ++k)
+        chamfer_filter_block<2, CH_FTILE>(qp, rp, nq, nr, qb * (WG / 128) + k, dout, iout, s_ref,
+                                          s_d, s_i);
+    } else {  // four 64-query blocks (keeps the kernel's registers low)
+      auto& s_d = *reinterpret_cast<T(*)[CH_WAVES][64]>(tail);
+      auto& s_i = *reinterpret_cast<int(*)[CH_WAVES][64]>(tail + sizeof(T) * CH_WAVES * 64);
+      for (int k = 0; k < WG / 64; ++k)
+        chamfer_dense_block<T, 1>(qp, rp, nq, nr, qb * (WG / 64) + k, dout, iout, s_d, s_i);
+    }
+    const int64_t nv = max(0, min(nq - (qb * WG + w * 64), 64));
+    if (lane == 0) stats[(size_t)bid * (WG / 64) + w] = (int32_t)min(nv * nr, (int64_t)0x7fffffff);
+    return;
+  }
   const int pos = qb * WG + (int)threadIdx.x;
   const bool valid = pos < nq;
   const float4 q = qs[min(pos, nq - 1)];
@@ -370,26 +453,35 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
   const bool rbad = __float_as_uint(h[12]) != 0u;
   const bool qbad = max(abs_bits(q.x), max(abs_bits(q.y), abs_bits(q.z))) >= CH_BIG;
   const bool fallback = valid && (rbad || qbad);
+  bool far = false;  // answered by the wave-wide scan below
   int examined = 0;
+  const unsigned long long kInit = ((unsigned long long)0x7f800000u << 32) | 0x7fffffffu;
 
   if (valid && !fallback) {
-    const float glo[3] = {h[0], h[1], h[2]}, ghi[3] = {h[3], h[4], h[5]};
-    const float gs[3] = {h[6], h[7], h[8]}, cs[3] = {h[9], h[10], h[11]};
+    // grid geometry at the search resolution: G cells per axis, cell
+    // (cx, cy, cz) holding the sorted points [cstart[code << 3 lv],
+    // cstart[(code + 1) << 3 lv]) -- a Morton-ordered 32^3 cell c lies in
+    // the coarser cell c >> 3 lv, and the coarser cell index equals
+    // floor((p - lo) * gs / 2^lv) exactly (scaling by a power of two
+    // commutes with rounding), so the two views agree
+    const int lv = (int)__float_as_uint(h[14]);
+    const int G = CG_GRID >> lv, sh = 3 * lv;
+    float glo[3], ghi[3], gs[3], cs[3], eps[3];
     const float qv[3] = {q.x, q.y, q.z};
     int ci[3], ga[3];
-    float eps[3];
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
-      ga[a] = gs[a] > 0.f ? CG_GRID : 1;
-      ci[a] = gs[a] > 0.f ? cg_axis_cell(qv[a], glo[a], gs[a]) : 0;
+      glo[a] = h[a];
+      ghi[a] = h[3 + a];
+      gs[a] = __builtin_ldexpf(h[6 + a], -lv);
+      cs[a] = __builtin_ldexpf(h[9 + a], lv);
+      ga[a] = gs[a] > 0.f ? G : 1;
+      ci[a] = gs[a] > 0.f ? cg_axis_cell(qv[a], glo[a], gs[a], G) : 0;
       eps[a] = 0x1p-20f * (__builtin_fabsf(glo[a]) + (ghi[a] - glo[a])) + 0x1p-126f;
     }
-    int rmax = 0;
-#pragma unroll
-    for (int a = 0; a < 3; ++a) rmax = max(rmax, max(ci[a], ga[a] - 1 - ci[a]));
     // best (distance, index) as one key: distances here are finite and >= 0,
     // so their bits order like the values, and the index breaks ties
-    uint64_t bkey = ((uint64_t)0x7f800000u << 32) | 0x7fffffffu;
+    unsigned long long bkey = kInit;
     auto bdist = [&]() { return __uint_as_float((uint32_t)(bkey >> 32)); };
     const char* __restrict__ rsb = reinterpret_cast<const char*>(rs);
     // evaluate every point of sorted positions [j0, j1)
@@ -404,13 +496,15 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
 #pragma unroll
         for (int u = 0; u < CG_UNROLL; ++u) {
           const float d = cg_dist<T>(p[u], q);
-          const uint64_t key = ((uint64_t)__float_as_uint(d) << 32) | __float_as_uint(p[u].w);
+          const unsigned long long key =
+              ((unsigned long long)__float_as_uint(d) << 32) | __float_as_uint(p[u].w);
           bkey = key < bkey ? key : bkey;
         }
       }
       examined += j1 - j0;
     };
-    // evaluate every point of cell cc unless its box is farther than bd
+    auto scan_cell = [&](uint32_t code) { scan(cstart[code << sh], cstart[(code + 1) << sh]); };
+    // evaluate every point of cell cc unless its box is farther than the best
     auto visit = [&](int cx, int cy, int cz) {
       const int cc[3] = {cx, cy, cz};
       float gap[3];
@@ -421,18 +515,17 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
         gap[a] = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
       }
       if (sq3(gap[0], gap[1], gap[2]) * Mg::lb - Mg::abs > bdist()) return;
-      const uint32_t code = cg_code(cx, cy, cz);
-      scan(cstart[code], cstart[code + 1]);
+      scan_cell(cg_code(cx, cy, cz));
     };
-    // phase 1: Chebyshev rings around the query's cell until a point is found
+    // phase 1: the query's cell; if it is empty, ring 1, nearest cells
+    // first: the six face neighbours (the nearer face of each axis first),
+    // then the 12 edge and 8 corner neighbours, each group skipped whole
+    // when a lower bound of its cells' gaps (the same per-axis gaps visit
+    // computes, combined monotonically) already exceeds the best distance.
+    // Nothing within ring 1: the wave-wide scan answers the query.
     visit(ci[0], ci[1], ci[2]);
     int rdone = 0;
-    if (bdist() == Lim<float>::inf() && rmax >= 1) {
-      // ring 1, nearest cells first: the six face neighbours (the nearer face
-      // of each axis first), then the 12 edge and 8 corner neighbours, each
-      // group skipped whole when a lower bound of its cells' gaps (the same
-      // per-axis gaps visit computes, combined monotonically) already exceeds
-      // the best distance
+    if (bdist() == Lim<float>::inf()) {
       float gn[3];
       int sn[3];
 #pragma unroll
@@ -470,23 +563,7 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
             cell((c & 1) ? 1 : -1, (c & 2) ? 1 : -1, (c & 4) ? 1 : -1);
       }
       rdone = 1;
-    }
-    for (int r = 2; r <= rmax && bdist() == Lim<float>::inf(); ++r) {
-      const int z0 = max(-r, -ci[2]), z1 = min(r, ga[2] - 1 - ci[2]);
-      const int y0 = max(-r, -ci[1]), y1 = min(r, ga[1] - 1 - ci[1]);
-      const int x0 = max(-r, -ci[0]), x1 = min(r, ga[0] - 1 - ci[0]);
-      for (int dz = z0; dz <= z1; ++dz)
-        for (int dy = y0; dy <= y1; ++dy) {
-          const bool full = dz == -r || dz == r || dy == -r || dy == r;
-          for (int dx = x0; dx <= x1; ++dx) {
-            if (!full && dx != -r && dx != r) {  // interior of the ring: jump to its far side
-              if (dx < r) dx = r - 1;
-              continue;
-            }
-            visit(ci[0] + dx, ci[1] + dy, ci[2] + dz);
-          }
-        }
-      rdone = r;
+      far = bdist() == Lim<float>::inf();
     }
     // phase 2: the box of cells within the best distance (cell assignment is
     // monotone in each coordinate, so the box holds every point within it);
@@ -494,50 +571,76 @@ __global__ __launch_bounds__(WG) void chamfer_grid_search_kernel(
     // accumulated per axis as the loops descend, so a slab or row whose
     // partial lower bound already exceeds the best distance is skipped whole
     // (the bound only grows with more axes; any summation order rounds by a
-    // few u, well inside the 2^-20 margin).
+    // few u, well inside the 2^-20 margin).  A box of more than
+    // cg_box_max(nr) cells goes to the wave-wide scan.
     int blo[3], bhi[3];
     const float bd = bdist();
     const float rad = __builtin_sqrtf((bd + Mg::abs) * Mg::inv) * (1.f + 0x1p-19f);
+    int cells = 1;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
       const float ra = rad + eps[a] + 0x1p-20f * __builtin_fabsf(qv[a]);
-      blo[a] = ga[a] > 1 ? cg_axis_cell(qv[a] - ra, glo[a], gs[a]) : 0;
-      bhi[a] = ga[a] > 1 ? cg_axis_cell(qv[a] + ra, glo[a], gs[a]) : 0;
+      blo[a] = ga[a] > 1 ? cg_axis_cell(qv[a] - ra, glo[a], gs[a], G) : 0;
+      bhi[a] = ga[a] > 1 ? cg_axis_cell(qv[a] + ra, glo[a], gs[a], G) : 0;
+      cells *= bhi[a] - blo[a] + 1;
     }
-    auto gap2 = [&](int a, int c) {
-      const float clo = (ga[a] > 1 ? glo[a] + (float)c * cs[a] : glo[a]) - eps[a];
-      const float chi = (ga[a] > 1 ? glo[a] + (float)(c + 1) * cs[a] : ghi[a]) + eps[a];
-      const float g = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
-      return g * g;
-    };
-    for (int cz = blo[2]; cz <= bhi[2]; ++cz) {
-      const float gz = gap2(2, cz);
-      if (gz * Mg::lb - Mg::abs > bdist()) continue;
-      const uint32_t kz = cg_spread((uint32_t)cz) << 2;
-      const int dz = abs(cz - ci[2]);
-      for (int cy = blo[1]; cy <= bhi[1]; ++cy) {
-        const float gzy = gz + gap2(1, cy);
-        if (gzy * Mg::lb - Mg::abs > bdist()) continue;
-        const uint32_t kzy = kz | (cg_spread((uint32_t)cy) << 1);
-        const int dzy = max(dz, abs(cy - ci[1]));
-        for (int cx = blo[0]; cx <= bhi[0]; ++cx) {
-          if (max(dzy, abs(cx - ci[0])) <= rdone) continue;
-          if ((gzy + gap2(0, cx)) * Mg::lb - Mg::abs > bdist()) continue;
-          const uint32_t code = kzy | cg_spread((uint32_t)cx);
-          const int j0 = cstart[code], j1 = cstart[code + 1];
-          scan(j0, j1);
+    far = far || cells > cg_box_max(nr);
+    if (!far) {
+      auto gap2 = [&](int a, int c) {
+        const float clo = (ga[a] > 1 ? glo[a] + (float)c * cs[a] : glo[a]) - eps[a];
+        const float chi = (ga[a] > 1 ? glo[a] + (float)(c + 1) * cs[a] : ghi[a]) + eps[a];
+        const float g = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
+        return g * g;
+      };
+      for (int cz = blo[2]; cz <= bhi[2]; ++cz) {
+        const float gz = gap2(2, cz);
+        if (gz * Mg::lb - Mg::abs > bdist()) continue;
+        const uint32_t kz = cg_spread((uint32_t)cz) << 2;
+        const int dz = abs(cz - ci[2]);
+        for (int cy = blo[1]; cy <= bhi[1]; ++cy) {
+          const float gzy = gz + gap2(1, cy);
+          if (gzy * Mg::lb - Mg::abs > bdist()) continue;
+          const uint32_t kzy = kz | (cg_spread((uint32_t)cy) << 1);
+          const int dzy = max(dz, abs(cy - ci[1]));
+          for (int cx = blo[0]; cx <= bhi[0]; ++cx) {
+            if (max(dzy, abs(cx - ci[0])) <= rdone) continue;
+            if ((gzy + gap2(0, cx)) * Mg::lb - Mg::abs > bdist()) continue;
+            scan_cell(kzy | cg_spread((uint32_t)cx));
+          }
         }
       }
+      dout[oq] = (T)bdist();
+      iout[oq] = (int)(uint32_t)bkey;
     }
-    dout[oq] = (T)bdist();
-    iout[oq] = (int)(uint32_t)bkey;
+  }
+  // far queries: the wave scans every reference point (sorted order, same
+  // key), one query at a time
+  for (uint64_t fm = __ballot(far); fm; fm &= fm - 1) {
+    const int l = __builtin_ctzll(fm);
+    const float4 ql = make_float4(__shfl(q.x, l), __shfl(q.y, l), __shfl(q.z, l), 0.f);
+    unsigned long long k = kInit;
+    for (int j = lane; j < nr; j += 64) {
+      const float4 p = rs[j];
+      const unsigned long long key =
+          ((unsigned long long)__float_as_uint(cg_dist<T>(p, ql)) << 32) | __float_as_uint(p.w);
+      k = key < k ? key : k;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const unsigned long long x = __shfl_xor(k, o);
+      k = x < k ? x : k;
+    }
+    if (lane == l) {
+      dout[oq] = (T)__uint_as_float((uint32_t)(k >> 32));
+      iout[oq] = (int)(uint32_t)k;
+    }
+    examined += lane == 0 ? nr : 0;
   }
   {  // points evaluated by this wave
     int e = examined;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o);
-    if (lane == 0)
-      reinterpret_cast<int32_t*>(const_cast<char*>(ws) + L.stats)[(size_t)bid * (WG / 64) + w] = e;
+    if (lane == 0) stats[(size_t)bid * (WG / 64) + w] = e;
   }
   // queries that need the reference's full rule: the wave scans one at a time
   uint64_t fb = __ballot(fallback);
