@@ -233,6 +233,21 @@ def _pruned_case(kind, g):
         p1[0, 17] = 1e3
         p1[1, 5:9] = torch.tensor([-50.0, 80.0, 3.0])
         return p1, p2
+    if kind == "heavy_tail":  # far points on several axes and sides: the box is cut
+        p1, p2 = workloads.chamfer_c2(seed=12, B=2, N=3000)
+        p1[0, :5] = torch.tensor([[1e2, 0, 0], [0, -1e3, 0], [0, 0, 1e4], [-3e2, 2e2, 0], [5e3, 5e3, 5e3]])
+        p2[0, 10:13] = torch.tensor([[-1e4, 0, 0], [0, 7e2, 0], [0, 0, -2e3]])
+        p1[1, 100] = torch.tensor([0.0, 0.0, -1e5])
+        p2[1, 7] = torch.tensor([1e5, 0.0, 0.0])
+        return p1, p2
+    if kind == "cut_flat":  # a flat cloud plus a few points off the plane
+        p1 = torch.rand(2, 2500, 3, generator=g)
+        p2 = torch.rand(2, 2300, 3, generator=g)
+        p1[..., 2] = 0.5
+        p2[..., 2] = 0.5
+        p1[:, :2, 2] = torch.tensor([900.0, -700.0])
+        p2[:, 5, 2] = 1e3
+        return p1, p2
     if kind == "far_clusters":  # two tight clusters far apart: one cell each
         p1 = torch.rand(2, 3000, 3, generator=g) * 0.01
         p2 = torch.rand(2, 2600, 3, generator=g) * 0.01
@@ -256,7 +271,8 @@ def _pruned_case(kind, g):
 
 @pytest.mark.parametrize("kind", ["uniform", "blobs", "flat", "single_point", "apart",
                                   "duplicates", "lattice", "line", "tiny", "offset", "huge",
-                                  "outlier", "outlier_query", "far_clusters", "sparse_tail",
+                                  "outlier", "outlier_query", "heavy_tail", "cut_flat",
+                                  "far_clusters", "sparse_tail",
                                   "nonfinite"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_pruned_forward_vs_oracle(tpo, O, dev, kind, dtype):

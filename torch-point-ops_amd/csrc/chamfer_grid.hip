@@ -58,7 +58,9 @@ __host__ __device__ inline int64_t cg_pad(int64_t n) { return (n + 63) & ~(int64
 // Byte offsets of the workspace regions (all 256-byte aligned).
 struct CgLayout {
   int64_t hdr;     // 2B x 16 floats: lo[3], hi[3], cells per unit[3], cell size[3] (32^3),
-                   // bad, degenerate, level (search cells are 2^level of them per axis)
+                   // bad, degenerate, level (search cells are 2^level of them per axis),
+                   // cut sides (bit a: axis a cut below, 3 + a: above; the boundary
+                   // cells on a cut side are unbounded)
   int64_t pts;     // float4 per padded point: sorted (x, y, z, original index bits)
   int64_t cstart;  // CG_CSTRIDE int32 per cloud: first sorted position of a cell, then n
   int64_t rank;    // int32 per point: rank within its cell (sort scratch)
@@ -247,21 +249,140 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
                    cg_axis_cell(z, glo[2], gs[2]));
   };
   uint32_t rk[R], hx[R];  // PPT > 0: rank within the cell, histogram slot of the cell
-  for (int i = 0; i < iters; ++i) {
-    const int k = tid + 1024 * i;
-    if (k >= n) break;
-    float x, y, z;
-    point(i, k, x, y, z);
-    const int h = cg_hidx(code_of(x, y, z));
-    const uint32_t r = atomicAdd(&cnt[h], 1u);
-    if constexpr (PPT > 0) {
-      rk[i] = r;
-      hx[i] = (uint32_t)h;
-    } else {
-      rank[k] = (int32_t)r;
+  auto histogram = [&]() {
+    for (int i = 0; i < iters; ++i) {
+      const int k = tid + 1024 * i;
+      if (k >= n) break;
+      float x, y, z;
+      point(i, k, x, y, z);
+      const int h = cg_hidx(code_of(x, y, z));
+      const uint32_t r = atomicAdd(&cnt[h], 1u);
+      if constexpr (PPT > 0) {
+        rk[i] = r;
+        hx[i] = (uint32_t)h;
+      } else {
+        rank[k] = (int32_t)r;
+      }
     }
+    __syncthreads();
+  };
+  // sum over points of their cell's count (= sum over cells of count^2),
+  // reduced in a fixed order: every thread gets the same value
+  auto own_occupancy = [&]() {
+    float o = 0.f;
+    for (int i = 0; i < iters; ++i) {
+      const int k = tid + 1024 * i;
+      if (k >= n) break;
+      uint32_t h;
+      if constexpr (PPT > 0) {
+        h = hx[i];
+      } else {
+        float x, y, z;
+        point(i, k, x, y, z);
+        h = (uint32_t)cg_hidx(code_of(x, y, z));
+      }
+      o += (float)cnt[h];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) o += __shfl_xor(o, m);
+    if (lane == 0) red[0][w] = o;
+    __syncthreads();
+    float t = 0.f;
+    for (int v = 0; v < 16; ++v) t += red[0][v];
+    __syncthreads();
+    return t;
+  };
+  histogram();
+  // A degenerate grid (a point's own cell holds more than max(256, n / 32)
+  // points on average) usually comes from a few far points stretching the
+  // box.  Per axis, the sparse tails (bins of the 32 that together hold at
+  // most n / 1024 points, walked in from each end) are cut off: the box
+  // becomes the extent of the remaining points, the cut points fall into the
+  // boundary cells (cell assignment clamps), and those boundary cells are
+  // unbounded on the cut side for the search's pruning (header word 15).
+  const float occ_lim = (float)max(256, n / 32) * (float)n;
+  uint32_t trim = 0;  // bit a: axis a cut below; bit 3 + a: cut above
+  if (own_occupancy() > occ_lim) {
+    for (int k = tid; k < 96; k += 1024) cnt[k] = 0u;
+    __syncthreads();
+    for (int i = 0; i < iters; ++i) {
+      const int k = tid + 1024 * i;
+      if (k >= n) break;
+      float v[3];
+      point(i, k, v[0], v[1], v[2]);
+#pragma unroll
+      for (int a = 0; a < 3; ++a) atomicAdd(&cnt[32 * a + cg_axis_cell(v[a], glo[a], gs[a])], 1u);
+    }
+    __syncthreads();
+    int blo[3], bhi[3];
+    const uint32_t thr = (uint32_t)n >> 10;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {  // every thread reads the same 32 counts
+      uint32_t cum = 0;
+      int lb = 0;
+      while (lb < CG_GRID - 1 && cum + cnt[32 * a + lb] <= thr) cum += cnt[32 * a + lb++];
+      cum = 0;
+      int ub = CG_GRID - 1;
+      while (ub > lb && cum + cnt[32 * a + ub] <= thr) cum += cnt[32 * a + ub--];
+      blo[a] = gs[a] > 0.f ? lb : 0;
+      bhi[a] = gs[a] > 0.f ? ub : CG_GRID - 1;
+    }
+    // extent of the points inside the kept bins, per axis
+    float tl[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
+    float th[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+    for (int i = 0; i < iters; ++i) {
+      const int k = tid + 1024 * i;
+      if (k >= n) break;
+      float v[3];
+      point(i, k, v[0], v[1], v[2]);
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        const int cb = cg_axis_cell(v[a], glo[a], gs[a]);
+        if (cb >= blo[a] && cb <= bhi[a]) {
+          tl[a] = fminf(tl[a], v[a]);
+          th[a] = fmaxf(th[a], v[a]);
+        }
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        tl[a] = fminf(tl[a], __shfl_xor(tl[a], m));
+        th[a] = fmaxf(th[a], __shfl_xor(th[a], m));
+      }
+    __syncthreads();
+    if (lane == 0)
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        red[a][w] = tl[a];
+        red[3 + a][w] = th[a];
+      }
+    __syncthreads();
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      float x = __builtin_inff(), z = -__builtin_inff();
+      for (int v = 0; v < 16; ++v) {
+        x = fminf(x, red[a][v]);
+        z = fmaxf(z, red[3 + a][v]);
+      }
+      if (gs[a] > 0.f && is_finite(x) && is_finite(z)) {
+        if (x > glo[a]) trim |= 1u << a;
+        if (z < ghi[a]) trim |= 8u << a;
+        glo[a] = x;
+        ghi[a] = z;
+        const float ext = z - x;
+        gs[a] = (ext > 0.f && is_finite(ext)) ? (float)CG_GRID / ext : 0.f;
+      }
+    }
+    __syncthreads();
+    // rebuild the cell histogram (on the new box; its first counters held
+    // the bins above either way)
+    for (int k = tid; k < (CG_CELLS + CG_CELLS / 32) / 4; k += 1024)
+      reinterpret_cast<uint4*>(cnt)[k] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    histogram();
   }
-  __syncthreads();
   {  // exclusive scan of the cell counts, CPT consecutive cells per thread
     constexpr int CPT = CG_CELLS / 1024;
     uint32_t v[CPT], sum = 0;
@@ -377,8 +498,9 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     }
     const float nn = (float)n;
     const uint32_t level = sq[0] >= CG_OCC * nn ? 0u : (sq[1] >= CG_OCC * nn ? 1u : 2u);
-    hdr[13] = __uint_as_float(n > 0 && sq[0] > (float)max(256, n / 32) * nn ? 1u : 0u);
+    hdr[13] = __uint_as_float(n > 0 && sq[0] > occ_lim ? 1u : 0u);
     hdr[14] = __uint_as_float(level);
+    hdr[15] = __uint_as_float(trim);
   }
 }
 
@@ -465,6 +587,7 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
     // floor((p - lo) * gs / 2^lv) exactly (scaling by a power of two
     // commutes with rounding), so the two views agree
     const int lv = (int)__float_as_uint(h[14]);
+    const uint32_t cut = __float_as_uint(h[15]);
     const int G = CG_GRID >> lv, sh = 3 * lv;
     float glo[3], ghi[3], gs[3], cs[3], eps[3];
     const float qv[3] = {q.x, q.y, q.z};
@@ -479,6 +602,17 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
       ci[a] = gs[a] > 0.f ? cg_axis_cell(qv[a], glo[a], gs[a], G) : 0;
       eps[a] = 0x1p-20f * (__builtin_fabsf(glo[a]) + (ghi[a] - glo[a])) + 0x1p-126f;
     }
+    // distance from the query to cell c's slab along axis a (a lower bound,
+    // widened by the margins); the first / last cell is unbounded on a cut side
+    auto axis_gap = [&](int a, int c) {
+      const float clo = (cut >> a) & 1u && c == 0
+                            ? -__builtin_inff()
+                            : (ga[a] > 1 ? glo[a] + (float)c * cs[a] : glo[a]) - eps[a];
+      const float chi = (cut >> (3 + a)) & 1u && c == ga[a] - 1
+                            ? __builtin_inff()
+                            : (ga[a] > 1 ? glo[a] + (float)(c + 1) * cs[a] : ghi[a]) + eps[a];
+      return fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
+    };
     // best (distance, index) as one key: distances here are finite and >= 0,
     // so their bits order like the values, and the index breaks ties
     unsigned long long bkey = kInit;
@@ -509,11 +643,7 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
       const int cc[3] = {cx, cy, cz};
       float gap[3];
 #pragma unroll
-      for (int a = 0; a < 3; ++a) {
-        const float clo = (ga[a] > 1 ? glo[a] + (float)cc[a] * cs[a] : glo[a]) - eps[a];
-        const float chi = (ga[a] > 1 ? glo[a] + (float)(cc[a] + 1) * cs[a] : ghi[a]) + eps[a];
-        gap[a] = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
-      }
+      for (int a = 0; a < 3; ++a) gap[a] = axis_gap(a, cc[a]);
       if (sq3(gap[0], gap[1], gap[2]) * Mg::lb - Mg::abs > bdist()) return;
       scan_cell(cg_code(cx, cy, cz));
     };
@@ -587,9 +717,7 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
     far = far || cells > cg_box_max(nr);
     if (!far) {
       auto gap2 = [&](int a, int c) {
-        const float clo = (ga[a] > 1 ? glo[a] + (float)c * cs[a] : glo[a]) - eps[a];
-        const float chi = (ga[a] > 1 ? glo[a] + (float)(c + 1) * cs[a] : ghi[a]) + eps[a];
-        const float g = fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
+        const float g = axis_gap(a, c);
         return g * g;
       };
       for (int cz = blo[2]; cz <= bhi[2]; ++cz) {
