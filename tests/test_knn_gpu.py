@@ -78,6 +78,59 @@ def test_quantised_ties_bit_exact(tpo, O, dev):
         assert_same(np_(d), ed)
 
 
+# ---- high-D float with the references sliced over workgroups (few query
+# workgroups, long reference clouds): local MinK candidates + exact replay
+
+def _hd_inputs(case, g, D):
+    N, P1, P2 = 2, 300, 20000
+    if case == "lattice":  # integer coordinates: many exactly equal distances
+        p1 = torch.randint(0, 3, (N, P1, D), generator=g).float()
+        p2 = torch.randint(0, 3, (N, P2, D), generator=g).float()
+    else:
+        p1 = torch.randn(N, P1, D, generator=g)
+        p2 = torch.randn(N, P2, D, generator=g)
+    if case == "descending":  # every reference closer than all before it: lists overflow
+        r = p2.norm(dim=-1)
+        p2 = torch.gather(p2, 1, r.argsort(dim=1, descending=True)[..., None].expand(-1, -1, D))
+        p1 = p1 * 1e-3
+    l1 = torch.tensor([P1, 211])
+    l2 = torch.tensor([P2, 9000]) if case != "short" else torch.tensor([P2, 20])
+    return p1, p2, l1, l2
+
+
+@pytest.mark.parametrize("case", ["random", "lattice", "descending", "short"])
+@pytest.mark.parametrize("D,K,norm", [(128, 32, 2), (128, 9, 1), (64, 16, 2)])
+def test_high_d_sliced_forward_bit_exact(tpo, O, dev, case, D, K, norm):
+    g = torch.Generator().manual_seed(D + K + norm + len(case))
+    p1, p2, l1, l2 = _hd_inputs(case, g, D)
+    print(f"high-D sliced case={case} D={D} K={K} norm={norm}", flush=True)
+    idx, d = raw(p1, p2, l1, l2, norm, K, -1, dev)
+    ei, ed = O.knn_fwd(np_(p1), np_(p2), np_(l1), np_(l2), norm=norm, K=K)
+    assert_same(np_(idx), ei)
+    assert_same(np_(d), ed)
+    a, b, la, lb = p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev)
+    si, sd = tpo.knn_points(a, b, la, lb, norm=norm, K=K)
+    wi, wd = _module_sort(torch.from_numpy(ei).to(dev), torch.from_numpy(ed).to(dev), lb, K)
+    assert torch.equal(si, wi) and torch.equal(sd, wd)
+
+
+def test_high_d_config5_shape_float_rows_vs_oracle(tpo, O, dev):
+    """Config 5's shape widened to float32 (B=4, 4096 x 65536, D=128, K=32):
+    the full forward on the GPU; 64 query rows of every cloud against the
+    oracle (each row depends only on its query and the reference cloud)."""
+    q, r = workloads.knn_c5()
+    a, b = q.float(), r.float()
+    B, P1, _ = a.shape
+    P2 = b.shape[1]
+    la = torch.full((B,), P1)
+    lb = torch.full((B,), P2)
+    idx, d = raw(a, b, la, lb, 2, 32, -1, dev)
+    rows = torch.tensor([0, 1, 777, 2048, 4095] + list(range(1000, 1059)))
+    ei, ed = O.knn_fwd(np_(a[:, rows]), np_(b), np.full(B, len(rows)), np_(lb), norm=2, K=32)
+    assert_same(np_(idx[:, rows]), ei)
+    assert_same(np_(d[:, rows]), ed)
+
+
 def _long_cloud_inputs(case, g):
     # long reference clouds (the staged float D=3 sweep over 5000 references,
     # lengths2 ragged, a cloud with a single query row)

@@ -503,6 +503,257 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
   }
 }
 
+// ------------------------------------------ high-D float, references sliced
+// A long reference cloud and few queries (config 5's shape in float: 16384
+// queries, 65536 references of 128 dimensions) leave most of the GPU idle
+// with one lane per query.  The references [K, lengths2) are cut into S
+// slices, and a workgroup per (cloud, 256 queries, slice) runs its own MinK
+// seeded with the K fill references (0 .. K-1) over its slice only.  That
+// local MinK keeps the K smallest values of a subset of every prefix the
+// real process has seen, so its threshold is never below the real one: every
+// reference the real process inserts is inserted locally too, and the local
+// insertions (distance, index) of a slice are a superset of the real ones.
+// The merge replays MinK over the fill and the slices' candidates in index
+// order; a candidate that is no real insertion fails the replay's test (the
+// replay's state equals the real state at every real insertion), so the
+// slot layout and values are the single sequential pass's, bit for bit.  A
+// slice with more than HD_CAP candidates is recomputed by the merge.
+constexpr int HD_CAP = 256;  // candidates kept per (query, slice)
+constexpr int HD_J = 4;      // references per step (independent FMA chains)
+
+struct HdLayout {
+  int64_t cnt, dist, idx, total;
+};
+HdLayout hd_layout(int64_t rows, int64_t S) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  HdLayout L;
+  L.cnt = 0;
+  L.dist = up(rows * S * 4);
+  L.idx = L.dist + up(rows * S * HD_CAP * 4);
+  L.total = L.idx + up(rows * S * HD_CAP * 4);
+  return L;
+}
+
+template <int DT, int NORM, int KC>
+__global__ __launch_bounds__(256) void knn_hd_slice_kernel(
+    const float* __restrict__ p1, const float* __restrict__ p2, const int64_t* __restrict__ len1,
+    const int64_t* __restrict__ len2, int P1, int P2, int K, int nqb, int S, int slen,
+    int32_t* __restrict__ cnt, float* __restrict__ cd, int32_t* __restrict__ ci) {
+  const int sl = blockIdx.x % S;
+  const int nb = blockIdx.x / S;
+  const int n = nb / nqb;
+  const int q = (nb - n * nqb) * 256 + threadIdx.x;
+  if (q >= P1) return;
+  int64_t l1 = len1[n], l2 = len2[n];
+  l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+  l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
+  const int L2 = (int)l2;
+  const size_t row = (size_t)n * P1 + q;
+  const size_t cs = row * S + sl;
+  const int a = K + sl * slen, b = min(L2, a + slen);
+  if (q >= l1 || a >= b) {
+    cnt[cs] = 0;
+    return;
+  }
+  const float* __restrict__ qp = p1 + row * DT;
+  const float* __restrict__ rp = p2 + (size_t)n * P2 * DT;
+  float qr[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) qr[d] = qp[d];
+  float sd[KC];
+#pragma unroll
+  for (int t = 0; t < KC; ++t)
+    sd[t] = t < K ? knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)t * DT, DT) : Lim<float>::inf();
+  float thr;
+  int ms;
+  first_max<float, KC>(sd, K, thr, ms);
+  int count = 0;
+  float* __restrict__ cdp = cd + cs * HD_CAP;
+  int32_t* __restrict__ cip = ci + cs * HD_CAP;
+  auto consider = [&](float d, int j) {
+    if (d < thr) {
+      if (count < HD_CAP) {
+        cdp[count] = d;
+        cip[count] = j;
+      }
+      ++count;
+#pragma unroll
+      for (int t = 0; t < KC; ++t)
+        if (t == ms) sd[t] = d;
+      first_max<float, KC>(sd, K, thr, ms);
+    }
+  };
+  int j = a;
+  for (; j + HD_J <= b; j += HD_J) {
+    float d[HD_J];
+#pragma unroll
+    for (int u = 0; u < HD_J; ++u) d[u] = knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)(j + u) * DT, DT);
+#pragma unroll
+    for (int u = 0; u < HD_J; ++u) consider(d[u], j + u);
+  }
+  for (; j < b; ++j) consider(knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)j * DT, DT), j);
+  cnt[cs] = count;
+}
+
+template <int DT, int NORM, int KC, bool SORT>
+__global__ __launch_bounds__(256) void knn_hd_merge_kernel(
+    const float* __restrict__ p1, const float* __restrict__ p2, const int64_t* __restrict__ len1,
+    const int64_t* __restrict__ len2, int N, int P1, int P2, int K, int S, int slen, int pad_sentinel,
+    const int32_t* __restrict__ cnt, const float* __restrict__ cd,
+    const int32_t* __restrict__ ci, int64_t* __restrict__ idxs, float* __restrict__ dists) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)N * P1) return;
+  const int n = (int)(t / P1), q = (int)(t - (int64_t)n * P1);
+  int64_t l1 = len1[n], l2 = len2[n];
+  l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+  l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
+  const int L2 = (int)l2;
+  const size_t row = (size_t)t;
+  int64_t* __restrict__ io = idxs + row * K;
+  float* __restrict__ dout = dists + row * K;
+  if (q >= l1) {  // never written by the reference: its zeros
+    for (int s = 0; s < K; ++s) {
+      io[s] = 0;
+      dout[s] = 0.f;
+    }
+    return;
+  }
+  const float* __restrict__ qp = p1 + row * DT;
+  const float* __restrict__ rp = p2 + (size_t)n * P2 * DT;
+  float qr[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) qr[d] = qp[d];
+  float sd[KC];
+  int si[KC];
+  const int fill = L2 < K ? L2 : K;
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    if (s < fill) {
+      sd[s] = knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)s * DT, DT);
+      si[s] = s;
+    } else {
+      sd[s] = Lim<float>::inf();
+      si[s] = -1;
+    }
+  }
+  const int size = fill;
+  if (L2 > K) {
+    float thr;
+    int ms;
+    first_max<float, KC>(sd, K, thr, ms);
+    auto replay = [&](float d, int j) {
+      if (d < thr) {
+#pragma unroll
+        for (int s = 0; s < KC; ++s) {
+          if (s == ms) {
+            sd[s] = d;
+            si[s] = j;
+          }
+        }
+        first_max<float, KC>(sd, K, thr, ms);
+      }
+    };
+    for (int sl = 0; sl < S; ++sl) {
+      const int a = K + sl * slen, b = min(L2, a + slen);
+      if (a >= b) break;
+      const int c = cnt[row * S + sl];
+      if (c <= HD_CAP) {
+        const float* __restrict__ cdp = cd + (row * S + sl) * HD_CAP;
+        const int32_t* __restrict__ cip = ci + (row * S + sl) * HD_CAP;
+        for (int k = 0; k < c; ++k) replay(cdp[k], cip[k]);
+      } else {  // the slice's list overflowed: recompute it in order
+        for (int j = a; j < b; ++j) replay(knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)j * DT, DT), j);
+      }
+    }
+  }
+  const int64_t pad_i = pad_sentinel ? -1 : 0;
+  const float pad_d = pad_sentinel ? Lim<float>::inf() : 0.f;
+  if constexpr (SORT) {
+#pragma unroll
+    for (int s = 0; s < KC; ++s) {
+      if (s >= size) {
+        sd[s] = Lim<float>::inf();
+        si[s] = (int)pad_i;
+      }
+    }
+    knn_sort_row<float, KC>(sd, si, K >= 32 ? 0xffffffffu : (1u << K) - 1u);
+#pragma unroll
+    for (int s = 0; s < KC; ++s) {
+      if (s < K) {
+        io[s] = (int64_t)si[s];
+        dout[s] = s < size ? sd[s] : 0.f;
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    if (s < K) {
+      io[s] = s < size ? (int64_t)si[s] : pad_i;
+      dout[s] = s < size ? sd[s] : pad_d;
+    }
+  }
+}
+
+// S slices for the sliced high-D path, or 0 when it does not apply: float,
+// D 64 or 128, 2 <= K <= 32, too few query workgroups to fill the GPU, and
+// slices of at least 1024 references.
+int hd_slices(int dtype, int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K) {
+  if (dtype != TPO_F32 || (D != 64 && D != 128) || K < 2 || K > 32) return 0;
+  const int64_t wgs = N * ((P1 + 255) / 256);
+  if (wgs <= 0 || wgs >= 256) return 0;
+  int64_t S = 512 / wgs;
+  S = S < 16 ? S : 16;
+  const int64_t smax = (P2 - K) / 1024;
+  S = S < smax ? S : smax;
+  return S >= 2 ? (int)S : 0;
+}
+
+template <int DT, int NORM, int KC>
+void launch_hd_kc(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
+                  int P1, int P2, int K, int S, int pad, bool sort, int64_t* idxs, void* dists,
+                  void* ws, hipStream_t s) {
+  const int nqb = (P1 + 255) / 256;
+  const int slen = (P2 - K + S - 1) / S;
+  const HdLayout L = hd_layout((int64_t)N * P1, S);
+  int32_t* cnt = (int32_t*)((char*)ws + L.cnt);
+  float* cd = (float*)((char*)ws + L.dist);
+  int32_t* ci = (int32_t*)((char*)ws + L.idx);
+  hipLaunchKernelGGL((knn_hd_slice_kernel<DT, NORM, KC>), dim3(N * nqb * S), dim3(256), 0, s,
+                     (const float*)p1, (const float*)p2, l1, l2, P1, P2, K, nqb, S, slen, cnt, cd,
+                     ci);
+  const unsigned mg = (unsigned)(((int64_t)N * P1 + 255) / 256);
+  if (sort)
+    hipLaunchKernelGGL((knn_hd_merge_kernel<DT, NORM, KC, true>), dim3(mg), dim3(256), 0, s,
+                       (const float*)p1, (const float*)p2, l1, l2, N, P1, P2, K, S, slen, pad, cnt,
+                       cd, ci, idxs, (float*)dists);
+  else
+    hipLaunchKernelGGL((knn_hd_merge_kernel<DT, NORM, KC, false>), dim3(mg), dim3(256), 0, s,
+                       (const float*)p1, (const float*)p2, l1, l2, N, P1, P2, K, S, slen, pad, cnt,
+                       cd, ci, idxs, (float*)dists);
+}
+
+template <int DT, int NORM>
+void launch_hd_norm(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
+                    int P1, int P2, int K, int S, int pad, bool sort, int64_t* idxs, void* dists,
+                    void* ws, hipStream_t s) {
+  if (K <= 8) launch_hd_kc<DT, NORM, 8>(p1, p2, l1, l2, N, P1, P2, K, S, pad, sort, idxs, dists, ws, s);
+  else if (K <= 16) launch_hd_kc<DT, NORM, 16>(p1, p2, l1, l2, N, P1, P2, K, S, pad, sort, idxs, dists, ws, s);
+  else launch_hd_kc<DT, NORM, 32>(p1, p2, l1, l2, N, P1, P2, K, S, pad, sort, idxs, dists, ws, s);
+}
+
+void launch_hd(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N, int P1,
+               int P2, int D, int K, int norm, int S, int pad, bool sort, int64_t* idxs,
+               void* dists, void* ws, hipStream_t s) {
+  if (D == 128) {
+    if (norm == 1) launch_hd_norm<128, 1>(p1, p2, l1, l2, N, P1, P2, K, S, pad, sort, idxs, dists, ws, s);
+    else launch_hd_norm<128, 2>(p1, p2, l1, l2, N, P1, P2, K, S, pad, sort, idxs, dists, ws, s);
+  } else {
+    if (norm == 1) launch_hd_norm<64, 1>(p1, p2, l1, l2, N, P1, P2, K, S, pad, sort, idxs, dists, ws, s);
+    else launch_hd_norm<64, 2>(p1, p2, l1, l2, N, P1, P2, K, S, pad, sort, idxs, dists, ws, s);
+  }
+}
+
 // K > 32: MinK held in the output row (the reference's V0/V1 layout).
 template <typename T, int NORM>
 __global__ __launch_bounds__(256) void knn_fwd_global_kernel(
@@ -705,7 +956,10 @@ extern "C" int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int6
                                           int64_t D, int64_t K, int norm) {
   if (N < 0 || P1 < 0 || P2 < 0 || D < 1 || K < 0) return -1;
   if (dtype == TPO_BF16) return knn_bf16_supported(D, K, norm) ? knn_bf16_workspace(N, P1, P2, K) : 0;
-  return ((N * P1 * 4 + 255) / 256) * 256;
+  const int64_t order = ((N * P1 * 4 + 255) / 256) * 256;
+  const int S = hd_slices(dtype, N, P1, P2, D, K);
+  const int64_t hd = S > 0 ? hd_layout(N * P1, S).total : 0;
+  return order > hd ? order : hd;
 }
 
 static int knn_fwd_impl(int dtype, const void* p1, const void* p2, const int64_t* lengths1,
@@ -741,9 +995,17 @@ static int knn_fwd_impl(int dtype, const void* p1, const void* p2, const int64_t
   if (N == 0 || P1 == 0 || K == 0) return TPO_OK;
   const int pad = v <= 1;
   const int sorted2 = (v == 3 && K == 2) | (sort_rows ? 2 : 0);  // the kernel's mode bits
+  hipStream_t s = (hipStream_t)stream;
+  {  // long reference clouds, few queries: references sliced over workgroups
+    const int S = hd_slices(dtype, N, P1, P2, D, K);
+    if (S > 0 && workspace && workspace_bytes >= hd_layout(N * P1, S).total && v <= 1) {
+      launch_hd(p1, p2, lengths1, lengths2, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, S,
+                pad, sort_rows, idxs, dists, workspace, s);
+      return check_launch("tpo_knn_fwd");
+    }
+  }
   // the query ordering is an optimisation: without workspace, keep row order
   int32_t* order = (workspace && workspace_bytes >= N * P1 * 4) ? (int32_t*)workspace : nullptr;
-  hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case TPO_F32: launch_fwd<float>(p1, p2, lengths1, lengths2, order, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
     case TPO_F64: launch_fwd<double>(p1, p2, lengths1, lengths2, order, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
