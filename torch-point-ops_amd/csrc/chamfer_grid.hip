@@ -157,7 +157,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   static_assert(sizeof(cnt) >= 1024 * 8 * sizeof(float4), "staging area");
   __shared__ float red[6][16];
   __shared__ uint32_t part[16];
-  __shared__ uint32_t s_bad;
+  __shared__ uint32_t s_bad, s_maxc;
   __shared__ float s_sq[3][16];  // per wave: sum of count^2 over the cells of 32^3, 16^3, 8^3
   const int c = blockIdx.x & 1, b = blockIdx.x >> 1;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   const int iters = PPT > 0 ? PPT : (n + 1023) / 1024;
 
   // bounding box (NaN ignored) and the bad flag (non-finite or >= 2^60)
-  if (tid == 0) s_bad = 0;
+  if (tid == 0) s_bad = s_maxc = 0;
   float lo[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
   float hi[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
   uint32_t big = 0;
@@ -249,7 +249,10 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
                    cg_axis_cell(z, glo[2], gs[2]));
   };
   uint32_t rk[R], hx[R];  // PPT > 0: rank within the cell, histogram slot of the cell
+  // the cell histogram; every point's rank within its cell, and the largest
+  // cell count (the atomics' returned ranks, maximised)
   auto histogram = [&]() {
+    uint32_t mr = 0;
     for (int i = 0; i < iters; ++i) {
       const int k = tid + 1024 * i;
       if (k >= n) break;
@@ -257,6 +260,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
       point(i, k, x, y, z);
       const int h = cg_hidx(code_of(x, y, z));
       const uint32_t r = atomicAdd(&cnt[h], 1u);
+      mr = max(mr, r + 1);
       if constexpr (PPT > 0) {
         rk[i] = r;
         hx[i] = (uint32_t)h;
@@ -264,45 +268,22 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
         rank[k] = (int32_t)r;
       }
     }
-    __syncthreads();
-  };
-  // sum over points of their cell's count (= sum over cells of count^2),
-  // reduced in a fixed order: every thread gets the same value
-  auto own_occupancy = [&]() {
-    float o = 0.f;
-    for (int i = 0; i < iters; ++i) {
-      const int k = tid + 1024 * i;
-      if (k >= n) break;
-      uint32_t h;
-      if constexpr (PPT > 0) {
-        h = hx[i];
-      } else {
-        float x, y, z;
-        point(i, k, x, y, z);
-        h = (uint32_t)cg_hidx(code_of(x, y, z));
-      }
-      o += (float)cnt[h];
-    }
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) o += __shfl_xor(o, m);
-    if (lane == 0) red[0][w] = o;
+    for (int m = 32; m >= 1; m >>= 1) mr = max(mr, (uint32_t)__shfl_xor((int)mr, m));
+    if (lane == 0) atomicMax(&s_maxc, mr);
     __syncthreads();
-    float t = 0.f;
-    for (int v = 0; v < 16; ++v) t += red[0][v];
-    __syncthreads();
-    return t;
   };
   histogram();
-  // A degenerate grid (a point's own cell holds more than max(256, n / 32)
-  // points on average) usually comes from a few far points stretching the
-  // box.  Per axis, the sparse tails (bins of the 32 that together hold at
-  // most n / 1024 points, walked in from each end) are cut off: the box
+  // A degenerate grid (a cell of more than max(256, n / 32) points) usually
+  // comes from a few far points stretching the box.  Per axis, the sparse
+  // tails (bins of the 32 that together hold at most n / 1024 points,
+  // walked in from each end) are cut off: the box
   // becomes the extent of the remaining points, the cut points fall into the
   // boundary cells (cell assignment clamps), and those boundary cells are
   // unbounded on the cut side for the search's pruning (header word 15).
   const float occ_lim = (float)max(256, n / 32) * (float)n;
   uint32_t trim = 0;  // bit a: axis a cut below; bit 3 + a: cut above
-  if (own_occupancy() > occ_lim) {
+  if (s_maxc > (uint32_t)max(256, n / 32)) {
     for (int k = tid; k < 96; k += 1024) cnt[k] = 0u;
     __syncthreads();
     for (int i = 0; i < iters; ++i) {
