@@ -26,6 +26,8 @@
 //   One thread per query row sums its K contributions to grad_p1 in
 //   registers (plain stores, every row written) and scatters -diff onto
 //   grad_p2 with hardware atomics (grad_p2 zero-filled first).
+#include <utility>
+
 #include "tpo_common.hpp"
 
 namespace tpo {
@@ -518,8 +520,47 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
 // replay's state equals the real state at every real insertion), so the
 // slot layout and values are the single sequential pass's, bit for bit.  A
 // slice with more than HD_CAP candidates is recomputed by the merge.
+//
+// Reference points reach the lanes through DPP: each 16-lane row of the wave
+// loads the same reference row with ordinary vector loads (lane k of a row:
+// dimensions 64g + 4k .. + 3), issued HD_J references ahead, and
+// dimension 64g + 4k + e enters the subtraction as VGPR (g, e) of lane k
+// broadcast over its row (row_newbcast:k, folded into v_sub_f32_dpp), so a
+// dimension costs one subtraction and one FMA and nothing waits on scalar
+// loads.  Every lane of a wave that has a query takes part (lanes past
+// lengths1 or P1 compute on zeros and never insert).  Candidates are found
+// per chunk of 32 references: the chunk's distances go to LDS and into a mask
+// against the lane's threshold; each lane then walks its own candidates in
+// order against the updated threshold, so the wave pays the O(K) slot update
+// max-over-lanes(candidates per chunk) times.
 constexpr int HD_CAP = 256;  // candidates kept per (query, slice)
-constexpr int HD_J = 4;      // references per step (independent FMA chains)
+constexpr int HD_J = 4;      // references per load step
+
+// lane L of each 16-lane row, broadcast over the row (gfx950 DPP row_newbcast)
+template <int L>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x150 + L, 0xF, 0xF, false));
+}
+template <int E>
+__device__ __forceinline__ float f4_at(const float4& v) {
+  if constexpr (E == 0) return v.x;
+  else if constexpr (E == 1) return v.y;
+  else if constexpr (E == 2) return v.z;
+  else return v.w;
+}
+// knn.cu:148-158 over dimensions 0 .. DT-1 in order; dimension d of the
+// reference is lane (d % 64) / 4 of the row, VGPR (d / 64, d % 4)
+template <int NORM, int DT, int... D>
+__device__ __forceinline__ float hd_dist(const float (&qr)[DT], const float4 (&rv)[DT / 64],
+                                         std::integer_sequence<int, D...>) {
+  float acc = 0.f;
+  ((acc = NORM == 2
+              ? knn_acc2(acc, qr[D] - row_bcast<(D % 64) / 4>(f4_at<D % 4>(rv[D / 64])), D == 0)
+              : knn_acc1(acc, qr[D] - row_bcast<(D % 64) / 4>(f4_at<D % 4>(rv[D / 64])), D == 0)),
+   ...);
+  return acc;
+}
 
 struct HdLayout {
   int64_t cnt, dist, idx, total;
@@ -539,60 +580,102 @@ __global__ __launch_bounds__(256) void knn_hd_slice_kernel(
     const float* __restrict__ p1, const float* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, int P1, int P2, int K, int nqb, int S, int slen,
     int32_t* __restrict__ cnt, float* __restrict__ cd, int32_t* __restrict__ ci) {
+  constexpr int G = DT / 64;
+  __shared__ float s_d[4][32][64];
   const int sl = blockIdx.x % S;
   const int nb = blockIdx.x / S;
   const int n = nb / nqb;
-  const int q = (nb - n * nqb) * 256 + threadIdx.x;
-  if (q >= P1) return;
+  const int w = wave_id(), lane = lane_id();
+  const int qw = (nb - n * nqb) * 256 + 64 * w;
+  if (qw >= P1) return;  // the whole wave
+  const int q = qw + lane;
   int64_t l1 = len1[n], l2 = len2[n];
   l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
   l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
   const int L2 = (int)l2;
-  const size_t row = (size_t)n * P1 + q;
+  const bool act = q < l1;  // l1 <= P1
+  const size_t row = (size_t)n * P1 + min(q, P1 - 1);
   const size_t cs = row * S + sl;
   const int a = K + sl * slen, b = min(L2, a + slen);
-  if (q >= l1 || a >= b) {
-    cnt[cs] = 0;
+  if (a >= b) {
+    if (q < P1) cnt[cs] = 0;
     return;
   }
-  const float* __restrict__ qp = p1 + row * DT;
-  const float* __restrict__ rp = p2 + (size_t)n * P2 * DT;
+  const float* __restrict__ rp = p2 + (size_t)n * P2 * DT + 4 * (lane & 15);
   float qr[DT];
+  {
+    const float4* __restrict__ qp = reinterpret_cast<const float4*>(p1 + row * DT);
 #pragma unroll
-  for (int d = 0; d < DT; ++d) qr[d] = qp[d];
+    for (int d = 0; d < DT / 4; ++d) {
+      const float4 v = act ? qp[d] : make_float4(0.f, 0.f, 0.f, 0.f);
+      qr[4 * d] = v.x;
+      qr[4 * d + 1] = v.y;
+      qr[4 * d + 2] = v.z;
+      qr[4 * d + 3] = v.w;
+    }
+  }
+  auto load_ref = [&](float4 (&rv)[G], int j) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) rv[g] = *reinterpret_cast<const float4*>(rp + (size_t)j * DT + 64 * g);
+  };
+  constexpr auto dims = std::make_integer_sequence<int, DT>{};
+  // the fill: references 0 .. K-1 (K < L2 here)
   float sd[KC];
 #pragma unroll
-  for (int t = 0; t < KC; ++t)
-    sd[t] = t < K ? knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)t * DT, DT) : Lim<float>::inf();
+  for (int t = 0; t < KC; ++t) {
+    if (t < K) {
+      float4 rv[G];
+      load_ref(rv, t);
+      sd[t] = hd_dist<NORM>(qr, rv, dims);
+    } else {
+      sd[t] = Lim<float>::inf();
+    }
+  }
   float thr;
   int ms;
   first_max<float, KC>(sd, K, thr, ms);
+  if (!act) thr = -Lim<float>::inf();  // no candidates
   int count = 0;
   float* __restrict__ cdp = cd + cs * HD_CAP;
   int32_t* __restrict__ cip = ci + cs * HD_CAP;
-  auto consider = [&](float d, int j) {
-    if (d < thr) {
-      if (count < HD_CAP) {
-        cdp[count] = d;
-        cip[count] = j;
+
+  // a ring of HD_J references in flight: buffer u holds reference
+  // j = u (mod HD_J) and is reloaded with j + HD_J once its distance is taken
+  float4 rb[HD_J][G];
+#pragma unroll
+  for (int u = 0; u < HD_J; ++u) load_ref(rb[u], min(a + u, b - 1));
+  for (int base = a; base < b; base += 32) {
+    uint32_t mask = 0;
+    for (int u0 = 0; u0 < 32; u0 += HD_J) {
+#pragma unroll
+      for (int u = 0; u < HD_J; ++u) {
+        float d = hd_dist<NORM>(qr, rb[u], dims);
+        // the next reference for this buffer (clamped into the slice)
+        load_ref(rb[u], min(base + u0 + HD_J + u, b - 1));
+        d = base + u0 + u < b ? d : Lim<float>::inf();
+        s_d[w][u0 + u][lane] = d;
+        mask |= (d < thr ? 1u : 0u) << (u0 + u);
       }
-      ++count;
-#pragma unroll
-      for (int t = 0; t < KC; ++t)
-        if (t == ms) sd[t] = d;
-      first_max<float, KC>(sd, K, thr, ms);
     }
-  };
-  int j = a;
-  for (; j + HD_J <= b; j += HD_J) {
-    float d[HD_J];
+    // this lane's candidates in index order, against the current threshold
+    while (mask != 0) {
+      const int u = __builtin_ctz(mask);
+      mask &= mask - 1;
+      const float d = s_d[w][u][lane];
+      if (d < thr) {
+        if (count < HD_CAP) {
+          cdp[count] = d;
+          cip[count] = base + u;
+        }
+        ++count;
 #pragma unroll
-    for (int u = 0; u < HD_J; ++u) d[u] = knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)(j + u) * DT, DT);
-#pragma unroll
-    for (int u = 0; u < HD_J; ++u) consider(d[u], j + u);
+        for (int t = 0; t < KC; ++t)
+          if (t == ms) sd[t] = d;
+        first_max<float, KC>(sd, K, thr, ms);
+      }
+    }
   }
-  for (; j < b; ++j) consider(knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)j * DT, DT), j);
-  cnt[cs] = count;
+  if (q < P1) cnt[cs] = act ? count : 0;
 }
 
 template <int DT, int NORM, int KC, bool SORT>
