@@ -8,11 +8,6 @@ class EarthMoverDistance(torch.nn.Module):
     """Mean over the batch of the earth mover's distance of two point clouds."""
 
     def forward(self, xyz1, xyz2):
-        """
-        Args:
-            xyz1 (torch.Tensor): (B, N, 3)
-            xyz2 (torch.Tensor): (B, M, 3)
-        Returns:
-            torch.Tensor: () mean EMD distance
-        """
+        # xyz1 is (B, N, 3) and xyz2 is (B, M, 3), of one floating dtype on
+        # one device; the per-cloud distances are averaged to a 0-d tensor
         return earth_movers_distance(xyz1, xyz2).mean()
