@@ -533,7 +533,7 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
 // against the lane's threshold; each lane then walks its own candidates in
 // order against the updated threshold, so the wave pays the O(K) slot update
 // max-over-lanes(candidates per chunk) times.
-constexpr int HD_CAP = 256;  // candidates kept per (query, slice)
+constexpr int HD_CAP = 256;  // candidates kept per (query, slice); a multiple of 16
 constexpr int HD_J = 4;      // references per load step
 
 // lane L of each 16-lane row, broadcast over the row (gfx950 DPP row_newbcast)
@@ -559,6 +559,21 @@ __device__ __forceinline__ float hd_dist(const float (&qr)[DT], const float4 (&r
               ? knn_acc2(acc, qr[D] - row_bcast<(D % 64) / 4>(f4_at<D % 4>(rv[D / 64])), D == 0)
               : knn_acc1(acc, qr[D] - row_bcast<(D % 64) / 4>(f4_at<D % 4>(rv[D / 64])), D == 0)),
    ...);
+  return acc;
+}
+
+// the same distance with both points read from memory (float4 steps)
+template <int NORM, int DT>
+__device__ __forceinline__ float hd_dist_mem(const float4* __restrict__ q, const float4* __restrict__ r) {
+  float acc = 0.f;
+#pragma unroll 4
+  for (int v = 0; v < DT / 4; ++v) {
+    const float4 a = q[v], b = r[v];
+    const float x[4] = {a.x - b.x, a.y - b.y, a.z - b.z, a.w - b.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      acc = NORM == 2 ? knn_acc2(acc, x[e], v == 0 && e == 0) : knn_acc1(acc, x[e], v == 0 && e == 0);
+  }
   return acc;
 }
 
@@ -701,18 +716,18 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
     }
     return;
   }
-  const float* __restrict__ qp = p1 + row * DT;
+  // the query stays in memory (a register copy would be live through the
+  // whole replay): distances here are the fill's and an overflowed slice's
+  const float4* __restrict__ qp = reinterpret_cast<const float4*>(p1 + row * DT);
   const float* __restrict__ rp = p2 + (size_t)n * P2 * DT;
-  float qr[DT];
-#pragma unroll
-  for (int d = 0; d < DT; ++d) qr[d] = qp[d];
+  auto dist = [&](int j) { return hd_dist_mem<NORM, DT>(qp, reinterpret_cast<const float4*>(rp + (size_t)j * DT)); };
   float sd[KC];
   int si[KC];
   const int fill = L2 < K ? L2 : K;
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
     if (s < fill) {
-      sd[s] = knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)s * DT, DT);
+      sd[s] = dist(s);
       si[s] = s;
     } else {
       sd[s] = Lim<float>::inf();
@@ -741,11 +756,40 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
       if (a >= b) break;
       const int c = cnt[row * S + sl];
       if (c <= HD_CAP) {
-        const float* __restrict__ cdp = cd + (row * S + sl) * HD_CAP;
-        const int32_t* __restrict__ cip = ci + (row * S + sl) * HD_CAP;
-        for (int k = 0; k < c; ++k) replay(cdp[k], cip[k]);
+        // 16 candidates a step, loaded together (the list holds HD_CAP
+        // entries, a multiple of 16, so a step never reads past it); the
+        // step's mask against the threshold at its start is a superset of
+        // its insertions, each re-checked against the current threshold
+        const float4* __restrict__ cdp = reinterpret_cast<const float4*>(cd + (row * S + sl) * HD_CAP);
+        const int4* __restrict__ cip = reinterpret_cast<const int4*>(ci + (row * S + sl) * HD_CAP);
+        for (int k0 = 0; k0 < c; k0 += 16) {
+          float dv[16];
+          int iv[16];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float4 d4 = cdp[k0 / 4 + v];
+            const int4 i4 = cip[k0 / 4 + v];
+            dv[4 * v] = d4.x, dv[4 * v + 1] = d4.y, dv[4 * v + 2] = d4.z, dv[4 * v + 3] = d4.w;
+            iv[4 * v] = i4.x, iv[4 * v + 1] = i4.y, iv[4 * v + 2] = i4.z, iv[4 * v + 3] = i4.w;
+          }
+          uint32_t m = 0;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) m |= (k0 + e < c && dv[e] < thr ? 1u : 0u) << e;
+          while (m != 0) {
+            const int e = __builtin_ctz(m);
+            m &= m - 1;
+            float d = dv[0];
+            int j = iv[0];
+#pragma unroll
+            for (int x = 1; x < 16; ++x) {
+              d = x == e ? dv[x] : d;
+              j = x == e ? iv[x] : j;
+            }
+            replay(d, j);
+          }
+        }
       } else {  // the slice's list overflowed: recompute it in order
-        for (int j = a; j < b; ++j) replay(knn_dist<float, DT, NORM>(qr, qp, rp + (size_t)j * DT, DT), j);
+        for (int j = a; j < b; ++j) replay(dist(j), j);
       }
     }
   }
