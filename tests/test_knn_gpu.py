@@ -169,6 +169,65 @@ def test_long_clouds_forward_bit_exact(tpo, O, dev, case, K, norm, version):
     assert_same(np_(d), ed)
 
 
+def _grid_inputs(case, g):
+    # float 3-D against clouds of 6000 references: the brute-force prefix
+    # plus grid-candidate path (lengths2 ragged around the prefix length)
+    N, P1, P2 = 4, 700, 6000
+    if case == "sphere":  # config 3's distribution
+        def sph(n):
+            v = torch.randn(N, n, 3, generator=g)
+            v = v / v.norm(dim=-1, keepdim=True)
+            return v * (1 + 0.02 * torch.randn(N, n, 1, generator=g))
+        p1, p2 = sph(P1), sph(P2)
+    elif case == "clusters":  # tight blobs: small, crowded boxes
+        cen = torch.rand(N, 6, 3, generator=g) * 2 - 1
+        pick = lambda n: cen[torch.arange(N)[:, None], torch.randint(0, 6, (N, n), generator=g)]
+        p1 = pick(P1) + 0.01 * torch.randn(N, P1, 3, generator=g)
+        p2 = pick(P2) + 0.01 * torch.randn(N, P2, 3, generator=g)
+    elif case == "outlier":  # one far reference stretches the grid
+        p1 = torch.rand(N, P1, 3, generator=g)
+        p2 = torch.rand(N, P2, 3, generator=g)
+        p2[:, 4000] = 1e4
+        p2[1, 10] = -1e6
+    elif case == "flat":  # one axis without extent, integer ties
+        p1 = torch.randint(0, 40, (N, P1, 3), generator=g).float() / 8
+        p2 = torch.randint(0, 40, (N, P2, 3), generator=g).float() / 8
+        p1[..., 2] = 0.5
+        p2[..., 2] = 0.5
+    else:  # "nonfinite"
+        p1 = torch.rand(N, P1, 3, generator=g)
+        p2 = torch.rand(N, P2, 3, generator=g)
+        p2[0, 5, 1] = float("nan")  # in the fill
+        p2[0, 3000, 0] = float("inf")
+        p2[1, 100:110, 2] = float("nan")
+        p2[2, 5000, 0] = -float("inf")
+        p1[2, 5, 1] = float("nan")
+        p1[3, 7, 0] = float("inf")
+    l1 = torch.tensor([P1, 650, 1, 333])
+    l2 = torch.tensor([P2, 300, 2100, 5999])
+    return p1, p2, l1, l2
+
+
+@pytest.mark.parametrize("case", ["sphere", "clusters", "outlier", "flat", "nonfinite"])
+@pytest.mark.parametrize("K,norm,version", [(1, 2, -1), (16, 2, -1), (16, 1, 0), (32, 2, 1),
+                                            (7, 2, 3), (2, 2, 2)])
+def test_grid_candidates_forward_bit_exact(tpo, O, dev, case, K, norm, version):
+    g = torch.Generator().manual_seed(K * 17 + norm + 3 * len(case))
+    p1, p2, l1, l2 = _grid_inputs(case, g)
+    print(f"grid case={case} K={K} norm={norm} version={version}", flush=True)
+    idx, d = raw(p1, p2, l1, l2, norm, K, version, dev)
+    ei, ed = O.knn_fwd(np_(p1), np_(p2), np_(l1), np_(l2), norm=norm, K=K, version=version)
+    assert_same(np_(idx), ei)
+    assert_same(np_(d), ed)
+    if K >= 2:  # sorted rows: the in-kernel sort equals the module's sort of the raw rows
+        a, b, la, lb = p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev)
+        si, sd = tpo.knn_points(a, b, la, lb, norm=norm, K=K, version=version)
+        wi, wd = _module_sort(torch.from_numpy(ei).to(dev), torch.from_numpy(ed).to(dev), lb, K)
+        assert torch.equal(si, wi)
+        assert torch.equal(sd.isnan(), wd.isnan())
+        assert torch.equal(torch.nan_to_num(sd), torch.nan_to_num(wd))
+
+
 @pytest.mark.parametrize("case", ["random", "lattice", "nonfinite"])
 @pytest.mark.parametrize("K", [2, 8, 16, 32])
 def test_long_clouds_sorted_rows_match_torch_sort(tpo, dev, case, K):

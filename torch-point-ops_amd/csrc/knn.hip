@@ -28,7 +28,7 @@
 //   grad_p2 with hardware atomics (grad_p2 zero-filled first).
 #include <utility>
 
-#include "tpo_common.hpp"
+#include "knn_common.hpp"
 
 namespace tpo {
 // knn_bf16.hip
@@ -37,6 +37,12 @@ bool knn_bf16_supported(int64_t D, int64_t K, int norm);
 void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
                      int P1, int P2, int D, int K, int64_t* idxs, void* dists, void* ws,
                      hipStream_t s);
+// knn_grid.hip
+bool knn_grid_applies(int dtype, int64_t D, int64_t K, int64_t P2);
+int64_t knn_grid_workspace(int64_t N, int64_t P2);
+void launch_knn_grid(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
+                     int32_t* order, int N, int P1, int P2, int K, int norm, int pad,
+                     bool sort, int64_t* idxs, void* dists, void* ws, hipStream_t s);
 }  // namespace tpo
 
 #pragma clang fp contract(off)
@@ -44,116 +50,11 @@ void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const in
 namespace tpo {
 namespace {
 
-constexpr int KNN_CHUNK = 32;
-
 template <typename T>
 __global__ __launch_bounds__(256) void fill_kernel(T* __restrict__ p, int64_t n, T v) {
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n;
        t += (int64_t)gridDim.x * blockDim.x)
     p[t] = v;
-}
-
-// Distance between the lane's query and reference r (knn.cu:148-158).
-// DT > 0: compile-time dimension, query in registers; DT == 0: runtime D,
-// query read through qp.
-template <typename T, int DT, int NORM>
-__device__ __forceinline__ T knn_dist(const T* qr, const T* __restrict__ qp,
-                                      const T* __restrict__ r, int D) {
-  T acc = (T)0;
-  if constexpr (DT > 0) {
-#pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      const T diff = (T)(qr[d] - r[d]);
-      acc = NORM == 2 ? knn_acc2(acc, diff, d == 0) : knn_acc1(acc, diff, d == 0);
-    }
-  } else {
-    for (int d = 0; d < D; ++d) {
-      const T diff = (T)(qp[d] - r[d]);
-      acc = NORM == 2 ? knn_acc2(acc, diff, d == 0) : knn_acc1(acc, diff, d == 0);
-    }
-  }
-  return acc;
-}
-
-// First slot holding the maximum among slots [0, K) (mink.cuh:96-104).
-template <typename T, int KC>
-__device__ __forceinline__ void first_max(const T (&sd)[KC], int K, T& m, int& ms) {
-  m = sd[0];
-  ms = 0;
-#pragma unroll
-  for (int s = 1; s < KC; ++s) {
-    if (s < K && sd[s] > m) {
-      m = sd[s];
-      ms = s;
-    }
-  }
-}
-
-// Broadcast a wave-uniform value into a VGPR so the subtractions that use it
-// are VGPR-only VALU ops (an SGPR source costs 4 cycles per wave64 op).
-__device__ __forceinline__ float to_vgpr(float s) {
-  float v;
-  asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(s));
-  return v;
-}
-__device__ __forceinline__ double to_vgpr(double s) { return s; }
-__device__ __forceinline__ half_t to_vgpr(half_t s) { return s; }
-
-// mask = 2 * mask + (d < thr): one compare and one add-with-carry.
-__device__ __forceinline__ uint32_t push_lt(uint32_t mask, float d, float thr) {
-  uint32_t r;
-  asm("v_cmp_lt_f32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %3, %3, vcc"
-      : "=v"(r)
-      : "v"(d), "v"(thr), "v"(mask)
-      : "vcc");
-  return r;
-}
-__device__ __forceinline__ uint32_t push_lt(uint32_t mask, double d, double thr) {
-  return mask + mask + (uint32_t)(d < thr);
-}
-__device__ __forceinline__ uint32_t push_lt(uint32_t mask, half_t d, half_t thr) {
-  return mask + mask + (uint32_t)(d < thr);
-}
-
-// Per-lane select between two registers by a lane mask (bit set -> b).  Kept
-// as v_cndmask so the compiler cannot turn the select tree below back into a
-// dynamically indexed (stack) array.
-__device__ __forceinline__ uint32_t csel_u32(uint64_t m, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(m));
-  return r;
-}
-__device__ __forceinline__ float csel(uint64_t m, float a, float b) {
-  return __uint_as_float(csel_u32(m, __float_as_uint(a), __float_as_uint(b)));
-}
-__device__ __forceinline__ double csel(uint64_t m, double a, double b) {
-  const uint64_t x = __double_as_longlong(a), y = __double_as_longlong(b);
-  const uint64_t lo = csel_u32(m, (uint32_t)x, (uint32_t)y);
-  const uint64_t hi = csel_u32(m, (uint32_t)(x >> 32), (uint32_t)(y >> 32));
-  return __longlong_as_double((long long)((hi << 32) | lo));
-}
-__device__ __forceinline__ half_t csel(uint64_t m, half_t a, half_t b) {
-  const uint32_t x = __builtin_bit_cast(uint16_t, a), y = __builtin_bit_cast(uint16_t, b);
-  return __builtin_bit_cast(half_t, (uint16_t)csel_u32(m, x, y));
-}
-
-// d[c] for a per-lane c in [0, 32): a 5-level select tree over registers
-// (one ballot per level, 31 selects).  Inactive lanes take no part: both the
-// ballots and the selects run under the current exec mask.
-template <typename T>
-__device__ __forceinline__ T select32(const T (&d)[KNN_CHUNK], int c) {
-  T a[16], b[8], e[4], f[2];
-  const uint64_t m0 = __ballot(c & 1), m1 = __ballot(c & 2), m2 = __ballot(c & 4);
-  const uint64_t m3 = __ballot(c & 8), m4 = __ballot(c & 16);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) a[i] = csel(m0, d[2 * i], d[2 * i + 1]);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) b[i] = csel(m1, a[2 * i], a[2 * i + 1]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) e[i] = csel(m2, b[2 * i], b[2 * i + 1]);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) f[i] = csel(m3, e[2 * i], e[2 * i + 1]);
-  return csel(m4, f[0], f[1]);
 }
 
 // Per cloud, the valid queries (row < lengths1) in Morton order of a 16^3
@@ -254,52 +155,6 @@ __global__ __launch_bounds__(1024) void knn_order_kernel(const T* __restrict__ p
   __syncthreads();
   for (int k = tid; k < L1; k += 1024) out[atomicAdd(&cnt[cell_of(k)], 1u)] = k;
   for (int k = L1 + tid; k < P1; k += 1024) out[k] = k;  // rows past lengths1 keep their place
-}
-
-// knn_points(return_sorted=True) sorts each row with torch's sort along the
-// last dim (knn/__init__.py:111-131).  For rows of at most 32 entries torch
-// runs a 32-wide bitonic network (entries past the row invalid, sorting last)
-// whose compare-exchange swaps unless the first key is valid and strictly
-// less (NaN counts as largest) -- so ties come out in the network's order, not
-// a stable one.  This replays that network on a lane's row in registers.
-// Only the first KC positions can hold valid entries: KC is a power of two,
-// every exchange within blocks of at most KC positions stays inside one
-// block, and an exchange across position KC (a valid entry against an
-// invalid one) runs in ascending direction, which never moves the entry up.
-template <typename T>
-__device__ __forceinline__ bool knn_isnan(T x) {
-  return x != x;
-}
-template <typename T, int KC>
-__device__ __forceinline__ void knn_sort_row(T (&d)[KC], int (&ix)[KC], uint32_t valid) {
-  auto cas = [&](int a, int b, bool up) {  // branch-free compare-exchange
-    const bool va = (valid >> a) & 1u, vb = (valid >> b) & 1u;
-    const bool lt = !knn_isnan(d[a]) && (knn_isnan(d[b]) || d[a] < d[b]);
-    const bool x = ((lt && va) || !vb) == up;
-    const T da = d[a], db = d[b];
-    const int ia = ix[a], ib = ix[b];
-    d[a] = x ? db : da;
-    d[b] = x ? da : db;
-    ix[a] = x ? ib : ia;
-    ix[b] = x ? ia : ib;
-    valid ^= (x && va != vb) ? (1u << a) | (1u << b) : 0u;
-  };
-#pragma unroll
-  for (int size = 2; size < 32; size *= 2)
-#pragma unroll
-    for (int stride = size / 2; stride > 0; stride /= 2)
-#pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        const int a = 2 * t - (t & (stride - 1));
-        if (a + stride < KC) cas(a, a + stride, (t & (size / 2)) != 0);
-      }
-#pragma unroll
-  for (int stride = 16; stride > 0; stride /= 2)
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int a = 2 * t - (t & (stride - 1));
-      if (a + stride < KC) cas(a, a + stride, false);
-    }
 }
 
 // mode bit 0: RegisterMinK<2> (version 3, K = 2); bit 1 (= SORT): rows
@@ -536,12 +391,6 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
 constexpr int HD_CAP = 256;  // candidates kept per (query, slice); a multiple of 16
 constexpr int HD_J = 4;      // references per load step
 
-// lane L of each 16-lane row, broadcast over the row (gfx950 DPP row_newbcast)
-template <int L>
-__device__ __forceinline__ float row_bcast(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x150 + L, 0xF, 0xF, false));
-}
 template <int E>
 __device__ __forceinline__ float f4_at(const float4& v) {
   if constexpr (E == 0) return v.x;
@@ -1083,7 +932,8 @@ extern "C" int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int6
                                           int64_t D, int64_t K, int norm) {
   if (N < 0 || P1 < 0 || P2 < 0 || D < 1 || K < 0) return -1;
   if (dtype == TPO_BF16) return knn_bf16_supported(D, K, norm) ? knn_bf16_workspace(N, P1, P2, K) : 0;
-  const int64_t order = ((N * P1 * 4 + 255) / 256) * 256;
+  int64_t order = ((N * P1 * 4 + 255) / 256) * 256;
+  if (knn_grid_applies(dtype, D, K, P2)) order += knn_grid_workspace(N, P2);
   const int S = hd_slices(dtype, N, P1, P2, D, K);
   const int64_t hd = S > 0 ? hd_layout(N * P1, S).total : 0;
   return order > hd ? order : hd;
@@ -1132,7 +982,15 @@ static int knn_fwd_impl(int dtype, const void* p1, const void* p2, const int64_t
     }
   }
   // the query ordering is an optimisation: without workspace, keep row order
+  const int64_t order_bytes = ((N * P1 * 4 + 255) / 256) * 256;
   int32_t* order = (workspace && workspace_bytes >= N * P1 * 4) ? (int32_t*)workspace : nullptr;
+  // float 3-D against long clouds: brute-force prefix, then a grid's candidates
+  if (order && !(sorted2 & 1) && knn_grid_applies(dtype, D, K, P2) &&
+      workspace_bytes >= order_bytes + knn_grid_workspace(N, P2)) {
+    launch_knn_grid(p1, p2, lengths1, lengths2, order, (int)N, (int)P1, (int)P2, (int)K, norm, pad,
+                    sort_rows, idxs, dists, (char*)workspace + order_bytes, s);
+    return check_launch("tpo_knn_fwd");
+  }
   switch (dtype) {
     case TPO_F32: launch_fwd<float>(p1, p2, lengths1, lengths2, order, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
     case TPO_F64: launch_fwd<double>(p1, p2, lengths1, lengths2, order, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, pad, sorted2, idxs, dists, s); break;
