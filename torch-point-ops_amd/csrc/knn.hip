@@ -315,13 +315,7 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
           const int c = cn - 1 - top;
           const T d = select32(dch, c);
           if (d < thr) {
-#pragma unroll
-            for (int s = 0; s < KC; ++s) {
-              if (s == ms) {
-                sd[s] = d;
-                si[s] = j0 + c;
-              }
-            }
+            mink_put<T, KC>(sd, si, ms, d, j0 + c);
             first_max<T, KC>(sd, K, thr, ms);
           }
         }
@@ -532,9 +526,7 @@ __global__ __launch_bounds__(256) void knn_hd_slice_kernel(
           cip[count] = base + u;
         }
         ++count;
-#pragma unroll
-        for (int t = 0; t < KC; ++t)
-          if (t == ms) sd[t] = d;
+        mink_put<float, KC>(sd, ms, d);
         first_max<float, KC>(sd, K, thr, ms);
       }
     }
@@ -590,13 +582,7 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
     first_max<float, KC>(sd, K, thr, ms);
     auto replay = [&](float d, int j) {
       if (d < thr) {
-#pragma unroll
-        for (int s = 0; s < KC; ++s) {
-          if (s == ms) {
-            sd[s] = d;
-            si[s] = j;
-          }
-        }
+        mink_put<float, KC>(sd, si, ms, d, j);
         first_max<float, KC>(sd, K, thr, ms);
       }
     };

@@ -96,6 +96,25 @@ __device__ __forceinline__ half_t csel(uint64_t m, half_t a, half_t b) {
   return __builtin_bit_cast(half_t, (uint16_t)csel_u32(m, x, y));
 }
 
+// Slot ms of the lane's MinK takes (d, j): a compare and a select per slot,
+// written with explicit selects so that the compiler cannot lower the
+// dynamically indexed store into a branch tree (which lanes that diverge
+// would all walk).
+template <typename T, int KC>
+__device__ __forceinline__ void mink_put(T (&sd)[KC], int (&si)[KC], int ms, T d, int j) {
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    const uint64_t hit = __ballot(s == ms);
+    sd[s] = csel(hit, sd[s], d);
+    si[s] = (int)csel_u32(hit, (uint32_t)si[s], (uint32_t)j);
+  }
+}
+template <typename T, int KC>
+__device__ __forceinline__ void mink_put(T (&sd)[KC], int ms, T d) {
+#pragma unroll
+  for (int s = 0; s < KC; ++s) sd[s] = csel(__ballot(s == ms), sd[s], d);
+}
+
 // d[c] for a per-lane c in [0, 32): a 5-level select tree over registers
 // (one ballot per level, 31 selects).  Inactive lanes take no part: both the
 // ballots and the selects run under the current exec mask.

@@ -344,13 +344,7 @@ __global__ __launch_bounds__(256) void knn_grid_kernel(
         const float d = dl[64 * c];
         if (d < thr) {
           const int j = index_of(c);
-#pragma unroll
-          for (int s = 0; s < KC; ++s) {
-            if (s == ms) {
-              sd[s] = d;
-              si[s] = j;
-            }
-          }
+          mink_put<float, KC>(sd, si, ms, d, j);
           first_max<float, KC>(sd, K, thr, ms);
         }
       }
