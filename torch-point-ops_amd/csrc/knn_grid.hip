@@ -111,35 +111,56 @@ __device__ __forceinline__ float kg_dist(const float (&q)[3], float x, float y, 
 // query processing order: consecutive cells are face neighbours, so the 64
 // queries of a wave stay in a compact region), otherwise by (x, y, z)
 // row-major (the reference grid, whose cells along z then sit next to each
-// other).  Writes the box to hdr
-// and the exclusive cell starts to cs when given, and the point indices
-// grouped by cell to out[0, L) (any order within a cell).  Loads are issued
-// four per thread at a time.
-template <bool HILBERT>
+// other).  Writes the box to hdr and the exclusive cell starts to cs when
+// given, and the point indices grouped by cell to out[0, L) (any order
+// within a cell).  PPT > 0 (L <= 1024 PPT): each thread's points are loaded
+// once into registers, their cells computed once, and placed by the rank
+// the histogram's atomics returned; PPT == 0 streams the cloud three times.
+struct KgBinLds {
+  uint32_t cnt[KG_CELLS];
+  float red[6][16];
+  uint32_t part[16];
+};
+
+template <bool HILBERT, int PPT>
 __device__ void kg_bin(const float* __restrict__ P, int L, float* __restrict__ hdr,
-                       int32_t* __restrict__ cs, int32_t* __restrict__ out) {
-  __shared__ uint32_t cnt[KG_CELLS];
-  __shared__ float red[6][16];
-  __shared__ uint32_t part[16];
+                       int32_t* __restrict__ cs, int32_t* __restrict__ out, KgBinLds& sm) {
+  uint32_t* __restrict__ cnt = sm.cnt;
+  float (*red)[16] = sm.red;
+  uint32_t* __restrict__ part = sm.part;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  float lo[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
-  float hi[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
-  for (int k0 = tid; k0 < L; k0 += 4096) {
-    float v[4][3];
+  constexpr int R = PPT > 0 ? PPT : 4;  // points a thread holds at once
+  float v[R][3];
+  auto load = [&](int k0) {  // points k0 + 1024 u, clamped (a repeat changes no bound)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int k = min(k0 + 1024 * u, L - 1);  // a repeated point changes no bound
+    for (int u = 0; u < R; ++u) {
+      const int k = min(k0 + 1024 * u, L - 1);
 #pragma unroll
       for (int c = 0; c < 3; ++c) v[u][c] = P[3 * k + c];
     }
+  };
+  float lo[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
+  float hi[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  auto bound = [&]() {
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < R; ++u)
 #pragma unroll
       for (int c = 0; c < 3; ++c)
         if (__builtin_fabsf(v[u][c]) < __builtin_inff()) {
           lo[c] = fminf(lo[c], v[u][c]);
           hi[c] = fmaxf(hi[c], v[u][c]);
         }
+  };
+  if (L > 0) {
+    if constexpr (PPT > 0) {
+      load(tid);
+      bound();
+    } else {
+      for (int k0 = tid; k0 < L; k0 += 1024 * R) {
+        load(k0);
+        bound();
+      }
+    }
   }
 #pragma unroll
   for (int c = 0; c < 3; ++c)
@@ -160,9 +181,9 @@ __device__ void kg_bin(const float* __restrict__ P, int L, float* __restrict__ h
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
     float a = __builtin_inff(), z = -__builtin_inff();
-    for (int v = 0; v < 16; ++v) {
-      a = fminf(a, red[c][v]);
-      z = fmaxf(z, red[3 + c][v]);
+    for (int x = 0; x < 16; ++x) {
+      a = fminf(a, red[c][x]);
+      z = fmaxf(z, red[3 + c][x]);
     }
     const float ext = z - a;
     const bool fin = ext > 0.f && ext < __builtin_inff();
@@ -182,34 +203,32 @@ __device__ void kg_bin(const float* __restrict__ P, int L, float* __restrict__ h
       return (ci[0] * KG_G + ci[1]) * KG_G + ci[2];
     }
   };
-  // histogram, then ranks: each pass loads four points a thread at once
-  auto pass = [&](bool place) {
-    for (int k0 = tid; k0 < L; k0 += 4096) {
-      float v[4][3];
+  int cell[PPT > 0 ? PPT : 1];
+  uint32_t rank[PPT > 0 ? PPT : 1];
+  if constexpr (PPT > 0) {  // histogram from registers, ranks kept
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int k = min(k0 + 1024 * u, L - 1);
-#pragma unroll
-        for (int c = 0; c < 3; ++c) v[u][c] = P[3 * k + c];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int k = k0 + 1024 * u;
-        if (k < L) {
-          const uint32_t r = atomicAdd(&cnt[cell_of(v[u][0], v[u][1], v[u][2])], 1u);
-          if (place) out[r] = k;
-        }
+    for (int u = 0; u < PPT; ++u) {
+      const int k = tid + 1024 * u;
+      if (k < L) {
+        cell[u] = cell_of(v[u][0], v[u][1], v[u][2]);
+        rank[u] = atomicAdd(&cnt[cell[u]], 1u);
       }
     }
-  };
-  pass(false);
+  } else {  // histogram, then (after the scan) ranks, streaming R points a thread
+    for (int k0 = tid; k0 < L; k0 += 1024 * R) {
+      load(k0);
+#pragma unroll
+      for (int u = 0; u < R; ++u)
+        if (k0 + 1024 * u < L) atomicAdd(&cnt[cell_of(v[u][0], v[u][1], v[u][2])], 1u);
+    }
+  }
   __syncthreads();
   {  // exclusive scan, 4 cells per thread
-    uint32_t v[4], sum = 0;
+    uint32_t c4[4], sum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      v[i] = cnt[tid * 4 + i];
-      sum += v[i];
+      c4[i] = cnt[tid * 4 + i];
+      sum += c4[i];
     }
     uint32_t incl = sum;
 #pragma unroll
@@ -225,13 +244,30 @@ __device__ void kg_bin(const float* __restrict__ P, int L, float* __restrict__ h
     for (int i = 0; i < 4; ++i) {
       cnt[tid * 4 + i] = run;
       if (cs) cs[tid * 4 + i] = (int32_t)run;
-      run += v[i];
+      run += c4[i];
     }
     if (cs && tid == 0) cs[KG_CELLS] = L;
   }
   __syncthreads();
-  pass(true);
+  if constexpr (PPT > 0) {
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+      const int k = tid + 1024 * u;
+      if (k < L) out[cnt[cell[u]] + rank[u]] = k;
+    }
+  } else {
+    for (int k0 = tid; k0 < L; k0 += 1024 * R) {
+      load(k0);
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        const int k = k0 + 1024 * u;
+        if (k < L) out[atomicAdd(&cnt[cell_of(v[u][0], v[u][1], v[u][2])], 1u)] = k;
+      }
+    }
+  }
 }
+
+constexpr int KG_PPT = 16;  // register-resident binning up to 16384 points
 
 // Blocks [0, N): the processing order of cloud n's queries (valid rows in
 // Hilbert order of their own grid, rows past lengths1 after them in place);
@@ -241,19 +277,24 @@ __global__ __launch_bounds__(1024) void knn_grid_setup_kernel(
     int32_t* __restrict__ order, const float* __restrict__ p2, const int64_t* __restrict__ len2,
     int P2, int N, float* __restrict__ hdr, int32_t* __restrict__ cstart,
     int32_t* __restrict__ list) {
+  __shared__ KgBinLds sm;
   if ((int)blockIdx.x < N) {
     const int n = blockIdx.x;
     const int64_t l1 = len1[n];
     const int L1 = (int)(l1 < 0 ? 0 : (l1 > P1 ? P1 : l1));
     int32_t* __restrict__ out = order + (size_t)n * P1;
-    kg_bin<true>(p1 + (size_t)n * P1 * 3, L1, nullptr, nullptr, out);  // Hilbert order
+    if (L1 <= 1024 * KG_PPT) kg_bin<true, KG_PPT>(p1 + (size_t)n * P1 * 3, L1, nullptr, nullptr, out, sm);
+    else kg_bin<true, 0>(p1 + (size_t)n * P1 * 3, L1, nullptr, nullptr, out, sm);
     for (int k = L1 + (int)threadIdx.x; k < P1; k += 1024) out[k] = k;
   } else {
     const int n = blockIdx.x - N;
     const int64_t l2 = len2[n];
     const int L2 = (int)(l2 < 0 ? 0 : (l2 > P2 ? P2 : l2));
-    kg_bin<false>(p2 + (size_t)n * P2 * 3, L2, hdr + (size_t)n * 8,
-                  cstart + (size_t)n * (KG_CELLS + 1), list + (size_t)n * P2);
+    float* h = hdr + (size_t)n * 8;
+    int32_t* cs = cstart + (size_t)n * (KG_CELLS + 1);
+    int32_t* ls = list + (size_t)n * P2;
+    if (L2 <= 1024 * KG_PPT) kg_bin<false, KG_PPT>(p2 + (size_t)n * P2 * 3, L2, h, cs, ls, sm);
+    else kg_bin<false, 0>(p2 + (size_t)n * P2 * 3, L2, h, cs, ls, sm);
   }
 }
 
@@ -335,13 +376,17 @@ __global__ __launch_bounds__(256) void knn_grid_kernel(
           std::make_integer_sequence<int, KNN_CHUNK>{});
       return mask;
     };
-    // this lane's candidates of the chunk in order, against the current maximum
+    // this lane's candidates of the chunk in order, against the current
+    // maximum; the next candidate's distance is read ahead
     auto walk = [&](uint32_t mask, auto&& index_of) {
+      int top = mask ? 31 - __builtin_clz(mask) : 0;
+      float dn = dl[64 * (31 - top)];
       while (mask) {
-        const int top = 31 - __builtin_clz(mask);
-        mask ^= 1u << top;
         const int c = 31 - top;
-        const float d = dl[64 * c];
+        const float d = dn;
+        mask ^= 1u << top;
+        top = mask ? 31 - __builtin_clz(mask) : 0;
+        dn = dl[64 * (31 - top)];
         if (d < thr) {
           const int j = index_of(c);
           mink_put<float, KC>(sd, si, ms, d, j);
