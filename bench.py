@@ -47,6 +47,7 @@ EMD_REF_MS = 32.366  # README.md:314, EMD FP32 eager, B16_N2048_M2048, RTX 3090
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense MFMA
 FLOP_PER_PAIR = 9  # 3 sub + 3 mul + 2 add + 1 compare per directed pair
+VALU_LANE_PEAK_T = 1024 * 16 * 2.4e9 / 1e12  # fp32 VALU lane ops/s (no packed FP32), 39.32e12
 
 
 def cpu_model():
@@ -609,6 +610,38 @@ def main():
     traffic = (profile_json("chamfer_grid_fwd_c2_traffic.json") or {}).get("hbm_bytes_per_launch")
     counters = profile_json("chamfer_grid_search_c2_counters.json")
 
+    # The dominant launch (sort + search) is VALU-issue bound, and divergent:
+    # its roofline is the fp32 VALU lane-op peak (1024 SIMDs x 16 lanes x
+    # 2.4 GHz; this build emits no packed FP32), the achieved rate the lane
+    # operations the committed counters count per launch (SQ_INSTS_VALU x 64
+    # x VALUUtilization) over this run's HIP-event time of the launch.
+    lane_ops = (counters or {}).get("lane_ops_per_launch")
+    achieved_lane = lane_ops / fwd_t / 1e12 if lane_ops else None
+    roofline = {"bound": "valu",
+                "compute_unit": "fp32 vector ALU; the kernels use no MFMA",
+                "kernel": "chamfer_grid_sort_kernel<float,8> + chamfer_grid_search_kernel"
+                          "<float,256> (tpo_chamfer_fwd with a workspace)",
+                "achieved": round(achieved_lane, 3) if achieved_lane else None,
+                "peak": VALU_LANE_PEAK_T, "unit": "T VALU lane-ops/s",
+                "frac": round(achieved_lane / VALU_LANE_PEAK_T, 4) if achieved_lane else None,
+                "traffic": traffic, "fwd_ms": round(fwd_t * 1e3, 4),
+                "work": "VALU lane operations per launch from the committed rocprofv3 counters "
+                        "(SQ_INSTS_VALU x 64 x VALUUtilization, sort + search)",
+                "lane_ops_per_launch": lane_ops,
+                "useful_tflops": round(achieved, 4),
+                "useful_frac_fp32_peak": round(achieved / FP32_PEAK_TFLOPS, 5),
+                "useful_work": "9 FLOP (3 sub, 3 mul, 2 add, 1 compare) per (query, reference) "
+                               "pair the exact grid search evaluates, counted by the kernel",
+                "pairs_evaluated": ch["pairs_evaluated"],
+                "algorithmic_pairs_brute_force": ch["pairs"],
+                "brute_force_equivalent_tflops": round(brute, 3),
+                "module_fwd_ms": round(ch["loss_fwd_sec"] * 1e3, 4),
+                "valu_counters": counters,
+                "note": "frac = VALUBusy x VALUUtilization of the launch: the search walks "
+                        "cells lane by lane, so most lanes idle in its VALU instructions; "
+                        "useful_tflops counts only the distance work it needs, "
+                        "brute_force_equivalent_tflops 9 FLOP x all 2BNM directed pairs over "
+                        "the same time"}
     out = {
         "metric": "Chamfer/KNN G pair-dists/s & % FP32 VALU peak; FPS ms at N=64K->4K",
         "value": round(value, 3),
@@ -626,26 +659,7 @@ def main():
                                "ChamferDistance('mean') (BASELINE.json configs[1])",
                    "global_batch": ch["B"], "points": [ch["N"], ch["M"]],
                    "pairs_per_step": ch["pairs"], "parallelism": "single GPU"},
-        "roofline": {"bound": "valu",
-                     "compute_unit": "fp32 vector ALU (157.3 TFLOP/s is MI355X's fp32 peak); "
-                                     "the kernels use no MFMA",
-                     "kernel": "chamfer_grid_sort_kernel<float,8> + chamfer_grid_search_kernel"
-                               "<float,256> (tpo_chamfer_fwd with a workspace)",
-                     "achieved": round(achieved, 4), "peak": FP32_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 5),
-                     "traffic": traffic, "fwd_ms": round(fwd_t * 1e3, 4),
-                     "work": "9 FLOP (3 sub, 3 mul, 2 add, 1 compare) per (query, reference) "
-                             "pair the exact grid search evaluates, counted by the kernel",
-                     "pairs_evaluated": ch["pairs_evaluated"],
-                     "algorithmic_pairs_brute_force": ch["pairs"],
-                     "brute_force_equivalent_tflops": round(brute, 3),
-                     "module_fwd_ms": round(ch["loss_fwd_sec"] * 1e3, 4),
-                     "valu_counters": counters,
-                     "note": "frac is the exact search's useful distance work against the "
-                             "FP32 peak; brute_force_equivalent_tflops is 9 FLOP x all 2BNM "
-                             "directed pairs over the same time (the search evaluates "
-                             "pairs_evaluated of them); valu_counters come from the committed "
-                             "rocprofv3 --pmc summary of the search kernel"},
+        "roofline": roofline,
     }
     threads = min(host_cores(), int(os.environ.get("OMP_NUM_THREADS", host_cores())))
     sec = {}
@@ -669,8 +683,11 @@ def main():
                          "G_pair_dists_per_s_module": round(kn["pairs"] / kn["sec_module"] / 1e9, 2),
                          "ms_kernel": round(kn["sec_kernel"] * 1e3, 4),
                          "ms_module_return_nn": round(kn["sec_module"] * 1e3, 4),
-                         "frac_fp32_peak": round(FLOP_PER_PAIR * kn["pairs"] / kn["sec_kernel"]
-                                                 / 1e12 / FP32_PEAK_TFLOPS, 4),
+                         "brute_force_equivalent_tflops": round(FLOP_PER_PAIR * kn["pairs"]
+                                                                / kn["sec_kernel"] / 1e12, 3),
+                         "note": "the kernel runs a brute-force prefix and then only the "
+                                 "references a grid leaves as candidates (exact MinK replay); "
+                                 "pair rates count all lengths1 x lengths2 pairs per cloud",
                          "ms_backward": round(kn["sec_bwd"] * 1e3, 4),
                          "G_slots_per_s_backward": round(kn["slots"] / kn["sec_bwd"] / 1e9, 2)}
         log("[bench] knn c5 (bf16, matrix cores; float32 reference semantics)")
@@ -685,7 +702,9 @@ def main():
                              "tflops": round(f32, 2),
                              "frac_fp32_peak": round(f32 / FP32_PEAK_TFLOPS, 4),
                              "note": "config-5 shape widened to float32, version-0 semantics "
-                                     "(knn.cu:16-60, MinK in the output slots), 2*D FLOP/pair"}
+                                     "(knn.cu:16-60, MinK in the output slots), 2*D FLOP/pair; "
+                                     "the slice kernel's VALUBusy and VALUUtilization are in "
+                                     "profiles/valu_counters_profile_run.md"}
         log("[bench] fps + gather c4")
         fp = bench_fps(tpo, torch, args.steps)
         sec["fps_c4"] = {"ms": round(fp["fps_sec"] * 1e3, 3),
