@@ -95,7 +95,13 @@ def test_argument_errors_are_reported(lib):
     assert lib.tpo_chamfer_pairs_evaluated(0, None, 2, 4096, 4096, None, None) == -1
     lib.tpo_knn_workspace_size.argtypes = [ctypes.c_int, I, I, I, I, I, ctypes.c_int]
     lib.tpo_knn_workspace_size.restype = I
-    assert lib.tpo_knn_workspace_size(0, 8, 16384, 16384, 3, 16, 2) == 8 * 16384 * 4
+    # float 3-D against long clouds: the query order, then the reference grid
+    # (8 floats of box per cloud, 16^3 + 1 cell starts, the indices by cell)
+    up = lambda x: (x + 255) // 256 * 256
+    assert lib.tpo_knn_workspace_size(0, 8, 16384, 16384, 3, 16, 2) == \
+        8 * 16384 * 4 + up(8 * 8 * 4) + up(8 * 4097 * 4) + up(8 * 16384 * 4)
+    assert lib.tpo_knn_workspace_size(1, 8, 16384, 16384, 3, 16, 2) == 8 * 16384 * 4  # order only
+    assert lib.tpo_knn_workspace_size(0, 8, 16384, 1000, 3, 16, 2) == 8 * 16384 * 4  # short clouds
     # bf16: squared norms (float per point), then a partial list of K (d, index)
     # pairs per query and reference slice (config 5 runs 8 slices)
     assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 128, 32, 2) == \
