@@ -33,10 +33,15 @@
 //    (the reference's NaN rule included).
 // The best (distance, index) pair is one 64-bit key: distances here are
 // finite and non-negative, so their bits order like their values.
-// Results are identical to the reference's; the work depends on the data
-// (clustered and spread clouds need a few dozen points per query, a cloud
-// squeezed into one cell degrades to a full scan).  Each wave records the
-// number of points it evaluated (tpo_chamfer_pairs_evaluated sums them).
+// Uneven clouds: the search runs at the finest of 32^3, 16^3 and 8^3 cells
+// whose mean own-cell occupancy is small; a box stretched by a few far
+// points is rebuilt on the remaining points (the cut sides' boundary cells
+// unbounded); a cloud still crowded into few cells runs the dense block
+// inside the search kernel; a query whose box would hold too many cells
+// joins a wave-wide scan of the reference cloud.  Results are identical to
+// the reference's in every case; only the work depends on the data.  Each
+// wave records the number of points it evaluated
+// (tpo_chamfer_pairs_evaluated sums them).
 #include <algorithm>
 
 #include "chamfer_common.hpp"
