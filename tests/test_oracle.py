@@ -635,6 +635,48 @@ def test_emd_transport_plan_properties(O, n, m):
     assert np.allclose(cost, (d * match).sum((1, 2)), rtol=1e-9)
 
 
+def _emd_clusters(seed, n, m, dtype):
+    # clustered clouds: pairs at every scale, so every level of the schedule
+    # (exp(-4^j d), j = 7 .. -1, then 1) moves mass
+    r = rng(seed)
+    cen = r.uniform(-1, 1, (2, 4, 3))
+    p1 = cen[np.arange(2)[:, None], r.integers(0, 4, (2, n))] + 0.05 * r.standard_normal((2, n, 3))
+    p2 = cen[np.arange(2)[:, None], r.integers(0, 4, (2, m))] + 0.05 * r.standard_normal((2, m, 3))
+    return p1.astype(dtype), p2.astype(dtype)
+
+
+@pytest.mark.parametrize("dtype,tol", [(np.float64, 1e-9), (np.float32, 2e-4)])
+@pytest.mark.parametrize("n,m", [(40, 40), (60, 25), (25, 60), (1, 9)])
+def test_emd_matches_independent_numpy_statement(O, dtype, tol, n, m):
+    """The oracle's EMD against a second statement of emd.cu written with
+    numpy (tests/emd_numpy.py): plan, cost and both gradients."""
+    from tests import emd_numpy
+
+    p1, p2 = _emd_clusters(n * 3 + m, n, m, dtype)
+    cost, match = O.emd_fwd(p1, p2)
+    ec, em = emd_numpy.emd_forward(p1, p2)
+    assert np.allclose(cost, ec, rtol=tol, atol=0)
+    assert np.abs(match.astype(np.float64) - em).max() <= tol * max(1.0, float(np.abs(em).max()))
+    g = rng(5).standard_normal(2).astype(dtype)
+    g1, g2 = O.emd_bwd(g, p1, p2, match)
+    e1, e2 = emd_numpy.emd_backward(g, p1, p2, match)
+    for got, want in ((g1, e1), (g2, e2)):
+        assert np.abs(got.astype(np.float64) - want).max() <= tol * max(1.0, float(np.abs(want).max()))
+
+
+def test_emd_numpy_statement_detects_schedule_slips(O):
+    """The comparison above separates the reference's level schedule from
+    plausible slips (one level fewer at either end, a level missed) by far
+    more than its tolerance."""
+    from tests import emd_numpy
+
+    p1, p2 = _emd_clusters(11, 40, 40, np.float64)
+    cost, _ = O.emd_fwd(p1, p2)
+    for levels in (range(6, -3, -1), range(7, -2, -1), [7, 6, 5, 4, 2, 1, 0, -1, -2]):
+        slip, _ = emd_numpy.emd_forward(p1, p2, levels)
+        assert np.abs(slip - cost).max() > 1e-6 * np.abs(cost).max(), list(levels)
+
+
 def test_emd_symmetric_for_equal_sizes(O):
     """test_emd.py:323-350 swaps the clouds at n = m = 256.  The matching is
     not symmetric (pass 1 normalises over xyz1's points first): at these
