@@ -420,16 +420,19 @@ __device__ __forceinline__ float hd_dist_mem(const float4* __restrict__ q, const
   return acc;
 }
 
+// workspace: per (row, slice) the candidate count, distances and indices;
+// per row the K fill distances (written by the first slice's workgroups)
 struct HdLayout {
-  int64_t cnt, dist, idx, total;
+  int64_t cnt, dist, idx, fill, total;
 };
-HdLayout hd_layout(int64_t rows, int64_t S) {
+HdLayout hd_layout(int64_t rows, int64_t S, int64_t K) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   HdLayout L;
   L.cnt = 0;
   L.dist = up(rows * S * 4);
   L.idx = L.dist + up(rows * S * HD_CAP * 4);
-  L.total = L.idx + up(rows * S * HD_CAP * 4);
+  L.fill = L.idx + up(rows * S * HD_CAP * 4);
+  L.total = L.fill + up(rows * K * 4);
   return L;
 }
 
@@ -437,7 +440,8 @@ template <int DT, int NORM, int KC>
 __global__ __launch_bounds__(256) void knn_hd_slice_kernel(
     const float* __restrict__ p1, const float* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, int P1, int P2, int K, int nqb, int S, int slen,
-    int32_t* __restrict__ cnt, float* __restrict__ cd, int32_t* __restrict__ ci) {
+    int32_t* __restrict__ cnt, float* __restrict__ cd, int32_t* __restrict__ ci,
+    float* __restrict__ fd) {
   constexpr int G = DT / 64;
   __shared__ float s_d[4][32][64];
   const int sl = blockIdx.x % S;
@@ -489,6 +493,11 @@ __global__ __launch_bounds__(256) void knn_hd_slice_kernel(
       sd[t] = Lim<float>::inf();
     }
   }
+  if (sl == 0 && act) {  // the merge's fill
+#pragma unroll
+    for (int t = 0; t < KC; ++t)
+      if (t < K) fd[row * K + t] = sd[t];
+  }
   float thr;
   int ms;
   first_max<float, KC>(sd, K, thr, ms);
@@ -539,7 +548,8 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
     const float* __restrict__ p1, const float* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, int N, int P1, int P2, int K, int S, int slen, int pad_sentinel,
     const int32_t* __restrict__ cnt, const float* __restrict__ cd,
-    const int32_t* __restrict__ ci, int64_t* __restrict__ idxs, float* __restrict__ dists) {
+    const int32_t* __restrict__ ci, const float* __restrict__ fd, int64_t* __restrict__ idxs,
+    float* __restrict__ dists) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (int64_t)N * P1) return;
   const int n = (int)(t / P1), q = (int)(t - (int64_t)n * P1);
@@ -568,7 +578,8 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
     if (s < fill) {
-      sd[s] = dist(s);
+      // with more than K references the first slice stored them
+      sd[s] = L2 > K ? fd[row * K + s] : dist(s);
       si[s] = s;
     } else {
       sd[s] = Lim<float>::inf();
@@ -677,22 +688,23 @@ void launch_hd_kc(const void* p1, const void* p2, const int64_t* l1, const int64
                   void* ws, hipStream_t s) {
   const int nqb = (P1 + 255) / 256;
   const int slen = (P2 - K + S - 1) / S;
-  const HdLayout L = hd_layout((int64_t)N * P1, S);
+  const HdLayout L = hd_layout((int64_t)N * P1, S, K);
   int32_t* cnt = (int32_t*)((char*)ws + L.cnt);
   float* cd = (float*)((char*)ws + L.dist);
   int32_t* ci = (int32_t*)((char*)ws + L.idx);
+  float* fd = (float*)((char*)ws + L.fill);
   hipLaunchKernelGGL((knn_hd_slice_kernel<DT, NORM, KC>), dim3(N * nqb * S), dim3(256), 0, s,
                      (const float*)p1, (const float*)p2, l1, l2, P1, P2, K, nqb, S, slen, cnt, cd,
-                     ci);
+                     ci, fd);
   const unsigned mg = (unsigned)(((int64_t)N * P1 + 255) / 256);
   if (sort)
     hipLaunchKernelGGL((knn_hd_merge_kernel<DT, NORM, KC, true>), dim3(mg), dim3(256), 0, s,
                        (const float*)p1, (const float*)p2, l1, l2, N, P1, P2, K, S, slen, pad, cnt,
-                       cd, ci, idxs, (float*)dists);
+                       cd, ci, fd, idxs, (float*)dists);
   else
     hipLaunchKernelGGL((knn_hd_merge_kernel<DT, NORM, KC, false>), dim3(mg), dim3(256), 0, s,
                        (const float*)p1, (const float*)p2, l1, l2, N, P1, P2, K, S, slen, pad, cnt,
-                       cd, ci, idxs, (float*)dists);
+                       cd, ci, fd, idxs, (float*)dists);
 }
 
 template <int DT, int NORM>
@@ -921,7 +933,7 @@ extern "C" int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int6
   int64_t order = ((N * P1 * 4 + 255) / 256) * 256;
   if (knn_grid_applies(dtype, D, K, P2)) order += knn_grid_workspace(N, P2);
   const int S = hd_slices(dtype, N, P1, P2, D, K);
-  const int64_t hd = S > 0 ? hd_layout(N * P1, S).total : 0;
+  const int64_t hd = S > 0 ? hd_layout(N * P1, S, K).total : 0;
   return order > hd ? order : hd;
 }
 
@@ -961,7 +973,7 @@ static int knn_fwd_impl(int dtype, const void* p1, const void* p2, const int64_t
   hipStream_t s = (hipStream_t)stream;
   {  // long reference clouds, few queries: references sliced over workgroups
     const int S = hd_slices(dtype, N, P1, P2, D, K);
-    if (S > 0 && workspace && workspace_bytes >= hd_layout(N * P1, S).total && v <= 1) {
+    if (S > 0 && workspace && workspace_bytes >= hd_layout(N * P1, S, K).total && v <= 1) {
       launch_hd(p1, p2, lengths1, lengths2, (int)N, (int)P1, (int)P2, (int)D, (int)K, norm, S,
                 pad, sort_rows, idxs, dists, workspace, s);
       return check_launch("tpo_knn_fwd");
