@@ -30,7 +30,7 @@
 // knn_bf16_merge_kernel merges a query's slices.
 #include <type_traits>
 
-#include "tpo_common.hpp"
+#include "knn_common.hpp"
 
 #pragma clang fp contract(off)
 
@@ -69,6 +69,21 @@ __global__ __launch_bounds__(256) void knn_bf16_norms_kernel(const __bf16* __res
     const int64_t b = r / rows_per_batch;
     out[b * stride_out + (r - b * rows_per_batch)] = acc;
   }
+}
+
+// d[v] for a per-lane v in [0, 16): a 4-level select tree over registers
+// (one ballot per level), so the array is never indexed dynamically
+__device__ __forceinline__ float kb_sel16(const float (&d)[16], int v) {
+  float a[8], b[4], e[2];
+  const uint64_t m0 = __ballot(v & 1), m1 = __ballot(v & 2), m2 = __ballot(v & 4),
+                 m3 = __ballot(v & 8);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = csel(m0, d[2 * i], d[2 * i + 1]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = csel(m1, a[2 * i], a[2 * i + 1]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) e[i] = csel(m2, b[2 * i], b[2 * i + 1]);
+  return csel(m3, e[0], e[1]);
 }
 
 template <int KC>
@@ -222,7 +237,7 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
       for (int c = 0; c < 2; ++c) {
         const float thr = ld[KC - 1];
         float dv[16];
-        float mn = Lim<float>::inf();
+        uint32_t m = 0;  // bit v: row 16c + v is below the list's end
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
           const int g = 2 * c + gg;
@@ -235,23 +250,23 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
               const float a = hh ? acc1[4 * g + e] : acc0[4 * g + e];
               float d = __builtin_fmaf(-2.f, a, qq + rv[e]);
               if (partial) d = base + 8 * g + 4 * hh + e < L2 ? d : Lim<float>::inf();
-              dv[8 * gg + 4 * hh + e] = d;  // row 16c + 8gg + 4hh + e
-              mn = fminf(mn, d);
+              const int v = 8 * gg + 4 * hh + e;  // row 16c + v
+              dv[v] = d;
+              m |= (d < thr ? 1u : 0u) << v;
             }
           }
         }
-        if (__ballot(mn < thr) != 0) {  // some lane has a candidate in these rows
-          int pc = 0;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) pc += dv[v] < thr ? 1 : 0;
-          if (__ballot(nq_ + pc > KB_QCAP) != 0) drain();  // keep every queue within capacity
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            if (dv[v] < thr) {  // thr may predate a drain: a stale entry inserts as a no-op
-              s_qd[w][nq_][lane] = fmaxf(dv[v], 0.f);
-              s_qi[w][nq_][lane] = base + 16 * c + v;
-              ++nq_;
-            }
+        if (__ballot(m != 0) != 0) {  // some lane has a candidate in these rows
+          if (__ballot(nq_ + __builtin_popcount(m) > KB_QCAP) != 0) drain();  // queues within capacity
+          // only the set bits: the wave pays max-over-lanes(candidates), not 16
+          // rows of branches (thr may predate a drain: a stale entry inserts
+          // as a no-op)
+          while (m) {
+            const int v = __builtin_ctz(m);
+            m &= m - 1;
+            s_qd[w][nq_][lane] = fmaxf(kb_sel16(dv, v), 0.f);
+            s_qi[w][nq_][lane] = base + 16 * c + v;
+            ++nq_;
           }
         }
       }
