@@ -558,6 +558,41 @@ def test_bf16_config5_subset(tpo, dev):
     check_bf16_knn(idx[:, sel], d[:, sel], q[:, sel], r, torch.full((B,), len(sel)), l2, 32)
 
 
+def test_bf16_equal_distances_take_lower_indices(tpo, dev):
+    # every reference point four times: rows 2i, 2i + 1 (neighbours in one
+    # tile) and 2P + 2i, 2P + 2i + 1 (another slice); the copies give equal
+    # float distances, so each query's list is its nearest point's four copies
+    # in index order, then the two lowest copies of its second nearest --
+    # exactly, on the rows whose three nearest distinct points are clearly
+    # apart (float64 gaps above the error band)
+    g = torch.Generator().manual_seed(91)
+    B, P1, P, D, K = 2, 256, 768, 64, 6
+    q = torch.randn(B, P1, D, generator=g).to(torch.bfloat16)
+    r0 = torch.randn(B, P, D, generator=g).to(torch.bfloat16)
+    r = torch.cat([r0.repeat_interleave(2, 1), r0.repeat_interleave(2, 1)], 1)
+    l1 = torch.full((B,), P1, dtype=torch.int64)
+    l2 = torch.full((B,), 4 * P, dtype=torch.int64)
+    idx, d = raw(q, r, l1, l2, 2, K, -1, dev)
+    idx = idx.cpu()
+    ex = bf16_expected(q, r0, l1, l2, K)  # (B, P1, P)
+    top = ex.sort(-1)
+    qq = (q.to(torch.float64) ** 2).sum(-1)
+    rmax = (r0.to(torch.float64) ** 2).sum(-1).max(-1).values
+    checked = 0
+    for n in range(B):
+        for row in range(P1):
+            v, j = top.values[n, row], top.indices[n, row]
+            band = 8 * (D + 4) * 2.0 ** -24 * float((qq[n, row].sqrt() + rmax[n].sqrt()) ** 2)
+            if not (v[1] - v[0] > band and v[2] - v[1] > band):
+                continue
+            a, b = int(j[0]), int(j[1])
+            want = [2 * a, 2 * a + 1, 2 * P + 2 * a, 2 * P + 2 * a + 1, 2 * b, 2 * b + 1]
+            assert idx[n, row].tolist() == want, (n, row)
+            checked += 1
+    assert checked > B * P1 // 2
+    assert bool((d[..., :4] == d[..., :1]).all())
+
+
 def test_bf16_knn_points_and_fallbacks(tpo, dev):
     g = torch.Generator().manual_seed(77)
     q = torch.randn(2, 40, 64, generator=g).to(torch.bfloat16).to(dev)

@@ -14,10 +14,12 @@ namespace tpo {
 // Copy a wave-uniform (SGPR) value into a VGPR.  On gfx950 a VALU op with an
 // SGPR source issues at 4 cycles per wave64 instruction, while VGPR-only
 // FP32 ops issue at ~2.3-2.7; one v_mov per reference coordinate, shared by
-// the Q queries of the lane, lets every subtraction use VGPR operands.
+// the Q queries of the lane, lets every subtraction use VGPR operands.  The
+// empty asm only pins the value to a VGPR: the compiler emits the move (and
+// any wait it needs) itself.
 __device__ __forceinline__ float to_vgpr(float s) {
-  float v;
-  asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(s));
+  float v = s;
+  asm("" : "+v"(v));
   return v;
 }
 __device__ __forceinline__ double to_vgpr(double s) { return s; }

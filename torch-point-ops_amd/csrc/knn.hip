@@ -274,17 +274,16 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
             prefetch(j0 + 64);
           }
         }
-        // distances of the chunk stay in registers; bit (cn-1-c) of mask
-        // flags reference j0+c as a candidate against the current maximum
+        // distances of the chunk stay in registers (+inf past cn); bit 31-c
+        // of mask flags reference j0+c as a candidate against the current
+        // maximum
         T dch[KNN_CHUNK];
-        uint32_t mask = 0;
         if (STAGED && cn == KNN_CHUNK) {
 #pragma unroll
           for (int c = 0; c < KNN_CHUNK; ++c) {
             const float4 r4 = s_ref[STAGED ? wv : 0][ph + c];
             const T rv[3] = {(T)r4.x, (T)r4.y, (T)r4.z};
             dch[c] = knn_dist<T, DT, NORM>(qr, qp, rv, D);
-            mask = push_lt(mask, dch[c], thr);
           }
         } else if (cn == KNN_CHUNK) {
 #pragma unroll
@@ -296,23 +295,24 @@ __global__ __launch_bounds__(256) void knn_fwd_kernel(
             } else {
               dch[c] = knn_dist<T, DT, NORM>(qr, qp, r, D);
             }
-            mask = push_lt(mask, dch[c], thr);
           }
         } else {
 #pragma unroll
           for (int c = 0; c < KNN_CHUNK; ++c) {
-            if (c < cn) {
+            if (c < cn)
               dch[c] = knn_dist<T, DT, NORM>(qr, qp, rp + (size_t)(j0 + c) * Dd, D);
-              mask = push_lt(mask, dch[c], thr);
-            } else {
+            else
               dch[c] = Lim<T>::inf();
-            }
           }
         }
+        uint32_t mask = 0;
+#pragma unroll
+        for (int c = 0; c < KNN_CHUNK; c += 4)
+          mask = push_lt4(mask, dch[c], dch[c + 1], dch[c + 2], dch[c + 3], thr);
         while (mask) {
           const int top = 31 - __builtin_clz(mask);  // earliest candidate first
           mask ^= 1u << top;
-          const int c = cn - 1 - top;
+          const int c = KNN_CHUNK - 1 - top;
           const T d = select32(dch, c);
           if (d < thr) {
             mink_put<T, KC>(sd, si, ms, d, j0 + c);

@@ -22,10 +22,11 @@
 // two accumulators' half-waves (checked on the device: swap(x, y) leaves
 // x = [x_lo, y_lo], y = [x_hi, y_hi]), after which lane l holds all 32 rows of
 // one query: block l/32, column l%32.  Each lane keeps its own sorted list of
-// the KC best (KC >= K): candidates are queued per lane in LDS in increasing
-// reference order and inserted in bulk by a branch-free network when some
-// queue could overflow, so one pass serves every lane that has work;
-// strict-less insertion keeps the lower index first among equal distances.
+// the KC best (KC >= K) as 64-bit (distance, index) keys: candidates are
+// queued per lane in LDS and, when some queue could overflow, merged in
+// groups of 8 by a sorting network and a bitonic merge in registers, so one
+// branch-free pass serves every lane of the wave; the key order puts the
+// lower index first among equal distances.
 // Each lane writes the first K entries of its list for its slice, and
 // knn_bf16_merge_kernel merges a query's slices.
 #include <type_traits>
@@ -72,11 +73,11 @@ __global__ __launch_bounds__(256) void knn_bf16_norms_kernel(const __bf16* __res
 }
 
 // d[v] for a per-lane v in [0, 16): a 4-level select tree over registers
-// (one ballot per level), so the array is never indexed dynamically
+// (a lane mask per level), so the array is never indexed dynamically
 __device__ __forceinline__ float kb_sel16(const float (&d)[16], int v) {
   float a[8], b[4], e[2];
-  const uint64_t m0 = __ballot(v & 1), m1 = __ballot(v & 2), m2 = __ballot(v & 4),
-                 m3 = __ballot(v & 8);
+  const uint32_t m0 = bit_mask(v, 0), m1 = bit_mask(v, 1), m2 = bit_mask(v, 2),
+                 m3 = bit_mask(v, 3);
 #pragma unroll
   for (int i = 0; i < 8; ++i) a[i] = csel(m0, d[2 * i], d[2 * i + 1]);
 #pragma unroll
@@ -86,19 +87,97 @@ __device__ __forceinline__ float kb_sel16(const float (&d)[16], int v) {
   return csel(m3, e[0], e[1]);
 }
 
+// A list entry is one 64-bit key: the distance's bits above the reference
+// index.  Pushed distances are finite and >= +0 (negative values are clamped
+// to +0, NaN and inf never pass the filter), so the unsigned key order is the
+// (distance, index) order; the empty entry (inf, KB_NONE) is above every
+// pushed key and ~0 above it.
+__device__ __forceinline__ uint64_t kb_key(float d, int i) {
+  return ((uint64_t)__float_as_uint(d) << 32) | (uint32_t)i;
+}
+
+// (a, b) := (min, max) and (c, d) := (min, max): two independent exchanges,
+// each one 64-bit compare (into vcc, and into an SGPR pair) and four 32-bit
+// selects.  The compiler expands the same C++ as a min and a max, a compare
+// each.  A 64-bit compare's vcc write takes two wait states before its first
+// read (the ones the compiler inserts there): the second compare and one nop.
+__device__ __forceinline__ void kb_ce2(uint64_t& a, uint64_t& b, uint64_t& c, uint64_t& d) {
+  uint32_t r0, r1, r2, r3, r4, r5, r6, r7;
+  uint64_t m;
+  asm("v_cmp_lt_u64 vcc, %10, %9\n\t"
+      "v_cmp_lt_u64 %8, %12, %11\n\t"
+      "s_nop 0\n\t"
+      "v_cndmask_b32 %0, %13, %15, vcc\n\t"
+      "v_cndmask_b32 %1, %14, %16, vcc\n\t"
+      "v_cndmask_b32 %2, %15, %13, vcc\n\t"
+      "v_cndmask_b32 %3, %16, %14, vcc\n\t"
+      "v_cndmask_b32 %4, %17, %19, %8\n\t"
+      "v_cndmask_b32 %5, %18, %20, %8\n\t"
+      "v_cndmask_b32 %6, %19, %17, %8\n\t"
+      "v_cndmask_b32 %7, %20, %18, %8"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6),
+        "=&v"(r7), "=&s"(m)
+      : "v"(a), "v"(b), "v"(c), "v"(d),                                  // 9 .. 12
+        "v"((uint32_t)a), "v"((uint32_t)(a >> 32)), "v"((uint32_t)b),   // 13 .. 15
+        "v"((uint32_t)(b >> 32)), "v"((uint32_t)c), "v"((uint32_t)(c >> 32)),  // 16 .. 18
+        "v"((uint32_t)d), "v"((uint32_t)(d >> 32))                        // 19, 20
+      : "vcc");
+  a = ((uint64_t)r1 << 32) | r0;
+  b = ((uint64_t)r3 << 32) | r2;
+  c = ((uint64_t)r5 << 32) | r4;
+  d = ((uint64_t)r7 << 32) | r6;
+}
+
+// a := min(a, b), c := min(c, d), as above
+__device__ __forceinline__ void kb_min2(uint64_t& a, uint64_t b, uint64_t& c, uint64_t d) {
+  uint32_t r0, r1, r2, r3;
+  uint64_t m;
+  asm("v_cmp_lt_u64 vcc, %6, %5\n\t"
+      "v_cmp_lt_u64 %4, %8, %7\n\t"
+      "s_nop 0\n\t"
+      "v_cndmask_b32 %0, %9, %11, vcc\n\t"
+      "v_cndmask_b32 %1, %10, %12, vcc\n\t"
+      "v_cndmask_b32 %2, %13, %15, %4\n\t"
+      "v_cndmask_b32 %3, %14, %16, %4"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&s"(m)
+      : "v"(a), "v"(b), "v"(c), "v"(d),
+        "v"((uint32_t)a), "v"((uint32_t)(a >> 32)), "v"((uint32_t)b), "v"((uint32_t)(b >> 32)),
+        "v"((uint32_t)c), "v"((uint32_t)(c >> 32)), "v"((uint32_t)d), "v"((uint32_t)(d >> 32))
+      : "vcc");
+  a = ((uint64_t)r1 << 32) | r0;
+  c = ((uint64_t)r3 << 32) | r2;
+}
+
+// 19-comparator sorting network for 8 keys (checked on every 0/1 input), in
+// its six layers of independent exchanges
+__device__ __forceinline__ void kb_sort8(uint64_t (&x)[8]) {
+  kb_ce2(x[0], x[2], x[1], x[3]); kb_ce2(x[4], x[6], x[5], x[7]);
+  kb_ce2(x[0], x[4], x[1], x[5]); kb_ce2(x[2], x[6], x[3], x[7]);
+  kb_ce2(x[0], x[1], x[2], x[3]); kb_ce2(x[4], x[5], x[6], x[7]);
+  kb_ce2(x[2], x[4], x[3], x[5]);
+  kb_ce2(x[1], x[4], x[3], x[6]);
+  kb_ce2(x[1], x[2], x[3], x[4]);
+  uint64_t t = 0;
+  kb_ce2(x[5], x[6], t, t);  // the layer's third exchange, paired with a no-op
+}
+
+// l := the KC smallest of the sorted list l and the sorted keys x, sorted.
+// The list's last 8 take the minimum with x reversed (an ascending and a
+// descending run: the KC smallest, as a bitonic sequence), then log2(KC)
+// half-cleaner stages sort it.
 template <int KC>
-__device__ __forceinline__ void kb_insert(float (&ld)[KC], int (&li)[KC], float d, int id) {
-  // sorted insertion; a no-op when d is not below the last entry
-  bool c[KC];
+__device__ __forceinline__ void kb_merge8(uint64_t (&l)[KC], const uint64_t (&x)[8]) {
 #pragma unroll
-  for (int s = 0; s < KC; ++s) c[s] = d < ld[s];
+  for (int i = 0; i < 8; i += 2) kb_min2(l[KC - 8 + i], x[7 - i], l[KC - 7 + i], x[6 - i]);
 #pragma unroll
-  for (int s = KC - 1; s > 0; --s) {
-    ld[s] = c[s - 1] ? ld[s - 1] : (c[s] ? d : ld[s]);
-    li[s] = c[s - 1] ? li[s - 1] : (c[s] ? id : li[s]);
+  for (int st = KC / 2; st > 0; st >>= 1) {
+    // the stage's KC/2 exchanges (i, i + st), i without bit st, two at a time
+#pragma unroll
+    for (int p = 0; p < KC / 2; p += 2) {
+      const int i0 = (p / st) * 2 * st + p % st, i1 = ((p + 1) / st) * 2 * st + (p + 1) % st;
+      kb_ce2(l[i0], l[i0 + st], l[i1], l[i1 + st]);
+    }
   }
-  ld[0] = c[0] ? d : ld[0];
-  li[0] = c[0] ? id : li[0];
 }
 
 // Work split: query blocks of 256 and reference slices (one workgroup each).
@@ -123,8 +202,7 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
     const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb, int slices,
     const float* __restrict__ qn, const float* __restrict__ rn, int2* __restrict__ part) {
-  __shared__ float s_qd[KB_WAVES][KB_QCAP][64];
-  __shared__ int s_qi[KB_WAVES][KB_QCAP][64];
+  __shared__ uint64_t s_q[KB_WAVES][KB_QCAP][64];
 
   // logical block = ((n * slices) + slice) * nqb + query block: the blocks
   // reading one slice are consecutive, hence on one XCD
@@ -161,26 +239,26 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
   const int tps = (ntiles + slices - 1) / slices;
   const int t0 = min(sl * tps, ntiles), t1 = min(ntiles, t0 + tps);
 
-  float ld[KC];
-  int li[KC];
+  uint64_t lk[KC];  // this lane's list, ascending keys
 #pragma unroll
-  for (int s = 0; s < KC; ++s) {
-    ld[s] = Lim<float>::inf();
-    li[s] = KB_NONE;
-  }
+  for (int s = 0; s < KC; ++s) lk[s] = kb_key(Lim<float>::inf(), KB_NONE);
   int nq_ = 0;  // queued candidates of this lane
-  // insert the queue in order: each pass a lane first skips (cheaply) the
-  // entries no longer below its list's last one, then inserts its next entry,
-  // so the passes number the largest count of useful insertions in the wave
-  auto drain = [&]() {
-    int k = 0;
-    for (;;) {
-      while (k < nq_ && !(s_qd[w][k][lane] < ld[KC - 1])) ++k;
-      if (__ballot(k < nq_) == 0) break;
-      if (k < nq_) {
-        kb_insert<KC>(ld, li, s_qd[w][k][lane], s_qi[w][k][lane]);
-        ++k;
+  // merge the queue into the list 8 entries at a time (slots past the lane's
+  // count read as ~0): a sorting network, then a bitonic merge, all in
+  // registers with fixed indices; a stale entry (pushed against an older
+  // threshold) simply falls off the end
+  auto drain = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int g8 = 0; g8 < KB_QCAP / 8; ++g8) {
+      if (__ballot(nq_ > 8 * g8) == 0) break;
+      uint64_t x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint64_t e = s_q[w][8 * g8 + i][lane];
+        x[i] = 8 * g8 + i < nq_ ? e : ~0ull;
       }
+      kb_sort8(x);
+      kb_merge8<KC>(lk, x);
     }
     nq_ = 0;
   };
@@ -191,7 +269,7 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
   // zeroed at use), so they issue together, one tile ahead.
   bf8_t an[KS];
   float4 rn4[8];  // norms of rows 4i .. 4i + 3
-  auto load_rows = [&](int t) {
+  auto load_rows = [&](int t) __attribute__((always_inline)) {
     const int tc = min(t, ntiles - 1), base = tc * KB_T;  // a tile past the slice re-reads the last
     const __bf16* __restrict__ ra = rb + (size_t)min(base + j, L2 - 1) * D;
 #pragma unroll
@@ -202,8 +280,11 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) rn4[i] = *reinterpret_cast<const float4*>(rr + base + 4 * i);
   };
-  if (t0 < t1) load_rows(t0);
-  for (int t = t0; t < t1; ++t) {
+  // Tile t: multiply, swap, filter, queue.  PARTIAL: the tile may hold rows
+  // past L2 (only the slice's last tile can), whose distances become +inf;
+  // the full tiles carry no such check.
+  auto tile = [&](int t, auto partial_tag) __attribute__((always_inline)) {
+    constexpr bool PARTIAL = decltype(partial_tag)::value;
     const int base = t * KB_T;
     bf8_t a[KS];
 #pragma unroll
@@ -227,51 +308,52 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
       acc0[v] = __uint_as_float(r[0]);
       acc1[v] = __uint_as_float(r[1]);
     }
-    // Two halves of 16 rows (8-row groups 2c, 2c + 1), in increasing row
-    // order.  The filter compares the unclamped value (a negative one passes
-    // it, and the pushed value is clamped at 0); only the last tile can hold
-    // rows past L2.
-    const bool partial = base + KB_T > L2;
-    {
+    // Two halves of 16 rows (8-row groups 2c, 2c + 1).  The filter compares
+    // the unclamped value (a negative one passes it, and the pushed value is
+    // clamped at 0).
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const float thr = ld[KC - 1];
-        float dv[16];
-        uint32_t m = 0;  // bit v: row 16c + v is below the list's end
+    for (int c = 0; c < 2; ++c) {
+      const float thr = __uint_as_float((uint32_t)(lk[KC - 1] >> 32));
+      float dv[16];
+      uint32_t m = 0;  // bit 15 - v: row 16c + v is below the list's end
 #pragma unroll
-        for (int gg = 0; gg < 2; ++gg) {
-          const int g = 2 * c + gg;
+      for (int gg = 0; gg < 2; ++gg) {
+        const int g = 2 * c + gg;
 #pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const float4 rq = r4[2 * g + hh];  // rows 8g + 4hh ..
-            const float rv[4] = {rq.x, rq.y, rq.z, rq.w};
+        for (int hh = 0; hh < 2; ++hh) {
+          const float4 rq = r4[2 * g + hh];  // rows 8g + 4hh ..
+          const float rv[4] = {rq.x, rq.y, rq.z, rq.w};
+          float d4[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float a = hh ? acc1[4 * g + e] : acc0[4 * g + e];
-              float d = __builtin_fmaf(-2.f, a, qq + rv[e]);
-              if (partial) d = base + 8 * g + 4 * hh + e < L2 ? d : Lim<float>::inf();
-              const int v = 8 * gg + 4 * hh + e;  // row 16c + v
-              dv[v] = d;
-              m |= (d < thr ? 1u : 0u) << v;
-            }
+          for (int e = 0; e < 4; ++e) {
+            const float a = hh ? acc1[4 * g + e] : acc0[4 * g + e];
+            float d = __builtin_fmaf(-2.f, a, qq + rv[e]);
+            if constexpr (PARTIAL) d = base + 8 * g + 4 * hh + e < L2 ? d : Lim<float>::inf();
+            dv[8 * gg + 4 * hh + e] = d;  // row 16c + 8gg + 4hh + e
+            d4[e] = d;
           }
+          m = push_lt4(m, d4[0], d4[1], d4[2], d4[3], thr);
         }
-        if (__ballot(m != 0) != 0) {  // some lane has a candidate in these rows
-          if (__ballot(nq_ + __builtin_popcount(m) > KB_QCAP) != 0) drain();  // queues within capacity
-          // only the set bits: the wave pays max-over-lanes(candidates), not 16
-          // rows of branches (thr may predate a drain: a stale entry inserts
-          // as a no-op)
-          while (m) {
-            const int v = __builtin_ctz(m);
-            m &= m - 1;
-            s_qd[w][nq_][lane] = fmaxf(kb_sel16(dv, v), 0.f);
-            s_qi[w][nq_][lane] = base + 16 * c + v;
-            ++nq_;
-          }
+      }
+      if (__ballot(m != 0) != 0) {  // some lane has a candidate in these rows
+        if (__ballot(nq_ + __builtin_popcount(m) > KB_QCAP) != 0) drain();  // queues within capacity
+        // only the set bits: the wave pays max-over-lanes(candidates), not 16
+        // rows of branches (thr may predate a drain: a stale entry is merged
+        // and falls off the list's end; the queue's order is immaterial)
+        while (m) {
+          const int v = 15 - __builtin_ctz(m);
+          m &= m - 1;
+          s_q[w][nq_][lane] = kb_key(fmaxf(kb_sel16(dv, v), 0.f), base + 16 * c + v);
+          ++nq_;
         }
       }
     }
-  }
+  };
+  const int tfull = min(t1, max(t0, L2 / KB_T));  // tiles before tfull lie below L2
+  if (t0 < t1) load_rows(t0);
+  int t = t0;
+  for (; t < tfull; ++t) tile(t, std::false_type{});
+  for (; t < t1; ++t) tile(t, std::true_type{});
   drain();
 
   // the first K entries of this lane's list
@@ -279,7 +361,7 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
     int2* __restrict__ out = part + (((size_t)n * P1 + q) * slices + sl) * K;
 #pragma unroll
     for (int s = 0; s < KC; ++s)
-      if (s < K) out[s] = make_int2(__float_as_int(ld[s]), li[s]);
+      if (s < K) out[s] = make_int2((int)(uint32_t)(lk[s] >> 32), (int)(uint32_t)lk[s]);
   }
 }
 

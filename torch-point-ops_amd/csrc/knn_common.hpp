@@ -49,80 +49,105 @@ __device__ __forceinline__ void first_max(const T (&sd)[KC], int K, T& m, int& m
 }
 
 // Broadcast a wave-uniform value into a VGPR so the subtractions that use it
-// are VGPR-only VALU ops (an SGPR source costs 4 cycles per wave64 op).
+// are VGPR-only VALU ops (an SGPR source costs 4 cycles per wave64 op).  The
+// empty asm only pins the value to a VGPR: the compiler emits the move (and
+// any wait it needs) itself.
 __device__ __forceinline__ float to_vgpr(float s) {
-  float v;
-  asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(s));
+  float v = s;
+  asm("" : "+v"(v));
   return v;
 }
 __device__ __forceinline__ double to_vgpr(double s) { return s; }
 __device__ __forceinline__ half_t to_vgpr(half_t s) { return s; }
 
-// mask = 2 * mask + (d < thr): one compare and one add-with-carry.
-__device__ __forceinline__ uint32_t push_lt(uint32_t mask, float d, float thr) {
+// Inline asm on this GPU (gfx950, as gfx942) must not read an SGPR or vcc
+// that a VALU op wrote fewer than two wait states before: the compiler
+// inserts those waits between its own instructions but not inside or in
+// front of an asm statement.  The asm below either reads VGPRs only or
+// spaces each such read itself.
+
+// mask = 16 * mask + 8 (d0 < thr) + 4 (d1 < thr) + 2 (d2 < thr) + (d3 < thr):
+// four compares into four SGPR pairs, then four add-with-carry doublings;
+// each carry-in is read three instructions after its compare wrote it.
+__device__ __forceinline__ uint32_t push_lt4(uint32_t mask, float d0, float d1, float d2, float d3,
+                                             float thr) {
   uint32_t r;
-  asm("v_cmp_lt_f32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %3, %3, vcc"
-      : "=v"(r)
-      : "v"(d), "v"(thr), "v"(mask)
+  uint64_t c0, c1, c2, c3;
+  asm("v_cmp_lt_f32 %1, %6, %10\n\t"
+      "v_cmp_lt_f32 %2, %7, %10\n\t"
+      "v_cmp_lt_f32 %3, %8, %10\n\t"
+      "v_cmp_lt_f32 %4, %9, %10\n\t"
+      "v_addc_co_u32 %0, vcc, %5, %5, %1\n\t"
+      "v_addc_co_u32 %0, vcc, %0, %0, %2\n\t"
+      "v_addc_co_u32 %0, vcc, %0, %0, %3\n\t"
+      "v_addc_co_u32 %0, vcc, %0, %0, %4"
+      : "=&v"(r), "=&s"(c0), "=&s"(c1), "=&s"(c2), "=&s"(c3)
+      : "v"(mask), "v"(d0), "v"(d1), "v"(d2), "v"(d3), "v"(thr)
       : "vcc");
   return r;
 }
-__device__ __forceinline__ uint32_t push_lt(uint32_t mask, double d, double thr) {
-  return mask + mask + (uint32_t)(d < thr);
-}
-__device__ __forceinline__ uint32_t push_lt(uint32_t mask, half_t d, half_t thr) {
-  return mask + mask + (uint32_t)(d < thr);
+template <typename T>
+__device__ __forceinline__ uint32_t push_lt4(uint32_t mask, T d0, T d1, T d2, T d3, T thr) {
+  return 16 * mask + 8 * (uint32_t)(d0 < thr) + 4 * (uint32_t)(d1 < thr) +
+         2 * (uint32_t)(d2 < thr) + (uint32_t)(d3 < thr);
 }
 
-// Per-lane select between two registers by a lane mask (bit set -> b).  Kept
-// as v_cndmask so the compiler cannot turn the select tree below back into a
-// dynamically indexed (stack) array.
-__device__ __forceinline__ uint32_t csel_u32(uint64_t m, uint32_t a, uint32_t b) {
+// Per-lane selects by a lane mask held in a VGPR (all ones: b, zero: a).
+// v_bfi_b32 reads VGPRs only.  Kept as asm so that the compiler cannot turn
+// the select trees below back into dynamically indexed (stack) arrays.
+__device__ __forceinline__ uint32_t vsel_u32(uint32_t sel, uint32_t a, uint32_t b) {
   uint32_t r;
-  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(m));
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(sel), "v"(b), "v"(a));
   return r;
 }
-__device__ __forceinline__ float csel(uint64_t m, float a, float b) {
-  return __uint_as_float(csel_u32(m, __float_as_uint(a), __float_as_uint(b)));
+__device__ __forceinline__ float csel(uint32_t sel, float a, float b) {
+  return __uint_as_float(vsel_u32(sel, __float_as_uint(a), __float_as_uint(b)));
 }
-__device__ __forceinline__ double csel(uint64_t m, double a, double b) {
+__device__ __forceinline__ double csel(uint32_t sel, double a, double b) {
   const uint64_t x = __double_as_longlong(a), y = __double_as_longlong(b);
-  const uint64_t lo = csel_u32(m, (uint32_t)x, (uint32_t)y);
-  const uint64_t hi = csel_u32(m, (uint32_t)(x >> 32), (uint32_t)(y >> 32));
+  const uint64_t lo = vsel_u32(sel, (uint32_t)x, (uint32_t)y);
+  const uint64_t hi = vsel_u32(sel, (uint32_t)(x >> 32), (uint32_t)(y >> 32));
   return __longlong_as_double((long long)((hi << 32) | lo));
 }
-__device__ __forceinline__ half_t csel(uint64_t m, half_t a, half_t b) {
+__device__ __forceinline__ half_t csel(uint32_t sel, half_t a, half_t b) {
   const uint32_t x = __builtin_bit_cast(uint16_t, a), y = __builtin_bit_cast(uint16_t, b);
-  return __builtin_bit_cast(half_t, (uint16_t)csel_u32(m, x, y));
+  return __builtin_bit_cast(half_t, (uint16_t)vsel_u32(sel, x, y));
+}
+// all ones where bit k of x is set (one bit-field extract)
+__device__ __forceinline__ uint32_t bit_mask(uint32_t x, int k) {
+  return (uint32_t)((int32_t)(x << (31 - k)) >> 31);
 }
 
-// Slot ms of the lane's MinK takes (d, j): a compare and a select per slot,
+// Slot ms of the lane's MinK takes (d, j): a mask and a select per slot,
 // written with explicit selects so that the compiler cannot lower the
 // dynamically indexed store into a branch tree (which lanes that diverge
 // would all walk).
 template <typename T, int KC>
 __device__ __forceinline__ void mink_put(T (&sd)[KC], int (&si)[KC], int ms, T d, int j) {
+  static_assert(KC <= 32, "one bit per slot");
+  const uint32_t one = 1u << ms;
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
-    const uint64_t hit = __ballot(s == ms);
+    const uint32_t hit = bit_mask(one, s);
     sd[s] = csel(hit, sd[s], d);
-    si[s] = (int)csel_u32(hit, (uint32_t)si[s], (uint32_t)j);
+    si[s] = (int)vsel_u32(hit, (uint32_t)si[s], (uint32_t)j);
   }
 }
 template <typename T, int KC>
 __device__ __forceinline__ void mink_put(T (&sd)[KC], int ms, T d) {
+  static_assert(KC <= 32, "one bit per slot");
+  const uint32_t one = 1u << ms;
 #pragma unroll
-  for (int s = 0; s < KC; ++s) sd[s] = csel(__ballot(s == ms), sd[s], d);
+  for (int s = 0; s < KC; ++s) sd[s] = csel(bit_mask(one, s), sd[s], d);
 }
 
 // d[c] for a per-lane c in [0, 32): a 5-level select tree over registers
-// (one ballot per level, 31 selects).  Inactive lanes take no part: both the
-// ballots and the selects run under the current exec mask.
+// (a lane mask per level, 31 selects).
 template <typename T>
 __device__ __forceinline__ T select32(const T (&d)[KNN_CHUNK], int c) {
   T a[16], b[8], e[4], f[2];
-  const uint64_t m0 = __ballot(c & 1), m1 = __ballot(c & 2), m2 = __ballot(c & 4);
-  const uint64_t m3 = __ballot(c & 8), m4 = __ballot(c & 16);
+  const uint32_t m0 = bit_mask(c, 0), m1 = bit_mask(c, 1), m2 = bit_mask(c, 2);
+  const uint32_t m3 = bit_mask(c, 3), m4 = bit_mask(c, 4);
 #pragma unroll
   for (int i = 0; i < 16; ++i) a[i] = csel(m0, d[2 * i], d[2 * i + 1]);
 #pragma unroll

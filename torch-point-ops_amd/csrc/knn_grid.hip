@@ -363,7 +363,7 @@ __global__ __launch_bounds__(256) void knn_grid_kernel(
     // entries l % 16 (b = 0) and 16 + l % 16 (b = 1).  Entries past cn are
     // +inf.  The distances go to LDS; mask bit 31 - c flags entry c.
     auto chunk = [&](const float (&bx)[2], const float (&by)[2], const float (&bz)[2], int cn) {
-      uint32_t mask = 0;
+      float dd[KNN_CHUNK];
       kg_static_for(
           [&](auto cc) {
             constexpr int c = decltype(cc)::value;
@@ -371,9 +371,13 @@ __global__ __launch_bounds__(256) void knn_grid_kernel(
                                     row_bcast<c % 16>(bz[c / 16]));
             d = c < cn ? d : Lim<float>::inf();
             dl[64 * c] = d;
-            mask = push_lt(mask, d, thr);
+            dd[c] = d;
           },
           std::make_integer_sequence<int, KNN_CHUNK>{});
+      uint32_t mask = 0;
+#pragma unroll
+      for (int c = 0; c < KNN_CHUNK; c += 4)
+        mask = push_lt4(mask, dd[c], dd[c + 1], dd[c + 2], dd[c + 3], thr);
       return mask;
     };
     // this lane's candidates of the chunk in order, against the current
