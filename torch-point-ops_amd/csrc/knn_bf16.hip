@@ -161,14 +161,15 @@ __device__ __forceinline__ void kb_sort8(uint64_t (&x)[8]) {
   kb_ce2(x[5], x[6], t, t);  // the layer's third exchange, paired with a no-op
 }
 
-// l := the KC smallest of the sorted list l and the sorted keys x, sorted.
-// The list's last 8 take the minimum with x reversed (an ascending and a
-// descending run: the KC smallest, as a bitonic sequence), then log2(KC)
-// half-cleaner stages sort it.
-template <int KC>
-__device__ __forceinline__ void kb_merge8(uint64_t (&l)[KC], const uint64_t (&x)[8]) {
+// l := the KC smallest of the sorted list l and the NB <= KC sorted keys x,
+// sorted.  The list's last NB take the minimum with x reversed (an ascending
+// and a descending run: the KC smallest, as a bitonic sequence), then
+// log2(KC) half-cleaner stages sort it.
+template <int KC, int NB>
+__device__ __forceinline__ void kb_merge(uint64_t (&l)[KC], const uint64_t (&x)[NB]) {
+  static_assert(NB % 2 == 0 && NB <= KC, "pairs of exchanges");
 #pragma unroll
-  for (int i = 0; i < 8; i += 2) kb_min2(l[KC - 8 + i], x[7 - i], l[KC - 7 + i], x[6 - i]);
+  for (int i = 0; i < NB; i += 2) kb_min2(l[KC - NB + i], x[NB - 1 - i], l[KC - NB + 1 + i], x[NB - 2 - i]);
 #pragma unroll
   for (int st = KC / 2; st > 0; st >>= 1) {
     // the stage's KC/2 exchanges (i, i + st), i without bit st, two at a time
@@ -201,7 +202,7 @@ template <int KS, bool HALF, int KC>
 __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
     const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb, int slices,
-    const float* __restrict__ qn, const float* __restrict__ rn, int2* __restrict__ part) {
+    const float* __restrict__ qn, const float* __restrict__ rn, uint64_t* __restrict__ part) {
   __shared__ uint64_t s_q[KB_WAVES][KB_QCAP][64];
 
   // logical block = ((n * slices) + slice) * nqb + query block: the blocks
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
         x[i] = 8 * g8 + i < nq_ ? e : ~0ull;
       }
       kb_sort8(x);
-      kb_merge8<KC>(lk, x);
+      kb_merge<KC, 8>(lk, x);
     }
     nq_ = 0;
   };
@@ -358,69 +359,87 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
 
   // the first K entries of this lane's list
   if (q < P1 && q < l1) {
-    int2* __restrict__ out = part + (((size_t)n * P1 + q) * slices + sl) * K;
+    // entry s of (cloud n, slice sl) for all queries is one run of P1 keys:
+    // a wave's stores are 64 consecutive keys
+    uint64_t* __restrict__ out = part + (size_t)(n * slices + sl) * K * P1 + q;
 #pragma unroll
     for (int s = 0; s < KC; ++s)
-      if (s < K) out[s] = make_int2((int)(uint32_t)(lk[s] >> 32), (int)(uint32_t)lk[s]);
+      if (s < K) out[(size_t)s * P1] = lk[s];
   }
 }
 
-// One thread per query row: merge its nl sorted lists of K, smallest
-// (distance, index) first; rows past lengths1 and empty slots are (0, 0).
-template <int MAXL>
-__global__ __launch_bounds__(256) void knn_bf16_merge_kernel(const int2* __restrict__ part,
+// Two lanes per query row (lanes j and j + 32 of a wave; 32 rows a wave):
+// each merges its half of the row's nl slice lists (sorted keys, K a list,
+// padded to KC with the empty key) in registers, v_permlane32_swap gives both
+// lanes both halves' lists, and both merge those; lane j writes entries
+// [0, KC/2) of the row, lane j + 32 entries [KC/2, KC) (those below K).  Rows
+// past lengths1 and empty entries are (0, 0).
+template <int KC>
+__global__ __launch_bounds__(256) void knn_bf16_merge_kernel(const uint64_t* __restrict__ part,
                                                              const int64_t* __restrict__ len1,
                                                              int64_t rows, int P1, int K, int nl,
                                                              int64_t* __restrict__ idxs,
                                                              __bf16* __restrict__ dists) {
-  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int lane = lane_id(), j = lane & 31, h = lane >> 5;
+  const int64_t row = ((int64_t)blockIdx.x * KB_WAVES + wave_id()) * 32 + j;
+  const uint64_t empty = kb_key(Lim<float>::inf(), KB_NONE);
+  bool real = false;
+  if (row < rows) {
+    const int64_t n = row / P1;
+    int64_t l1 = len1[n];
+    l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+    real = row - n * P1 < l1;
+  }
+  uint64_t a[KC];
+#pragma unroll
+  for (int s = 0; s < KC; ++s) a[s] = empty;
+  const int hl = (nl + 1) / 2, L0 = h * hl, L1 = min(nl, L0 + hl);
+  if (real && L0 < L1) {
+    // entry s of list L: part[((n nl + L) K + s) P1 + q], so the 32 lanes
+    // of a half-wave read consecutive keys; the next list is loaded while
+    // the current one is merged
+    const int64_t n = row / P1;
+    const uint64_t* __restrict__ base = part + (size_t)n * nl * K * P1 + (row - n * P1);
+    auto load = [&](uint64_t (&b)[KC], int L) __attribute__((always_inline)) {
+#pragma unroll
+      for (int s = 0; s < KC; ++s) b[s] = s < K ? base[((size_t)L * K + s) * P1] : empty;
+    };
+    load(a, L0);
+    uint64_t b[KC];
+    if (L0 + 1 < L1) load(b, L0 + 1);
+    for (int L = L0 + 1; L < L1; ++L) {
+      uint64_t c[KC];
+      if (L + 1 < L1) load(c, L + 1);
+      kb_merge<KC, KC>(a, b);
+#pragma unroll
+      for (int s = 0; s < KC; ++s) b[s] = c[s];
+    }
+  }
+  // every lane takes part: lane j's list to lanes j and j + 32 as x, lane
+  // j + 32's as y (swap(x, y) leaves x = [x_lo, y_lo], y = [x_hi, y_hi])
+  uint64_t x[KC], y[KC];
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    const uint32_t lo = (uint32_t)a[s], hi = (uint32_t)(a[s] >> 32);
+    const auto rl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto rh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    x[s] = ((uint64_t)rh[0] << 32) | rl[0];
+    y[s] = ((uint64_t)rh[1] << 32) | rl[1];
+  }
+  kb_merge<KC, KC>(x, y);
   if (row >= rows) return;
-  const int64_t n = row / P1;
-  const int q = (int)(row - n * P1);
-  int64_t l1 = len1[n];
-  l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
   int64_t* __restrict__ io = idxs + row * K;
   __bf16* __restrict__ dout = dists + row * K;
-  if (q >= l1) {
-    for (int k = 0; k < K; ++k) {
-      io[k] = 0;
-      dout[k] = (__bf16)0.f;
-    }
-    return;
-  }
-  const int2* __restrict__ lists = part + row * (int64_t)nl * K;
-  int ptr[MAXL];
-  float hd[MAXL];
-  int hi[MAXL];
+  const uint32_t upper = bit_mask((uint32_t)h, 0);
 #pragma unroll
-  for (int L = 0; L < MAXL; ++L) {
-    ptr[L] = 0;
-    const int2 e = L < nl ? lists[(size_t)L * K] : make_int2(__float_as_int(Lim<float>::inf()), KB_NONE);
-    hd[L] = __int_as_float(e.x);
-    hi[L] = e.y;
-  }
-  for (int k = 0; k < K; ++k) {
-    float bd = hd[0];
-    int bi = hi[0], bl = 0;
-#pragma unroll
-    for (int L = 1; L < MAXL; ++L) {
-      if (hd[L] < bd || (hd[L] == bd && hi[L] < bi)) {
-        bd = hd[L];
-        bi = hi[L];
-        bl = L;
-      }
-    }
-    const bool real = bi != KB_NONE;  // fewer than K references
-    io[k] = real ? (int64_t)bi : 0;
-    dout[k] = real ? (__bf16)bd : (__bf16)0.f;
-#pragma unroll
-    for (int L = 0; L < MAXL; ++L) {
-      if (L == bl) {
-        const int p = ++ptr[L];
-        const int2 e = p < K ? lists[(size_t)L * K + p] : make_int2(__float_as_int(Lim<float>::inf()), KB_NONE);
-        hd[L] = __int_as_float(e.x);
-        hi[L] = e.y;
-      }
+  for (int s = 0; s < KC / 2; ++s) {
+    const int k = s + (h ? KC / 2 : 0);
+    const uint32_t kl = vsel_u32(upper, (uint32_t)x[s], (uint32_t)x[s + KC / 2]);
+    const uint32_t kh = vsel_u32(upper, (uint32_t)(x[s] >> 32), (uint32_t)(x[s + KC / 2] >> 32));
+    if (k < K) {
+      const bool ok = real && kl != (uint32_t)KB_NONE;  // fewer than K references
+      io[k] = ok ? (int64_t)kl : 0;
+      dout[k] = ok ? (__bf16)__uint_as_float(kh) : (__bf16)0.f;
     }
   }
 }
@@ -440,7 +459,7 @@ bool knn_bf16_supported(int64_t D, int64_t K, int norm) {
 template <int KS, bool HALF, int KC>
 static void kb_launch(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
                       int N, int P1, int P2, int D, int K, const float* qn, const float* rn,
-                      int2* part, hipStream_t s) {
+                      uint64_t* part, hipStream_t s) {
   const KbPlan p = kb_plan(N, P1, P2);
   hipLaunchKernelGGL((knn_bf16_slice_kernel<KS, HALF, KC>), dim3(N * p.nqb * p.slices), dim3(256), 0, s,
                      (const __bf16*)p1, (const __bf16*)p2, l1, l2, P1, P2, D, K, p.nqb, p.slices,
@@ -450,7 +469,7 @@ static void kb_launch(const void* p1, const void* p2, const int64_t* l1, const i
 template <int KC>
 static void kb_dispatch_ks(int D, const void* p1, const void* p2, const int64_t* l1,
                            const int64_t* l2, int N, int P1, int P2, int K, const float* qn,
-                           const float* rn, int2* part, hipStream_t s) {
+                           const float* rn, uint64_t* part, hipStream_t s) {
   // D % 8 == 0, 8 <= D <= 128: D / 8 = 2 KS - HALF
 #define KB_CASE(DD, KS_, HALF_) \
   case DD: kb_launch<KS_, HALF_, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, part, s); break;
@@ -470,8 +489,8 @@ void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const in
   const KbPlan p = kb_plan(N, P1, P2);
   float* qn = reinterpret_cast<float*>(ws);
   float* rn = qn + (size_t)N * kb_pad(P1);
-  int2* part = reinterpret_cast<int2*>(reinterpret_cast<char*>(ws) +
-                                       kb_align((int64_t)N * (kb_pad(P1) + kb_pad(P2)) * 4));
+  uint64_t* part = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(ws) +
+                                               kb_align((int64_t)N * (kb_pad(P1) + kb_pad(P2)) * 4));
   const int64_t r1 = (int64_t)N * P1, r2 = (int64_t)N * P2;
   if (r1 > 0)
     hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)std::min<int64_t>((r1 + 255) / 256, 65536)),
@@ -483,13 +502,11 @@ void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const in
   if (K <= 16) kb_dispatch_ks<16>(D, p1, p2, l1, l2, N, P1, P2, K, qn, rn, part, s);
   else kb_dispatch_ks<32>(D, p1, p2, l1, l2, N, P1, P2, K, qn, rn, part, s);
   const int nl = p.slices;
-  const dim3 mg((unsigned)((r1 + 255) / 256)), mb(256);
-  if (nl <= 4)
-    hipLaunchKernelGGL(knn_bf16_merge_kernel<4>, mg, mb, 0, s, (const int2*)part, l1, r1, P1, K, nl, idxs, (__bf16*)dists);
-  else if (nl <= 8)
-    hipLaunchKernelGGL(knn_bf16_merge_kernel<8>, mg, mb, 0, s, (const int2*)part, l1, r1, P1, K, nl, idxs, (__bf16*)dists);
+  const dim3 mg((unsigned)((r1 + 32 * KB_WAVES - 1) / (32 * KB_WAVES))), mb(64 * KB_WAVES);
+  if (K <= 16)
+    hipLaunchKernelGGL(knn_bf16_merge_kernel<16>, mg, mb, 0, s, part, l1, r1, P1, K, nl, idxs, (__bf16*)dists);
   else
-    hipLaunchKernelGGL(knn_bf16_merge_kernel<KB_MAX_SLICES>, mg, mb, 0, s, (const int2*)part, l1, r1, P1, K, nl, idxs, (__bf16*)dists);
+    hipLaunchKernelGGL(knn_bf16_merge_kernel<32>, mg, mb, 0, s, part, l1, r1, P1, K, nl, idxs, (__bf16*)dists);
 }
 
 }  // namespace tpo
