@@ -2,9 +2,12 @@
 // cores (the high-D path; the reference's knn_cuda_forward, knn.cu:295-398,
 // has no bfloat16 kernel and raises for it).
 //
-// Distances are squared L2 in float: d = |q|^2 + |r|^2 - 2 q.r, with the
-// bfloat16 products exact in float, q.r summed by v_mfma_f32_32x32x16_bf16 and
-// |q|^2, |r|^2 by a float FMA chain (knn_bf16_norms_kernel); d is clamped at 0.
+// Distances are squared L2 in float: d = |q|^2 + |r|^2 - 2 q.r, summed as one
+// v_mfma_f32_32x32x16_bf16 chain: the query operand is -2 q (exact in
+// bfloat16; the products are exact in float), and one more k-step adds |q|^2
+// and |r|^2 (float, each from an FMA chain over the point's bfloat16 values,
+// knn_bf16_norms_kernel) as three bfloat16 pieces each, whose sum is the float
+// exactly (for norms above ~1e-33); d is clamped at 0.
 // Each query's K nearest are returned sorted by (distance, index), distances
 // rounded to bfloat16; rows past lengths1 and slots past lengths2 are (0, 0)
 // as in the reference's version-2 layout.
@@ -85,6 +88,28 @@ __device__ __forceinline__ float kb_sel16(const float (&d)[16], int v) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) e[i] = csel(m2, b[2 * i], b[2 * i + 1]);
   return csel(m3, e[0], e[1]);
+}
+
+// The norm operand of the extra k-step: [h, m, l, 1, 1, 1, 0, 0] for a
+// reference row, [1, 1, 1, h, m, l, 0, 0] for a query column, with
+// h + m + l = x: x rounded to bfloat16, the (exact) remainder rounded, and the
+// rest, itself exact in bfloat16 unless it is denormal (|x| below ~1e-33: an
+// absolute error under 1e-38).  x = +inf gives NaN pieces.
+__device__ __forceinline__ bf8_t kb_norm_operand(float x, bool row) {
+  const __bf16 hi = (__bf16)x;
+  const float r = x - (float)hi;
+  const __bf16 mi = (__bf16)r;
+  const __bf16 lo = (__bf16)(r - (float)mi);
+  const __bf16 one = (__bf16)1.f, z = (__bf16)0.f;
+  return row ? bf8_t{hi, mi, lo, one, one, one, z, z} : bf8_t{one, one, one, hi, mi, lo, z, z};
+}
+
+// -2 v elementwise (exact in bfloat16 below the overflow range)
+__device__ __forceinline__ bf8_t kb_neg2(bf8_t v) {
+  bf8_t r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (__bf16)(-2.f * (float)v[i]);
+  return r;
 }
 
 // A list entry is one 64-bit key: the distance's bits above the reference
@@ -198,8 +223,11 @@ static KbPlan kb_plan(int64_t N, int64_t P1, int64_t P2) {
 
 // KS k-steps of 16 dims; HALF: D % 16 == 8, so the upper half of the last
 // step lies past D (its operands are zero)
+// (two waves a SIMD: one wave's MFMA chain runs under the other's selection
+// work; the register budget of 256 is held with a few spills outside the tile
+// loop's hot path)
 template <int KS, bool HALF, int KC>
-__global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void knn_bf16_slice_kernel(
     const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb, int slices,
     const float* __restrict__ qn, const float* __restrict__ rn, uint64_t* __restrict__ part) {
@@ -218,20 +246,28 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
   const int qw = qb * KB_QW + 64 * w;  // the wave's blocks: queries qw + 32 b + column
   const int q = qw + lane;             // this lane's query after the swap: block h, column j
 
+  // k-steps of the MFMA chain: KS of dims, and the norms' step -- the upper
+  // half of the last dims step when D % 16 == 8 (lanes h = 1 there lie past
+  // D), else a step of its own (in its lower half)
+  constexpr int KX = HALF ? KS : KS + 1, XS = KX - 1, XH = HALF ? 1 : 0;
   // column operands of both blocks: query qw + 32 b + j, dims 16s + 8h .. + 7
-  // (zero past D)
-  bf8_t bq0[KS], bq1[KS];
+  // times -2 (zero past D), then the query's norm pieces
+  bf8_t bq0[KX], bq1[KX];
   {
-    const __bf16* __restrict__ qp0 = p1 + ((size_t)n * P1 + min(qw + j, P1 - 1)) * D;
-    const __bf16* __restrict__ qp1 = p1 + ((size_t)n * P1 + min(qw + 32 + j, P1 - 1)) * D;
+    const int c0 = min(qw + j, P1 - 1), c1 = min(qw + 32 + j, P1 - 1);
+    const __bf16* __restrict__ qp0 = p1 + ((size_t)n * P1 + c0) * D;
+    const __bf16* __restrict__ qp1 = p1 + ((size_t)n * P1 + c1) * D;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int d0 = 16 * s + 8 * h;
-      bq0[s] = d0 < D ? *reinterpret_cast<const bf8_t*>(qp0 + d0) : bf8_t{};
-      bq1[s] = d0 < D ? *reinterpret_cast<const bf8_t*>(qp1 + d0) : bf8_t{};
+      bq0[s] = d0 < D ? kb_neg2(*reinterpret_cast<const bf8_t*>(qp0 + d0)) : bf8_t{};
+      bq1[s] = d0 < D ? kb_neg2(*reinterpret_cast<const bf8_t*>(qp1 + d0)) : bf8_t{};
     }
+    const bf8_t x0 = kb_norm_operand(qn[(size_t)n * kb_pad(P1) + c0], false);
+    const bf8_t x1 = kb_norm_operand(qn[(size_t)n * kb_pad(P1) + c1], false);
+    bq0[XS] = h == XH ? x0 : (HALF ? bq0[XS] : bf8_t{});
+    bq1[XS] = h == XH ? x1 : (HALF ? bq1[XS] : bf8_t{});
   }
-  const float qq = qn[(size_t)n * kb_pad(P1) + min(q, P1 - 1)];
   const __bf16* __restrict__ rb = p2 + (size_t)n * P2 * D;
   const float* __restrict__ rr = rn + (size_t)n * kb_pad(P2);
 
@@ -265,39 +301,37 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
   };
 
   // Row operand of tile t for this lane: reference base + j, dims 16s + 8h
-  // .. + 7, and the norms of the lane's rows.  Loads are unconditional (row
-  // clamped into [0, L2), a half past D re-reads the step's lower half and is
-  // zeroed at use), so they issue together, one tile ahead.
+  // .. + 7, and the row's norm.  Loads are unconditional (row clamped into
+  // [0, L2), a half past D re-reads the step's lower half and is replaced at
+  // use), so they issue together, one tile ahead.  A row past L2 takes the
+  // norm +inf: its distances are NaN and never pass the filter.
   bf8_t an[KS];
-  float4 rn4[8];  // norms of rows 4i .. 4i + 3
+  float nn;
   auto load_rows = [&](int t) __attribute__((always_inline)) {
     const int tc = min(t, ntiles - 1), base = tc * KB_T;  // a tile past the slice re-reads the last
-    const __bf16* __restrict__ ra = rb + (size_t)min(base + j, L2 - 1) * D;
+    const int row = min(base + j, L2 - 1);
+    const __bf16* __restrict__ ra = rb + (size_t)row * D;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int d0 = (HALF && s == KS - 1) ? 16 * s : 16 * s + 8 * h;
       an[s] = *reinterpret_cast<const bf8_t*>(ra + d0);
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rn4[i] = *reinterpret_cast<const float4*>(rr + base + 4 * i);
+    nn = rr[row];
   };
-  // Tile t: multiply, swap, filter, queue.  PARTIAL: the tile may hold rows
-  // past L2 (only the slice's last tile can), whose distances become +inf;
-  // the full tiles carry no such check.
-  auto tile = [&](int t, auto partial_tag) __attribute__((always_inline)) {
-    constexpr bool PARTIAL = decltype(partial_tag)::value;
+  // Tile t: multiply, swap, filter, queue.
+  auto tile = [&](int t) __attribute__((always_inline)) {
     const int base = t * KB_T;
-    bf8_t a[KS];
+    bf8_t a[KX];
 #pragma unroll
     for (int s = 0; s < KS; ++s) a[s] = an[s];
-    if constexpr (HALF) a[KS - 1] = h ? bf8_t{} : a[KS - 1];
-    float4 r4[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r4[i] = rn4[i];
+    {
+      const bf8_t xr = kb_norm_operand(base + j < L2 ? nn : Lim<float>::inf(), true);
+      a[XS] = h == XH ? xr : (HALF ? a[XS] : bf8_t{});
+    }
     load_rows(t + 1);  // the next tile's loads are in flight during this one
     f16v_t acc0 = {}, acc1 = {};
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
+    for (int s = 0; s < KX; ++s) {
       acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq0[s], acc0, 0, 0, 0);
       acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq1[s], acc1, 0, 0, 0);
     }
@@ -322,14 +356,10 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
         const int g = 2 * c + gg;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const float4 rq = r4[2 * g + hh];  // rows 8g + 4hh ..
-          const float rv[4] = {rq.x, rq.y, rq.z, rq.w};
           float d4[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float a = hh ? acc1[4 * g + e] : acc0[4 * g + e];
-            float d = __builtin_fmaf(-2.f, a, qq + rv[e]);
-            if constexpr (PARTIAL) d = base + 8 * g + 4 * hh + e < L2 ? d : Lim<float>::inf();
+            const float d = hh ? acc1[4 * g + e] : acc0[4 * g + e];
             dv[8 * gg + 4 * hh + e] = d;  // row 16c + 8gg + 4hh + e
             d4[e] = d;
           }
@@ -350,11 +380,8 @@ __global__ __launch_bounds__(256) void knn_bf16_slice_kernel(
       }
     }
   };
-  const int tfull = min(t1, max(t0, L2 / KB_T));  // tiles before tfull lie below L2
   if (t0 < t1) load_rows(t0);
-  int t = t0;
-  for (; t < tfull; ++t) tile(t, std::false_type{});
-  for (; t < t1; ++t) tile(t, std::true_type{});
+  for (int t = t0; t < t1; ++t) tile(t);
   drain();
 
   // the first K entries of this lane's list
