@@ -205,23 +205,49 @@ __global__ __launch_bounds__(CH_BWD_THREADS) void chamfer_bwd_fused_kernel(
   const T* __restrict__ gd_oth = pg_oth.p + (uni_oth ? 0 : (size_t)b * n_oth);
   T* __restrict__ out = (c ? g2 : g1) + (size_t)b * n_own * 3;
 
-  // direct-term inputs of the first CH_BWD_PF points per thread, fetched
-  // now so their latency hides behind the staging and the scan
+  // Every phase issues all of its loads before it waits on any: the
+  // direct-term inputs of the first CH_BWD_PF points per thread (their nearest
+  // indices, then the other cloud's coordinates at them, which land during
+  // the staging and the scan), and the slice's coordinates for LDS, 8 values
+  // a thread per round.
   int pj[CH_BWD_PF];
   T pg[CH_BWD_PF], po[CH_BWD_PF][3];
 #pragma unroll
   for (int u = 0; u < CH_BWD_PF; ++u) {
     const int i = lo + (int)threadIdx.x + CH_BWD_THREADS * u;
-    const int j2 = i < hi ? idx_own[i] : -1;
-    const bool ok = j2 >= 0 && j2 < n_oth;
-    pj[u] = ok ? j2 : -1;
+    pj[u] = i < hi ? idx_own[i] : -1;
     pg[u] = i < hi ? (T)((uni_own ? u_own : gd_own[i]) * (T)2) : (T)0;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) po[u][k] = ok ? oth[3 * j2 + k] : (T)0;
   }
-  for (int t = threadIdx.x; t < 3 * (hi - lo); t += CH_BWD_THREADS) {
-    acc[t] = 0.f;
-    s_own[t] = (float)own[3 * lo + t];
+  const int nv = 3 * (hi - lo);
+  const T* __restrict__ own_s = own + 3 * lo;
+  for (int t0 = 0; t0 < nv; t0 += CH_BWD_THREADS * 8) {
+    T v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = t0 + (int)threadIdx.x + CH_BWD_THREADS * u;
+      v[u] = t < nv ? own_s[t] : (T)0;
+    }
+    if (t0 == 0) {
+#pragma unroll
+      for (int u = 0; u < CH_BWD_PF; ++u) {
+        const bool ok = pj[u] >= 0 && pj[u] < n_oth;
+        pj[u] = ok ? pj[u] : -1;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) po[u][k] = ok ? oth[3 * pj[u] + k] : (T)0;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = t0 + (int)threadIdx.x + CH_BWD_THREADS * u;
+      if (t < nv) {
+        acc[t] = 0.f;
+        s_own[t] = (float)v[u];
+      }
+    }
+  }
+  if (nv == 0) {
+#pragma unroll
+    for (int u = 0; u < CH_BWD_PF; ++u) pj[u] = -1;
   }
   __syncthreads();
   // other cloud's point j whose nearest point i is in [lo, hi)
@@ -238,16 +264,31 @@ __global__ __launch_bounds__(CH_BWD_THREADS) void chamfer_bwd_fused_kernel(
     const int4* __restrict__ iv = reinterpret_cast<const int4*>(idx_oth);
     const float4* __restrict__ rv = reinterpret_cast<const float4*>(oth);
     const float4* __restrict__ gv = reinterpret_cast<const float4*>(gd_oth);
-#pragma unroll 2
-    for (int q = threadIdx.x; q < n_oth / 4; q += CH_BWD_THREADS) {
-      const int4 ii = iv[q];
-      const float4 r0 = rv[3 * q], r1 = rv[3 * q + 1], r2 = rv[3 * q + 2];
-      float4 gg = make_float4(u_oth, u_oth, u_oth, u_oth);
-      if (!uni_oth) gg = gv[q];
-      scatter(4 * q, ii.x, r0.x, r0.y, r0.z, gg.x);
-      scatter(4 * q + 1, ii.y, r0.w, r1.x, r1.y, gg.y);
-      scatter(4 * q + 2, ii.z, r1.z, r1.w, r2.x, gg.z);
-      scatter(4 * q + 3, ii.w, r2.y, r2.z, r2.w, gg.w);
+    // four groups of four points per thread: all their loads before the
+    // first scatter
+    constexpr int U = 4;
+    const int nq4 = n_oth / 4;
+    for (int q0 = threadIdx.x; q0 < nq4; q0 += CH_BWD_THREADS * U) {
+      int4 ii[U];
+      float4 r[U][3], gg[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = min(q0 + CH_BWD_THREADS * u, nq4 - 1);  // a repeat is not scattered
+        ii[u] = iv[q];
+        r[u][0] = rv[3 * q];
+        r[u][1] = rv[3 * q + 1];
+        r[u][2] = rv[3 * q + 2];
+        gg[u] = uni_oth ? make_float4(u_oth, u_oth, u_oth, u_oth) : gv[q];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = q0 + CH_BWD_THREADS * u;
+        if (q >= nq4) break;
+        scatter(4 * q, ii[u].x, r[u][0].x, r[u][0].y, r[u][0].z, gg[u].x);
+        scatter(4 * q + 1, ii[u].y, r[u][0].w, r[u][1].x, r[u][1].y, gg[u].y);
+        scatter(4 * q + 2, ii[u].z, r[u][1].z, r[u][1].w, r[u][2].x, gg[u].z);
+        scatter(4 * q + 3, ii[u].w, r[u][2].y, r[u][2].z, r[u][2].w, gg[u].w);
+      }
     }
   } else {
 #pragma unroll 4
