@@ -158,10 +158,14 @@ int tpo_chamfer_loss_bwd(int dtype, const void* xyz1, const void* xyz2,
  *   spatial order, which is faster; results are identical.
  *   BF16 (no reference kernel; the reference raises): norm 2, D % 8 == 0,
  *   8 <= D <= 128, K <= 32, points 16-byte aligned, workspace required.
- *   Squared distances |q|^2 + |r|^2 - 2 q.r in float (q.r on the matrix
- *   cores), clamped at 0; each row's K nearest sorted by (distance, index),
- *   dists rounded to bfloat16; rows >= lengths1 and slots >= lengths2 are
- *   (0,0).  version is ignored and version_out receives -1.
+ *   Squared distances |q|^2 + |r|^2 - 2 q.r in float, summed on the matrix
+ *   cores (the norms, float sums of the bf16 squares, enter as exact
+ *   three-piece bf16 splits), clamped at 0; each row's K nearest sorted by
+ *   (distance, index), dists rounded to bfloat16; rows >= lengths1 and
+ *   slots >= lengths2 are (0,0).  version is ignored and version_out
+ *   receives -1.  For P2 >= 4096 the workspace also holds a per-query bound
+ *   sampled from 64 tiles of 32 references and a list of the rows it left
+ *   short, which are recomputed without it; results do not depend on it.
  *   If version_out is not NULL it receives the version that ran.
  */
 int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int64_t P2,

@@ -566,7 +566,7 @@ def test_bf16_equal_distances_take_lower_indices(tpo, dev):
     # exactly, on the rows whose three nearest distinct points are clearly
     # apart (float64 gaps above the error band)
     g = torch.Generator().manual_seed(91)
-    B, P1, P, D, K = 2, 256, 768, 64, 6
+    B, P1, P, D, K = 2, 256, 3072, 64, 6  # 12288 references: the sampled bound applies
     q = torch.randn(B, P1, D, generator=g).to(torch.bfloat16)
     r0 = torch.randn(B, P, D, generator=g).to(torch.bfloat16)
     r = torch.cat([r0.repeat_interleave(2, 1), r0.repeat_interleave(2, 1)], 1)
@@ -591,6 +591,73 @@ def test_bf16_equal_distances_take_lower_indices(tpo, dev):
             checked += 1
     assert checked > B * P1 // 2
     assert bool((d[..., :4] == d[..., :1]).all())
+
+
+def test_bf16_rows_the_sampled_bound_leaves_short_are_rerun(tpo, dev):
+    # Clouds of >= 4096 references first bound each query by the 8th smallest
+    # of its minimum distances over 64 sampled tiles of 32 references (tiles
+    # i * (tiles // 64)); only distances under the bound are candidates, and a
+    # row left with fewer than K is rerun without it.  Here the first 32
+    # queries of each cloud have 8 near copies in 8 different sampled tiles
+    # and their next 24 neighbours outside them: their bound admits 8
+    # candidates, so they take the rerun; the other queries have their near
+    # points outside the sample and keep the bound.  The lists must be the K
+    # nearest either way (float64 check).
+    g = torch.Generator().manual_seed(17)
+    B, P1, P2, D, K = 2, 64, 65536, 64, 32
+    l2 = torch.tensor([P2, 40000])
+    q = torch.randn(B, P1, D, generator=g)
+    q = q / q.norm(dim=-1, keepdim=True)
+    r = torch.randn(B, P2, D, generator=g)
+    r = r / r.norm(dim=-1, keepdim=True)
+    for b in range(B):
+        tiles = (int(l2[b]) + 31) // 32
+        stride = tiles // 64
+        sampled = torch.cat([torch.arange(32) + 32 * stride * i for i in range(64)])
+        others = torch.tensor(sorted(set(range(int(l2[b]))) - set(sampled.tolist())))
+        pick = others[torch.randperm(len(others), generator=g)]
+        for k in range(P1):
+            if k < 32:
+                slot = 8 * k + torch.arange(8)  # tiles slot % 64, row slot // 64 of the tile
+                near = 32 * stride * (slot % 64) + slot // 64
+                r[b, near] = q[b, k] + 0.02 * torch.randn(8, D, generator=g)
+                mid = pick[24 * k:24 * k + 24]
+                r[b, mid] = q[b, k] + 0.06 * torch.randn(24, D, generator=g)
+            else:
+                spread = pick[24 * k:24 * k + 40]
+                r[b, spread] = q[b, k] + 0.04 * torch.randn(40, D, generator=g)
+    q, r = q.to(torch.bfloat16), r.to(torch.bfloat16)
+    l1 = torch.tensor([P1, 50])
+    idx, d = raw(q, r, l1, l2, 2, K, -1, dev)
+    check_bf16_knn(idx, d, q, r, l1, l2, K)
+    # the same call through the C ABI with a caller workspace, whose rerun
+    # counts (after the norms, the 8 slices' lists and the bound's parts)
+    # show that exactly the 32 planted rows of each cloud were rerun
+    import ctypes
+    from torch_point_ops import _native
+
+    lib = ctypes.CDLL(_native.HIP_LIB)
+    P, I = ctypes.c_void_p, ctypes.c_int64
+    lib.tpo_knn_fwd.argtypes = [ctypes.c_int, P, P, P, P, I, I, I, I, I, ctypes.c_int,
+                                ctypes.c_int, P, P, P, P, I, P]
+    lib.tpo_knn_workspace_size.argtypes = [ctypes.c_int, I, I, I, I, I, ctypes.c_int]
+    lib.tpo_knn_workspace_size.restype = I
+    size = lib.tpo_knn_workspace_size(3, B, P1, P2, D, K, 2)
+    ws = torch.zeros(size, dtype=torch.uint8, device=dev)
+    qd, rd, l1d, l2d = q.to(dev), r.to(dev), l1.to(dev), l2.to(dev)
+    idx2 = torch.empty(B, P1, K, dtype=torch.int64, device=dev)
+    d2 = torch.empty(B, P1, K, dtype=torch.bfloat16, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.tpo_knn_fwd(3, qd.data_ptr(), rd.data_ptr(), l1d.data_ptr(), l2d.data_ptr(), B, P1,
+                           P2, D, K, 2, -1, idx2.data_ptr(), d2.data_ptr(), None, ws.data_ptr(),
+                           size, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(idx2, idx.to(dev)) and torch.equal(d2, d.to(dev))
+    up = lambda x: (x + 255) // 256 * 256
+    at = up(B * (P1 + 32 * ((P2 + 31) // 32)) * 4) + up(B * P1 * 8 * K * 8) + up(B * P1 * 64 * 4)
+    assert at + up(B * 4) + up(B * P1 * 4) == size
+    counts = ws[at:at + 4 * B].cpu().view(torch.int32)
+    assert counts.tolist() == [32, 32]
 
 
 def test_bf16_knn_points_and_fallbacks(tpo, dev):

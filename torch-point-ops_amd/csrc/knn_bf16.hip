@@ -50,6 +50,13 @@ constexpr int KB_DMAX = 128;
 constexpr int KB_QCAP = 16;              // queued candidates per lane
 constexpr int KB_MAX_SLICES = 8;
 constexpr int KB_NONE = 0x7fffffff;      // index of an empty list entry
+// The sampled bound: the KB_TK-th smallest of each query's minimum distances
+// over KB_TS reference tiles spread over its cloud (KB_TP workgroups of query
+// blocks, KB_TS / KB_TP tiles each); clouds of fewer than 2 KB_TS tiles take
+// none.
+constexpr int KB_TS = 64;
+constexpr int KB_TP = 8;
+constexpr int KB_TK = 8;
 
 __host__ __device__ inline int64_t kb_pad(int64_t n) { return (n + 31) & ~(int64_t)31; }
 
@@ -206,6 +213,22 @@ __device__ __forceinline__ void kb_merge(uint64_t (&l)[KC], const uint64_t (&x)[
   }
 }
 
+// The next float above x (x finite; +inf and NaN give +inf): d < kb_next_up(x)
+// holds exactly when d <= x.
+__device__ __forceinline__ float kb_next_up(float x) {
+  if (!(x < Lim<float>::inf())) return Lim<float>::inf();
+  if (x == 0.f) return __uint_as_float(1u);
+  const uint32_t b = __float_as_uint(x);
+  return __uint_as_float(x > 0.f ? b + 1u : b - 1u);
+}
+
+// s := the KB_TK smallest of the sorted s and one more value (sorted)
+__device__ __forceinline__ void kb_tk_insert(float (&s)[KB_TK], float d) {
+#pragma unroll
+  for (int i = KB_TK - 1; i > 0; --i) s[i] = d < s[i - 1] ? s[i - 1] : (d < s[i] ? d : s[i]);
+  s[0] = d < s[0] ? d : s[0];
+}
+
 // Work split: query blocks of 256 and reference slices (one workgroup each).
 struct KbPlan {
   int nqb, slices;
@@ -230,8 +253,16 @@ template <int KS, bool HALF, int KC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void knn_bf16_slice_kernel(
     const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb, int slices,
-    const float* __restrict__ qn, const float* __restrict__ rn, uint64_t* __restrict__ part) {
+    const float* __restrict__ qn, const float* __restrict__ rn, uint64_t* __restrict__ part,
+    const float* __restrict__ taup, const int32_t* __restrict__ qlist,
+    const int32_t* __restrict__ qcount) {
   __shared__ uint64_t s_q[KB_WAVES][KB_QCAP][64];
+  // a tile's reference rows (D bfloat16 each, rows 2D + 16 bytes apart so a
+  // half-wave's 16-byte reads of 16 rows fall in distinct banks) and their
+  // norms, double-buffered: the workgroup loads each tile once for its waves
+  constexpr int RS = 2 * KB_DMAX + 16;
+  __shared__ __align__(16) char s_rows[2][KB_T * RS];
+  __shared__ float s_rn[2][KB_T];
 
   // logical block = ((n * slices) + slice) * nqb + query block: the blocks
   // reading one slice are consecutive, hence on one XCD
@@ -243,8 +274,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
   const int L2 = (int)l2;
   const int tid = threadIdx.x, w = wave_id(), lane = lane_id(), j = lane & 31, h = lane >> 5;
-  const int qw = qb * KB_QW + 64 * w;  // the wave's blocks: queries qw + 32 b + column
-  const int q = qw + lane;             // this lane's query after the swap: block h, column j
+  // Positions: queries themselves, or (qlist: the rerun of the rows the
+  // sampled bound left short) entries of cloud n's list of qcount[n] rows.
+  const int npos = qlist ? qcount[n] : (int)l1;
+  if (qlist && qb * KB_QW >= npos) return;  // the whole workgroup past the list
+  const int32_t* __restrict__ ql = qlist ? qlist + (size_t)n * P1 : nullptr;
+  auto query_at = [&](int pos) { return ql ? ql[min(pos, npos - 1)] : min(pos, P1 - 1); };
+  const int qw = qb * KB_QW + 64 * w;  // the wave's blocks: positions qw + 32 b + column
+  const int q = qw + lane;             // this lane's position after the swap: block h, column j
 
   // k-steps of the MFMA chain: KS of dims, and the norms' step -- the upper
   // half of the last dims step when D % 16 == 8 (lanes h = 1 there lie past
@@ -254,7 +291,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   // times -2 (zero past D), then the query's norm pieces
   bf8_t bq0[KX], bq1[KX];
   {
-    const int c0 = min(qw + j, P1 - 1), c1 = min(qw + 32 + j, P1 - 1);
+    const int c0 = query_at(qw + j), c1 = query_at(qw + 32 + j);
     const __bf16* __restrict__ qp0 = p1 + ((size_t)n * P1 + c0) * D;
     const __bf16* __restrict__ qp1 = p1 + ((size_t)n * P1 + c1) * D;
 #pragma unroll
@@ -275,6 +312,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int ntiles = (L2 + KB_T - 1) / KB_T;
   const int tps = (ntiles + slices - 1) / slices;
   const int t0 = min(sl * tps, ntiles), t1 = min(ntiles, t0 + tps);
+
+  // The lane's bound: with taup, the KB_TK-th smallest of its query's KB_TP
+  // sorted part lists (a bitonic merge of each into the running KB_TK); only
+  // distances <= it are candidates.  The rows it leaves with fewer than K
+  // candidates in all slices are rerun without it.
+  float lim = Lim<float>::inf();
+  if (taup && q < npos) {
+    const float* __restrict__ tq = taup + (size_t)n * KB_TP * KB_TK * P1 + q;
+    float t[KB_TK];
+#pragma unroll
+    for (int i = 0; i < KB_TK; ++i) t[i] = tq[(size_t)i * P1];
+#pragma unroll 1
+    for (int pp = 1; pp < KB_TP; ++pp) {
+      float u[KB_TK];
+#pragma unroll
+      for (int i = 0; i < KB_TK; ++i) u[i] = tq[((size_t)pp * KB_TK + i) * P1];
+#pragma unroll
+      for (int i = 0; i < KB_TK; ++i) t[i] = fminf(t[i], u[KB_TK - 1 - i]);
+#pragma unroll
+      for (int st = KB_TK / 2; st > 0; st >>= 1)
+#pragma unroll
+        for (int i = 0; i < KB_TK; ++i)
+          if (!(i & st)) {
+            const float lo = fminf(t[i], t[i + st]), hi = fmaxf(t[i], t[i + st]);
+            t[i] = lo;
+            t[i + st] = hi;
+          }
+    }
+    lim = kb_next_up(t[KB_TK - 1]);
+  }
 
   uint64_t lk[KC];  // this lane's list, ascending keys
 #pragma unroll
@@ -300,35 +367,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     nq_ = 0;
   };
 
-  // Row operand of tile t for this lane: reference base + j, dims 16s + 8h
-  // .. + 7, and the row's norm.  Loads are unconditional (row clamped into
-  // [0, L2), a half past D re-reads the step's lower half and is replaced at
-  // use), so they issue together, one tile ahead.  A row past L2 takes the
-  // norm +inf: its distances are NaN and never pass the filter.
-  bf8_t an[KS];
-  float nn;
-  auto load_rows = [&](int t) __attribute__((always_inline)) {
-    const int tc = min(t, ntiles - 1), base = tc * KB_T;  // a tile past the slice re-reads the last
-    const int row = min(base + j, L2 - 1);
-    const __bf16* __restrict__ ra = rb + (size_t)row * D;
+  // Staging of tile t: thread tid loads row tid / 8 (clamped into [0, L2);
+  // a tile past the slice re-reads the last), 16-byte chunks tid % 8 and
+  // tid % 8 + 8 of its D / 8, and threads < 32 the norm of row tid (+inf past
+  // L2: the row's distances are NaN and never pass the filter).  The loads go
+  // to registers one tile ahead and to LDS after the tile's work.
+  const int rrow = tid >> 3, rch = tid & 7, rstride = 2 * D + 16;
+  bf8_t st0, st1;
+  float stn;
+  auto stage_load = [&](int t) __attribute__((always_inline)) {
+    const int base = min(t, ntiles - 1) * KB_T;
+    const __bf16* __restrict__ ra = rb + (size_t)min(base + rrow, L2 - 1) * D;
+    st0 = 8 * rch < D ? *reinterpret_cast<const bf8_t*>(ra + 8 * rch) : bf8_t{};
+    st1 = 8 * rch + 64 < D ? *reinterpret_cast<const bf8_t*>(ra + 8 * rch + 64) : bf8_t{};
+    stn = tid < KB_T ? (base + tid < L2 ? rr[min(base + tid, L2 - 1)] : Lim<float>::inf()) : 0.f;
+  };
+  auto stage_store = [&](int b) __attribute__((always_inline)) {
+    char* __restrict__ dst = s_rows[b] + rrow * rstride;
+    if (8 * rch < D) *reinterpret_cast<bf8_t*>(dst + 16 * rch) = st0;
+    if (8 * rch + 64 < D) *reinterpret_cast<bf8_t*>(dst + 16 * rch + 128) = st1;
+    if (tid < KB_T) s_rn[b][tid] = stn;
+  };
+  // Tile t (staged in buffer b): multiply, swap, filter, queue.  Row operand
+  // for this lane: row j, dims 16s + 8h .. + 7 (a half past D re-reads the
+  // step's lower half and is replaced by the norm operand).
+  auto tile = [&](int t, int b) __attribute__((always_inline)) {
+    const int base = t * KB_T;
+    const char* __restrict__ src = s_rows[b] + j * rstride;
+    bf8_t a[KX];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int d0 = (HALF && s == KS - 1) ? 16 * s : 16 * s + 8 * h;
-      an[s] = *reinterpret_cast<const bf8_t*>(ra + d0);
+      a[s] = *reinterpret_cast<const bf8_t*>(src + 2 * d0);
     }
-    nn = rr[row];
-  };
-  // Tile t: multiply, swap, filter, queue.
-  auto tile = [&](int t) __attribute__((always_inline)) {
-    const int base = t * KB_T;
-    bf8_t a[KX];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) a[s] = an[s];
     {
-      const bf8_t xr = kb_norm_operand(base + j < L2 ? nn : Lim<float>::inf(), true);
+      const bf8_t xr = kb_norm_operand(s_rn[b][j], true);
       a[XS] = h == XH ? xr : (HALF ? a[XS] : bf8_t{});
     }
-    load_rows(t + 1);  // the next tile's loads are in flight during this one
     f16v_t acc0 = {}, acc1 = {};
 #pragma unroll
     for (int s = 0; s < KX; ++s) {
@@ -348,7 +423,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     // clamped at 0).
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const float thr = __uint_as_float((uint32_t)(lk[KC - 1] >> 32));
+      const float thr = fminf(__uint_as_float((uint32_t)(lk[KC - 1] >> 32)), lim);
       float dv[16];
       uint32_t m = 0;  // bit 15 - v: row 16c + v is below the list's end
 #pragma unroll
@@ -380,12 +455,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
       }
     }
   };
-  if (t0 < t1) load_rows(t0);
-  for (int t = t0; t < t1; ++t) tile(t);
+  if (t0 < t1) {
+    stage_load(t0);
+    stage_store(0);
+  }
+  for (int t = t0; t < t1; ++t) {
+    const int b = (t - t0) & 1;
+    __syncthreads();  // tile t staged; every wave is past its reads of buffer b ^ 1
+    if (t + 1 < t1) stage_load(t + 1);
+    tile(t, b);
+    if (t + 1 < t1) stage_store(b ^ 1);
+  }
   drain();
 
   // the first K entries of this lane's list
-  if (q < P1 && q < l1) {
+  if (q < npos) {
     // entry s of (cloud n, slice sl) for all queries is one run of P1 keys:
     // a wave's stores are 64 consecutive keys
     uint64_t* __restrict__ out = part + (size_t)(n * slices + sl) * K * P1 + q;
@@ -395,28 +479,143 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   }
 }
 
+// The sampled bound's parts: workgroup (cloud n, part pt, query block qb)
+// runs the slice kernel's products over tiles (pt + KB_TP k) * stride,
+// k < KB_TK = KB_TS / KB_TP, stride = ntiles / KB_TS, and keeps each query's
+// smallest distance of every tile: the part's KB_TK tile minima, sorted
+// (+inf when none), stored [n][pt][i][query].  The KB_TK-th smallest of a
+// query's KB_TS tile minima is a sampled distance with at least KB_TK sampled
+// distances at or below it.  Workgroup 0 also clears the rerun counts.
+template <int KS, bool HALF>
+__global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
+    const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
+    const int64_t* __restrict__ len2, int N, int P1, int P2, int D, int nqb,
+    const float* __restrict__ qn, const float* __restrict__ rn, float* __restrict__ taup,
+    int32_t* __restrict__ rcount) {
+  static_assert(KB_TS / KB_TP == KB_TK, "a part is KB_TK tiles");
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < N; i += 256) rcount[i] = 0;
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int qb = lb % nqb, ns = lb / nqb;
+  const int pt = ns % KB_TP, n = ns / KB_TP;
+  int64_t l1 = len1[n], l2 = len2[n];
+  l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+  l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
+  const int L2 = (int)l2;
+  const int w = wave_id(), lane = lane_id(), j = lane & 31, h = lane >> 5;
+  const int qw = qb * KB_QW + 64 * w;
+  const int q = qw + lane;
+  constexpr int KX = HALF ? KS : KS + 1, XS = KX - 1, XH = HALF ? 1 : 0;
+  float s[KB_TK];
+#pragma unroll
+  for (int i = 0; i < KB_TK; ++i) s[i] = Lim<float>::inf();
+  const int ntiles = (L2 + KB_T - 1) / KB_T;
+  if (ntiles >= 2 * KB_TS) {
+    bf8_t bq0[KX], bq1[KX];
+    {
+      const int c0 = min(qw + j, P1 - 1), c1 = min(qw + 32 + j, P1 - 1);
+      const __bf16* __restrict__ qp0 = p1 + ((size_t)n * P1 + c0) * D;
+      const __bf16* __restrict__ qp1 = p1 + ((size_t)n * P1 + c1) * D;
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        const int d0 = 16 * st + 8 * h;
+        bq0[st] = d0 < D ? kb_neg2(*reinterpret_cast<const bf8_t*>(qp0 + d0)) : bf8_t{};
+        bq1[st] = d0 < D ? kb_neg2(*reinterpret_cast<const bf8_t*>(qp1 + d0)) : bf8_t{};
+      }
+      const bf8_t x0 = kb_norm_operand(qn[(size_t)n * kb_pad(P1) + c0], false);
+      const bf8_t x1 = kb_norm_operand(qn[(size_t)n * kb_pad(P1) + c1], false);
+      bq0[XS] = h == XH ? x0 : (HALF ? bq0[XS] : bf8_t{});
+      bq1[XS] = h == XH ? x1 : (HALF ? bq1[XS] : bf8_t{});
+    }
+    const __bf16* __restrict__ rb = p2 + (size_t)n * P2 * D;
+    const float* __restrict__ rr = rn + (size_t)n * kb_pad(P2);
+    const int stride = ntiles / KB_TS;
+    // the next sampled tile's rows are loaded while this one is processed
+    bf8_t an[KS];
+    float nn;
+    auto load_rows = [&](int k) __attribute__((always_inline)) {
+      const int base = (pt + KB_TP * min(k, KB_TK - 1)) * stride * KB_T;
+      const int row = min(base + j, L2 - 1);
+      const __bf16* __restrict__ ra = rb + (size_t)row * D;
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        const int d0 = (HALF && st == KS - 1) ? 16 * st : 16 * st + 8 * h;
+        an[st] = *reinterpret_cast<const bf8_t*>(ra + d0);
+      }
+      nn = rr[row];
+    };
+    load_rows(0);
+#pragma unroll 1
+    for (int k = 0; k < KB_TK; ++k) {
+      const int base = (pt + KB_TP * k) * stride * KB_T;
+      bf8_t a[KX];
+#pragma unroll
+      for (int st = 0; st < KS; ++st) a[st] = an[st];
+      const bf8_t xr = kb_norm_operand(base + j < L2 ? nn : Lim<float>::inf(), true);
+      a[XS] = h == XH ? xr : (HALF ? a[XS] : bf8_t{});
+      load_rows(k + 1);
+      f16v_t acc0 = {}, acc1 = {};
+#pragma unroll
+      for (int st = 0; st < KX; ++st) {
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[st], bq0[st], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[st], bq1[st], acc1, 0, 0, 0);
+      }
+      // the tile's smallest distance for the lane's query: lane l holds 16
+      // rows of column l % 32 of each block, its partner l ^ 32 the other 16,
+      // combined by one swap (NaN rows, past the cloud, drop out of fminf)
+      float m0 = acc0[0], m1 = acc1[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) {
+        m0 = fminf(m0, acc0[v]);
+        m1 = fminf(m1, acc1[v]);
+      }
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(m0), __float_as_uint(m1), false, false);
+      kb_tk_insert(s, fminf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+    }
+  }
+  if (q < P1 && q < l1) {
+    float* __restrict__ out = taup + ((size_t)(n * KB_TP + pt) * KB_TK) * P1 + q;
+#pragma unroll
+    for (int i = 0; i < KB_TK; ++i) out[(size_t)i * P1] = s[i];
+  }
+}
+
 // Two lanes per query row (lanes j and j + 32 of a wave; 32 rows a wave):
 // each merges its half of the row's nl slice lists (sorted keys, K a list,
 // padded to KC with the empty key) in registers, v_permlane32_swap gives both
 // lanes both halves' lists, and both merge those; lane j writes entries
 // [0, KC/2) of the row, lane j + 32 entries [KC/2, KC) (those below K).  Rows
 // past lengths1 and empty entries are (0, 0).
+// Positions are rows (cloud n, position p: list entry of row n P1 + p), or
+// with qlist the rerun list's entries, whose rows are n P1 + qlist[n P1 + p].
+// rlist: the slices ran under the sampled bound; a row left with fewer than
+// min(K, lengths2) real entries is appended to its cloud's rerun list
+// (rcount[n] entries) and written by the rerun instead.
 template <int KC>
-__global__ __launch_bounds__(256) void knn_bf16_merge_kernel(const uint64_t* __restrict__ part,
-                                                             const int64_t* __restrict__ len1,
-                                                             int64_t rows, int P1, int K, int nl,
-                                                             int64_t* __restrict__ idxs,
-                                                             __bf16* __restrict__ dists) {
+__global__ __launch_bounds__(256) void knn_bf16_merge_kernel(
+    const uint64_t* __restrict__ part, const int64_t* __restrict__ len1,
+    const int64_t* __restrict__ len2, int64_t rows, int P1, int P2, int K, int nl,
+    int64_t* __restrict__ idxs, __bf16* __restrict__ dists, int32_t* __restrict__ rlist,
+    int32_t* __restrict__ rcount, const int32_t* __restrict__ qlist,
+    const int32_t* __restrict__ qcount) {
   const int lane = lane_id(), j = lane & 31, h = lane >> 5;
-  const int64_t row = ((int64_t)blockIdx.x * KB_WAVES + wave_id()) * 32 + j;
+  const int64_t prow = ((int64_t)blockIdx.x * KB_WAVES + wave_id()) * 32 + j;
   const uint64_t empty = kb_key(Lim<float>::inf(), KB_NONE);
   bool real = false;
-  if (row < rows) {
-    const int64_t n = row / P1;
-    int64_t l1 = len1[n];
-    l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
-    real = row - n * P1 < l1;
+  int64_t row = prow;  // the output row
+  const int64_t n = prow < rows ? prow / P1 : 0;
+  const int pos = (int)(prow - n * P1);
+  if (prow < rows) {
+    if (qlist) {
+      real = pos < qcount[n];
+      row = real ? n * P1 + qlist[n * P1 + pos] : prow;
+    } else {
+      int64_t l1 = len1[n];
+      l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+      real = pos < l1;
+    }
   }
+  if (qlist && !real && __ballot(real) == 0) return;  // a wave past the rerun list
   uint64_t a[KC];
 #pragma unroll
   for (int s = 0; s < KC; ++s) a[s] = empty;
@@ -425,8 +624,7 @@ __global__ __launch_bounds__(256) void knn_bf16_merge_kernel(const uint64_t* __r
     // entry s of list L: part[((n nl + L) K + s) P1 + q], so the 32 lanes
     // of a half-wave read consecutive keys; the next list is loaded while
     // the current one is merged
-    const int64_t n = row / P1;
-    const uint64_t* __restrict__ base = part + (size_t)n * nl * K * P1 + (row - n * P1);
+    const uint64_t* __restrict__ base = part + (size_t)n * nl * K * P1 + pos;
     auto load = [&](uint64_t (&b)[KC], int L) __attribute__((always_inline)) {
 #pragma unroll
       for (int s = 0; s < KC; ++s) b[s] = s < K ? base[((size_t)L * K + s) * P1] : empty;
@@ -454,7 +652,19 @@ __global__ __launch_bounds__(256) void knn_bf16_merge_kernel(const uint64_t* __r
     y[s] = ((uint64_t)rh[1] << 32) | rl[1];
   }
   kb_merge<KC, KC>(x, y);
-  if (row >= rows) return;
+  if (prow >= rows) return;
+  if (rlist && real) {
+    int64_t l2 = len2[n];
+    l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
+    int got = 0;
+#pragma unroll
+    for (int s = 0; s < KC; ++s) got += (s < K && (uint32_t)x[s] != (uint32_t)KB_NONE) ? 1 : 0;
+    if (got < min((int64_t)K, l2)) {
+      if (h == 0) rlist[n * P1 + atomicAdd(&rcount[n], 1)] = pos;
+      return;
+    }
+  }
+  if (qlist && !real) return;
   int64_t* __restrict__ io = idxs + row * K;
   __bf16* __restrict__ dout = dists + row * K;
   const uint32_t upper = bit_mask((uint32_t)h, 0);
@@ -473,39 +683,95 @@ __global__ __launch_bounds__(256) void knn_bf16_merge_kernel(const uint64_t* __r
 
 static int64_t kb_align(int64_t x) { return (x + 255) / 256 * 256; }
 
-// norms (float per point, rows padded to 32), then the partial lists
-int64_t knn_bf16_workspace(int64_t N, int64_t P1, int64_t P2, int64_t K) {
+// The sampled bound applies to clouds of at least 2 KB_TS tiles.
+static bool kb_sampled(int64_t P2) { return (P2 + KB_T - 1) / KB_T >= 2 * KB_TS; }
+
+// Workspace: norms (float per point, rows padded to 32), the partial lists,
+// then (sampled bound) its parts (KB_TP x KB_TK floats per query), the rerun
+// counts (int32 per cloud) and the rerun lists (int32 per query).
+struct KbWs {
+  int64_t part, taup, rcount, rlist, total;
+};
+static KbWs kb_ws(int64_t N, int64_t P1, int64_t P2, int64_t K) {
   const KbPlan p = kb_plan(N, P1, P2);
-  return kb_align(N * (kb_pad(P1) + kb_pad(P2)) * 4) + kb_align(N * P1 * p.slices * K * 8);
+  KbWs w;
+  w.part = kb_align(N * (kb_pad(P1) + kb_pad(P2)) * 4);
+  int64_t o = w.part + kb_align(N * P1 * p.slices * K * 8);
+  w.taup = w.rcount = w.rlist = -1;
+  if (kb_sampled(P2)) {
+    w.taup = o;
+    o += kb_align(N * P1 * KB_TP * KB_TK * 4);
+    w.rcount = o;
+    o += kb_align(N * 4);
+    w.rlist = o;
+    o += kb_align(N * P1 * 4);
+  }
+  w.total = o;
+  return w;
+}
+
+int64_t knn_bf16_workspace(int64_t N, int64_t P1, int64_t P2, int64_t K) {
+  return kb_ws(N, P1, P2, K).total;
 }
 
 bool knn_bf16_supported(int64_t D, int64_t K, int norm) {
   return norm == 2 && D % 8 == 0 && D >= 8 && D <= KB_DMAX && K >= 1 && K <= 32;
 }
 
+struct KbArgs {
+  const __bf16 *p1, *p2;
+  const int64_t *l1, *l2;
+  int N, P1, P2, D, K;
+  const float *qn, *rn;
+  uint64_t* part;
+  float* taup;  // null: no sampled bound
+  int32_t *rlist, *rcount;
+  int64_t* idxs;
+  __bf16* dists;
+  hipStream_t s;
+};
+
+// Sampled bound (when it applies): its parts, the slices under it, the merge
+// (which lists the rows left short), then the slices and the merge again over
+// those rows only, without the bound.
 template <int KS, bool HALF, int KC>
-static void kb_launch(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
-                      int N, int P1, int P2, int D, int K, const float* qn, const float* rn,
-                      uint64_t* part, hipStream_t s) {
-  const KbPlan p = kb_plan(N, P1, P2);
-  hipLaunchKernelGGL((knn_bf16_slice_kernel<KS, HALF, KC>), dim3(N * p.nqb * p.slices), dim3(256), 0, s,
-                     (const __bf16*)p1, (const __bf16*)p2, l1, l2, P1, P2, D, K, p.nqb, p.slices,
-                     qn, rn, part);
+static void kb_launch(const KbArgs& a) {
+  const KbPlan p = kb_plan(a.N, a.P1, a.P2);
+  const dim3 grid(a.N * p.nqb * p.slices), blk(256);
+  const int64_t r1 = (int64_t)a.N * a.P1;
+  const dim3 mg((unsigned)((r1 + 32 * KB_WAVES - 1) / (32 * KB_WAVES))), mb(64 * KB_WAVES);
+  if (a.taup)
+    hipLaunchKernelGGL((knn_bf16_tau_kernel<KS, HALF>), dim3(a.N * p.nqb * KB_TP), blk, 0, a.s,
+                       a.p1, a.p2, a.l1, a.l2, a.N, a.P1, a.P2, a.D, p.nqb, a.qn, a.rn, a.taup,
+                       a.rcount);
+  hipLaunchKernelGGL((knn_bf16_slice_kernel<KS, HALF, KC>), grid, blk, 0, a.s, a.p1, a.p2, a.l1,
+                     a.l2, a.P1, a.P2, a.D, a.K, p.nqb, p.slices, a.qn, a.rn, a.part,
+                     (const float*)a.taup, (const int32_t*)nullptr, (const int32_t*)nullptr);
+  hipLaunchKernelGGL(knn_bf16_merge_kernel<KC>, mg, mb, 0, a.s, (const uint64_t*)a.part, a.l1,
+                     a.l2, r1, a.P1, a.P2, a.K, p.slices, a.idxs, a.dists,
+                     a.taup ? a.rlist : nullptr, a.taup ? a.rcount : nullptr,
+                     (const int32_t*)nullptr, (const int32_t*)nullptr);
+  if (a.taup) {
+    hipLaunchKernelGGL((knn_bf16_slice_kernel<KS, HALF, KC>), grid, blk, 0, a.s, a.p1, a.p2, a.l1,
+                       a.l2, a.P1, a.P2, a.D, a.K, p.nqb, p.slices, a.qn, a.rn, a.part,
+                       (const float*)nullptr, (const int32_t*)a.rlist, (const int32_t*)a.rcount);
+    hipLaunchKernelGGL(knn_bf16_merge_kernel<KC>, mg, mb, 0, a.s, (const uint64_t*)a.part, a.l1,
+                       a.l2, r1, a.P1, a.P2, a.K, p.slices, a.idxs, a.dists, (int32_t*)nullptr,
+                       (int32_t*)nullptr, (const int32_t*)a.rlist, (const int32_t*)a.rcount);
+  }
 }
 
 template <int KC>
-static void kb_dispatch_ks(int D, const void* p1, const void* p2, const int64_t* l1,
-                           const int64_t* l2, int N, int P1, int P2, int K, const float* qn,
-                           const float* rn, uint64_t* part, hipStream_t s) {
+static void kb_dispatch_ks(const KbArgs& a) {
   // D % 8 == 0, 8 <= D <= 128: D / 8 = 2 KS - HALF
 #define KB_CASE(DD, KS_, HALF_) \
-  case DD: kb_launch<KS_, HALF_, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, part, s); break;
-  switch (D) {
+  case DD: kb_launch<KS_, HALF_, KC>(a); break;
+  switch (a.D) {
     KB_CASE(8, 1, true) KB_CASE(16, 1, false) KB_CASE(24, 2, true) KB_CASE(32, 2, false)
     KB_CASE(40, 3, true) KB_CASE(48, 3, false) KB_CASE(56, 4, true) KB_CASE(64, 4, false)
     KB_CASE(72, 5, true) KB_CASE(80, 5, false) KB_CASE(88, 6, true) KB_CASE(96, 6, false)
     KB_CASE(104, 7, true) KB_CASE(112, 7, false) KB_CASE(120, 8, true)
-    default: kb_launch<8, false, KC>(p1, p2, l1, l2, N, P1, P2, D, K, qn, rn, part, s); break;
+    default: kb_launch<8, false, KC>(a); break;
   }
 #undef KB_CASE
 }
@@ -513,11 +779,10 @@ static void kb_dispatch_ks(int D, const void* p1, const void* p2, const int64_t*
 void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2, int N,
                      int P1, int P2, int D, int K, int64_t* idxs, void* dists, void* ws,
                      hipStream_t s) {
-  const KbPlan p = kb_plan(N, P1, P2);
+  const KbWs L = kb_ws(N, P1, P2, K);
+  char* wb = reinterpret_cast<char*>(ws);
   float* qn = reinterpret_cast<float*>(ws);
   float* rn = qn + (size_t)N * kb_pad(P1);
-  uint64_t* part = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(ws) +
-                                               kb_align((int64_t)N * (kb_pad(P1) + kb_pad(P2)) * 4));
   const int64_t r1 = (int64_t)N * P1, r2 = (int64_t)N * P2;
   if (r1 > 0)
     hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)std::min<int64_t>((r1 + 255) / 256, 65536)),
@@ -526,14 +791,27 @@ void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const in
     hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)std::min<int64_t>((r2 + 255) / 256, 65536)),
                        dim3(256), 0, s, (const __bf16*)p2, r2, kb_pad(P2), (int64_t)P2, D, rn);
   if (r1 == 0) return;
-  if (K <= 16) kb_dispatch_ks<16>(D, p1, p2, l1, l2, N, P1, P2, K, qn, rn, part, s);
-  else kb_dispatch_ks<32>(D, p1, p2, l1, l2, N, P1, P2, K, qn, rn, part, s);
-  const int nl = p.slices;
-  const dim3 mg((unsigned)((r1 + 32 * KB_WAVES - 1) / (32 * KB_WAVES))), mb(64 * KB_WAVES);
-  if (K <= 16)
-    hipLaunchKernelGGL(knn_bf16_merge_kernel<16>, mg, mb, 0, s, part, l1, r1, P1, K, nl, idxs, (__bf16*)dists);
-  else
-    hipLaunchKernelGGL(knn_bf16_merge_kernel<32>, mg, mb, 0, s, part, l1, r1, P1, K, nl, idxs, (__bf16*)dists);
+  KbArgs a;
+  a.p1 = (const __bf16*)p1;
+  a.p2 = (const __bf16*)p2;
+  a.l1 = l1;
+  a.l2 = l2;
+  a.N = N;
+  a.P1 = P1;
+  a.P2 = P2;
+  a.D = D;
+  a.K = K;
+  a.qn = qn;
+  a.rn = rn;
+  a.part = reinterpret_cast<uint64_t*>(wb + L.part);
+  a.taup = L.taup >= 0 ? reinterpret_cast<float*>(wb + L.taup) : nullptr;
+  a.rcount = L.rcount >= 0 ? reinterpret_cast<int32_t*>(wb + L.rcount) : nullptr;
+  a.rlist = L.rlist >= 0 ? reinterpret_cast<int32_t*>(wb + L.rlist) : nullptr;
+  a.idxs = idxs;
+  a.dists = (__bf16*)dists;
+  a.s = s;
+  if (K <= 16) kb_dispatch_ks<16>(a);
+  else kb_dispatch_ks<32>(a);
 }
 
 }  // namespace tpo
