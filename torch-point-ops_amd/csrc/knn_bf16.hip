@@ -60,23 +60,29 @@ constexpr int KB_TK = 8;
 
 __host__ __device__ inline int64_t kb_pad(int64_t n) { return (n + 31) & ~(int64_t)31; }
 
-// out[r] = sum over d of p[r][d]^2 in float (rows of D bfloat16, D % 8 == 0)
+// out[r] = sum over d of p[r][d]^2 in float (rows of D bfloat16, D % 8 == 0,
+// D <= 128): 16 lanes a row, lane c summing dims 8c .. 8c + 7 by an FMA chain
+// from one 16-byte load, then the 16 partial sums added pairwise in a fixed
+// order (lanes 8 apart, then 4, 2, 1)
 __global__ __launch_bounds__(256) void knn_bf16_norms_kernel(const __bf16* __restrict__ p,
                                                              int64_t rows, int64_t stride_out,
                                                              int64_t rows_per_batch, int D,
                                                              float* __restrict__ out) {
-  for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < rows;
-       r += (int64_t)gridDim.x * 256) {
-    const bf8_t* x = reinterpret_cast<const bf8_t*>(p + r * D);
-    float acc = 0.f;
-    for (int d = 0; d < D / 8; ++d) {
-      const bf8_t v = x[d];
+  const int c = threadIdx.x & 15;
+  const int64_t r = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const bool live = r < rows;
+  float acc = 0.f;
+  if (live && 8 * c < D) {
+    const bf8_t v = *reinterpret_cast<const bf8_t*>(p + r * D + 8 * c);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float f = (float)v[e];
-        acc = __builtin_fmaf(f, f, acc);
-      }
+    for (int e = 0; e < 8; ++e) {
+      const float f = (float)v[e];
+      acc = __builtin_fmaf(f, f, acc);
     }
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if (live && c == 0) {
     const int64_t b = r / rows_per_batch;
     out[b * stride_out + (r - b * rows_per_batch)] = acc;
   }
@@ -785,11 +791,11 @@ void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const in
   float* rn = qn + (size_t)N * kb_pad(P1);
   const int64_t r1 = (int64_t)N * P1, r2 = (int64_t)N * P2;
   if (r1 > 0)
-    hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)std::min<int64_t>((r1 + 255) / 256, 65536)),
-                       dim3(256), 0, s, (const __bf16*)p1, r1, kb_pad(P1), (int64_t)P1, D, qn);
+    hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)((r1 + 15) / 16)), dim3(256), 0, s,
+                       (const __bf16*)p1, r1, kb_pad(P1), (int64_t)P1, D, qn);
   if (r2 > 0)
-    hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)std::min<int64_t>((r2 + 255) / 256, 65536)),
-                       dim3(256), 0, s, (const __bf16*)p2, r2, kb_pad(P2), (int64_t)P2, D, rn);
+    hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)((r2 + 15) / 16)), dim3(256), 0, s,
+                       (const __bf16*)p2, r2, kb_pad(P2), (int64_t)P2, D, rn);
   if (r1 == 0) return;
   KbArgs a;
   a.p1 = (const __bf16*)p1;
