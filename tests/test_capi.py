@@ -103,11 +103,14 @@ def test_argument_errors_are_reported(lib):
     assert lib.tpo_knn_workspace_size(1, 8, 16384, 16384, 3, 16, 2) == 8 * 16384 * 4  # order only
     assert lib.tpo_knn_workspace_size(0, 8, 16384, 1000, 3, 16, 2) == 8 * 16384 * 4  # short clouds
     # bf16: squared norms (float per point), a partial list of K (distance,
-    # index) keys per query and reference slice (config 5 runs 8 slices), then
-    # for clouds of >= 4096 references the sampled bound's 8 x 8 floats per
-    # query, the rerun counts (int32 per cloud) and lists (int32 per query)
+    # index) keys per query and reference slice of the exact pass (config 5:
+    # 8 slices), then for clouds of >= 4096 references the sampled bound's
+    # 8 x 8 floats per query, the rerun counts (int32 per cloud) and lists
+    # (int32 per query), and per query and slice of the candidate pass
+    # (config 5: 12 slices) 128 candidate keys and two int32 counts
     assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 128, 32, 2) == \
-        4 * (4096 + 65536) * 4 + 4 * 4096 * 8 * 32 * 8 + 4 * 4096 * 64 * 4 + 256 + 4 * 4096 * 4
+        4 * (4096 + 65536) * 4 + 4 * 4096 * 8 * 32 * 8 + 4 * 4096 * 64 * 4 + 256 + \
+        4 * 4096 * 4 + 4 * 4096 * 12 * 128 * 8 + 4 * 4096 * 12 * 2 * 4
     assert lib.tpo_knn_workspace_size(3, 2, 100, 1000, 64, 8, 2) == \
         up(2 * (128 + 1024) * 4) + up(2 * 100 * 2 * 8 * 8)  # 2 slices; short clouds: no bound
     assert lib.tpo_knn_workspace_size(3, 4, 4096, 65536, 128, 32, 1) == 0  # no bf16 L1 kernel

@@ -655,7 +655,9 @@ def test_bf16_rows_the_sampled_bound_leaves_short_are_rerun(tpo, dev):
     assert torch.equal(idx2, idx.to(dev)) and torch.equal(d2, d.to(dev))
     up = lambda x: (x + 255) // 256 * 256
     at = up(B * (P1 + 32 * ((P2 + 31) // 32)) * 4) + up(B * P1 * 8 * K * 8) + up(B * P1 * 64 * 4)
-    assert at + up(B * 4) + up(B * P1 * 4) == size
+    # then the rerun lists and the candidate pass's 16 slices of 128 keys and
+    # two counts per query
+    assert at + up(B * 4) + up(B * P1 * 4) + up(B * P1 * 16 * 128 * 8) + up(B * P1 * 16 * 2 * 4) == size
     counts = ws[at:at + 4 * B].cpu().view(torch.int32)
     assert counts.tolist() == [32, 32]
 

@@ -57,6 +57,11 @@ constexpr int KB_NONE = 0x7fffffff;      // index of an empty list entry
 constexpr int KB_TS = 64;
 constexpr int KB_TP = 8;
 constexpr int KB_TK = 8;
+// Under the bound: candidate slots per (query, slice), shared by the two
+// half-waves that hold the query's rows (one fills up from slot 0, the other
+// down from the last; a multiple of 64), and at most KB_CMAX_SLICES slices
+constexpr int KB_CAP = 128;
+constexpr int KB_CMAX_SLICES = 16;
 
 __host__ __device__ inline int64_t kb_pad(int64_t n) { return (n + 31) & ~(int64_t)31; }
 
@@ -235,6 +240,35 @@ __device__ __forceinline__ void kb_tk_insert(float (&s)[KB_TK], float d) {
   s[0] = d < s[0] ? d : s[0];
 }
 
+// The sampled bound of query position q of cloud n, as the filter limit: the
+// KB_TK-th smallest of its KB_TP sorted part lists (a bitonic merge of each
+// into the running KB_TK), moved one float up, so d < limit exactly when
+// d <= the bound.
+__device__ __forceinline__ float kb_tau(const float* __restrict__ taup, int n, int P1, int q) {
+  const float* __restrict__ tq = taup + (size_t)n * KB_TP * KB_TK * P1 + q;
+  float t[KB_TK];
+#pragma unroll
+  for (int i = 0; i < KB_TK; ++i) t[i] = tq[(size_t)i * P1];
+#pragma unroll 1
+  for (int pp = 1; pp < KB_TP; ++pp) {
+    float u[KB_TK];
+#pragma unroll
+    for (int i = 0; i < KB_TK; ++i) u[i] = tq[((size_t)pp * KB_TK + i) * P1];
+#pragma unroll
+    for (int i = 0; i < KB_TK; ++i) t[i] = fminf(t[i], u[KB_TK - 1 - i]);
+#pragma unroll
+    for (int st = KB_TK / 2; st > 0; st >>= 1)
+#pragma unroll
+      for (int i = 0; i < KB_TK; ++i)
+        if (!(i & st)) {
+          const float lo = fminf(t[i], t[i + st]), hi = fmaxf(t[i], t[i + st]);
+          t[i] = lo;
+          t[i + st] = hi;
+        }
+  }
+  return kb_next_up(t[KB_TK - 1]);
+}
+
 // Work split: query blocks of 256 and reference slices (one workgroup each).
 struct KbPlan {
   int nqb, slices;
@@ -260,8 +294,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
     const int64_t* __restrict__ len2, int P1, int P2, int D, int K, int nqb, int slices,
     const float* __restrict__ qn, const float* __restrict__ rn, uint64_t* __restrict__ part,
-    const float* __restrict__ taup, const int32_t* __restrict__ qlist,
-    const int32_t* __restrict__ qcount) {
+    const int32_t* __restrict__ qlist, const int32_t* __restrict__ qcount) {
   __shared__ uint64_t s_q[KB_WAVES][KB_QCAP][64];
   // a tile's reference rows (D bfloat16 each, rows 2D + 16 bytes apart so a
   // half-wave's 16-byte reads of 16 rows fall in distinct banks) and their
@@ -281,7 +314,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int L2 = (int)l2;
   const int tid = threadIdx.x, w = wave_id(), lane = lane_id(), j = lane & 31, h = lane >> 5;
   // Positions: queries themselves, or (qlist: the rerun of the rows the
-  // sampled bound left short) entries of cloud n's list of qcount[n] rows.
+  // candidate pass under the sampled bound could not settle) entries of
+  // cloud n's list of qcount[n] rows.
   const int npos = qlist ? qcount[n] : (int)l1;
   if (qlist && qb * KB_QW >= npos) return;  // the whole workgroup past the list
   const int32_t* __restrict__ ql = qlist ? qlist + (size_t)n * P1 : nullptr;
@@ -319,35 +353,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int tps = (ntiles + slices - 1) / slices;
   const int t0 = min(sl * tps, ntiles), t1 = min(ntiles, t0 + tps);
 
-  // The lane's bound: with taup, the KB_TK-th smallest of its query's KB_TP
-  // sorted part lists (a bitonic merge of each into the running KB_TK); only
-  // distances <= it are candidates.  The rows it leaves with fewer than K
-  // candidates in all slices are rerun without it.
-  float lim = Lim<float>::inf();
-  if (taup && q < npos) {
-    const float* __restrict__ tq = taup + (size_t)n * KB_TP * KB_TK * P1 + q;
-    float t[KB_TK];
-#pragma unroll
-    for (int i = 0; i < KB_TK; ++i) t[i] = tq[(size_t)i * P1];
-#pragma unroll 1
-    for (int pp = 1; pp < KB_TP; ++pp) {
-      float u[KB_TK];
-#pragma unroll
-      for (int i = 0; i < KB_TK; ++i) u[i] = tq[((size_t)pp * KB_TK + i) * P1];
-#pragma unroll
-      for (int i = 0; i < KB_TK; ++i) t[i] = fminf(t[i], u[KB_TK - 1 - i]);
-#pragma unroll
-      for (int st = KB_TK / 2; st > 0; st >>= 1)
-#pragma unroll
-        for (int i = 0; i < KB_TK; ++i)
-          if (!(i & st)) {
-            const float lo = fminf(t[i], t[i + st]), hi = fmaxf(t[i], t[i + st]);
-            t[i] = lo;
-            t[i + st] = hi;
-          }
-    }
-    lim = kb_next_up(t[KB_TK - 1]);
-  }
 
   uint64_t lk[KC];  // this lane's list, ascending keys
 #pragma unroll
@@ -429,7 +434,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     // clamped at 0).
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const float thr = fminf(__uint_as_float((uint32_t)(lk[KC - 1] >> 32)), lim);
+      const float thr = __uint_as_float((uint32_t)(lk[KC - 1] >> 32));
       float dv[16];
       uint32_t m = 0;  // bit 15 - v: row 16c + v is below the list's end
 #pragma unroll
@@ -586,6 +591,390 @@ __global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
   }
 }
 
+// Work split of the candidate pass: query blocks of 256 and up to
+// KB_CMAX_SLICES reference slices, about three workgroups a CU (as many as
+// are resident at once).
+static KbPlan kb_cplan(int64_t N, int64_t P1, int64_t P2) {
+  KbPlan p;
+  p.nqb = (int)((P1 + KB_QW - 1) / KB_QW);
+  const int64_t wgs = N * (int64_t)p.nqb;
+  int64_t s = wgs > 0 ? (768 + wgs - 1) / wgs : 1;
+  const int64_t tiles = (P2 + KB_T - 1) / KB_T;
+  s = std::min<int64_t>(s, std::max<int64_t>(1, tiles / 16));  // at least 16 tiles a slice
+  p.slices = (int)std::max<int64_t>(1, std::min<int64_t>(s, KB_CMAX_SLICES));
+  return p;
+}
+
+// The candidate pass under the sampled bound.  Workgroup (cloud n, slice sl,
+// query block qb) stages the slice's tiles in LDS and runs the slice
+// kernel's MFMA chain, but keeps no list: every distance at or below its
+// query's bound is stored at once, as a 64-bit key, in the region of (query,
+// slice) -- KB_CAP slots, which the half-wave h = 0 fills upwards from the
+// first and h = 1 downwards from the last.  No swap is needed: lane (h, j)
+// tests its block-0 column (position qw + j) against that query's bound and
+// its block-1 column (qw + 32 + j) against that one's.  A row is skipped by
+// the wave unless some lane has a candidate in it.  Counts run on past the
+// capacity (the last slot is overwritten); the merge sends such a query, and
+// one left with fewer than min(K, lengths2) candidates, to the exact pass.
+template <int KS, bool HALF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void knn_bf16_cand_kernel(
+    const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
+    const int64_t* __restrict__ len2, int P1, int P2, int nqb, int slices,
+    const float* __restrict__ qn, const float* __restrict__ rn, const float* __restrict__ taup,
+    uint64_t* __restrict__ cand, int32_t* __restrict__ ccount) {
+  constexpr int D = 16 * KS - (HALF ? 8 : 0);  // the dimension (the dispatch's choice of KS, HALF)
+  constexpr int RS = 2 * KB_DMAX + 16;
+  // two tiles a stage (one barrier for both), double-buffered
+  constexpr int TC = 2, CR = TC * KB_T;
+  __shared__ __align__(16) char s_rows[2][CR * RS];
+  __shared__ bf8_t s_rx[2][CR];  // the rows' norm operands
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int qb = lb % nqb, ns = lb / nqb;
+  const int sl = ns % slices, n = ns / slices;
+  int64_t l1 = len1[n], l2 = len2[n];
+  l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+  l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
+  if (qb * KB_QW >= l1) return;  // the whole workgroup past the cloud's queries
+  const int L2 = (int)l2;
+  const int tid = threadIdx.x, w = wave_id(), lane = lane_id(), j = lane & 31, h = lane >> 5;
+  const int qw = qb * KB_QW + 64 * w;
+
+  constexpr int KX = HALF ? KS : KS + 1, XS = KX - 1, XH = HALF ? 1 : 0;
+  bf8_t bq0[KX], bq1[KX];
+  {
+    const int c0 = min(qw + j, P1 - 1), c1 = min(qw + 32 + j, P1 - 1);
+    const __bf16* __restrict__ qp0 = p1 + ((size_t)n * P1 + c0) * D;
+    const __bf16* __restrict__ qp1 = p1 + ((size_t)n * P1 + c1) * D;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int d0 = 16 * s + 8 * h;
+      bq0[s] = d0 < D ? kb_neg2(*reinterpret_cast<const bf8_t*>(qp0 + d0)) : bf8_t{};
+      bq1[s] = d0 < D ? kb_neg2(*reinterpret_cast<const bf8_t*>(qp1 + d0)) : bf8_t{};
+    }
+    const bf8_t x0 = kb_norm_operand(qn[(size_t)n * kb_pad(P1) + c0], false);
+    const bf8_t x1 = kb_norm_operand(qn[(size_t)n * kb_pad(P1) + c1], false);
+    bq0[XS] = h == XH ? x0 : (HALF ? bq0[XS] : bf8_t{});
+    bq1[XS] = h == XH ? x1 : (HALF ? bq1[XS] : bf8_t{});
+  }
+  const __bf16* __restrict__ rb = p2 + (size_t)n * P2 * D;
+  const float* __restrict__ rr = rn + (size_t)n * kb_pad(P2);
+  const int ntiles = (L2 + KB_T - 1) / KB_T;
+  const int tps = (ntiles + slices - 1) / slices;
+  const int t0 = min(sl * tps, ntiles), t1 = min(ntiles, t0 + tps);
+
+  // Bounds: lane l computes that of position qw + l (-inf past the cloud's
+  // queries: nothing passes it); the swap hands lane (h, j) those of qw + j
+  // and qw + 32 + j.
+  const float lim = qw + lane < l1 ? kb_tau(taup, n, P1, qw + lane) : -Lim<float>::inf();
+  const auto lr = __builtin_amdgcn_permlane32_swap(__float_as_uint(lim), __float_as_uint(lim), false, false);
+  const float lim0 = __uint_as_float(lr[0]), lim1 = __uint_as_float(lr[1]);
+  // The wave's regions: (position qw + x, slice sl) starts x * rstep bytes
+  // past wbase; this lane's slot c of its half lies o + e8 * c bytes past it.
+  char* __restrict__ wbase =
+      reinterpret_cast<char*>(cand + (((size_t)n * P1 + qw) * slices + sl) * KB_CAP);
+  const int rstep = slices * KB_CAP * 8, e8 = h ? -8 : 8;
+  const int o0 = j * rstep + (h ? (KB_CAP - 1) * 8 : 0), o1 = o0 + 32 * rstep;
+  int c0 = 0, c1 = 0;  // candidates of this lane's half for its two queries
+  // (a row without candidates costs the wave one compare and an exec-mask
+  // branch; a negative distance, stored as +0, is clamped on its bits)
+  auto push = [&](float d, float lm, int o, int& c, int rb, int rv) __attribute__((always_inline)) {
+    if (d < lm) {  // NaN (rows past the cloud) never passes
+      const uint32_t db = (uint32_t)max((int32_t)__float_as_uint(d), 0);
+      *reinterpret_cast<uint64_t*>(wbase + (uint32_t)(o + e8 * min(c, KB_CAP - 1))) =
+          ((uint64_t)db << 32) | (uint32_t)(rb + rv);
+      ++c;
+    }
+  };
+
+  // Staging of tiles t, t + 1 as in the slice kernel (thread tid: rows
+  // tid / 8 and tid / 8 + 32); threads < 64 also turn their row's norm into
+  // its MFMA operand.
+  const int rrow = tid >> 3, rch = tid & 7;
+  constexpr int rstride = 2 * D + 16;
+  bf8_t st0, st1, st2, st3;
+  float stn;
+  auto stage_load = [&](int t) __attribute__((always_inline)) {
+    const int base = min(t, ntiles - 1) * KB_T;
+    const __bf16* __restrict__ ra = rb + (size_t)min(base + rrow, L2 - 1) * D;
+    const __bf16* __restrict__ rc = rb + (size_t)min(base + 32 + rrow, L2 - 1) * D;
+    st0 = 8 * rch < D ? *reinterpret_cast<const bf8_t*>(ra + 8 * rch) : bf8_t{};
+    st1 = 8 * rch + 64 < D ? *reinterpret_cast<const bf8_t*>(ra + 8 * rch + 64) : bf8_t{};
+    st2 = 8 * rch < D ? *reinterpret_cast<const bf8_t*>(rc + 8 * rch) : bf8_t{};
+    st3 = 8 * rch + 64 < D ? *reinterpret_cast<const bf8_t*>(rc + 8 * rch + 64) : bf8_t{};
+    stn = tid < CR ? (base + tid < L2 ? rr[min(base + tid, L2 - 1)] : Lim<float>::inf()) : 0.f;
+  };
+  auto stage_store = [&](int b) __attribute__((always_inline)) {
+    char* __restrict__ dst = s_rows[b] + rrow * rstride;
+    if (8 * rch < D) *reinterpret_cast<bf8_t*>(dst + 16 * rch) = st0;
+    if (8 * rch + 64 < D) *reinterpret_cast<bf8_t*>(dst + 16 * rch + 128) = st1;
+    if (8 * rch < D) *reinterpret_cast<bf8_t*>(dst + 32 * rstride + 16 * rch) = st2;
+    if (8 * rch + 64 < D) *reinterpret_cast<bf8_t*>(dst + 32 * rstride + 16 * rch + 128) = st3;
+    if (tid < CR) s_rx[b][tid] = kb_norm_operand(stn, true);
+  };
+  // tile tt of the stage in buffer b times both query blocks; the operand
+  // reads run three k-steps ahead of the MFMAs (the schedule is pinned: left
+  // alone, the compiler waits for each read right before its MFMAs)
+  auto mma = [&](int b, int tt, f16v_t& acc0, f16v_t& acc1) __attribute__((always_inline)) {
+    const char* __restrict__ src = s_rows[b] + (32 * tt + j) * rstride;
+    bf8_t a[KX];
+#pragma unroll
+    for (int s = 0; s < KS - (HALF ? 1 : 0); ++s)
+      a[s] = *reinterpret_cast<const bf8_t*>(src + 2 * (16 * s + 8 * h));
+    // the norm step: without HALF both halves read the operand (the query
+    // operand's upper half is zero there); with HALF the lower half is the
+    // last dims step's lower half
+    a[XS] = *(HALF && h == 0 ? reinterpret_cast<const bf8_t*>(src + 2 * 16 * (KS - 1))
+                             : &s_rx[b][32 * tt + j]);
+    acc0 = f16v_t{};
+    acc1 = f16v_t{};
+#pragma unroll
+    for (int s = 0; s < KX; ++s) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq0[s], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], bq1[s], acc1, 0, 0, 0);
+    }
+    constexpr int AH = KX < 3 ? KX : 3;  // reads ahead
+    __builtin_amdgcn_sched_group_barrier(0x100, AH, 0);  // DS reads
+#pragma unroll
+    for (int s = 0; s < KX - AH; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * AH, 0);
+  };
+  if (t0 < t1) {
+    stage_load(t0);
+    stage_store(0);
+  }
+  for (int tc = t0; tc < t1; tc += TC) {
+    const int b = ((tc - t0) / TC) & 1;
+    __syncthreads();  // stage tc staged; every wave is past its reads of buffer b ^ 1
+    if (tc + TC < t1) stage_load(tc + TC);
+#pragma unroll
+    for (int tt = 0; tt < TC; ++tt) {
+      const int t = tc + tt;
+      if (t < t1) {
+        f16v_t acc0, acc1;
+        mma(b, tt, acc0, acc1);
+        // The next stage goes to LDS before this tile's candidates are
+        // stored: the wait for its loads then covers no store of this tile.
+        if (tt == 0 && tc + TC < t1) stage_store(b ^ 1);
+        // acc0[v], acc1[v]: row 8 (v / 4) + 4 h + v % 4 of the tile
+        const int rb = __builtin_amdgcn_readfirstlane(t * KB_T) + 4 * h;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          push(acc0[v], lim0, o0, c0, rb, 8 * (v / 4) + v % 4);
+          push(acc1[v], lim1, o1, c1, rb, 8 * (v / 4) + v % 4);
+        }
+      }
+    }
+  }
+  // counts of (position, slice, half)
+  const size_t cr = ((size_t)n * P1 + qw) * slices + sl;
+  if (qw + j < l1) ccount[(cr + (size_t)j * slices) * 2 + h] = c0;
+  if (qw + 32 + j < l1) ccount[(cr + (size_t)(32 + j) * slices) * 2 + h] = c1;
+}
+
+// LDS written by some lanes of a wave, then read by others
+__device__ __forceinline__ void kb_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave reductions and scans over DPP (every lane active).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t kb_dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xf, true);
+}
+// the minimum (MAX: maximum) over the wave, uniform
+template <bool MAX>
+__device__ __forceinline__ uint32_t kb_wave_uext(uint32_t v) {
+  auto f = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+  // quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror: every lane
+  // holds its row's result; row_bcast:15 into rows 1, 3 and row_bcast:31 into
+  // rows 2, 3 (masked-off rows read 0, which a maximum ignores; a minimum
+  // skips those steps' effect through v itself)
+  v = f(v, __builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xa, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xc, 0xf, false));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+// inclusive prefix sum over lanes: row_shr 1, 2, 4, 8 within each row of 16
+// (lanes past the row's start read 0), then the rows' totals by row_bcast:15
+// into rows 1, 3 and row_bcast:31 into rows 2, 3
+__device__ __forceinline__ uint32_t kb_wave_scan(uint32_t v) {
+  v += kb_dpp<0x111, 0xf>(v);
+  v += kb_dpp<0x112, 0xf>(v);
+  v += kb_dpp<0x114, 0xf>(v);
+  v += kb_dpp<0x118, 0xf>(v);
+  v += kb_dpp<0x142, 0xa>(v);
+  v += kb_dpp<0x143, 0xc>(v);
+  return v;
+}
+
+// The exact K smallest of a row's candidate keys, held NK to a lane (~0
+// where none), total of them, for the candidate pass's merge: above 64
+// candidates a 64-bin histogram of the distances, linear between their
+// minimum and maximum (a monotone map), finds the bin B of the K-th smallest
+// -- only candidates in bins <= B can be among the K, and at least K are.
+// Those are gathered in sel (up to KB_SEL, past which each lane has a spare
+// slot; false when more: the row is rerun exactly); as keys are distinct
+// (the index is part of the key), each one's rank among them is its output
+// slot.  Slots past the candidates (fewer than K references) are (0, 0).
+constexpr int KB_SEL = 512;
+template <int NK>
+__device__ __forceinline__ bool kb_select(const uint64_t (&key)[NK], int total, int K,
+                                          uint32_t* __restrict__ hist,
+                                          uint64_t* __restrict__ sel, int64_t* __restrict__ io,
+                                          __bf16* __restrict__ dout) {
+  constexpr int NB = 64;
+  const int lane = lane_id();
+  const uint64_t none = ~0ull;
+  // the distance bits (a candidate's distance is >= +0, so its bits order as
+  // the distance does; the empty key's are ~0)
+  uint32_t db[NK];
+#pragma unroll
+  for (int s = 0; s < NK; ++s) db[s] = (uint32_t)(key[s] >> 32);
+  bool all = true;  // every candidate is gathered
+  uint32_t bsel = NB, lo = 0;
+  float mn = 0.f, scale = 0.f;
+  if (total > 64) {
+    uint32_t a = ~0u, b = 0;
+#pragma unroll
+    for (int s = 0; s < NK; ++s) {
+      a = min(a, db[s]);
+      b = max(b, db[s] != ~0u ? db[s] : 0u);
+    }
+    lo = kb_wave_uext<false>(a);
+    const uint32_t hi = kb_wave_uext<true>(b);
+    mn = __uint_as_float(lo);
+    scale = (float)NB / (__uint_as_float(hi) - mn);
+    if (scale < Lim<float>::inf()) {  // else one value (or a tiny span): gather all
+      all = false;
+      hist[lane] = 0;
+      kb_wave_sync();
+#pragma unroll
+      for (int s = 0; s < NK; ++s)
+        if (db[s] != ~0u) atomicAdd(&hist[min(NB - 1, (int)((__uint_as_float(db[s]) - mn) * scale))], 1u);
+      kb_wave_sync();
+      const uint32_t c = kb_wave_scan(hist[lane]);  // candidates in bins <= lane
+      const uint64_t reach = __ballot(c >= (uint32_t)K);
+      bsel = reach ? (uint32_t)__builtin_ctzll(reach) : NB;
+    }
+  }
+  // the candidates that can be among the K: this lane's count, its offset
+  // among the wave's, then its keys in order
+  bool take[NK];
+  uint32_t q = 0;
+#pragma unroll
+  for (int s = 0; s < NK; ++s) {
+    take[s] = db[s] != ~0u &&
+              (all || (uint32_t)min(NB - 1, (int)((__uint_as_float(db[s]) - mn) * scale)) <= bsel);
+    q += take[s] ? 1u : 0u;
+  }
+  const uint32_t incl = kb_wave_scan(q);
+  const int nsel = (int)__builtin_amdgcn_readlane((int)incl, 63);
+  if (nsel > KB_SEL) return false;  // a mass of equal or nearly equal distances
+  uint32_t at = incl - q;
+#pragma unroll
+  for (int s = 0; s < NK; ++s) {
+    sel[take[s] ? at : KB_SEL + lane] = key[s];
+    at += take[s] ? 1u : 0u;
+  }
+  kb_wave_sync();
+  for (int c = 0; c < nsel; c += 64) {
+    const int i = c + lane;
+    const uint64_t y = i < nsel ? sel[i] : none;
+    int rank = 0;
+#pragma unroll 4
+    for (int x = 0; x < nsel; ++x) rank += sel[x] < y ? 1 : 0;
+    if (i < nsel && rank < K) {
+      io[rank] = (int64_t)(uint32_t)y;
+      dout[rank] = (__bf16)__uint_as_float((uint32_t)(y >> 32));
+    }
+  }
+  if (lane >= nsel && lane < K) {
+    io[lane] = 0;
+    dout[lane] = (__bf16)0.f;
+  }
+  return true;
+}
+
+// The candidate pass's merge: one wave per query row (four a workgroup).  A
+// row whose regions overflowed, or that holds fewer than min(K, lengths2)
+// candidates, joins its cloud's rerun list.  Region s's m = a + b candidates
+// (the h = 0 half's first a slots, the h = 1 half's last b), in slot order,
+// go to lanes 0 .. m - 1 of one register (two when m > 64 for some region).
+// NSL: slices rounded up to a multiple of 4.  Rows past lengths1 are (0, 0).
+template <int NSL>
+__global__ __launch_bounds__(256) void knn_bf16_cmerge_kernel(
+    const uint64_t* __restrict__ cand, const int32_t* __restrict__ ccount,
+    const int64_t* __restrict__ len1, const int64_t* __restrict__ len2, int64_t rows, int P1,
+    int P2, int K, int slices, int64_t* __restrict__ idxs, __bf16* __restrict__ dists,
+    int32_t* __restrict__ rlist, int32_t* __restrict__ rcount) {
+  static_assert(KB_CAP == 128, "at most two registers a region");
+  __shared__ uint32_t s_hist[KB_WAVES][64];
+  __shared__ uint64_t s_sel[KB_WAVES][KB_SEL + 64];
+  const int w = wave_id(), lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * KB_WAVES + w;
+  if (row >= rows) return;
+  const int64_t n = row / P1;
+  const int pos = (int)(row - n * P1);
+  int64_t l1 = len1[n], l2 = len2[n];
+  l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
+  l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
+  int64_t* __restrict__ io = idxs + row * K;
+  __bf16* __restrict__ dout = dists + row * K;
+  if (pos >= l1) {
+    if (lane < K) {
+      io[lane] = 0;
+      dout[lane] = (__bf16)0.f;
+    }
+    return;
+  }
+  auto rerun = [&]() {
+    if (lane == 0) rlist[n * P1 + atomicAdd(&rcount[n], 1)] = pos;
+  };
+  const int32_t* __restrict__ cc = ccount + (size_t)row * slices * 2;
+  int ca = 0, cb = 0;
+  if (lane < slices) {
+    ca = cc[2 * lane];
+    cb = cc[2 * lane + 1];
+  }
+  const bool over = __ballot(ca + cb > KB_CAP) != 0;
+  const bool wide = __ballot(ca + cb > 64) != 0;
+  const int total = (int)__builtin_amdgcn_readlane((int)kb_wave_scan((uint32_t)(ca + cb)), 63);
+  if (over || total < min((int64_t)K, l2)) {
+    rerun();
+    return;
+  }
+  const uint64_t* __restrict__ rg = cand + (size_t)row * slices * KB_CAP;
+  // element e of region s (e < a + b) lies in slot e (e < a) or e + 128 - a - b
+  auto load = [&](int s, int e) __attribute__((always_inline)) {
+    const int a = __builtin_amdgcn_readlane(ca, s), b = __builtin_amdgcn_readlane(cb, s);
+    return e < a + b ? rg[(size_t)s * KB_CAP + (e < a ? e : e + KB_CAP - a - b)] : ~0ull;
+  };
+  bool ok;
+  if (!wide) {
+    uint64_t key[NSL];
+#pragma unroll
+    for (int s = 0; s < NSL; ++s) key[s] = s < slices ? load(s, lane) : ~0ull;
+    ok = kb_select(key, total, K, s_hist[w], s_sel[w], io, dout);
+  } else {
+    uint64_t key[2 * NSL];
+#pragma unroll
+    for (int s = 0; s < NSL; ++s) {
+      key[2 * s] = s < slices ? load(s, lane) : ~0ull;
+      key[2 * s + 1] = s < slices ? load(s, 64 + lane) : ~0ull;
+    }
+    ok = kb_select(key, total, K, s_hist[w], s_sel[w], io, dout);
+  }
+  if (!ok) rerun();
+}
+
 // Two lanes per query row (lanes j and j + 32 of a wave; 32 rows a wave):
 // each merges its half of the row's nl slice lists (sorted keys, K a list,
 // padded to KC with the empty key) in registers, v_permlane32_swap gives both
@@ -594,16 +983,11 @@ __global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
 // past lengths1 and empty entries are (0, 0).
 // Positions are rows (cloud n, position p: list entry of row n P1 + p), or
 // with qlist the rerun list's entries, whose rows are n P1 + qlist[n P1 + p].
-// rlist: the slices ran under the sampled bound; a row left with fewer than
-// min(K, lengths2) real entries is appended to its cloud's rerun list
-// (rcount[n] entries) and written by the rerun instead.
 template <int KC>
 __global__ __launch_bounds__(256) void knn_bf16_merge_kernel(
-    const uint64_t* __restrict__ part, const int64_t* __restrict__ len1,
-    const int64_t* __restrict__ len2, int64_t rows, int P1, int P2, int K, int nl,
-    int64_t* __restrict__ idxs, __bf16* __restrict__ dists, int32_t* __restrict__ rlist,
-    int32_t* __restrict__ rcount, const int32_t* __restrict__ qlist,
-    const int32_t* __restrict__ qcount) {
+    const uint64_t* __restrict__ part, const int64_t* __restrict__ len1, int64_t rows, int P1,
+    int K, int nl, int64_t* __restrict__ idxs, __bf16* __restrict__ dists,
+    const int32_t* __restrict__ qlist, const int32_t* __restrict__ qcount) {
   const int lane = lane_id(), j = lane & 31, h = lane >> 5;
   const int64_t prow = ((int64_t)blockIdx.x * KB_WAVES + wave_id()) * 32 + j;
   const uint64_t empty = kb_key(Lim<float>::inf(), KB_NONE);
@@ -659,17 +1043,6 @@ __global__ __launch_bounds__(256) void knn_bf16_merge_kernel(
   }
   kb_merge<KC, KC>(x, y);
   if (prow >= rows) return;
-  if (rlist && real) {
-    int64_t l2 = len2[n];
-    l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
-    int got = 0;
-#pragma unroll
-    for (int s = 0; s < KC; ++s) got += (s < K && (uint32_t)x[s] != (uint32_t)KB_NONE) ? 1 : 0;
-    if (got < min((int64_t)K, l2)) {
-      if (h == 0) rlist[n * P1 + atomicAdd(&rcount[n], 1)] = pos;
-      return;
-    }
-  }
   if (qlist && !real) return;
   int64_t* __restrict__ io = idxs + row * K;
   __bf16* __restrict__ dout = dists + row * K;
@@ -694,23 +1067,30 @@ static bool kb_sampled(int64_t P2) { return (P2 + KB_T - 1) / KB_T >= 2 * KB_TS;
 
 // Workspace: norms (float per point, rows padded to 32), the partial lists,
 // then (sampled bound) its parts (KB_TP x KB_TK floats per query), the rerun
-// counts (int32 per cloud) and the rerun lists (int32 per query).
+// counts (int32 per cloud), the rerun lists (int32 per query), the candidate
+// regions (KB_CAP keys per query and candidate slice) and their counts (two
+// int32 per query and candidate slice).
 struct KbWs {
-  int64_t part, taup, rcount, rlist, total;
+  int64_t part, taup, rcount, rlist, cand, ccount, total;
 };
 static KbWs kb_ws(int64_t N, int64_t P1, int64_t P2, int64_t K) {
   const KbPlan p = kb_plan(N, P1, P2);
   KbWs w;
   w.part = kb_align(N * (kb_pad(P1) + kb_pad(P2)) * 4);
   int64_t o = w.part + kb_align(N * P1 * p.slices * K * 8);
-  w.taup = w.rcount = w.rlist = -1;
+  w.taup = w.rcount = w.rlist = w.cand = w.ccount = -1;
   if (kb_sampled(P2)) {
+    const int64_t cs = kb_cplan(N, P1, P2).slices;
     w.taup = o;
     o += kb_align(N * P1 * KB_TP * KB_TK * 4);
     w.rcount = o;
     o += kb_align(N * 4);
     w.rlist = o;
     o += kb_align(N * P1 * 4);
+    w.cand = o;
+    o += kb_align(N * P1 * cs * KB_CAP * 8);
+    w.ccount = o;
+    o += kb_align(N * P1 * cs * 2 * 4);
   }
   w.total = o;
   return w;
@@ -732,39 +1112,57 @@ struct KbArgs {
   uint64_t* part;
   float* taup;  // null: no sampled bound
   int32_t *rlist, *rcount;
+  uint64_t* cand;
+  int32_t* ccount;
   int64_t* idxs;
   __bf16* dists;
   hipStream_t s;
 };
 
-// Sampled bound (when it applies): its parts, the slices under it, the merge
-// (which lists the rows left short), then the slices and the merge again over
-// those rows only, without the bound.
+// Sampled bound (when it applies): its parts, the candidate pass under it
+// and its merge (which lists the rows it cannot settle), then the exact pass
+// -- slices with lists, and their merge -- over those rows only.  Without the
+// bound, the exact pass over every row.
 template <int KS, bool HALF, int KC>
 static void kb_launch(const KbArgs& a) {
   const KbPlan p = kb_plan(a.N, a.P1, a.P2);
   const dim3 grid(a.N * p.nqb * p.slices), blk(256);
   const int64_t r1 = (int64_t)a.N * a.P1;
   const dim3 mg((unsigned)((r1 + 32 * KB_WAVES - 1) / (32 * KB_WAVES))), mb(64 * KB_WAVES);
-  if (a.taup)
-    hipLaunchKernelGGL((knn_bf16_tau_kernel<KS, HALF>), dim3(a.N * p.nqb * KB_TP), blk, 0, a.s,
-                       a.p1, a.p2, a.l1, a.l2, a.N, a.P1, a.P2, a.D, p.nqb, a.qn, a.rn, a.taup,
-                       a.rcount);
-  hipLaunchKernelGGL((knn_bf16_slice_kernel<KS, HALF, KC>), grid, blk, 0, a.s, a.p1, a.p2, a.l1,
-                     a.l2, a.P1, a.P2, a.D, a.K, p.nqb, p.slices, a.qn, a.rn, a.part,
-                     (const float*)a.taup, (const int32_t*)nullptr, (const int32_t*)nullptr);
-  hipLaunchKernelGGL(knn_bf16_merge_kernel<KC>, mg, mb, 0, a.s, (const uint64_t*)a.part, a.l1,
-                     a.l2, r1, a.P1, a.P2, a.K, p.slices, a.idxs, a.dists,
-                     a.taup ? a.rlist : nullptr, a.taup ? a.rcount : nullptr,
-                     (const int32_t*)nullptr, (const int32_t*)nullptr);
-  if (a.taup) {
+  if (!a.taup) {
     hipLaunchKernelGGL((knn_bf16_slice_kernel<KS, HALF, KC>), grid, blk, 0, a.s, a.p1, a.p2, a.l1,
                        a.l2, a.P1, a.P2, a.D, a.K, p.nqb, p.slices, a.qn, a.rn, a.part,
-                       (const float*)nullptr, (const int32_t*)a.rlist, (const int32_t*)a.rcount);
+                       (const int32_t*)nullptr, (const int32_t*)nullptr);
     hipLaunchKernelGGL(knn_bf16_merge_kernel<KC>, mg, mb, 0, a.s, (const uint64_t*)a.part, a.l1,
-                       a.l2, r1, a.P1, a.P2, a.K, p.slices, a.idxs, a.dists, (int32_t*)nullptr,
-                       (int32_t*)nullptr, (const int32_t*)a.rlist, (const int32_t*)a.rcount);
+                       r1, a.P1, a.K, p.slices, a.idxs, a.dists, (const int32_t*)nullptr,
+                       (const int32_t*)nullptr);
+    return;
   }
+  const KbPlan cp = kb_cplan(a.N, a.P1, a.P2);
+  hipLaunchKernelGGL((knn_bf16_tau_kernel<KS, HALF>), dim3(a.N * p.nqb * KB_TP), blk, 0, a.s,
+                     a.p1, a.p2, a.l1, a.l2, a.N, a.P1, a.P2, a.D, p.nqb, a.qn, a.rn, a.taup,
+                     a.rcount);
+  hipLaunchKernelGGL((knn_bf16_cand_kernel<KS, HALF>), dim3(a.N * cp.nqb * cp.slices), blk, 0, a.s,
+                     a.p1, a.p2, a.l1, a.l2, a.P1, a.P2, cp.nqb, cp.slices, a.qn, a.rn,
+                     (const float*)a.taup, a.cand, a.ccount);
+  {
+    const dim3 g((unsigned)((r1 + KB_WAVES - 1) / KB_WAVES));
+#define KB_CM(NSL)                                                                               \
+  hipLaunchKernelGGL(knn_bf16_cmerge_kernel<NSL>, g, blk, 0, a.s, (const uint64_t*)a.cand,       \
+                     (const int32_t*)a.ccount, a.l1, a.l2, r1, a.P1, a.P2, a.K, cp.slices, a.idxs, \
+                     a.dists, a.rlist, a.rcount)
+    if (cp.slices <= 4) KB_CM(4);
+    else if (cp.slices <= 8) KB_CM(8);
+    else if (cp.slices <= 12) KB_CM(12);
+    else KB_CM(16);
+#undef KB_CM
+  }
+  hipLaunchKernelGGL((knn_bf16_slice_kernel<KS, HALF, KC>), grid, blk, 0, a.s, a.p1, a.p2, a.l1,
+                     a.l2, a.P1, a.P2, a.D, a.K, p.nqb, p.slices, a.qn, a.rn, a.part,
+                     (const int32_t*)a.rlist, (const int32_t*)a.rcount);
+  hipLaunchKernelGGL(knn_bf16_merge_kernel<KC>, mg, mb, 0, a.s, (const uint64_t*)a.part, a.l1,
+                     r1, a.P1, a.K, p.slices, a.idxs, a.dists, (const int32_t*)a.rlist,
+                     (const int32_t*)a.rcount);
 }
 
 template <int KC>
@@ -813,6 +1211,8 @@ void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const in
   a.taup = L.taup >= 0 ? reinterpret_cast<float*>(wb + L.taup) : nullptr;
   a.rcount = L.rcount >= 0 ? reinterpret_cast<int32_t*>(wb + L.rcount) : nullptr;
   a.rlist = L.rlist >= 0 ? reinterpret_cast<int32_t*>(wb + L.rlist) : nullptr;
+  a.cand = L.cand >= 0 ? reinterpret_cast<uint64_t*>(wb + L.cand) : nullptr;
+  a.ccount = L.ccount >= 0 ? reinterpret_cast<int32_t*>(wb + L.ccount) : nullptr;
   a.idxs = idxs;
   a.dists = (__bf16*)dists;
   a.s = s;
