@@ -68,13 +68,19 @@ __host__ __device__ inline int64_t kb_pad(int64_t n) { return (n + 31) & ~(int64
 // out[r] = sum over d of p[r][d]^2 in float (rows of D bfloat16, D % 8 == 0,
 // D <= 128): 16 lanes a row, lane c summing dims 8c .. 8c + 7 by an FMA chain
 // from one 16-byte load, then the 16 partial sums added pairwise in a fixed
-// order (lanes 8 apart, then 4, 2, 1)
-__global__ __launch_bounds__(256) void knn_bf16_norms_kernel(const __bf16* __restrict__ p,
-                                                             int64_t rows, int64_t stride_out,
-                                                             int64_t rows_per_batch, int D,
-                                                             float* __restrict__ out) {
+// order (lanes 8 apart, then 4, 2, 1).  One launch for both clouds: the
+// first nb1 blocks take p1's rows (padded to 32 a batch in the output), the
+// rest p2's.
+__global__ __launch_bounds__(256) void knn_bf16_norms_kernel(
+    const __bf16* __restrict__ p1, int64_t rows1, int64_t per1, float* __restrict__ out1,
+    const __bf16* __restrict__ p2, int64_t rows2, int64_t per2, float* __restrict__ out2, int D,
+    int64_t nb1) {
+  const bool second = blockIdx.x >= nb1;  // block-uniform
+  const __bf16* __restrict__ p = second ? p2 : p1;
+  const int64_t rows = second ? rows2 : rows1, per = second ? per2 : per1;
+  float* __restrict__ out = second ? out2 : out1;
   const int c = threadIdx.x & 15;
-  const int64_t r = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const int64_t r = ((int64_t)(blockIdx.x - (second ? nb1 : 0)) * 256 + threadIdx.x) >> 4;
   const bool live = r < rows;
   float acc = 0.f;
   if (live && 8 * c < D) {
@@ -88,8 +94,8 @@ __global__ __launch_bounds__(256) void knn_bf16_norms_kernel(const __bf16* __res
 #pragma unroll
   for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
   if (live && c == 0) {
-    const int64_t b = r / rows_per_batch;
-    out[b * stride_out + (r - b * rows_per_batch)] = acc;
+    const int64_t b = r / per;
+    out[b * kb_pad(per) + (r - b * per)] = acc;
   }
 }
 
@@ -496,14 +502,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 // smallest distance of every tile: the part's KB_TK tile minima, sorted
 // (+inf when none), stored [n][pt][i][query].  The KB_TK-th smallest of a
 // query's KB_TS tile minima is a sampled distance with at least KB_TK sampled
-// distances at or below it.  Workgroup 0 also clears the rerun counts.
+// distances at or below it.  The workgroup stages its KB_TK tiles in LDS at
+// once (every load in flight together), then each wave runs them back to
+// back.  Workgroup 0 also clears the rerun counts.
 template <int KS, bool HALF>
 __global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
     const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
-    const int64_t* __restrict__ len2, int N, int P1, int P2, int D, int nqb,
+    const int64_t* __restrict__ len2, int N, int P1, int P2, int nqb,
     const float* __restrict__ qn, const float* __restrict__ rn, float* __restrict__ taup,
     int32_t* __restrict__ rcount) {
   static_assert(KB_TS / KB_TP == KB_TK, "a part is KB_TK tiles");
+  constexpr int D = 16 * KS - (HALF ? 8 : 0);  // the dimension (the dispatch's choice of KS, HALF)
+  constexpr int RS = 2 * D + 16, NR = KB_TK * KB_T;  // row stride, rows staged
+  __shared__ __align__(16) char s_rows[NR * RS];
+  __shared__ bf8_t s_rx[NR];
   if (blockIdx.x == 0)
     for (int i = threadIdx.x; i < N; i += 256) rcount[i] = 0;
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
@@ -513,7 +525,7 @@ __global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
   l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
   l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
   const int L2 = (int)l2;
-  const int w = wave_id(), lane = lane_id(), j = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, w = wave_id(), lane = lane_id(), j = lane & 31, h = lane >> 5;
   const int qw = qb * KB_QW + 64 * w;
   const int q = qw + lane;
   constexpr int KX = HALF ? KS : KS + 1, XS = KX - 1, XH = HALF ? 1 : 0;
@@ -521,7 +533,31 @@ __global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
 #pragma unroll
   for (int i = 0; i < KB_TK; ++i) s[i] = Lim<float>::inf();
   const int ntiles = (L2 + KB_T - 1) / KB_T;
-  if (ntiles >= 2 * KB_TS) {
+  if (ntiles >= 2 * KB_TS) {  // workgroup-uniform
+    const __bf16* __restrict__ rb = p2 + (size_t)n * P2 * D;
+    const float* __restrict__ rr = rn + (size_t)n * kb_pad(P2);
+    const int stride = ntiles / KB_TS;
+    // staging: tile k's row r (thread tid: r = tid / 8, 16-byte chunks
+    // tid % 8 and tid % 8 + 8 of every tile; thread tid: the norm of staged
+    // row tid); the sampled tiles lie inside the cloud
+    const int rrow = tid >> 3, rch = tid & 7;
+    {
+      bf8_t st[KB_TK][2];
+#pragma unroll
+      for (int k = 0; k < KB_TK; ++k) {
+        const __bf16* __restrict__ ra = rb + ((size_t)(pt + KB_TP * k) * stride * KB_T + rrow) * D;
+        st[k][0] = 8 * rch < D ? *reinterpret_cast<const bf8_t*>(ra + 8 * rch) : bf8_t{};
+        st[k][1] = 8 * rch + 64 < D ? *reinterpret_cast<const bf8_t*>(ra + 8 * rch + 64) : bf8_t{};
+      }
+      const float nrm = rr[(size_t)(pt + KB_TP * (tid / KB_T)) * stride * KB_T + tid % KB_T];
+#pragma unroll
+      for (int k = 0; k < KB_TK; ++k) {
+        char* __restrict__ dst = s_rows + (k * KB_T + rrow) * RS;
+        if (8 * rch < D) *reinterpret_cast<bf8_t*>(dst + 16 * rch) = st[k][0];
+        if (8 * rch + 64 < D) *reinterpret_cast<bf8_t*>(dst + 16 * rch + 128) = st[k][1];
+      }
+      s_rx[tid] = kb_norm_operand(nrm, true);
+    }
     bf8_t bq0[KX], bq1[KX];
     {
       const int c0 = min(qw + j, P1 - 1), c1 = min(qw + 32 + j, P1 - 1);
@@ -538,33 +574,17 @@ __global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
       bq0[XS] = h == XH ? x0 : (HALF ? bq0[XS] : bf8_t{});
       bq1[XS] = h == XH ? x1 : (HALF ? bq1[XS] : bf8_t{});
     }
-    const __bf16* __restrict__ rb = p2 + (size_t)n * P2 * D;
-    const float* __restrict__ rr = rn + (size_t)n * kb_pad(P2);
-    const int stride = ntiles / KB_TS;
-    // the next sampled tile's rows are loaded while this one is processed
-    bf8_t an[KS];
-    float nn;
-    auto load_rows = [&](int k) __attribute__((always_inline)) {
-      const int base = (pt + KB_TP * min(k, KB_TK - 1)) * stride * KB_T;
-      const int row = min(base + j, L2 - 1);
-      const __bf16* __restrict__ ra = rb + (size_t)row * D;
-#pragma unroll
-      for (int st = 0; st < KS; ++st) {
-        const int d0 = (HALF && st == KS - 1) ? 16 * st : 16 * st + 8 * h;
-        an[st] = *reinterpret_cast<const bf8_t*>(ra + d0);
-      }
-      nn = rr[row];
-    };
-    load_rows(0);
+    __syncthreads();
 #pragma unroll 1
     for (int k = 0; k < KB_TK; ++k) {
-      const int base = (pt + KB_TP * k) * stride * KB_T;
+      const char* __restrict__ src = s_rows + (k * KB_T + j) * RS;
       bf8_t a[KX];
 #pragma unroll
-      for (int st = 0; st < KS; ++st) a[st] = an[st];
-      const bf8_t xr = kb_norm_operand(base + j < L2 ? nn : Lim<float>::inf(), true);
-      a[XS] = h == XH ? xr : (HALF ? a[XS] : bf8_t{});
-      load_rows(k + 1);
+      for (int st = 0; st < KS - (HALF ? 1 : 0); ++st)
+        a[st] = *reinterpret_cast<const bf8_t*>(src + 2 * (16 * st + 8 * h));
+      // the norm step as in the candidate pass
+      a[XS] = *(HALF && h == 0 ? reinterpret_cast<const bf8_t*>(src + 2 * 16 * (KS - 1))
+                               : &s_rx[k * KB_T + j]);
       f16v_t acc0 = {}, acc1 = {};
 #pragma unroll
       for (int st = 0; st < KX; ++st) {
@@ -573,7 +593,7 @@ __global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
       }
       // the tile's smallest distance for the lane's query: lane l holds 16
       // rows of column l % 32 of each block, its partner l ^ 32 the other 16,
-      // combined by one swap (NaN rows, past the cloud, drop out of fminf)
+      // combined by one swap
       float m0 = acc0[0], m1 = acc1[0];
 #pragma unroll
       for (int v = 1; v < 16; ++v) {
@@ -612,8 +632,7 @@ static KbPlan kb_cplan(int64_t N, int64_t P1, int64_t P2) {
 // slice) -- KB_CAP slots, which the half-wave h = 0 fills upwards from the
 // first and h = 1 downwards from the last.  No swap is needed: lane (h, j)
 // tests its block-0 column (position qw + j) against that query's bound and
-// its block-1 column (qw + 32 + j) against that one's.  A row is skipped by
-// the wave unless some lane has a candidate in it.  Counts run on past the
+// its block-1 column (qw + 32 + j) against that one's.  Counts run on past the
 // capacity (the last slot is overwritten); the merge sends such a query, and
 // one left with fewer than min(K, lengths2) candidates, to the exact pass.
 template <int KS, bool HALF>
@@ -675,14 +694,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   const int rstep = slices * KB_CAP * 8, e8 = h ? -8 : 8;
   const int o0 = j * rstep + (h ? (KB_CAP - 1) * 8 : 0), o1 = o0 + 32 * rstep;
   int c0 = 0, c1 = 0;  // candidates of this lane's half for its two queries
-  // (a row without candidates costs the wave one compare and an exec-mask
-  // branch; a negative distance, stored as +0, is clamped on its bits)
-  auto push = [&](float d, float lm, int o, int& c, int rb, int rv) __attribute__((always_inline)) {
-    if (d < lm) {  // NaN (rows past the cloud) never passes
+  // A tile's 32 distances per lane are tested into one 32-bit mask (bit
+  // 31 - v: acc0[v] for v < 16, else acc1[v - 16], is at or below its
+  // query's bound), without branches; then each lane stores its candidates
+  // one at a time (the wave loops max-over-lanes times, ~1.4 a tile), the
+  // value picked by a select tree.  A negative distance, stored as +0, is
+  // clamped on its bits; NaN (rows past the cloud) never passes.
+  auto filter = [&](const f16v_t& acc0, const f16v_t& acc1, int rb) __attribute__((always_inline)) {
+    // The compares are inline asm, after which the compiler would not wait
+    // for the MFMA results: a compiler-visible read of both accumulators
+    // (the last written) comes first, and the mask depends on it (its bit
+    // is shifted out).
+    uint32_t m = __builtin_isnan(acc0[15] + acc1[15]) ? 1u : 0u;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      m = push_lt4(m, acc0[4 * g], acc0[4 * g + 1], acc0[4 * g + 2], acc0[4 * g + 3], lim0);
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      m = push_lt4(m, acc1[4 * g], acc1[4 * g + 1], acc1[4 * g + 2], acc1[4 * g + 3], lim1);
+    if (__ballot(m != 0) == 0) return;
+    while (m) {
+      const int v = 31 - __builtin_ctz(m);
+      m &= m - 1;
+      const uint32_t m4 = bit_mask(v, 4);
+      float e[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) e[i] = csel(m4, acc0[i], acc1[i]);
+      const float d = kb_sel16(e, v & 15);
+      const bool second = v >= 16;
+      const int c = second ? c1 : c0, o = second ? o1 : o0;
       const uint32_t db = (uint32_t)max((int32_t)__float_as_uint(d), 0);
       *reinterpret_cast<uint64_t*>(wbase + (uint32_t)(o + e8 * min(c, KB_CAP - 1))) =
-          ((uint64_t)db << 32) | (uint32_t)(rb + rv);
-      ++c;
+          ((uint64_t)db << 32) | (uint32_t)(rb + 8 * ((v >> 2) & 3) + (v & 3));
+      c0 += second ? 0 : 1;
+      c1 += second ? 1 : 0;
     }
   };
 
@@ -759,12 +804,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
         // stored: the wait for its loads then covers no store of this tile.
         if (tt == 0 && tc + TC < t1) stage_store(b ^ 1);
         // acc0[v], acc1[v]: row 8 (v / 4) + 4 h + v % 4 of the tile
-        const int rb = __builtin_amdgcn_readfirstlane(t * KB_T) + 4 * h;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          push(acc0[v], lim0, o0, c0, rb, 8 * (v / 4) + v % 4);
-          push(acc1[v], lim1, o1, c1, rb, 8 * (v / 4) + v % 4);
-        }
+        filter(acc0, acc1, __builtin_amdgcn_readfirstlane(t * KB_T) + 4 * h);
       }
     }
   }
@@ -1140,8 +1180,7 @@ static void kb_launch(const KbArgs& a) {
   }
   const KbPlan cp = kb_cplan(a.N, a.P1, a.P2);
   hipLaunchKernelGGL((knn_bf16_tau_kernel<KS, HALF>), dim3(a.N * p.nqb * KB_TP), blk, 0, a.s,
-                     a.p1, a.p2, a.l1, a.l2, a.N, a.P1, a.P2, a.D, p.nqb, a.qn, a.rn, a.taup,
-                     a.rcount);
+                     a.p1, a.p2, a.l1, a.l2, a.N, a.P1, a.P2, p.nqb, a.qn, a.rn, a.taup, a.rcount);
   hipLaunchKernelGGL((knn_bf16_cand_kernel<KS, HALF>), dim3(a.N * cp.nqb * cp.slices), blk, 0, a.s,
                      a.p1, a.p2, a.l1, a.l2, a.P1, a.P2, cp.nqb, cp.slices, a.qn, a.rn,
                      (const float*)a.taup, a.cand, a.ccount);
@@ -1188,12 +1227,11 @@ void launch_knn_bf16(const void* p1, const void* p2, const int64_t* l1, const in
   float* qn = reinterpret_cast<float*>(ws);
   float* rn = qn + (size_t)N * kb_pad(P1);
   const int64_t r1 = (int64_t)N * P1, r2 = (int64_t)N * P2;
-  if (r1 > 0)
-    hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)((r1 + 15) / 16)), dim3(256), 0, s,
-                       (const __bf16*)p1, r1, kb_pad(P1), (int64_t)P1, D, qn);
-  if (r2 > 0)
-    hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)((r2 + 15) / 16)), dim3(256), 0, s,
-                       (const __bf16*)p2, r2, kb_pad(P2), (int64_t)P2, D, rn);
+  const int64_t nb1 = (r1 + 15) / 16, nb2 = (r2 + 15) / 16;
+  if (nb1 + nb2 > 0)
+    hipLaunchKernelGGL(knn_bf16_norms_kernel, dim3((unsigned)(nb1 + nb2)), dim3(256), 0, s,
+                       (const __bf16*)p1, r1, (int64_t)P1, qn, (const __bf16*)p2, r2, (int64_t)P2,
+                       rn, D, nb1);
   if (r1 == 0) return;
   KbArgs a;
   a.p1 = (const __bf16*)p1;

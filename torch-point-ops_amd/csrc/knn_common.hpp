@@ -64,7 +64,9 @@ __device__ __forceinline__ half_t to_vgpr(half_t s) { return s; }
 // that a VALU op wrote fewer than two wait states before: the compiler
 // inserts those waits between its own instructions but not inside or in
 // front of an asm statement.  The asm below either reads VGPRs only or
-// spaces each such read itself.
+// spaces each such read itself.  Likewise the compiler waits for an MFMA's
+// result only before its own instructions: asm reading MFMA accumulators
+// must follow (by a data dependence) a compiler-visible read of them.
 
 // mask = 16 * mask + 8 (d0 < thr) + 4 (d1 < thr) + 2 (d2 < thr) + (d3 < thr):
 // four compares into four SGPR pairs, then four add-with-carry doublings;
