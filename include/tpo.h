@@ -164,8 +164,10 @@ int tpo_chamfer_loss_bwd(int dtype, const void* xyz1, const void* xyz2,
  *   (distance, index), dists rounded to bfloat16; rows >= lengths1 and
  *   slots >= lengths2 are (0,0).  version is ignored and version_out
  *   receives -1.  For P2 >= 4096 the workspace also holds a per-query bound
- *   sampled from 64 tiles of 32 references and a list of the rows it left
- *   short, which are recomputed without it; results do not depend on it.
+ *   sampled from 64 tiles of 32 references, the candidates at or below it
+ *   (up to 128 per query and reference slice) and a list of the rows that
+ *   overflowed or fell short, which are recomputed without it; results do
+ *   not depend on it.
  *   If version_out is not NULL it receives the version that ran.
  */
 int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int64_t P2,
