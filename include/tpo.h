@@ -163,11 +163,12 @@ int tpo_chamfer_loss_bwd(int dtype, const void* xyz1, const void* xyz2,
  *   three-piece bf16 splits), clamped at 0; each row's K nearest sorted by
  *   (distance, index), dists rounded to bfloat16; rows >= lengths1 and
  *   slots >= lengths2 are (0,0).  version is ignored and version_out
- *   receives -1.  For P2 >= 4096 the workspace also holds a per-query bound
- *   sampled from 64 tiles of 32 references, the candidates at or below it
- *   (up to 128 per query and reference slice) and a list of the rows that
- *   overflowed or fell short, which are recomputed without it; results do
- *   not depend on it.
+ *   receives -1.  For P2 >= max(4096, 1536 K) the workspace also holds a
+ *   per-query bound sampled from 64 tiles of 32 references, the candidates
+ *   at or below it (up to 128 per query and reference slice) and a list of
+ *   the rows that overflowed or fell short (and every row of a cloud whose
+ *   lengths2 is below that size), which are recomputed without it; results
+ *   do not depend on it.
  *   If version_out is not NULL it receives the version that ran.
  */
 int64_t tpo_knn_workspace_size(int dtype, int64_t N, int64_t P1, int64_t P2,

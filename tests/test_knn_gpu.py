@@ -594,15 +594,16 @@ def test_bf16_equal_distances_take_lower_indices(tpo, dev):
 
 
 def test_bf16_rows_the_sampled_bound_leaves_short_are_rerun(tpo, dev):
-    # Clouds of >= 4096 references first bound each query by the 8th smallest
-    # of its minimum distances over 64 sampled tiles of 32 references (tiles
-    # i * (tiles // 64)); only distances under the bound are candidates, and a
-    # row left with fewer than K is rerun without it.  Here the first 32
-    # queries of each cloud have 8 near copies in 8 different sampled tiles
-    # and their next 24 neighbours outside them: their bound admits 8
-    # candidates, so they take the rerun; the other queries have their near
-    # points outside the sample and keep the bound.  The lists must be the K
-    # nearest either way (float64 check).
+    # Clouds of >= max(4096, 1536 K) references first bound each query by the
+    # 8th smallest of its minimum distances over 64 sampled tiles of 32
+    # references (tiles i * (tiles // 64)); only distances under the bound are
+    # candidates, and a row left with fewer than K is rerun without it.  Here
+    # the first 32 queries of cloud 0 have 8 near copies in 8 different
+    # sampled tiles and their next 24 neighbours outside them: their bound
+    # admits 8 candidates, so they take the rerun; the other queries have
+    # their near points outside the sample and keep the bound.  Cloud 1 has
+    # 40000 references, below 1536 K: all its 50 rows take the exact pass.
+    # The lists must be the K nearest either way (float64 check).
     g = torch.Generator().manual_seed(17)
     B, P1, P2, D, K = 2, 64, 65536, 64, 32
     l2 = torch.tensor([P2, 40000])
@@ -632,7 +633,8 @@ def test_bf16_rows_the_sampled_bound_leaves_short_are_rerun(tpo, dev):
     check_bf16_knn(idx, d, q, r, l1, l2, K)
     # the same call through the C ABI with a caller workspace, whose rerun
     # counts (after the norms, the 8 slices' lists and the bound's parts)
-    # show that exactly the 32 planted rows of each cloud were rerun
+    # show that exactly the 32 planted rows of cloud 0 and all 50 rows of
+    # cloud 1 were rerun
     import ctypes
     from torch_point_ops import _native
 
@@ -659,7 +661,68 @@ def test_bf16_rows_the_sampled_bound_leaves_short_are_rerun(tpo, dev):
     # two counts per query
     assert at + up(B * 4) + up(B * P1 * 4) + up(B * P1 * 16 * 128 * 8) + up(B * P1 * 16 * 2 * 4) == size
     counts = ws[at:at + 4 * B].cpu().view(torch.int32)
-    assert counts.tolist() == [32, 32]
+    assert counts.tolist() == [32, 50]
+
+
+def test_bf16_candidate_regions_wide_overflowed_and_tied(tpo, dev):
+    # Clouds of >= 4096 references run the candidate pass: each (query,
+    # slice) region holds up to 128 candidates, one register a slice in the
+    # merge while every region holds <= 64, two otherwise; an overflowed
+    # region, or more than 512 candidates left by the merge's histogram (a
+    # mass of equal distances), sends the row to the exact pass.  Here 16
+    # slices of 512 references (16 tiles; tiles 4i are sampled; K = 4 so that
+    # 8192 references take the bound).  Query 0 of cloud 0 has 100 near
+    # points in slice 0 (two registers, no overflow), query 0 of cloud 1 has
+    # 200 there (overflow), and query 0 of cloud 2 has 38 exact copies of one
+    # near point at the head of every slice (608 equal distances: rerun, and
+    # the list must be their K lowest indices).
+    import ctypes
+    from torch_point_ops import _native
+    g = torch.Generator().manual_seed(29)
+    B, P1, P2, D, K = 3, 64, 8192, 64, 4
+    q = torch.randn(B, P1, D, generator=g)
+    q = q / q.norm(dim=-1, keepdim=True)
+    r = torch.randn(B, P2, D, generator=g)
+    r = r / r.norm(dim=-1, keepdim=True)
+    r[0, :100] = q[0, 0] + 0.05 * torch.randn(100, D, generator=g)
+    r[1, :200] = q[1, 0] + 0.05 * torch.randn(200, D, generator=g)
+    near = q[2, 0] + 0.05 * torch.randn(D, generator=g)
+    for sl in range(16):
+        r[2, 512 * sl:512 * sl + 38] = near
+    q, r = q.to(torch.bfloat16), r.to(torch.bfloat16)
+    l1 = torch.full((B,), P1, dtype=torch.int64)
+    l2 = torch.full((B,), P2, dtype=torch.int64)
+    idx, d = raw(q, r, l1, l2, 2, K, -1, dev)
+    check_bf16_knn(idx, d, q, r, l1, l2, K)
+    assert idx[2, 0].tolist() == list(range(K))
+    assert bool((d[2, 0] == d[2, 0, 0]).all())
+    # through the C ABI with a caller workspace: the rerun lists (after the
+    # norms, the exact pass's 8 slices of lists, the bound's parts and the
+    # rerun counts) hold query 0 of clouds 1 and 2, not of cloud 0 (other
+    # rows may fall short of K candidates and join them)
+    lib = ctypes.CDLL(_native.HIP_LIB)
+    P, I = ctypes.c_void_p, ctypes.c_int64
+    lib.tpo_knn_fwd.argtypes = [ctypes.c_int, P, P, P, P, I, I, I, I, I, ctypes.c_int,
+                                ctypes.c_int, P, P, P, P, I, P]
+    lib.tpo_knn_workspace_size.argtypes = [ctypes.c_int, I, I, I, I, I, ctypes.c_int]
+    lib.tpo_knn_workspace_size.restype = I
+    size = lib.tpo_knn_workspace_size(3, B, P1, P2, D, K, 2)
+    ws = torch.zeros(size, dtype=torch.uint8, device=dev)
+    qd, rd, l1d, l2d = q.to(dev), r.to(dev), l1.to(dev), l2.to(dev)
+    idx2 = torch.empty(B, P1, K, dtype=torch.int64, device=dev)
+    d2 = torch.empty(B, P1, K, dtype=torch.bfloat16, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.tpo_knn_fwd(3, qd.data_ptr(), rd.data_ptr(), l1d.data_ptr(), l2d.data_ptr(), B, P1,
+                           P2, D, K, 2, -1, idx2.data_ptr(), d2.data_ptr(), None, ws.data_ptr(),
+                           size, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(idx2, idx.to(dev)) and torch.equal(d2, d.to(dev))
+    up = lambda x: (x + 255) // 256 * 256
+    at = up(B * (P1 + P2) * 4) + up(B * P1 * 8 * K * 8) + up(B * P1 * 64 * 4)
+    counts = ws[at:at + 4 * B].cpu().view(torch.int32).tolist()
+    rl = ws[at + up(B * 4):at + up(B * 4) + 4 * B * P1].cpu().view(torch.int32).view(B, P1)
+    listed = [set(rl[n, :counts[n]].tolist()) for n in range(B)]
+    assert 0 not in listed[0] and 0 in listed[1] and 0 in listed[2], (counts, listed)
 
 
 def test_bf16_knn_points_and_fallbacks(tpo, dev):

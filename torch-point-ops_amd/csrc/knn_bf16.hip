@@ -52,11 +52,19 @@ constexpr int KB_MAX_SLICES = 8;
 constexpr int KB_NONE = 0x7fffffff;      // index of an empty list entry
 // The sampled bound: the KB_TK-th smallest of each query's minimum distances
 // over KB_TS reference tiles spread over its cloud (KB_TP workgroups of query
-// blocks, KB_TS / KB_TP tiles each); clouds of fewer than 2 KB_TS tiles take
-// none.
+// blocks, KB_TS / KB_TP tiles each); see kb_sampled for the clouds that take
+// one (the others' bound is +inf: every row then overflows or falls short and
+// takes the exact pass).
 constexpr int KB_TS = 64;
 constexpr int KB_TP = 8;
 constexpr int KB_TK = 8;
+// The sampled bound applies to clouds of at least 2 KB_TS tiles and 1536 K
+// references: about one reference in 260 lies at or below it (the 8th of 64
+// tile minima), so a row then has ~6 K candidates on average; with fewer,
+// rows left short (and rerun) would be common.
+__host__ __device__ inline bool kb_sampled(int64_t L2, int64_t K) {
+  return (L2 + KB_T - 1) / KB_T >= 2 * KB_TS && L2 >= 1536 * K;
+}
 // Under the bound: candidate slots per (query, slice), shared by the two
 // half-waves that hold the query's rows (one fills up from slot 0, the other
 // down from the last; a multiple of 64), and at most KB_CMAX_SLICES slices
@@ -508,7 +516,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 template <int KS, bool HALF>
 __global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
     const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
-    const int64_t* __restrict__ len2, int N, int P1, int P2, int nqb,
+    const int64_t* __restrict__ len2, int N, int P1, int P2, int K, int nqb,
     const float* __restrict__ qn, const float* __restrict__ rn, float* __restrict__ taup,
     int32_t* __restrict__ rcount) {
   static_assert(KB_TS / KB_TP == KB_TK, "a part is KB_TK tiles");
@@ -533,7 +541,7 @@ __global__ __launch_bounds__(256) void knn_bf16_tau_kernel(
 #pragma unroll
   for (int i = 0; i < KB_TK; ++i) s[i] = Lim<float>::inf();
   const int ntiles = (L2 + KB_T - 1) / KB_T;
-  if (ntiles >= 2 * KB_TS) {  // workgroup-uniform
+  if (kb_sampled(L2, K)) {  // workgroup-uniform
     const __bf16* __restrict__ rb = p2 + (size_t)n * P2 * D;
     const float* __restrict__ rr = rn + (size_t)n * kb_pad(P2);
     const int stride = ntiles / KB_TS;
@@ -638,7 +646,7 @@ static KbPlan kb_cplan(int64_t N, int64_t P1, int64_t P2) {
 template <int KS, bool HALF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void knn_bf16_cand_kernel(
     const __bf16* __restrict__ p1, const __bf16* __restrict__ p2, const int64_t* __restrict__ len1,
-    const int64_t* __restrict__ len2, int P1, int P2, int nqb, int slices,
+    const int64_t* __restrict__ len2, int P1, int P2, int K, int nqb, int slices,
     const float* __restrict__ qn, const float* __restrict__ rn, const float* __restrict__ taup,
     uint64_t* __restrict__ cand, int32_t* __restrict__ ccount) {
   constexpr int D = 16 * KS - (HALF ? 8 : 0);  // the dimension (the dispatch's choice of KS, HALF)
@@ -653,7 +661,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   int64_t l1 = len1[n], l2 = len2[n];
   l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
   l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
-  if (qb * KB_QW >= l1) return;  // the whole workgroup past the cloud's queries
+  // the whole workgroup past the cloud's queries, or a cloud without the
+  // bound (its rows all take the exact pass; the merge lists them)
+  if (qb * KB_QW >= l1 || !kb_sampled(l2, K)) return;
   const int L2 = (int)l2;
   const int tid = threadIdx.x, w = wave_id(), lane = lane_id(), j = lane & 31, h = lane >> 5;
   const int qw = qb * KB_QW + 64 * w;
@@ -945,7 +955,8 @@ __device__ __forceinline__ bool kb_select(const uint64_t (&key)[NK], int total, 
 
 // The candidate pass's merge: one wave per query row (four a workgroup).  A
 // row whose regions overflowed, or that holds fewer than min(K, lengths2)
-// candidates, joins its cloud's rerun list.  Region s's m = a + b candidates
+// candidates, joins its cloud's rerun list, as does every row of a cloud
+// without the bound (kb_sampled).  Region s's m = a + b candidates
 // (the h = 0 half's first a slots, the h = 1 half's last b), in slot order,
 // go to lanes 0 .. m - 1 of one register (two when m > 64 for some region).
 // NSL: slices rounded up to a multiple of 4.  Rows past lengths1 are (0, 0).
@@ -978,6 +989,10 @@ __global__ __launch_bounds__(256) void knn_bf16_cmerge_kernel(
   auto rerun = [&]() {
     if (lane == 0) rlist[n * P1 + atomicAdd(&rcount[n], 1)] = pos;
   };
+  if (!kb_sampled(l2, K)) {  // a cloud without the bound: no candidates were kept
+    rerun();
+    return;
+  }
   const int32_t* __restrict__ cc = ccount + (size_t)row * slices * 2;
   int ca = 0, cb = 0;
   if (lane < slices) {
@@ -1102,8 +1117,6 @@ __global__ __launch_bounds__(256) void knn_bf16_merge_kernel(
 
 static int64_t kb_align(int64_t x) { return (x + 255) / 256 * 256; }
 
-// The sampled bound applies to clouds of at least 2 KB_TS tiles.
-static bool kb_sampled(int64_t P2) { return (P2 + KB_T - 1) / KB_T >= 2 * KB_TS; }
 
 // Workspace: norms (float per point, rows padded to 32), the partial lists,
 // then (sampled bound) its parts (KB_TP x KB_TK floats per query), the rerun
@@ -1119,7 +1132,7 @@ static KbWs kb_ws(int64_t N, int64_t P1, int64_t P2, int64_t K) {
   w.part = kb_align(N * (kb_pad(P1) + kb_pad(P2)) * 4);
   int64_t o = w.part + kb_align(N * P1 * p.slices * K * 8);
   w.taup = w.rcount = w.rlist = w.cand = w.ccount = -1;
-  if (kb_sampled(P2)) {
+  if (kb_sampled(P2, K)) {
     const int64_t cs = kb_cplan(N, P1, P2).slices;
     w.taup = o;
     o += kb_align(N * P1 * KB_TP * KB_TK * 4);
@@ -1180,9 +1193,10 @@ static void kb_launch(const KbArgs& a) {
   }
   const KbPlan cp = kb_cplan(a.N, a.P1, a.P2);
   hipLaunchKernelGGL((knn_bf16_tau_kernel<KS, HALF>), dim3(a.N * p.nqb * KB_TP), blk, 0, a.s,
-                     a.p1, a.p2, a.l1, a.l2, a.N, a.P1, a.P2, p.nqb, a.qn, a.rn, a.taup, a.rcount);
+                     a.p1, a.p2, a.l1, a.l2, a.N, a.P1, a.P2, a.K, p.nqb, a.qn, a.rn, a.taup,
+                     a.rcount);
   hipLaunchKernelGGL((knn_bf16_cand_kernel<KS, HALF>), dim3(a.N * cp.nqb * cp.slices), blk, 0, a.s,
-                     a.p1, a.p2, a.l1, a.l2, a.P1, a.P2, cp.nqb, cp.slices, a.qn, a.rn,
+                     a.p1, a.p2, a.l1, a.l2, a.P1, a.P2, a.K, cp.nqb, cp.slices, a.qn, a.rn,
                      (const float*)a.taup, a.cand, a.ccount);
   {
     const dim3 g((unsigned)((r1 + KB_WAVES - 1) / KB_WAVES));
