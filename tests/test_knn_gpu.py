@@ -664,6 +664,21 @@ def test_bf16_rows_the_sampled_bound_leaves_short_are_rerun(tpo, dev):
     assert counts.tolist() == [32, 50]
 
 
+@pytest.mark.parametrize("D", [8, 16, 40, 72, 120])
+def test_bf16_candidate_pass_dims(tpo, dev, D):
+    # the sampled bound and the candidate pass (4096 references, K = 2 so the
+    # bound applies) for every operand layout: D % 16 == 8 puts the norm step
+    # in the upper half of the last dimension step, else in a step of its own
+    g = torch.Generator().manual_seed(300 + D)
+    B, P1, P2, K = 2, 96, 4096, 2
+    q = torch.randn(B, P1, D, generator=g).to(torch.bfloat16)
+    r = torch.randn(B, P2, D, generator=g).to(torch.bfloat16)
+    l1 = torch.tensor([P1, 70])
+    l2 = torch.tensor([P2, P2])
+    idx, d = raw(q, r, l1, l2, 2, K, -1, dev)
+    check_bf16_knn(idx, d, q, r, l1, l2, K)
+
+
 def test_bf16_candidate_regions_wide_overflowed_and_tied(tpo, dev):
     # Clouds of >= 4096 references run the candidate pass: each (query,
     # slice) region holds up to 128 candidates, one register a slice in the
