@@ -16,22 +16,31 @@
 // supplies 8 consecutive k of row/column l%32, k = 8(l/32)..8(l/32)+7, and
 // receives column l%32, rows 8(v/4) + 4(l/32) + v%4 for v = 0..15.
 //
-// knn_bf16_slice_kernel: a workgroup of 4 waves owns 256 queries and one
-// slice of the references; each wave multiplies two 32-query blocks (the
-// MFMA columns) by every 32-reference tile of the slice, so each row
-// fragment it loads feeds two MFMAs (operand traffic per FLOP halves against
-// one block a wave).  A tile's fragments are loaded one tile ahead, with no
-// synchronisation between waves.  v_permlane32_swap_b32 then exchanges the
-// two accumulators' half-waves (checked on the device: swap(x, y) leaves
-// x = [x_lo, y_lo], y = [x_hi, y_hi]), after which lane l holds all 32 rows of
-// one query: block l/32, column l%32.  Each lane keeps its own sorted list of
-// the KC best (KC >= K) as 64-bit (distance, index) keys: candidates are
-// queued per lane in LDS and, when some queue could overflow, merged in
+// Two passes share that arithmetic.  In both, a workgroup of 4 waves owns
+// 256 queries and one slice of the references, and each wave multiplies two
+// 32-query blocks (the MFMA columns) by every 32-reference tile of the slice,
+// staged once per workgroup in LDS, so each row fragment feeds two MFMAs.
+//
+// Candidate pass (clouds of at least max(4096, 1536 K) references):
+// knn_bf16_tau_kernel first bounds each query by the 8th smallest of its
+// minimum distances over 64 sampled tiles; knn_bf16_cand_kernel stores every
+// distance at or below the bound as a 64-bit (distance, index) key in a
+// region per (query, slice), and knn_bf16_cmerge_kernel selects each row's K
+// from its candidates (a distance histogram, then ranks among the few that
+// can be in the K).  Rows whose regions overflowed or that hold fewer than K
+// candidates are listed for the exact pass.
+//
+// Exact pass (smaller clouds, and the listed rows): knn_bf16_slice_kernel.
+// v_permlane32_swap_b32 exchanges the two accumulators' half-waves (checked
+// on the device: swap(x, y) leaves x = [x_lo, y_lo], y = [x_hi, y_hi]), after
+// which lane l holds all 32 rows of one query: block l/32, column l%32.  Each
+// lane keeps its own sorted list of the KC best (KC >= K) keys: candidates
+// are queued per lane in LDS and, when some queue could overflow, merged in
 // groups of 8 by a sorting network and a bitonic merge in registers, so one
-// branch-free pass serves every lane of the wave; the key order puts the
-// lower index first among equal distances.
-// Each lane writes the first K entries of its list for its slice, and
-// knn_bf16_merge_kernel merges a query's slices.
+// branch-free pass serves every lane of the wave.  Each lane writes the first
+// K entries of its list for its slice, and knn_bf16_merge_kernel merges a
+// query's slices.  The key order puts the lower index first among equal
+// distances in both passes.
 #include <type_traits>
 
 #include "knn_common.hpp"
