@@ -10,23 +10,30 @@
 //    (cells in Morton order, so neighbouring cells are mostly close in
 //    memory), the sorted points as (x, y, z, original index) and the start of
 //    every cell.
-// 2. chamfer_grid_search_kernel: one lane per query, queries taken in the
-//    sorted (Morton) order of their own cloud so a wave's lanes search nearby
-//    cells.  A lane walks Chebyshev rings of cells around its query's cell
-//    until it has a candidate (ring 1 nearest cells first, its edge and
-//    corner groups skipped whole when a lower bound of their gaps exceeds
-//    the best distance), then visits the box of cells that can hold a
-//    point within the best distance found (cell assignment is monotone in
-//    each coordinate, and the box is widened by 2^-19 relative plus the
-//    rounding of its bounds), evaluating every point of a visited cell with
-//    the reference formula (chamfer.cu:64-67, same bits) and keeping the
-//    smallest (distance, original index) -- the reference's first-index rule.
-//    A cell is skipped when a lower bound of its squared distance, rounded
-//    down by 2^-20 relative, exceeds the best distance: the reference's float
+// 2. chamfer_grid_search_kernel: one query per lane, queries taken in the
+//    sorted (Morton) order of their own cloud so a wave's queries lie close
+//    together.  Per query: its own cell; if that is empty, ring 1 (the 26
+//    cells around it); then the box of cells that can hold a point within
+//    the best distance found (cell assignment is monotone in each
+//    coordinate, and the box is widened by 2^-19 relative plus the rounding
+//    of its bounds), without the cells scanned before.  A cell is skipped
+//    when a lower bound of its squared distance, rounded down by 2^-20
+//    relative, exceeds the query's best distance: the reference's float
 //    distance of any of its points is then strictly larger (its relative
 //    error is <= 5u), so neither a smaller distance nor a tie with a lower
 //    index is missed.  Cell boxes are widened by 2^-20 (|lo| + extent) per
-//    side, which covers the rounding of the cell assignment.
+//    side, which covers the rounding of the cell assignment.  Every point of
+//    a scanned cell is evaluated with the reference formula
+//    (chamfer.cu:64-67, same bits), keeping the smallest (distance, original
+//    index) -- the reference's first-index rule.
+//    The wave shares this work out instead of each lane walking its own
+//    cells: every lane contributes segments of items (its box's cells; a
+//    scanned cell's points), and the wave takes the items in order, 64 R
+//    a round (R consecutive items to a lane), each lane finding the segment
+//    of its items from the marked segment starts and a running maximum over
+//    the lanes (DPP).  Lanes stay busy however unevenly the queries' work is
+//    spread.  Each query's best key sits in LDS and takes the items' results
+//    by 64-bit LDS atomicMin (one per run of a lane's items of one query).
 // 3. Queries with a coordinate that is non-finite or >= 2^60 in magnitude,
 //    and every query of a reference cloud holding such a coordinate, are
 //    scanned over the whole reference cloud in original order by chunk_scan
@@ -66,7 +73,7 @@ struct CgLayout {
                    // bad, degenerate, level (search cells are 2^level of them per axis),
                    // cut sides (bit a: axis a cut below, 3 + a: above; the boundary
                    // cells on a cut side are unbounded)
-  int64_t pts;     // float4 per padded point: sorted (x, y, z, original index bits)
+  int64_t pts;     // float4 per padded point: sorted (original index bits, x, y, z)
   int64_t cstart;  // CG_CSTRIDE int32 per cloud: first sorted position of a cell, then n
   int64_t rank;    // int32 per point: rank within its cell (sort scratch)
   int64_t stats;   // int32 per search wave: points evaluated
@@ -124,12 +131,12 @@ template <typename T>
 __device__ __forceinline__ float cg_dist(const float4& p, const float4& q);
 template <>
 __device__ __forceinline__ float cg_dist<float>(const float4& p, const float4& q) {
-  return sq3((float)(p.x - q.x), (float)(p.y - q.y), (float)(p.z - q.z));
+  return sq3((float)(p.y - q.y), (float)(p.z - q.z), (float)(p.w - q.w));
 }
 template <>
 __device__ __forceinline__ float cg_dist<half_t>(const float4& p, const float4& q) {
-  return (float)sq3((half_t)((half_t)p.x - (half_t)q.x), (half_t)((half_t)p.y - (half_t)q.y),
-                    (half_t)((half_t)p.z - (half_t)q.z));
+  return (float)sq3((half_t)((half_t)p.y - (half_t)q.y), (half_t)((half_t)p.z - (half_t)q.z),
+                    (half_t)((half_t)p.w - (half_t)q.w));
 }
 
 // Pruning margins: a cell whose float lower bound g2 of the exact squared
@@ -443,11 +450,11 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const int k = tid + 1024 * i;
-      if (k < n) stage[at[i]] = make_float4(px[i], py[i], pz[i], __int_as_float(k));
+      if (k < n) stage[at[i]] = make_float4(__int_as_float(k), px[i], py[i], pz[i]);
     }
     __syncthreads();
     for (int pos = tid; pos < cg_pad(n); pos += 1024)
-      pts[pos] = pos < n ? stage[pos] : make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
+      pts[pos] = pos < n ? stage[pos] : make_float4(__int_as_float(-1), 0.f, 0.f, 0.f);
   } else {
     for (int i = 0; i < iters; ++i) {
       const int k = tid + 1024 * i;
@@ -455,10 +462,10 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
       float x, y, z;
       point(i, k, x, y, z);
       pts[cnt[cg_hidx(code_of(x, y, z))] + (uint32_t)rank[k]] =
-          make_float4(x, y, z, __int_as_float(k));
+          make_float4(__int_as_float(k), x, y, z);
     }
     for (int pos = n + tid; pos < cg_pad(n); pos += 1024)
-      pts[pos] = make_float4(0.f, 0.f, 0.f, __int_as_float(-1));
+      pts[pos] = make_float4(__int_as_float(-1), 0.f, 0.f, 0.f);
   }
   if (tid == 0) {
 #pragma unroll
@@ -490,12 +497,100 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   }
 }
 
-// A lane walks cells one by one; a box of more cells than about nr / 64
-// costs more to walk than the whole cloud costs the wave to scan together,
-// so such lanes (and lanes with no point in their cell's 3x3x3
-// neighbourhood) are answered by a wave-wide scan instead.
-constexpr int CG_BOX_MIN = 128;  // cells a lane may always walk
+// A query whose box holds more cells than about nr / 64 would cost the wave
+// more than a scan of the whole cloud together, so such queries (and those
+// with no point in their cell's 3x3x3 neighbourhood) are answered by a
+// wave-wide scan instead.
+constexpr int CG_BOX_MIN = 128;  // cells a box may always hold
+// a search wave's LDS rows
+constexpr int CG_R = 4;   // points a lane evaluates per round of the search
+constexpr int CG_RC = 2;  // cells a lane tests per round of a walk
+struct CgWaveLds {
+  unsigned long long key[64];
+  float4 q[64];
+  int4 box[64];
+  int2 seg[64 * CG_RC];  // per segment: first sorted position - first item, query lane
+  int mark[64 * CG_R];
+};
 __host__ __device__ inline int cg_box_max(int nr) { return max(CG_BOX_MIN, nr >> 6); }
+
+// Wave-level pieces of the search (every lane of the wave active).
+__device__ __forceinline__ void cg_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ int cg_dpp(int v) {  // lanes without a source read 0
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWMASK, 0xf, true);
+}
+// inclusive prefix sum / maximum (of values >= 0) over the lanes: row_shr 1, 2,
+// 4, 8 within rows of 16, then row_bcast:15 into rows 1, 3 and row_bcast:31
+// into rows 2, 3
+__device__ __forceinline__ int cg_scan_add(int v) {
+  v += cg_dpp<0x111, 0xf>(v);
+  v += cg_dpp<0x112, 0xf>(v);
+  v += cg_dpp<0x114, 0xf>(v);
+  v += cg_dpp<0x118, 0xf>(v);
+  v += cg_dpp<0x142, 0xa>(v);
+  v += cg_dpp<0x143, 0xc>(v);
+  return v;
+}
+__device__ __forceinline__ int cg_scan_max(int v) {
+  v = max(v, cg_dpp<0x111, 0xf>(v));
+  v = max(v, cg_dpp<0x112, 0xf>(v));
+  v = max(v, cg_dpp<0x114, 0xf>(v));
+  v = max(v, cg_dpp<0x118, 0xf>(v));
+  v = max(v, cg_dpp<0x142, 0xa>(v));
+  v = max(v, cg_dpp<0x143, 0xc>(v));
+  return v;
+}
+// Every lane holds RC segments of len[v] >= 0 items (segment RC lane + v);
+// the wave hands the items out in order, 64 R a round, R consecutive ones to
+// a lane: body(ok, s, i) runs on every lane each round, with item i[u]
+// (ok[u]: it exists) of segment s[u], u < R (s is non-decreasing in u and
+// over the lanes).  The segment of each item comes from the segment starts
+// marked in the wave's LDS row mark (64 R ints) and a running maximum over
+// the items.
+template <int R, int RC, typename F>
+__device__ __forceinline__ void cg_flat(const int (&len)[RC], int* __restrict__ mark, F&& body) {
+  const int lane = lane_id();
+  int tot = 0;
+#pragma unroll
+  for (int v = 0; v < RC; ++v) tot += len[v];
+  const int incl = cg_scan_add(tot);
+  const int total = __builtin_amdgcn_readlane(incl, 63);
+  int ex[RC];  // first item of each segment
+#pragma unroll
+  for (int v = 0; v < RC; ++v) ex[v] = v ? ex[v - 1] + len[v - 1] : incl - tot;
+  int carry = 0;  // 1 + the segment holding the previous round's last item
+  for (int base = 0; base < total; base += 64 * R) {
+#pragma unroll
+    for (int u = 0; u < R; ++u) mark[R * lane + u] = 0;
+    cg_wave_sync();
+#pragma unroll
+    for (int v = 0; v < RC; ++v)
+      if (len[v] > 0 && ex[v] >= base && ex[v] < base + 64 * R) mark[ex[v] - base] = RC * lane + v + 1;
+    cg_wave_sync();
+    int lm[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) lm[u] = u ? max(lm[u - 1], mark[R * lane + u]) : mark[R * lane];
+    const int inc = cg_scan_max(lm[R - 1]);
+    // the maximum over the lanes before this one (DPP wave_shr:1, lane 0 reads 0)
+    const int c0 = max(carry, __builtin_amdgcn_update_dpp(0, inc, 0x138, 0xf, 0xf, true));
+    carry = max(carry, __builtin_amdgcn_readlane(inc, 63));
+    int sg[R], it[R];
+    bool ok[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      sg[u] = max(max(c0, lm[u]) - 1, 0);
+      it[u] = base + R * lane + u;
+      ok[u] = it[u] < total;
+    }
+    body(ok, sg, it);
+    cg_wave_sync();
+  }
+}
 
 template <typename T, int WG>
 __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
@@ -504,16 +599,17 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
     T* __restrict__ dist2, int32_t* __restrict__ idx1, int32_t* __restrict__ idx2) {
   using Mg = CgMargin<T>;
   static_assert(WG == 64 * CH_WAVES, "a search workgroup is one 256-query dense block");
-  // LDS: the dense block's arrays (degenerate grids only)
-  __shared__ __align__(16) char s_mem[sizeof(float4) * CH_WAVES * 64 +
-                                      (sizeof(T) + sizeof(int)) * CH_WAVES * WG];
+  // LDS: the dense block's arrays (degenerate grids only) or the waves' rows
+  constexpr size_t kDense = sizeof(float4) * CH_WAVES * 64 + (sizeof(T) + sizeof(int)) * CH_WAVES * WG;
+  __shared__ __align__(16) char s_mem[kDense > sizeof(CgWaveLds) * CH_WAVES ? kDense
+                                                                           : sizeof(CgWaveLds) * CH_WAVES];
   const int bid = xcd_logical_block(blockIdx.x, gridDim.x);
   int lb = bid;
   const int g1 = B * nqb1;
   const int dir = lb >= g1;
   if (dir) lb -= g1;
   const int nqb = dir ? nqb2 : nqb1;
-  const int b = lb / nqb;
+  const int b = __builtin_amdgcn_readfirstlane(lb / nqb);  // uniform: scalar loads below
   const int qb = lb - b * nqb;
   const int nq = dir ? M : N;
   const int nr = dir ? N : M;
@@ -557,186 +653,236 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   const int pos = qb * WG + (int)threadIdx.x;
   const bool valid = pos < nq;
   const float4 q = qs[min(pos, nq - 1)];
-  const int oq = __float_as_int(q.w);
+  const int oq = __float_as_int(q.x);
   const bool rbad = __float_as_uint(h[12]) != 0u;
-  const bool qbad = max(abs_bits(q.x), max(abs_bits(q.y), abs_bits(q.z))) >= CH_BIG;
+  const bool qbad = max(abs_bits(q.y), max(abs_bits(q.z), abs_bits(q.w))) >= CH_BIG;
   const bool fallback = valid && (rbad || qbad);
-  bool far = false;  // answered by the wave-wide scan below
+  const bool act = valid && !fallback;  // answered by the grid search
   int examined = 0;
   const unsigned long long kInit = ((unsigned long long)0x7f800000u << 32) | 0x7fffffffu;
 
-  if (valid && !fallback) {
-    // grid geometry at the search resolution: G cells per axis, cell
-    // (cx, cy, cz) holding the sorted points [cstart[code << 3 lv],
-    // cstart[(code + 1) << 3 lv]) -- a Morton-ordered 32^3 cell c lies in
-    // the coarser cell c >> 3 lv, and the coarser cell index equals
-    // floor((p - lo) * gs / 2^lv) exactly (scaling by a power of two
-    // commutes with rounding), so the two views agree
-    const int lv = (int)__float_as_uint(h[14]);
-    const uint32_t cut = __float_as_uint(h[15]);
-    const int G = CG_GRID >> lv, sh = 3 * lv;
-    float glo[3], ghi[3], gs[3], cs[3], eps[3];
-    const float qv[3] = {q.x, q.y, q.z};
-    int ci[3], ga[3];
+  // grid geometry at the search resolution: G cells per axis, cell
+  // (cx, cy, cz) holding the sorted points [cstart[code << 3 lv],
+  // cstart[(code + 1) << 3 lv]) -- a Morton-ordered 32^3 cell c lies in
+  // the coarser cell c >> 3 lv, and the coarser cell index equals
+  // floor((p - lo) * gs / 2^lv) exactly (scaling by a power of two
+  // commutes with rounding), so the two views agree
+  // (wave-uniform values, pinned to SGPRs)
+  auto U = [](float x) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x))); };
+  const int lv = __builtin_amdgcn_readfirstlane((int)__float_as_uint(h[14]));
+  const uint32_t cut = (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(h[15]));
+  const int G = CG_GRID >> lv, sh = 3 * lv;
+  float glo[3], ghi[3], gs[3], cs[3], eps[3];
+  const float qv[3] = {q.y, q.z, q.w};
+  int ci[3], ga[3];
 #pragma unroll
-    for (int a = 0; a < 3; ++a) {
-      glo[a] = h[a];
-      ghi[a] = h[3 + a];
-      gs[a] = __builtin_ldexpf(h[6 + a], -lv);
-      cs[a] = __builtin_ldexpf(h[9 + a], lv);
-      ga[a] = gs[a] > 0.f ? G : 1;
-      ci[a] = gs[a] > 0.f ? cg_axis_cell(qv[a], glo[a], gs[a], G) : 0;
-      eps[a] = 0x1p-20f * (__builtin_fabsf(glo[a]) + (ghi[a] - glo[a])) + 0x1p-126f;
+  for (int a = 0; a < 3; ++a) {
+    glo[a] = U(h[a]);
+    ghi[a] = U(h[3 + a]);
+    gs[a] = U(__builtin_ldexpf(h[6 + a], -lv));
+    cs[a] = U(__builtin_ldexpf(h[9 + a], lv));
+    ga[a] = gs[a] > 0.f ? G : 1;
+    ci[a] = gs[a] > 0.f ? cg_axis_cell(qv[a], glo[a], gs[a], G) : 0;
+    eps[a] = U(0x1p-20f * (__builtin_fabsf(glo[a]) + (ghi[a] - glo[a])) + 0x1p-126f);
+  }
+  // distance from coordinate x to cell c's slab along axis a (a lower bound,
+  // widened by the margins); the first / last cell is unbounded on a cut side
+  auto axis_gap = [&](int a, int c, float x) {
+    const float clo = (cut >> a) & 1u && c == 0
+                          ? -__builtin_inff()
+                          : (ga[a] > 1 ? glo[a] + (float)c * cs[a] : glo[a]) - eps[a];
+    const float chi = (cut >> (3 + a)) & 1u && c == ga[a] - 1
+                          ? __builtin_inff()
+                          : (ga[a] > 1 ? glo[a] + (float)(c + 1) * cs[a] : ghi[a]) + eps[a];
+    return fmaxf(fmaxf(clo - x, x - chi), 0.f);
+  };
+
+  // the wave's LDS rows: best (distance, index) key per query (distances here
+  // are finite and >= 0, so their bits order like the values and the index
+  // breaks ties), the queries, the cell boxes being walked, segment marks
+  auto& sg = *reinterpret_cast<CgWaveLds(*)[CH_WAVES]>(s_mem);
+  unsigned long long* __restrict__ wkey = sg[w].key;
+  float4* __restrict__ wq = sg[w].q;
+  int4* __restrict__ wbox = sg[w].box;
+  int* __restrict__ wmark = sg[w].mark;
+  int2* __restrict__ wseg = sg[w].seg;
+  wkey[lane] = kInit;
+  wq[lane] = q;
+  cg_wave_sync();
+  auto best = [&](int l) { return __uint_as_float((uint32_t)(wkey[l] >> 32)); };
+
+  // every lane holds cnt sorted points from j0 on, for the query of lane own:
+  // the wave evaluates them all, 64 a round, with the reference formula
+  // (chamfer.cu:64-67, same bits), keeping each query's smallest key
+  auto scan_segs = [&](auto rc, const int (&cnt)[decltype(rc)::value],
+                       const int (&j0)[decltype(rc)::value], const int (&own)[decltype(rc)::value]) {
+    constexpr int RC = decltype(rc)::value;
+    cg_wave_sync();
+    {
+      int tot = 0;
+#pragma unroll
+      for (int v = 0; v < RC; ++v) tot += cnt[v];
+      int e = cg_scan_add(tot) - tot;
+#pragma unroll
+      for (int v = 0; v < RC; ++v) {
+        wseg[RC * lane + v] = make_int2(j0[v] - e, own[v]);
+        e += cnt[v];
+      }
     }
-    // distance from the query to cell c's slab along axis a (a lower bound,
-    // widened by the margins); the first / last cell is unbounded on a cut side
-    auto axis_gap = [&](int a, int c) {
-      const float clo = (cut >> a) & 1u && c == 0
-                            ? -__builtin_inff()
-                            : (ga[a] > 1 ? glo[a] + (float)c * cs[a] : glo[a]) - eps[a];
-      const float chi = (cut >> (3 + a)) & 1u && c == ga[a] - 1
-                            ? __builtin_inff()
-                            : (ga[a] > 1 ? glo[a] + (float)(c + 1) * cs[a] : ghi[a]) + eps[a];
-      return fmaxf(fmaxf(clo - qv[a], qv[a] - chi), 0.f);
-    };
-    // best (distance, index) as one key: distances here are finite and >= 0,
-    // so their bits order like the values, and the index breaks ties
-    unsigned long long bkey = kInit;
-    auto bdist = [&]() { return __uint_as_float((uint32_t)(bkey >> 32)); };
-    const char* __restrict__ rsb = reinterpret_cast<const char*>(rs);
-    // evaluate every point of sorted positions [j0, j1)
-    auto scan = [&](int j0, int j1) {
-      for (int j = j0; j < j1; j += CG_UNROLL) {
-        // CG_UNROLL loads in flight; positions past the cell repeat its last
-        // point, whose second evaluation cannot change the result
-        float4 p[CG_UNROLL];
+    cg_flat<CG_R, RC>(cnt, wmark, [&](const bool (&ok)[CG_R], const int (&sn)[CG_R], const int (&it)[CG_R]) {
+      float4 p[CG_R];
+      int o[CG_R];
 #pragma unroll
-        for (int u = 0; u < CG_UNROLL; ++u)
-          p[u] = *reinterpret_cast<const float4*>(rsb + (uint32_t)min(j + u, j1 - 1) * 16u);
+      for (int u = 0; u < CG_R; ++u) {
+        const int2 e = wseg[sn[u]];
+        p[u] = rs[ok[u] ? e.x + it[u] : 0];
+        o[u] = e.y;
+      }
+      // the lane's points belong to non-decreasing query lanes: one atomic
+      // per run of one query
+      unsigned long long acc = ~0ull;
+      int cur = -1;
+      float4 qq = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int u = 0; u < CG_UNROLL; ++u) {
-          const float d = cg_dist<T>(p[u], q);
+      for (int u = 0; u < CG_R; ++u) {
+        if (ok[u]) {
+          if (o[u] != cur) {
+            if (cur >= 0) atomicMin(&wkey[cur], acc);
+            cur = o[u];
+            acc = ~0ull;
+            qq = wq[cur];
+          }
+          const float d = cg_dist<T>(p[u], qq);
           const unsigned long long key =
-              ((unsigned long long)__float_as_uint(d) << 32) | __float_as_uint(p[u].w);
-          bkey = key < bkey ? key : bkey;
+              ((unsigned long long)__float_as_uint(d) << 32) | __float_as_uint(p[u].x);
+          acc = key < acc ? key : acc;
+          ++examined;
         }
       }
-      examined += j1 - j0;
-    };
-    auto scan_cell = [&](uint32_t code) { scan(cstart[code << sh], cstart[(code + 1) << sh]); };
-    // evaluate every point of cell cc unless its box is farther than the best
-    auto visit = [&](int cx, int cy, int cz) {
-      const int cc[3] = {cx, cy, cz};
-      float gap[3];
+      if (cur >= 0) atomicMin(&wkey[cur], acc);
+    });
+  };
+  // every lane holds a box of V cells (its wbox row: lower corner, extents,
+  // own cell, skip radius rd): the wave walks all of them, 64 cells a round;
+  // a cell within Chebyshev distance rd of its query's cell was scanned
+  // before, and a cell whose lower bound of the squared distance, rounded
+  // down by 2^-20 relative, exceeds the query's best distance is skipped: the
+  // reference's float distance of any of its points is then strictly larger
+  // (its relative error is <= 5u), so neither a smaller distance nor a tie
+  // with a lower index is missed.  The cells that remain are scanned.
+  auto walk = [&](int V) {
+    cg_wave_sync();
+    const int vex = cg_scan_add(V) - V;  // first item of each box
+    const int Vv[1] = {V};
+    cg_flat<CG_RC, 1>(Vv, wmark, [&](const bool (&okv)[CG_RC], const int (&sv)[CG_RC], const int (&iv)[CG_RC]) {
+      int cnt[CG_RC], j0[CG_RC];
 #pragma unroll
-      for (int a = 0; a < 3; ++a) gap[a] = axis_gap(a, cc[a]);
-      if (sq3(gap[0], gap[1], gap[2]) * Mg::lb - Mg::abs > bdist()) return;
-      scan_cell(cg_code(cx, cy, cz));
-    };
-    // phase 1: the query's cell; if it is empty, ring 1, nearest cells
-    // first: the six face neighbours (the nearer face of each axis first),
-    // then the 12 edge and 8 corner neighbours, each group skipped whole
-    // when a lower bound of its cells' gaps (the same per-axis gaps visit
-    // computes, combined monotonically) already exceeds the best distance.
-    // Nothing within ring 1: the wave-wide scan answers the query.
-    visit(ci[0], ci[1], ci[2]);
-    int rdone = 0;
-    if (bdist() == Lim<float>::inf()) {
-      float gn[3];
-      int sn[3];
-#pragma unroll
-      for (int a = 0; a < 3; ++a) {
-        // gap to the neighbour below (its upper bound) and above (its lower bound)
-        const float gm = ci[a] > 0 ? fmaxf(qv[a] - (glo[a] + (float)ci[a] * cs[a] + eps[a]), 0.f)
-                                   : __builtin_inff();
-        const float gp = ci[a] < ga[a] - 1
-                             ? fmaxf((glo[a] + (float)(ci[a] + 1) * cs[a] - eps[a]) - qv[a], 0.f)
-                             : __builtin_inff();
-        sn[a] = gm <= gp ? -1 : 1;
-        gn[a] = fminf(gm, gp);
-      }
-      auto inb = [&](int a, int d) { return ci[a] + d >= 0 && ci[a] + d < ga[a]; };
-      auto cell = [&](int dx, int dy, int dz) {
-        if (inb(0, dx) && inb(1, dy) && inb(2, dz)) visit(ci[0] + dx, ci[1] + dy, ci[2] + dz);
-      };
-      cell(sn[0], 0, 0);
-      cell(0, sn[1], 0);
-      cell(0, 0, sn[2]);
-      cell(-sn[0], 0, 0);
-      cell(0, -sn[1], 0);
-      cell(0, 0, -sn[2]);
-      const float ge = fminf(fminf(sq3(gn[0], gn[1], 0.f), sq3(gn[0], 0.f, gn[2])),
-                             sq3(0.f, gn[1], gn[2]));
-      if (!(ge * Mg::lb - Mg::abs > bdist())) {
-        for (int e = 0; e < 12; ++e) {  // (a, b) axis pair with signs
-          const int pr = e >> 2, sa = (e & 1) ? 1 : -1, sb = (e & 2) ? 1 : -1;
-          const int dx = pr == 2 ? 0 : sa, dy = pr == 0 ? sb : (pr == 1 ? 0 : sa);
-          const int dz = pr == 0 ? 0 : sb;
-          cell(dx, dy, dz);
-        }
-        if (!(sq3(gn[0], gn[1], gn[2]) * Mg::lb - Mg::abs > bdist()))
-          for (int c = 0; c < 8; ++c)
-            cell((c & 1) ? 1 : -1, (c & 2) ? 1 : -1, (c & 4) ? 1 : -1);
-      }
-      rdone = 1;
-      far = bdist() == Lim<float>::inf();
-    }
-    // phase 2: the box of cells within the best distance (cell assignment is
-    // monotone in each coordinate, so the box holds every point within it);
-    // cells of the rings already walked are skipped.  The gap to a cell is
-    // accumulated per axis as the loops descend, so a slab or row whose
-    // partial lower bound already exceeds the best distance is skipped whole
-    // (the bound only grows with more axes; any summation order rounds by a
-    // few u, well inside the 2^-20 margin).  A box of more than
-    // cg_box_max(nr) cells goes to the wave-wide scan.
-    int blo[3], bhi[3];
-    const float bd = bdist();
-    const float rad = __builtin_sqrtf((bd + Mg::abs) * Mg::inv) * (1.f + 0x1p-19f);
-    int cells = 1;
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-      const float ra = rad + eps[a] + 0x1p-20f * __builtin_fabsf(qv[a]);
-      blo[a] = ga[a] > 1 ? cg_axis_cell(qv[a] - ra, glo[a], gs[a], G) : 0;
-      bhi[a] = ga[a] > 1 ? cg_axis_cell(qv[a] + ra, glo[a], gs[a], G) : 0;
-      cells *= bhi[a] - blo[a] + 1;
-    }
-    far = far || cells > cg_box_max(nr);
-    if (!far) {
-      auto gap2 = [&](int a, int c) {
-        const float g = axis_gap(a, c);
-        return g * g;
-      };
-      for (int cz = blo[2]; cz <= bhi[2]; ++cz) {
-        const float gz = gap2(2, cz);
-        if (gz * Mg::lb - Mg::abs > bdist()) continue;
-        const uint32_t kz = cg_spread((uint32_t)cz) << 2;
-        const int dz = abs(cz - ci[2]);
-        for (int cy = blo[1]; cy <= bhi[1]; ++cy) {
-          const float gzy = gz + gap2(1, cy);
-          if (gzy * Mg::lb - Mg::abs > bdist()) continue;
-          const uint32_t kzy = kz | (cg_spread((uint32_t)cy) << 1);
-          const int dzy = max(dz, abs(cy - ci[1]));
-          for (int cx = blo[0]; cx <= bhi[0]; ++cx) {
-            if (max(dzy, abs(cx - ci[0])) <= rdone) continue;
-            if ((gzy + gap2(0, cx)) * Mg::lb - Mg::abs > bdist()) continue;
-            scan_cell(kzy | cg_spread((uint32_t)cx));
+      for (int v = 0; v < CG_RC; ++v) {
+        const int s = sv[v];
+        const int k = iv[v] - __shfl(vex, s);
+        cnt[v] = 0;
+        j0[v] = 0;
+        if (okv[v]) {
+          const int4 bx = wbox[s];
+          const int nx = (bx.x >> 17) & 63, ny = (bx.x >> 23) & 63;
+          // k = (dz * ny + dy) * nx + dx; the float quotients are exact (the
+          // reciprocals' error is far below the 1/(2n) margin of k + 1/2)
+          const int t = (int)(((float)k + 0.5f) * __int_as_float(bx.z));
+          const int dz = (int)(((float)t + 0.5f) * __int_as_float(bx.w));
+          const int cx = (bx.x & 31) + (k - t * nx);
+          const int cy = ((bx.x >> 5) & 31) + (t - dz * ny);
+          const int cz = ((bx.x >> 10) & 31) + dz;
+          const int rd = ((bx.x >> 15) & 3) - 1;
+          const int cheb = max(abs(cx - (bx.y & 31)),
+                               max(abs(cy - ((bx.y >> 5) & 31)), abs(cz - ((bx.y >> 10) & 31))));
+          const float4 qq = wq[s];
+          const float g2 = sq3(axis_gap(0, cx, qq.y), axis_gap(1, cy, qq.z), axis_gap(2, cz, qq.w));
+          if (cheb > rd && !(g2 * Mg::lb - Mg::abs > best(s))) {
+            const uint32_t code = cg_code(cx, cy, cz);
+            j0[v] = cstart[code << sh];
+            cnt[v] = cstart[(code + 1) << sh] - j0[v];
           }
         }
       }
-      dout[oq] = (T)bdist();
-      iout[oq] = (int)(uint32_t)bkey;
+      scan_segs(std::integral_constant<int, CG_RC>{}, cnt, j0, sv);
+    });
+  };
+  auto set_box = [&](const int (&lo)[3], const int (&hi)[3], int rd) {
+    const int nx = hi[0] - lo[0] + 1, ny = hi[1] - lo[1] + 1;
+    wbox[lane] = make_int4(lo[0] | lo[1] << 5 | lo[2] << 10 | (rd + 1) << 15 | nx << 17 | ny << 23,
+                           ci[0] | ci[1] << 5 | ci[2] << 10, __float_as_int(1.f / (float)nx),
+                           __float_as_int(1.f / (float)ny));
+    return nx * ny * (hi[2] - lo[2] + 1);
+  };
+
+  // phase 1: the query's own cell
+  {
+    const uint32_t code = cg_code(ci[0], ci[1], ci[2]);
+    int j0 = 0, cnt = 0;
+    if (act) {
+      j0 = cstart[code << sh];
+      cnt = cstart[(code + 1) << sh] - j0;
     }
+    const int c1[1] = {cnt}, j1[1] = {j0}, o1[1] = {lane};
+    scan_segs(std::integral_constant<int, 1>{}, c1, j1, o1);
+  }
+  cg_wave_sync();
+  // phase 2: queries whose own cell is empty walk ring 1 (the 26 cells
+  // around it); nothing there: the wave-wide scan below answers the query
+  const bool ring = act && best(lane) == Lim<float>::inf();
+  if (__ballot(ring)) {
+    int V = 0;
+    if (ring) {
+      int lo[3], hi[3];
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        lo[a] = max(ci[a] - 1, 0);
+        hi[a] = min(ci[a] + 1, ga[a] - 1);
+      }
+      V = set_box(lo, hi, 0);
+    }
+    walk(V);
+    cg_wave_sync();
+  }
+  // phase 3: the box of cells within the best distance (cell assignment is
+  // monotone in each coordinate, so the box holds every point within it),
+  // without the cells walked before; a box of more than cg_box_max(nr)
+  // cells goes to the wave-wide scan
+  const float bd = best(lane);
+  bool far = act && bd == Lim<float>::inf();
+  {
+    int V = 0;
+    if (act && !far) {
+      const float rad = __builtin_sqrtf((bd + Mg::abs) * Mg::inv) * (1.f + 0x1p-19f);
+      int lo[3], hi[3], cells = 1;
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        const float ra = rad + eps[a] + 0x1p-20f * __builtin_fabsf(qv[a]);
+        lo[a] = ga[a] > 1 ? cg_axis_cell(qv[a] - ra, glo[a], gs[a], G) : 0;
+        hi[a] = ga[a] > 1 ? cg_axis_cell(qv[a] + ra, glo[a], gs[a], G) : 0;
+        cells *= hi[a] - lo[a] + 1;
+      }
+      far = cells > cg_box_max(nr);
+      if (!far) V = set_box(lo, hi, ring ? 1 : 0);
+    }
+    walk(V);
+    cg_wave_sync();
+  }
+  if (act && !far) {
+    const unsigned long long kb = wkey[lane];
+    dout[oq] = (T)__uint_as_float((uint32_t)(kb >> 32));
+    iout[oq] = (int)(uint32_t)kb;
   }
   // far queries: the wave scans every reference point (sorted order, same
   // key), one query at a time
   for (uint64_t fm = __ballot(far); fm; fm &= fm - 1) {
     const int l = __builtin_ctzll(fm);
-    const float4 ql = make_float4(__shfl(q.x, l), __shfl(q.y, l), __shfl(q.z, l), 0.f);
+    const float4 ql = make_float4(0.f, __shfl(q.y, l), __shfl(q.z, l), __shfl(q.w, l));
     unsigned long long k = kInit;
     for (int j = lane; j < nr; j += 64) {
       const float4 p = rs[j];
       const unsigned long long key =
-          ((unsigned long long)__float_as_uint(cg_dist<T>(p, ql)) << 32) | __float_as_uint(p.w);
+          ((unsigned long long)__float_as_uint(cg_dist<T>(p, ql)) << 32) | __float_as_uint(p.x);
       k = key < k ? key : k;
     }
 #pragma unroll
