@@ -139,6 +139,19 @@ __device__ __forceinline__ float cg_dist<half_t>(const float4& p, const float4& 
                     (half_t)((half_t)p.w - (half_t)q.w));
 }
 
+// The same distance with the query as three coordinates.
+template <typename T>
+__device__ __forceinline__ float cg_dist3(const float4& p, float qx, float qy, float qz);
+template <>
+__device__ __forceinline__ float cg_dist3<float>(const float4& p, float qx, float qy, float qz) {
+  return sq3((float)(p.y - qx), (float)(p.z - qy), (float)(p.w - qz));
+}
+template <>
+__device__ __forceinline__ float cg_dist3<half_t>(const float4& p, float qx, float qy, float qz) {
+  return (float)sq3((half_t)((half_t)p.y - (half_t)qx), (half_t)((half_t)p.z - (half_t)qy),
+                    (half_t)((half_t)p.w - (half_t)qz));
+}
+
 // Pruning margins: a cell whose float lower bound g2 of the exact squared
 // distance satisfies g2 * lb - abs > best holds no point whose computed
 // distance is <= best, and every point with computed distance <= best lies
@@ -565,16 +578,28 @@ __device__ __forceinline__ void cg_flat(const int (&len)[RC], int* __restrict__ 
   for (int v = 0; v < RC; ++v) ex[v] = v ? ex[v - 1] + len[v - 1] : incl - tot;
   int carry = 0;  // 1 + the segment holding the previous round's last item
   for (int base = 0; base < total; base += 64 * R) {
+    if constexpr (R == 4) {
+      reinterpret_cast<int4*>(mark)[lane] = make_int4(0, 0, 0, 0);
+    } else {
 #pragma unroll
-    for (int u = 0; u < R; ++u) mark[R * lane + u] = 0;
+      for (int u = 0; u < R; ++u) mark[R * lane + u] = 0;
+    }
     cg_wave_sync();
 #pragma unroll
     for (int v = 0; v < RC; ++v)
       if (len[v] > 0 && ex[v] >= base && ex[v] < base + 64 * R) mark[ex[v] - base] = RC * lane + v + 1;
     cg_wave_sync();
     int lm[R];
+    if constexpr (R == 4) {
+      const int4 m4 = reinterpret_cast<const int4*>(mark)[lane];
+      lm[0] = m4.x;
+      lm[1] = max(m4.x, m4.y);
+      lm[2] = max(lm[1], m4.z);
+      lm[3] = max(lm[2], m4.w);
+    } else {
 #pragma unroll
-    for (int u = 0; u < R; ++u) lm[u] = u ? max(lm[u - 1], mark[R * lane + u]) : mark[R * lane];
+      for (int u = 0; u < R; ++u) lm[u] = u ? max(lm[u - 1], mark[R * lane + u]) : mark[R * lane];
+    }
     const int inc = cg_scan_max(lm[R - 1]);
     // the maximum over the lanes before this one (DPP wave_shr:1, lane 0 reads 0)
     const int c0 = max(carry, __builtin_amdgcn_update_dpp(0, inc, 0x138, 0xf, 0xf, true));
@@ -707,7 +732,7 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   int* __restrict__ wmark = sg[w].mark;
   int2* __restrict__ wseg = sg[w].seg;
   wkey[lane] = kInit;
-  wq[lane] = q;
+  wq[lane] = make_float4(q.y, q.z, q.w, q.x);  // coordinates first
   cg_wave_sync();
   auto best = [&](int l) { return __uint_as_float((uint32_t)(wkey[l] >> 32)); };
 
@@ -732,34 +757,33 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
     cg_flat<CG_R, RC>(cnt, wmark, [&](const bool (&ok)[CG_R], const int (&sn)[CG_R], const int (&it)[CG_R]) {
       float4 p[CG_R];
       int o[CG_R];
+      const char* __restrict__ rsb = reinterpret_cast<const char*>(rs);
 #pragma unroll
       for (int u = 0; u < CG_R; ++u) {
+        // items past the last one load a valid point and count for nothing
         const int2 e = wseg[sn[u]];
-        p[u] = rs[ok[u] ? e.x + it[u] : 0];
+        p[u] = *reinterpret_cast<const float4*>(rsb + (uint32_t)min(e.x + it[u], nr - 1) * 16u);
         o[u] = e.y;
       }
-      // the lane's points belong to non-decreasing query lanes: one atomic
-      // per run of one query
-      unsigned long long acc = ~0ull;
-      int cur = -1;
-      float4 qq = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int u = 1; u < CG_R; ++u) o[u] = ok[u] ? o[u] : o[u - 1];
+      // the lane's items belong to non-decreasing query lanes: the minimum
+      // over each run of one query (branch-free), then one atomic per run
+      unsigned long long r[CG_R];
 #pragma unroll
       for (int u = 0; u < CG_R; ++u) {
-        if (ok[u]) {
-          if (o[u] != cur) {
-            if (cur >= 0) atomicMin(&wkey[cur], acc);
-            cur = o[u];
-            acc = ~0ull;
-            qq = wq[cur];
-          }
-          const float d = cg_dist<T>(p[u], qq);
-          const unsigned long long key =
-              ((unsigned long long)__float_as_uint(d) << 32) | __float_as_uint(p[u].x);
-          acc = key < acc ? key : acc;
-          ++examined;
-        }
+        const float4 qq = wq[o[u]];
+        const float d = cg_dist3<T>(p[u], qq.x, qq.y, qq.z);
+        const unsigned long long key =
+            ((unsigned long long)__float_as_uint(d) << 32 | __float_as_uint(p[u].x)) |
+            (ok[u] ? 0ull : ~0ull);
+        r[u] = u > 0 && o[u] == o[u - 1] && r[u - 1] < key ? r[u - 1] : key;
+        examined += ok[u] ? 1 : 0;
       }
-      if (cur >= 0) atomicMin(&wkey[cur], acc);
+#pragma unroll
+      for (int u = 0; u + 1 < CG_R; ++u)
+        if (o[u + 1] != o[u]) atomicMin(&wkey[o[u]], r[u]);
+      if (ok[0]) atomicMin(&wkey[o[CG_R - 1]], r[CG_R - 1]);
     });
   };
   // every lane holds a box of V cells (its wbox row: lower corner, extents,
@@ -796,7 +820,7 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
           const int cheb = max(abs(cx - (bx.y & 31)),
                                max(abs(cy - ((bx.y >> 5) & 31)), abs(cz - ((bx.y >> 10) & 31))));
           const float4 qq = wq[s];
-          const float g2 = sq3(axis_gap(0, cx, qq.y), axis_gap(1, cy, qq.z), axis_gap(2, cz, qq.w));
+          const float g2 = sq3(axis_gap(0, cx, qq.x), axis_gap(1, cy, qq.y), axis_gap(2, cz, qq.z));
           if (cheb > rd && !(g2 * Mg::lb - Mg::abs > best(s))) {
             const uint32_t code = cg_code(cx, cy, cz);
             j0[v] = cstart[code << sh];
