@@ -678,7 +678,6 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   const int pos = qb * WG + (int)threadIdx.x;
   const bool valid = pos < nq;
   const float4 q = qs[min(pos, nq - 1)];
-  const int oq = __float_as_int(q.x);
   const bool rbad = __float_as_uint(h[12]) != 0u;
   const bool qbad = max(abs_bits(q.y), max(abs_bits(q.z), abs_bits(q.w))) >= CH_BIG;
   const bool fallback = valid && (rbad || qbad);
@@ -732,7 +731,10 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   int* __restrict__ wmark = sg[w].mark;
   int2* __restrict__ wseg = sg[w].seg;
   wkey[lane] = kInit;
-  wq[lane] = make_float4(q.y, q.z, q.w, q.x);  // coordinates first
+  wq[lane] = make_float4(q.y, q.z, q.w, q.x);  // coordinates first, then the index
+  // the query's cell, packed (5 bits an axis); later phases read the query
+  // back from wq, which keeps the registers low
+  const int cpk = ci[0] | ci[1] << 5 | ci[2] << 10;
   cg_wave_sync();
   auto best = [&](int l) { return __uint_as_float((uint32_t)(wkey[l] >> 32)); };
 
@@ -834,7 +836,7 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   auto set_box = [&](const int (&lo)[3], const int (&hi)[3], int rd) {
     const int nx = hi[0] - lo[0] + 1, ny = hi[1] - lo[1] + 1;
     wbox[lane] = make_int4(lo[0] | lo[1] << 5 | lo[2] << 10 | (rd + 1) << 15 | nx << 17 | ny << 23,
-                           ci[0] | ci[1] << 5 | ci[2] << 10, __float_as_int(1.f / (float)nx),
+                           cpk, __float_as_int(1.f / (float)nx),
                            __float_as_int(1.f / (float)ny));
     return nx * ny * (hi[2] - lo[2] + 1);
   };
@@ -860,8 +862,9 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
       int lo[3], hi[3];
 #pragma unroll
       for (int a = 0; a < 3; ++a) {
-        lo[a] = max(ci[a] - 1, 0);
-        hi[a] = min(ci[a] + 1, ga[a] - 1);
+        const int c = (cpk >> (5 * a)) & 31;
+        lo[a] = max(c - 1, 0);
+        hi[a] = min(c + 1, ga[a] - 1);
       }
       V = set_box(lo, hi, 0);
     }
@@ -877,13 +880,15 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   {
     int V = 0;
     if (act && !far) {
+      const float4 qm = wq[lane];
+      const float qa[3] = {qm.x, qm.y, qm.z};
       const float rad = __builtin_sqrtf((bd + Mg::abs) * Mg::inv) * (1.f + 0x1p-19f);
       int lo[3], hi[3], cells = 1;
 #pragma unroll
       for (int a = 0; a < 3; ++a) {
-        const float ra = rad + eps[a] + 0x1p-20f * __builtin_fabsf(qv[a]);
-        lo[a] = ga[a] > 1 ? cg_axis_cell(qv[a] - ra, glo[a], gs[a], G) : 0;
-        hi[a] = ga[a] > 1 ? cg_axis_cell(qv[a] + ra, glo[a], gs[a], G) : 0;
+        const float ra = rad + eps[a] + 0x1p-20f * __builtin_fabsf(qa[a]);
+        lo[a] = ga[a] > 1 ? cg_axis_cell(qa[a] - ra, glo[a], gs[a], G) : 0;
+        hi[a] = ga[a] > 1 ? cg_axis_cell(qa[a] + ra, glo[a], gs[a], G) : 0;
         cells *= hi[a] - lo[a] + 1;
       }
       far = cells > cg_box_max(nr);
@@ -894,14 +899,16 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   }
   if (act && !far) {
     const unsigned long long kb = wkey[lane];
-    dout[oq] = (T)__uint_as_float((uint32_t)(kb >> 32));
-    iout[oq] = (int)(uint32_t)kb;
+    const int o = __float_as_int(wq[lane].w);
+    dout[o] = (T)__uint_as_float((uint32_t)(kb >> 32));
+    iout[o] = (int)(uint32_t)kb;
   }
   // far queries: the wave scans every reference point (sorted order, same
   // key), one query at a time
   for (uint64_t fm = __ballot(far); fm; fm &= fm - 1) {
     const int l = __builtin_ctzll(fm);
-    const float4 ql = make_float4(0.f, __shfl(q.y, l), __shfl(q.z, l), __shfl(q.w, l));
+    const float4 qf = wq[l];
+    const float4 ql = make_float4(0.f, qf.x, qf.y, qf.z);
     unsigned long long k = kInit;
     for (int j = lane; j < nr; j += 64) {
       const float4 p = rs[j];
@@ -915,8 +922,9 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
       k = x < k ? x : k;
     }
     if (lane == l) {
-      dout[oq] = (T)__uint_as_float((uint32_t)(k >> 32));
-      iout[oq] = (int)(uint32_t)k;
+      const int o = __float_as_int(qf.w);
+      dout[o] = (T)__uint_as_float((uint32_t)(k >> 32));
+      iout[o] = (int)(uint32_t)k;
     }
     examined += lane == 0 ? nr : 0;
   }
@@ -931,7 +939,7 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   while (fb) {
     const int l = __builtin_ctzll(fb);
     fb &= fb - 1;
-    const int o = __shfl(oq, l);
+    const int o = __float_as_int(wq[l].w);
     T md;
     int mi;
     chunk_scan(qp[3 * o], qp[3 * o + 1], qp[3 * o + 2], rp, 0, nr, lane, md, mi);
