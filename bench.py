@@ -637,9 +637,10 @@ def main():
                 "brute_force_equivalent_tflops": round(brute, 3),
                 "module_fwd_ms": round(ch["loss_fwd_sec"] * 1e3, 4),
                 "valu_counters": counters,
-                "note": "frac = VALUBusy x VALUUtilization of the launch: the search walks "
-                        "cells lane by lane, so most lanes idle in its VALU instructions; "
-                        "useful_tflops counts only the distance work it needs, "
+                "note": "frac = VALUBusy x VALUUtilization of the launch: each search wave "
+                        "shares its queries' cell tests and point evaluations across its "
+                        "lanes, so most of its VALU work is per-item bookkeeping around the "
+                        "distance; useful_tflops counts only the distance work it needs, "
                         "brute_force_equivalent_tflops 9 FLOP x all 2BNM directed pairs over "
                         "the same time"}
     out = {
