@@ -682,7 +682,7 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   const bool qbad = max(abs_bits(q.y), max(abs_bits(q.z), abs_bits(q.w))) >= CH_BIG;
   const bool fallback = valid && (rbad || qbad);
   const bool act = valid && !fallback;  // answered by the grid search
-  int examined = 0;
+  int examined = 0;  // points the wave evaluated (wave-uniform)
   const unsigned long long kInit = ((unsigned long long)0x7f800000u << 32) | 0x7fffffffu;
 
   // grid geometry at the search resolution: G cells per axis, cell
@@ -749,7 +749,9 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
       int tot = 0;
 #pragma unroll
       for (int v = 0; v < RC; ++v) tot += cnt[v];
-      int e = cg_scan_add(tot) - tot;
+      const int incl = cg_scan_add(tot);
+      examined += __builtin_amdgcn_readlane(incl, 63);  // the wave's points this call
+      int e = incl - tot;
 #pragma unroll
       for (int v = 0; v < RC; ++v) {
         wseg[RC * lane + v] = make_int2(j0[v] - e, own[v]);
@@ -762,7 +764,8 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
       const char* __restrict__ rsb = reinterpret_cast<const char*>(rs);
 #pragma unroll
       for (int u = 0; u < CG_R; ++u) {
-        // items past the last one load a valid point and count for nothing
+        // an item past the last one loads a point of the same reference
+        // cloud for some query of the wave: a valid candidate, harmless
         const int2 e = wseg[sn[u]];
         p[u] = *reinterpret_cast<const float4*>(rsb + (uint32_t)min(e.x + it[u], nr - 1) * 16u);
         o[u] = e.y;
@@ -777,15 +780,13 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
         const float4 qq = wq[o[u]];
         const float d = cg_dist3<T>(p[u], qq.x, qq.y, qq.z);
         const unsigned long long key =
-            ((unsigned long long)__float_as_uint(d) << 32 | __float_as_uint(p[u].x)) |
-            (ok[u] ? 0ull : ~0ull);
+            (unsigned long long)__float_as_uint(d) << 32 | __float_as_uint(p[u].x);
         r[u] = u > 0 && o[u] == o[u - 1] && r[u - 1] < key ? r[u - 1] : key;
-        examined += ok[u] ? 1 : 0;
       }
 #pragma unroll
       for (int u = 0; u + 1 < CG_R; ++u)
         if (o[u + 1] != o[u]) atomicMin(&wkey[o[u]], r[u]);
-      if (ok[0]) atomicMin(&wkey[o[CG_R - 1]], r[CG_R - 1]);
+      atomicMin(&wkey[o[CG_R - 1]], r[CG_R - 1]);
     });
   };
   // every lane holds a box of V cells (its wbox row: lower corner, extents,
@@ -926,14 +927,10 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
       dout[o] = (T)__uint_as_float((uint32_t)(k >> 32));
       iout[o] = (int)(uint32_t)k;
     }
-    examined += lane == 0 ? nr : 0;
+    examined += nr;
   }
-  {  // points evaluated by this wave
-    int e = examined;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o);
-    if (lane == 0) stats[(size_t)bid * (WG / 64) + w] = e;
-  }
+  // points evaluated by this wave (a wave-uniform count)
+  if (lane == 0) stats[(size_t)bid * (WG / 64) + w] = examined;
   // queries that need the reference's full rule: the wave scans one at a time
   uint64_t fb = __ballot(fallback);
   while (fb) {
