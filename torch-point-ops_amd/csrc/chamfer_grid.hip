@@ -111,9 +111,9 @@ __device__ __forceinline__ uint32_t cg_spread(uint32_t v) {  // 5 bits -> every 
   return v;
 }
 
+// (fmaxf returns its non-NaN operand, so a NaN position lands in cell 0)
 __device__ __forceinline__ int cg_axis_cell(float p, float lo, float sc, int g = CG_GRID) {
-  const float f = (p - lo) * sc;
-  return is_nan(f) ? 0 : (int)fminf(fmaxf(f, 0.f), (float)(g - 1));
+  return (int)fminf(fmaxf((p - lo) * sc, 0.f), (float)(g - 1));
 }
 
 __device__ __forceinline__ uint32_t cg_code(int cx, int cy, int cz) {
