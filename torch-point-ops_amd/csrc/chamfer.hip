@@ -185,10 +185,19 @@ __global__ __launch_bounds__(CH_BWD_THREADS) void chamfer_bwd_fused_kernel(
     const int32_t* __restrict__ idx2, PointGrad<T> gd1, PointGrad<T> gd2, int N, int M, int S,
     T* __restrict__ g1, T* __restrict__ g2) {
   extern __shared__ float sm[];
-  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
-  const int sl = lb % S;
-  const int c = (lb / S) & 1;  // 0: gradient of cloud 1, 1: of cloud 2
-  const int b = lb / (2 * S);
+  int b, c, sl;  // batch, cloud (0: gradient of cloud 1, 1: of cloud 2), slice
+  {
+    int j;
+    if (batch_home_block(blockIdx.x, gridDim.x / (2 * S), 2 * S, b, j)) {
+      c = j / S;
+      sl = j - c * S;
+    } else {
+      const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+      sl = lb % S;
+      c = (lb / S) & 1;
+      b = lb / (2 * S);
+    }
+  }
   const int n_own = c ? M : N, n_oth = c ? N : M;
   const int span = (n_own + S - 1) / S;
   const int lo = min(n_own, sl * span), hi = min(n_own, lo + span);

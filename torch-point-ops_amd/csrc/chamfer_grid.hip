@@ -184,17 +184,19 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   __shared__ uint32_t part[16];
   __shared__ uint32_t s_bad, s_maxc;
   __shared__ float s_sq[3][16];  // per wave: sum of count^2 over the cells of 32^3, 16^3, 8^3
-  const int c = blockIdx.x & 1, b = blockIdx.x >> 1;
+  int b = blockIdx.x >> 1, c = blockIdx.x & 1;  // batch, cloud
+  batch_home_block(blockIdx.x, gridDim.x >> 1, 2, b, c);
+  const int cl = 2 * b + c;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int n = c ? M : N;
   if (zero && blockIdx.x == 0 && tid == 0) *zero = 0u;
   const int64_t PN = cg_pad(N), PM = cg_pad(M);
   const int64_t base = (int64_t)b * (PN + PM) + (c ? PN : 0);
   const TI* __restrict__ P = (c ? xyz2 : xyz1) + (size_t)b * n * 3;
-  float* __restrict__ hdr = reinterpret_cast<float*>(ws + L.hdr) + (size_t)blockIdx.x * 16;
+  float* __restrict__ hdr = reinterpret_cast<float*>(ws + L.hdr) + (size_t)cl * 16;
   float4* __restrict__ pts = reinterpret_cast<float4*>(ws + L.pts) + base;
   int32_t* __restrict__ cstart =
-      reinterpret_cast<int32_t*>(ws + L.cstart) + (size_t)blockIdx.x * CG_CSTRIDE;
+      reinterpret_cast<int32_t*>(ws + L.cstart) + (size_t)cl * CG_CSTRIDE;
   int32_t* __restrict__ rank = reinterpret_cast<int32_t*>(ws + L.rank) + base;
 
   constexpr int R = PPT > 0 ? PPT : 1;
@@ -629,13 +631,22 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
   __shared__ __align__(16) char s_mem[kDense > sizeof(CgWaveLds) * CH_WAVES ? kDense
                                                                            : sizeof(CgWaveLds) * CH_WAVES];
   const int bid = xcd_logical_block(blockIdx.x, gridDim.x);
-  int lb = bid;
-  const int g1 = B * nqb1;
-  const int dir = lb >= g1;
-  if (dir) lb -= g1;
-  const int nqb = dir ? nqb2 : nqb1;
-  const int b = __builtin_amdgcn_readfirstlane(lb / nqb);  // uniform: scalar loads below
-  const int qb = lb - b * nqb;
+  int b, qb, dir;
+  {
+    int j;
+    if (batch_home_block(blockIdx.x, B, nqb1 + nqb2, b, j)) {
+      dir = j >= nqb1;
+      qb = dir ? j - nqb1 : j;
+    } else {
+      int lb = bid;
+      const int g1 = B * nqb1;
+      dir = lb >= g1;
+      if (dir) lb -= g1;
+      const int nqb = dir ? nqb2 : nqb1;
+      b = __builtin_amdgcn_readfirstlane(lb / nqb);  // uniform: scalar loads below
+      qb = lb - b * nqb;
+    }
+  }
   const int nq = dir ? M : N;
   const int nr = dir ? N : M;
   const int cq = dir, cr = 1 - dir;  // query / reference cloud

@@ -74,6 +74,20 @@ __device__ __forceinline__ int xcd_logical_block(int p, int grid) {
   return (p & 7) * (grid >> 3) + (p >> 3);
 }
 
+// Batch-affine block order: with B a multiple of 8 and `per` blocks per
+// batch (grid = B * per), block p runs batch (p % 8) + 8 ((p / 8) / per),
+// block (p / 8) % per of it.  Workgroups go to the XCDs round-robin by p, so
+// every kernel that uses this order runs batch b on XCD b % 8: what one
+// kernel writes for a batch is in that XCD's L2 when the next reads it.
+// Returns false (and leaves b, j alone) when B is not a multiple of 8.
+__device__ __forceinline__ bool batch_home_block(int p, int B, int per, int& b, int& j) {
+  if ((B & 7) != 0) return false;
+  const int s = p >> 3;
+  b = __builtin_amdgcn_readfirstlane((p & 7) + 8 * (s / per));
+  j = __builtin_amdgcn_readfirstlane(s % per);
+  return true;
+}
+
 // readfirstlane makes the wave index provably wave-uniform, so values derived
 // from it live in SGPRs and loads addressed by it become scalar loads.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
