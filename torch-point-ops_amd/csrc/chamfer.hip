@@ -468,11 +468,20 @@ __device__ void chamfer_loss_finish(const double* part, int p1, int p2, int mean
 template <typename T, bool LAST>
 __global__ __launch_bounds__(256) void chamfer_loss_part_kernel(
     const T* __restrict__ d1, const T* __restrict__ d2, int64_t n1, int64_t n2, int p1, int p2,
-    double* __restrict__ part, uint32_t* __restrict__ done, int mean, T* __restrict__ loss) {
+    double* __restrict__ part, uint32_t* __restrict__ done, int mean, T* __restrict__ loss,
+    int home_b, int home_c1, int home_c2) {
   using A = typename std::conditional<sizeof(T) == 8, double, float>::type;
   __shared__ A s_red[4];
   __shared__ int s_last;
-  const int k = blockIdx.x;
+  // chunk k of the arrays; with home_b > 0 (chunks aligned to the home_b
+  // batches, home_c1 / home_c2 of them per batch and array) batch b's chunks
+  // run on XCD b % 8, where the grid search wrote its distances
+  int k = blockIdx.x;
+  {
+    int b, j;
+    if (home_b > 0 && batch_home_block(blockIdx.x, home_b, home_c1 + home_c2, b, j))
+      k = j < home_c1 ? b * home_c1 + j : p1 + b * home_c2 + (j - home_c1);
+  }
   const bool second = k >= p1;
   const T* d = second ? d2 : d1;
   const int64_t n = second ? n2 : n1;
@@ -538,14 +547,19 @@ static void loss_reduce(const LossLayout& L, char* ws, int64_t B, int64_t N, int
   double* part = (double*)(ws + L.part);
   uint32_t* done = (uint32_t*)(ws + L.done);
   const int p1 = (int)loss_parts(B * N), p2 = (int)loss_parts(B * M);
+  // chunks aligned to batches (the grid search's batch-per-XCD order)
+  const bool home = B > 0 && B <= (1 << 20) && N % CH_LOSS_CHUNK == 0 && M % CH_LOSS_CHUNK == 0 &&
+                    p1 == B * N / CH_LOSS_CHUNK && p2 == B * M / CH_LOSS_CHUNK;
+  const int hb = home ? (int)B : 0;
+  const int hc1 = home ? (int)(N / CH_LOSS_CHUNK) : 0, hc2 = home ? (int)(M / CH_LOSS_CHUNK) : 0;
   if (counter_zeroed && p1 + p2 > 0) {
     hipLaunchKernelGGL((chamfer_loss_part_kernel<T, true>), dim3(p1 + p2), dim3(256), 0, s, d1,
-                       d2, B * N, B * M, p1, p2, part, done, mean, (T*)loss);
+                       d2, B * N, B * M, p1, p2, part, done, mean, (T*)loss, hb, hc1, hc2);
     return;
   }
   if (p1 + p2 > 0)
     hipLaunchKernelGGL((chamfer_loss_part_kernel<T, false>), dim3(p1 + p2), dim3(256), 0, s, d1,
-                       d2, B * N, B * M, p1, p2, part, done, mean, (T*)loss);
+                       d2, B * N, B * M, p1, p2, part, done, mean, (T*)loss, hb, hc1, hc2);
   hipLaunchKernelGGL(chamfer_loss_final_kernel<T>, dim3(1), dim3(64), 0, s, part, p1, p2, mean,
                      B * N, B * M, (T*)loss);
 }
