@@ -184,8 +184,13 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   __shared__ uint32_t part[16];
   __shared__ uint32_t s_bad, s_maxc;
   __shared__ float s_sq[3][16];  // per wave: sum of count^2 over the cells of 32^3, 16^3, 8^3
-  int b = blockIdx.x >> 1, c = blockIdx.x & 1;  // batch, cloud
-  batch_home_block(blockIdx.x, gridDim.x >> 1, 2, b, c);
+  // PPT > 0: two workgroups per cloud; both build the same grid (box,
+  // histogram, scan) and each writes half of it: the cell starts and the
+  // sorted points of cells [hf, hf + 1) * CG_CELLS / 2
+  constexpr int HALVES = PPT > 0 ? 2 : 1;
+  int b = blockIdx.x / (2 * HALVES), j = blockIdx.x % (2 * HALVES);
+  batch_home_block(blockIdx.x, gridDim.x / (2 * HALVES), 2 * HALVES, b, j);
+  const int c = j / HALVES, hf = j % HALVES;  // cloud, half
   const int cl = 2 * b + c;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int n = c ? M : N;
@@ -446,7 +451,8 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     if (tid == 1023) cstart[CG_CELLS] = (int32_t)run;
   }
   __syncthreads();
-  for (int k = tid; k < CG_CELLS / 4; k += 1024) {  // coalesced, 4 cells per store
+  for (int k = tid + hf * (CG_CELLS / 4 / HALVES); k < (hf + 1) * (CG_CELLS / 4 / HALVES);
+       k += 1024) {  // coalesced, 4 cells per store
     const int c0 = cg_hidx(4 * k);  // the 4 cells share one padded run of 32
     reinterpret_cast<int4*>(cstart)[k] =
         make_int4((int)cnt[c0], (int)cnt[c0 + 1], (int)cnt[c0 + 2], (int)cnt[c0 + 3]);
@@ -454,22 +460,28 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   if constexpr (PPT > 0) {
     // sorted positions into registers; once every read of the counts is done
     // the points are placed in LDS and written out in order, coalesced
+    // this half's sorted positions [p0, p1)
+    const uint32_t p0 = cnt[cg_hidx(hf * (CG_CELLS / 2))];
+    const uint32_t p1 = hf ? (uint32_t)n : cnt[cg_hidx(CG_CELLS / 2)];
     uint32_t at[R];
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const int k = tid + 1024 * i;
-      at[i] = k < n ? cnt[hx[i]] + rk[i] : 0u;
+      at[i] = k < n ? cnt[hx[i]] + rk[i] : 0xffffffffu;
     }
     __syncthreads();
     float4* __restrict__ stage = reinterpret_cast<float4*>(cnt);
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const int k = tid + 1024 * i;
-      if (k < n) stage[at[i]] = make_float4(__int_as_float(k), px[i], py[i], pz[i]);
+      if (at[i] >= p0 && at[i] < p1)
+        stage[at[i] - p0] = make_float4(__int_as_float(k), px[i], py[i], pz[i]);
     }
     __syncthreads();
-    for (int pos = tid; pos < cg_pad(n); pos += 1024)
-      pts[pos] = pos < n ? stage[pos] : make_float4(__int_as_float(-1), 0.f, 0.f, 0.f);
+    for (uint32_t pos = p0 + tid; pos < p1; pos += 1024) pts[pos] = stage[pos - p0];
+    if (hf == HALVES - 1)
+      for (int pos = n + tid; pos < cg_pad(n); pos += 1024)
+        pts[pos] = make_float4(__int_as_float(-1), 0.f, 0.f, 0.f);
   } else {
     for (int i = 0; i < iters; ++i) {
       const int k = tid + 1024 * i;
@@ -482,7 +494,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     for (int pos = n + tid; pos < cg_pad(n); pos += 1024)
       pts[pos] = make_float4(__int_as_float(-1), 0.f, 0.f, 0.f);
   }
-  if (tid == 0) {
+  if (tid == 0 && hf == 0) {
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
       hdr[a] = glo[a];
@@ -983,7 +995,7 @@ static void launch_prune(const void* x1, const void* x2, int B, int N, int M, vo
                          int32_t* i1, int32_t* i2, void* ws, hipStream_t s, uint32_t* zero) {
   const CgLayout L = cg_layout(B, N, M);
   if (std::max(N, M) <= 1024 * 8)
-    hipLaunchKernelGGL((chamfer_grid_sort_kernel<T, 8>), dim3(2 * B), dim3(1024), 0, s,
+    hipLaunchKernelGGL((chamfer_grid_sort_kernel<T, 8>), dim3(4 * B), dim3(1024), 0, s,
                        (const T*)x1, (const T*)x2, N, M, (char*)ws, L, zero);
   else
     hipLaunchKernelGGL((chamfer_grid_sort_kernel<T, 0>), dim3(2 * B), dim3(1024), 0, s,
