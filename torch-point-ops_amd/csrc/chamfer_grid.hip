@@ -5,11 +5,12 @@
 // are computed in half as the reference does, and the pruning margins cover
 // half rounding (CgMargin).
 //
-// 1. chamfer_grid_sort_kernel, one workgroup per (batch, cloud): the cloud's
-//    bounding box, a counting sort of its points into a 32^3 grid of cells
-//    (cells in Morton order, so neighbouring cells are mostly close in
-//    memory), the sorted points as (x, y, z, original index) and the start of
-//    every cell.
+// 1. chamfer_grid_sort_kernel, two workgroups per (batch, cloud) for clouds
+//    of up to 8192 points (one above): the cloud's bounding box, a counting
+//    sort of its points into a 32^3 grid of cells (cells in Morton order, so
+//    neighbouring cells are mostly close in memory), the sorted points as
+//    (original index, x, y, z) and the start of every cell.  The two
+//    workgroups build the same grid and each writes half of it.
 // 2. chamfer_grid_search_kernel: one query per lane, queries taken in the
 //    sorted (Morton) order of their own cloud so a wave's queries lie close
 //    together.  Per query: its own cell; if that is empty, ring 1 (the 26
