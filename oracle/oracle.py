@@ -55,6 +55,7 @@ def lib():
             "tpo_ref_emd_bwd": [ctypes.c_int, P, P, P, P, I64, I64, I64, P, P],
             "tpo_ref_f32_to_f16_array": [P, P, I64],
             "tpo_ref_f16_to_f32_array": [P, P, I64],
+            "tpo_ref_f16_round_check": [],
             "tpo_cpu_knn_fwd": [ctypes.c_int, P, P, P, P, I64, I64, I64, I64, I64, ctypes.c_int,
                                 P, P, ctypes.c_int],
             "tpo_cpu_knn_bwd": [ctypes.c_int, P, P, P, P, P, ctypes.c_int, P, I64, I64, I64, I64,
@@ -68,6 +69,7 @@ def lib():
             fn.argtypes = args
             fn.restype = ctypes.c_int
         L.tpo_ref_fps_rank.restype = I64
+        L.tpo_ref_f16_round_check.restype = I64
         _lib = L
     return _lib
 
@@ -106,6 +108,12 @@ def f16_bits_to_f32(h):
     out = np.empty(h.shape, np.float32)
     lib().tpo_ref_f16_to_f32_array(_p(h), _p(out), h.size)
     return out
+
+
+def f16_round_check():
+    """Float bit patterns where the direct binary16 rounding differs from the
+    encode/decode pair (0 expected)."""
+    return int(lib().tpo_ref_f16_round_check())
 
 
 def chamfer_fwd(xyz1, xyz2):

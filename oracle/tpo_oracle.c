@@ -119,7 +119,61 @@ void tpo_ref_f16_to_f32_array(const uint16_t* in, float* out, int64_t n) {
 /* switches fold away after inlining)                                   */
 /* ------------------------------------------------------------------ */
 
-INLINE double rh(float v) { return (double)tpo_ref_f16_to_f32(tpo_ref_f32_to_f16(v)); }
+/* A float rounded to the nearest binary16 value (ties to even), returned as a
+   float, without the round trip through the 16-bit encoding:
+   - |v| >= 2^-14 (normal halves): the 23-bit significand is rounded to 10
+     bits (add 0xfff plus the lowest kept bit, which breaks ties to even,
+     then clear the 13 dropped bits; a carry moves into the exponent as it
+     should); a result of 2^16 or more (from 65520 up) is infinite;
+   - |v| < 2^-14: halves there are the multiples of 2^-24, so the result is
+     |v| 2^24 rounded to an integer (adding and subtracting 2^23 in float
+     rounds a value below 2^23 to the nearest integer, ties to even), times
+     2^-24; both scalings are exact;
+   - NaN becomes the quiet NaN 0x7e00 and infinities stay, signs kept, as
+     tpo_ref_f32_to_f16 encodes them.
+   tpo_ref_f16_round_check compares it with tpo_ref_f16_to_f32 of
+   tpo_ref_f32_to_f16 over every float bit pattern. */
+INLINE float rh_float(float v) {
+  uint32_t x, r;
+  memcpy(&x, &v, 4);
+  const uint32_t sign = x & 0x80000000u, ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) {
+    r = ax == 0x7f800000u ? 0x7f800000u : 0x7fc00000u;
+  } else if (ax >= 0x38800000u) {
+    r = (ax + 0xfffu + ((ax >> 13) & 1u)) & 0xffffe000u;
+    if (r >= 0x47800000u) r = 0x7f800000u;
+  } else {
+    float a;
+    memcpy(&a, &ax, 4);
+    const float y = a * 0x1p24f;
+    const float q = ((y + 0x1p23f) - 0x1p23f) * 0x1p-24f;
+    memcpy(&r, &q, 4);
+  }
+  r |= sign;
+  float out;
+  memcpy(&out, &r, 4);
+  return out;
+}
+
+int64_t tpo_ref_f16_round_check(void) {
+  int64_t bad = 0;
+#ifdef _OPENMP
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+#endif
+  for (int64_t i = 0; i < ((int64_t)1 << 32); ++i) {
+    const uint32_t x = (uint32_t)i;
+    float f;
+    memcpy(&f, &x, 4);
+    const float a = rh_float(f), b = tpo_ref_f16_to_f32(tpo_ref_f32_to_f16(f));
+    uint32_t ua, ub;
+    memcpy(&ua, &a, 4);
+    memcpy(&ub, &b, 4);
+    bad += ua != ub;
+  }
+  return bad;
+}
+
+INLINE double rh(float v) { return (double)rh_float(v); }
 
 INLINE double ld(int dt, const void* p, int64_t i) {
   switch (dt) {

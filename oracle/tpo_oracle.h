@@ -38,6 +38,10 @@ uint16_t tpo_ref_f32_to_bf16(float f);
 float tpo_ref_bf16_to_f32(uint16_t h);
 void tpo_ref_f32_to_f16_array(const float* in, uint16_t* out, int64_t n);
 void tpo_ref_f16_to_f32_array(const uint16_t* in, float* out, int64_t n);
+/* Number of float bit patterns for which the oracle's direct binary16
+   rounding (used by every float16 operation) differs from
+   tpo_ref_f16_to_f32(tpo_ref_f32_to_f16(x)); 0 when they agree everywhere. */
+int64_t tpo_ref_f16_round_check(void);
 
 /* Chamfer: chamfer.cu:36-167 (forward), chamfer.cu:200-234 (backward). */
 int tpo_ref_chamfer_fwd(int dtype, const void* xyz1, const void* xyz2,

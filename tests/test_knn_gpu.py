@@ -114,23 +114,6 @@ def test_high_d_sliced_forward_bit_exact(tpo, O, dev, case, D, K, norm):
     assert torch.equal(si, wi) and torch.equal(sd, wd)
 
 
-def test_high_d_config5_shape_float_rows_vs_oracle(tpo, O, dev):
-    """Config 5's shape widened to float32 (B=4, 4096 x 65536, D=128, K=32):
-    the full forward on the GPU; 64 query rows of every cloud against the
-    oracle (each row depends only on its query and the reference cloud)."""
-    q, r = workloads.knn_c5()
-    a, b = q.float(), r.float()
-    B, P1, _ = a.shape
-    P2 = b.shape[1]
-    la = torch.full((B,), P1)
-    lb = torch.full((B,), P2)
-    idx, d = raw(a, b, la, lb, 2, 32, -1, dev)
-    rows = torch.tensor([0, 1, 777, 2048, 4095] + list(range(1000, 1059)))
-    ei, ed = O.knn_fwd(np_(a[:, rows]), np_(b), np.full(B, len(rows)), np_(lb), norm=2, K=32)
-    assert_same(np_(idx[:, rows]), ei)
-    assert_same(np_(d[:, rows]), ed)
-
-
 def _long_cloud_inputs(case, g):
     # long reference clouds (the staged float D=3 sweep over 5000 references,
     # lengths2 ragged, a cloud with a single query row)
@@ -546,16 +529,6 @@ def test_bf16_matrix_core_knn(tpo, dev, N, P1, P2, D, K):
     idx, d = raw(q, r, l1, l2, 2, K, -1, dev)
     assert idx.dtype == torch.int64 and d.dtype == torch.bfloat16
     check_bf16_knn(idx, d, q, r, l1, l2, K)
-
-
-def test_bf16_config5_subset(tpo, dev):
-    q, r = workloads.knn_c5()
-    B, P1, D = q.shape
-    l1 = torch.full((B,), P1, dtype=torch.int64)
-    l2 = torch.full((B,), r.shape[1], dtype=torch.int64)
-    idx, d = raw(q, r, l1, l2, 2, 32, -1, dev)
-    sel = torch.arange(0, P1, 61)  # 68 query rows per cloud, checked against float64
-    check_bf16_knn(idx[:, sel], d[:, sel], q[:, sel], r, torch.full((B,), len(sel)), l2, 32)
 
 
 def test_bf16_equal_distances_take_lower_indices(tpo, dev):

@@ -40,6 +40,13 @@ def test_f16_conversions_match_numpy(O):
         assert np.array_equal(x.astype(np.float16).view(np.uint16), O.f32_to_f16_bits(x))
 
 
+def test_f16_direct_rounding_every_float(O):
+    """Every float16 operation of the oracle rounds its float result with a
+    direct binary16 rounding; it must equal the encode/decode pair pinned
+    above on all 2^32 float bit patterns (NaN payloads included)."""
+    assert O.f16_round_check() == 0
+
+
 # ------------------------------------------------------------------ chamfer
 
 def test_chamfer_known_values(O):
@@ -241,6 +248,45 @@ def test_knn_brute_force(O):
         got = np.take_along_axis(idx, order, 2)
         assert np.array_equal(got, ref_idx)
         np.testing.assert_allclose(np.sort(d, 2), np.take_along_axis(full, ref_idx, 2), rtol=1e-5)
+
+
+def np_knn_f16(p1, p2, norm):
+    """knn.cu:148-158 with c10::Half operands: diff = q - r, then
+    dist += diff * diff (norm 2) or dist += (diff > 0 ? diff : -diff)
+    (norm 1), over d in order, every operation in numpy float16 (computed in
+    float and rounded to binary16, as c10::Half's operators do)."""
+    diff = p1[:, :, None, :] - p2[:, None, :, :]
+    acc = np.zeros(diff.shape[:3], np.float16)
+    for d in range(p1.shape[2]):
+        t = diff[..., d]
+        acc = acc + (t * t if norm == 2 else np.where(t > 0, t, -t))
+    return acc
+
+
+@pytest.mark.parametrize("D,K,norm,v", [(3, 8, 2, -1), (3, 2, 1, -1), (3, 16, 1, 2),
+                                        (5, 6, 2, -1), (20, 4, 2, 1), (40, 3, 1, 0)])
+def test_knn_f16_arithmetic_vs_numpy_half(O, D, K, norm, v):
+    """The oracle's float16 KNN against an independent numpy float16
+    statement: each returned distance has the bits of numpy's per-operation
+    half distance of its (query, reference) pair, each row holds the K
+    smallest of those distances, no reference twice; quantised inputs make
+    many distances tie exactly."""
+    r = rng(40 + D + K)
+    p1 = r.standard_normal((2, 40, D)).astype(np.float16)
+    p2 = r.standard_normal((2, 90, D)).astype(np.float16)
+    p1[1] = (r.integers(-8, 9, (40, D)) / 4).astype(np.float16)
+    p2[1] = (r.integers(-8, 9, (90, D)) / 4).astype(np.float16)
+    l2 = np.array([90, K + 5])
+    idx, d = O.knn_fwd(p1, p2, len2=l2, K=K, norm=norm, version=v)
+    full = np_knn_f16(p1, p2, norm)
+    for n in range(2):
+        L2 = int(l2[n])
+        for q in range(40):
+            row_i, row_d = idx[n, q, :min(K, L2)], d[n, q, :min(K, L2)]
+            assert len(set(row_i.tolist())) == len(row_i) and (row_i < L2).all()
+            assert np.array_equal(row_d.view(np.uint16), full[n, q, row_i].view(np.uint16))
+            want = np.sort(full[n, q, :L2].astype(np.float32))[:len(row_d)]
+            assert np.array_equal(np.sort(row_d.astype(np.float32)), want)
 
 
 def test_knn_f32_bits_exact_arithmetic(O):
@@ -493,6 +539,67 @@ def test_fps_brute_force(O):
     pts = r.standard_normal((1, 60, 3))
     assert O.fps(pts, 20)[0].tolist() == fps_f64(pts[0], 20)
     assert O.fps(pts.astype(np.float16), 10)[0, 0] == 0
+
+
+def np_fps_gpu_f16(pts, m):
+    """fps.cu:111-214 for one float16 cloud, in numpy float16 (each operation
+    rounded to binary16): mag = (x*x + y*y) + z*z; points with !(mag >
+    half(1e-3)) are skipped; temp starts at 1e4 and takes min(d, temp)
+    (d < temp in float); thread t of BS = min(512, 2^floor(log2 n)) keeps
+    its first strictly greatest temp starting from best = -1 (index 0 when it
+    has no candidate); the shared-memory tree then halves BS down to 1 with
+    __update: value max(v1, v2), index i2 only when v2 > v1."""
+    n = pts.shape[0]
+    bs = min(512, 1 << (n.bit_length() - 1))
+    per = -(-n // bs)
+    x, y, z = pts[:, 0], pts[:, 1], pts[:, 2]
+    mag = (x * x + y * y) + z * z
+    cand = mag.astype(np.float32) > np.float32(np.float16(np.float32(1e-3)))
+    temp = np.full(n, np.float16(1e4))
+    out = [0]
+    for _ in range(1, m):
+        c = pts[out[-1]]
+        dx, dy, dz = x - c[0], y - c[1], z - c[2]
+        d = (dx * dx + dy * dy) + dz * dz
+        temp = np.where(cand & (d.astype(np.float32) < temp.astype(np.float32)), d, temp)
+        vals = np.full(per * bs, -1.0, np.float32)
+        vals[:n] = np.where(cand, temp.astype(np.float32), -1.0)
+        vals = vals.reshape(per, bs)           # column t: thread t's points in order
+        pos = np.argmax(vals, axis=0)          # first maximum of each thread
+        dv = vals[pos, np.arange(bs)]
+        di = np.where(dv > -1.0, pos * bs + np.arange(bs), 0)
+        s = bs // 2
+        while s >= 1:
+            v1, v2, i1, i2 = dv[:s], dv[s:2 * s], di[:s], di[s:2 * s]
+            dv, di = np.where(v1 > v2, v1, v2), np.where(v2 > v1, i2, i1)
+            s //= 2
+        out.append(int(di[0]))
+    return out
+
+
+def test_fps_f16_vs_numpy_half_tree(O):
+    """The oracle's float16 FPS against the numpy float16 statement above:
+    random, lattice (many exact ties, resolved by the tree) and clouds with
+    points under the skip threshold, where half(1e-3) = 0.0010004 decides."""
+    r = rng(41)
+    clouds = [r.standard_normal((300, 3)),
+              r.integers(-3, 4, (256, 3)) / 2,
+              r.integers(-2, 3, (7, 3)).astype(np.float64)]
+    skip = r.standard_normal((200, 3))
+    skip[::7] = 0.0182574  # |p|^2 = 3 * 0.0182574^2 rounds near the threshold
+    skip[3::11] = 1e-3
+    clouds.append(skip)
+    # half magnitude exactly half(1e-3) = 0.0010004: above float 1e-3, not
+    # above the half threshold, so these points never take part; with every
+    # point sampled the difference shows
+    edge = r.standard_normal((24, 3))
+    edge[5] = (0.0316162109375, 0.0007119178771972656, 0.0)
+    edge[17] = (0.0, -0.0316162109375, 0.0007128715515136719)
+    clouds.append(edge)
+    for c in clouds:
+        pts = c.astype(np.float16)
+        m = min(60, pts.shape[0])
+        assert O.fps(pts[None], m)[0].tolist() == np_fps_gpu_f16(pts, m)
 
 
 def np_fps_cpu(pts, m):
