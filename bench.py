@@ -10,11 +10,12 @@ value = directed pair-distances per second (2*B*N*M per step) in G/s.
 roofline: the dominant kernels, the grid forward (sort + exact grid search),
 timed alone with HIP events on the stream they run on.  Bound: the FP32 VALU
 (157.3 TFLOP/s).  achieved = 9 FLOP x the (query, reference) pairs the exact
-search evaluated (counted by the kernel) / that time; the brute-force
-equivalent (9 FLOP x all 2BNM pairs) is reported in its own field, and the
-search kernel's VALU counters come from the committed rocprofv3 summary
-(profiles/).  traffic: FETCH_SIZE + WRITE_SIZE of the forward from the
-committed --pmc summary.
+search evaluated (counted by the kernel) / that time, frac = achieved / 157.3;
+the brute-force equivalent (9 FLOP x all 2BNM pairs) and the VALU issue rate
+(lane operations from the committed rocprofv3 counters, profiles/) are
+reported in their own fields.  traffic: FETCH_SIZE + WRITE_SIZE of the
+forward from the committed --pmc summary, traffic_ratio = traffic over the
+algorithmic bytes (inputs, distances, indices).
 
 Secondary lines (median of 5 repeats of >= 20 calls after >= 5 warm-ups,
 HIP events): Chamfer c2 float16 fwd+bwd, the dense Chamfer kernel, Chamfer
@@ -48,6 +49,9 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense MFMA
 FLOP_PER_PAIR = 9  # 3 sub + 3 mul + 2 add + 1 compare per directed pair
 VALU_LANE_PEAK_T = 1024 * 16 * 2.4e9 / 1e12  # fp32 VALU lane ops/s (no packed FP32), 39.32e12
+# config 2 forward, algorithmic HBM bytes: inputs (2 x 32 x 8192 x 3 fp32),
+# distances (2 x 32 x 8192 fp32) and indices (2 x 32 x 8192 int32)
+CHAMFER_FWD_BYTES = 2 * 32 * 8192 * (3 * 4 + 4 + 4)
 
 
 def cpu_model():
@@ -413,19 +417,40 @@ def cpu_chamfer(torch, budget_s=12.0):
                        f"512-query chunks, {threads} torch threads on {cpu_model()}")
 
 
-def cpu_knn(O, np, threads):
+def cpu_knn(O, np, threads, q=64):
+    """knn.cpp:30-99 restated on the first q query rows of every config-3
+    cloud; threads = 1 is the reference's own (single-threaded) loop."""
     import workloads
 
     p1, p2, l1, l2 = workloads.knn_c3()
-    q = 64  # queries per cloud
     a = p1[:, :q].numpy()
     ln1 = np.minimum(l1.numpy(), q)
     t0 = time.perf_counter()
     O.cpu_knn_fwd(a, p2.numpy(), ln1, l2.numpy(), 16, 2, nthreads=threads)
     sec = time.perf_counter() - t0
     pairs = float((ln1 * l2.numpy()).sum())
+    how = "one thread, as the reference runs it" if threads == 1 else \
+        f"{threads} OpenMP threads over (cloud, query)"
     return dict(value=pairs / sec / 1e9, unit="G pair-dists/s", cores=threads, kind="port",
-                sample=f"{q} queries per cloud x 8 clouds of config 3 (knn.cpp restated)")
+                sample=f"{q} queries per cloud x 8 clouds of config 3 (knn.cpp restated, {how})")
+
+
+def cpu_knn_c5_torch(torch, threads, nq=256):
+    """The torch 'equivalent' of high-D KNN on the CPU: torch.cdist + topk(32)
+    on float32 upcasts of the first nq queries of every config-5 cloud."""
+    import workloads
+
+    q, r = workloads.knn_c5()
+    a = q[:, :nq].float()
+    b = r.float()
+    t0 = time.perf_counter()
+    for n in range(a.shape[0]):
+        torch.cdist(a[n], b[n]).topk(32, dim=1, largest=False)
+    sec = time.perf_counter() - t0
+    pairs = float(a.shape[0] * nq * b.shape[1])
+    return dict(value=pairs / sec / 1e9, unit="G pair-dists/s", cores=threads, kind="port",
+                sample=f"{nq} queries per cloud x 4 clouds of config 5 widened to float32: "
+                       f"torch.cdist + topk(32), {threads} torch threads")
 
 
 def cpu_knn_c5(O, np, threads):
@@ -610,39 +635,49 @@ def main():
     traffic = (profile_json("chamfer_grid_fwd_c2_traffic.json") or {}).get("hbm_bytes_per_launch")
     counters = profile_json("chamfer_grid_search_c2_counters.json")
 
-    # The dominant launch (sort + search) is VALU-issue bound, and divergent:
-    # its roofline is the fp32 VALU lane-op peak (1024 SIMDs x 16 lanes x
-    # 2.4 GHz; this build emits no packed FP32), the achieved rate the lane
-    # operations the committed counters count per launch (SQ_INSTS_VALU x 64
-    # x VALUUtilization) over this run's HIP-event time of the launch.
+    # The dominant launch (sort + search) runs on the fp32 vector ALU.  Its
+    # algorithmic work is 9 FLOP per (query, reference) pair the exact grid
+    # search evaluates (the kernel counts them), so achieved = 9 x
+    # pairs_evaluated / fwd time against the published 157.3 TFLOP/s fp32
+    # peak.  The VALU issue rate (every lane operation the committed counters
+    # count per launch, bookkeeping included) is reported beside it.
     lane_ops = (counters or {}).get("lane_ops_per_launch")
     achieved_lane = lane_ops / fwd_t / 1e12 if lane_ops else None
     roofline = {"bound": "valu",
-                "compute_unit": "fp32 vector ALU; the kernels use no MFMA",
+                "compute_unit": "fp32 vector ALU (published fp32 peak 157.3 TFLOP/s); "
+                                "the kernels use no MFMA",
                 "kernel": "chamfer_grid_sort_kernel<float,8> + chamfer_grid_search_kernel"
                           "<float,256> (tpo_chamfer_fwd with a workspace)",
-                "achieved": round(achieved_lane, 3) if achieved_lane else None,
-                "peak": VALU_LANE_PEAK_T, "unit": "T VALU lane-ops/s",
-                "frac": round(achieved_lane / VALU_LANE_PEAK_T, 4) if achieved_lane else None,
-                "traffic": traffic, "fwd_ms": round(fwd_t * 1e3, 4),
-                "work": "VALU lane operations per launch from the committed rocprofv3 counters "
-                        "(SQ_INSTS_VALU x 64 x VALUUtilization, sort + search)",
-                "lane_ops_per_launch": lane_ops,
-                "useful_tflops": round(achieved, 4),
-                "useful_frac_fp32_peak": round(achieved / FP32_PEAK_TFLOPS, 5),
-                "useful_work": "9 FLOP (3 sub, 3 mul, 2 add, 1 compare) per (query, reference) "
-                               "pair the exact grid search evaluates, counted by the kernel",
+                "achieved": round(achieved, 4), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_PEAK_TFLOPS, 5),
+                "traffic": traffic,
+                "algorithmic_bytes": CHAMFER_FWD_BYTES,
+                "traffic_ratio": round(traffic / CHAMFER_FWD_BYTES, 3) if traffic else None,
+                "work": "achieved = flop_per_pair x pairs_evaluated / (fwd_ms / 1e3) / 1e12: "
+                        "9 FLOP (3 sub, 3 mul, 2 add, 1 compare) per (query, reference) pair "
+                        "the exact grid search evaluates, counted by the kernel",
+                "flop_per_pair": FLOP_PER_PAIR,
                 "pairs_evaluated": ch["pairs_evaluated"],
+                "fwd_ms": round(fwd_t * 1e3, 4),
+                "algorithmic_bytes_note": "inputs 2 x B x N x 3 x 4 + distances 2 x B x N x 4 + "
+                                          "indices 2 x B x N x 4 (int32)",
+                "valu_issue": {
+                    "achieved": round(achieved_lane, 3) if achieved_lane else None,
+                    "peak": VALU_LANE_PEAK_T, "unit": "T VALU lane-ops/s",
+                    "frac": round(achieved_lane / VALU_LANE_PEAK_T, 4) if achieved_lane else None,
+                    "lane_ops_per_launch": lane_ops,
+                    "source": "committed rocprofv3 counters (SQ_INSTS_VALU x 64 x "
+                              "VALUUtilization, sort + search) over this run's launch time"},
                 "algorithmic_pairs_brute_force": ch["pairs"],
                 "brute_force_equivalent_tflops": round(brute, 3),
                 "module_fwd_ms": round(ch["loss_fwd_sec"] * 1e3, 4),
                 "valu_counters": counters,
-                "note": "frac = VALUBusy x VALUUtilization of the launch: each search wave "
-                        "shares its queries' cell tests and point evaluations across its "
-                        "lanes, so most of its VALU work is per-item bookkeeping around the "
-                        "distance; useful_tflops counts only the distance work it needs, "
-                        "brute_force_equivalent_tflops 9 FLOP x all 2BNM directed pairs over "
-                        "the same time"}
+                "note": "the search prunes exactly: it evaluates pairs_evaluated of the "
+                        "2BNM directed pairs; brute_force_equivalent_tflops is 9 FLOP x all "
+                        "2BNM pairs over the same time. valu_issue.frac is the share of the "
+                        "VALU lane-op peak the launch issues; most of those operations are "
+                        "per-item bookkeeping (segment lookup, scans, key selects) around "
+                        "the distance"}
     out = {
         "metric": "Chamfer/KNN G pair-dists/s & % FP32 VALU peak; FPS ms at N=64K->4K",
         "value": round(value, 3),
@@ -709,7 +744,11 @@ def main():
         log("[bench] fps + gather c4")
         fp = bench_fps(tpo, torch, args.steps)
         sec["fps_c4"] = {"ms": round(fp["fps_sec"] * 1e3, 3),
-                         "G_point_updates_per_s": round(fp["updates"] / fp["fps_sec"] / 1e9, 2)}
+                         "G_point_updates_per_s": round(fp["updates"] / fp["fps_sec"] / 1e9, 2),
+                         "sweep_GBs": round(16 * fp["updates"] / fp["fps_sec"] / 1e9, 1),
+                         "sweep_note": "16 B per point-update (the x, y, z, running minimum a "
+                                       "brute-force sweep reads) x B x N x (m - 1) / time: "
+                                       "on-chip traffic, not HBM"}
         sec["gather_c4"] = {
             "fwd_us": round(fp["gather_fwd_sec"] * 1e6, 2),
             "fwd_GBs": round(fp["fwd_bytes"] / fp["gather_fwd_sec"] / 1e9, 1),
@@ -737,10 +776,12 @@ def main():
 
             sec["emd_b16_n2048"]["cpu_baseline"] = cpu_emd(O, threads)
             sec["knn_c3"]["cpu_baseline"] = cpu_knn(O, np, threads)
+            sec["knn_c3"]["cpu_baseline_1thread"] = cpu_knn(O, np, 1, q=16)
             sec["knn_c3"]["cpu_baseline_backward"] = cpu_knn_bwd(O, np, threads)
             sec["fps_c4"]["cpu_baseline"] = cpu_fps(O, np, fp["pts"], threads)
             sec["gather_c4"]["cpu_baseline"] = cpu_gather(O, np, fp["idx"], threads)
             sec["knn_c5_bf16"]["cpu_baseline"] = cpu_knn_c5(O, np, threads)
+            sec["knn_c5_bf16"]["cpu_baseline_torch"] = cpu_knn_c5_torch(torch, threads)
     if sec:
         out["secondary"] = sec
     out["host"] = {"cpu": cpu_model(), "cores": threads,
