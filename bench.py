@@ -3,8 +3,12 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
 
 Headline: one step = Chamfer forward + backward
-(ChamferDistance('mean') and its gradient) at B=32, N=M=8192, float32, inputs
-resident in HBM; K steps after W warm-ups between two synchronisations.
+(ChamferDistance('mean') and its gradient through autograd) at B=32,
+N=M=8192, float32, inputs resident in HBM; K steps after W warm-ups between
+two synchronisations.  The backward runs on the calling thread
+(torch.autograd.set_multithreading_enabled(False)); the step time with
+PyTorch's default multithreaded engine, whose device-thread handoff costs
+more host time per backward than the kernels take, is reported beside it.
 value = directed pair-distances per second (2*B*N*M per step) in G/s.
 
 roofline: the dominant kernels, the grid forward (sort + exact grid search),
@@ -115,14 +119,34 @@ def bench_chamfer(tpo, torch, steps, warmup):
         loss = model(a, b)
         return torch.autograd.grad(loss, (a, b))
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    sec = (time.perf_counter() - t0) / steps
+    def timed(multithreaded):
+        # multithreaded=False runs the backward graph on the calling thread
+        # (torch.autograd.set_multithreading_enabled(False)); PyTorch's default
+        # engine hands each backward to a device thread and back, a fixed
+        # host cost per backward that on these hosts exceeds the kernels' time
+        with torch.autograd.set_multithreading_enabled(multithreaded):
+            for _ in range(warmup):
+                step()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) / steps
+
+    sec_default = timed(True)
+    sec = timed(False)
+    # the fixed cost of one default-engine backward, on a trivial graph
+    x = torch.ones(16, device=dev, requires_grad=True)
+    with torch.autograd.set_multithreading_enabled(True):
+        for _ in range(warmup):
+            torch.autograd.grad((x * 2).sum(), (x,))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            torch.autograd.grad((x * 2).sum(), (x,))
+        torch.cuda.synchronize()
+        sec_trivial = (time.perf_counter() - t0) / steps
     # the module's forward alone (sort, search and the loss kernels), HIP
     # events on the current stream, which is the one the op launches on
     # (events inside every step would add their own gaps to the step time)
@@ -133,8 +157,8 @@ def bench_chamfer(tpo, torch, steps, warmup):
         model(a0, b0)
     e1.record()
     torch.cuda.synchronize()
-    out = dict(pairs=2 * B * N * M, sec=sec, B=B, N=N, M=M,
-               loss_fwd_sec=e0.elapsed_time(e1) / steps / 1e3)
+    out = dict(pairs=2 * B * N * M, sec=sec, B=B, N=N, M=M, sec_default_engine=sec_default,
+               sec_trivial_grad=sec_trivial, loss_fwd_sec=e0.elapsed_time(e1) / steps / 1e3)
     out.update(chamfer_forward_paths(torch, a0, b0, steps))
     return out
 
@@ -198,7 +222,8 @@ def bench_chamfer_fp16(tpo, torch, steps):
     a = p1.to(dev).requires_grad_(True)
     b = p2.to(dev).requires_grad_(True)
     model = tpo.ChamferDistance("mean")
-    sec = time_events(lambda: torch.autograd.grad(model(a, b), (a, b)), torch, steps)
+    with torch.autograd.set_multithreading_enabled(False):  # as the headline step
+        sec = time_events(lambda: torch.autograd.grad(model(a, b), (a, b)), torch, steps)
     return dict(pairs=2 * a.shape[0] * a.shape[1] * b.shape[1], sec=sec)
 
 
@@ -686,6 +711,13 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ch["sec"] * 1e3, 4),
+        "ms_per_step_default_autograd_engine": round(ch["sec_default_engine"] * 1e3, 4),
+        "autograd_engine": "backward run on the calling thread "
+                           "(torch.autograd.set_multithreading_enabled(False)); with PyTorch's "
+                           "default multithreaded engine the step takes "
+                           "ms_per_step_default_autograd_engine, and an autograd.grad of the "
+                           "trivial graph (x*2).sum() alone takes trivial_grad_ms_default_engine",
+        "trivial_grad_ms_default_engine": round(ch["sec_trivial_grad"] * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -224,6 +224,24 @@ int tpo_knn_bwd(int dtype, const void* p1, const void* p2,
                 void* grad_p1, void* grad_p2, void* stream);
 
 /*
+ * tpo_knn_bwd with a workspace (the same reference function,
+ * knn_cuda_backward, knn.cu:469-534).  With workspace_bytes >=
+ * tpo_knn_bwd_workspace_size() (non-zero for D <= 7, K <= 256 and
+ * reference clouds up to ~750 K points) grad_p2 is accumulated without
+ * global atomics: the terms are grouped by reference rows in the workspace
+ * and each group is summed in LDS.  A smaller or NULL workspace runs the
+ * atomic scatter of tpo_knn_bwd.  workspace: 256-byte aligned.
+ */
+int64_t tpo_knn_bwd_workspace_size(int dtype, int64_t N, int64_t P1, int64_t P2, int64_t D,
+                                   int64_t K);
+int tpo_knn_bwd_ws(int dtype, const void* p1, const void* p2,
+                   const int64_t* lengths1, const int64_t* lengths2,
+                   const int64_t* idxs, int norm, const void* grad_dists,
+                   int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K,
+                   void* grad_p1, void* grad_p2, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
+/*
  * Furthest point sampling.  Replaces fps_cuda_forward
  * (torch_point_ops/fps/csrc/cuda/fps.cu:273-315),
  * torch_point_ops_fps::fps_forward (fps.cpp:159).

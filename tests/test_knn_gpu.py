@@ -374,6 +374,82 @@ def test_backward_vs_oracle(tpo, O, dev, norm, version):
         assert np.abs(got - ref).max() <= 1e-5 * max(np.abs(ref).max(), 1e-30)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
+@pytest.mark.parametrize("D,K,version", [(3, 16, -1), (1, 1, -1), (3, 5, 0), (5, 7, 1),
+                                         (8, 32, -1), (3, 40, -1), (2, 256, 0), (3, 300, 0),
+                                         (9, 4, -1), (64, 10, -1), (130, 3, 0)])
+@pytest.mark.parametrize("norm", [1, 2])
+def test_backward_shapes_vs_oracle(tpo, O, dev, dtype, D, K, version, norm):
+    """Both backward kernels (a lane per (row, slot) for D <= 8 and K <= 256,
+    a wave per row otherwise) on the oracle's raw rows: -1 padding of
+    versions 0/1, clouds shorter than K, rows past lengths1, lattice ties
+    (norm 1's sign 0 on equal coordinates)."""
+    g = torch.Generator().manual_seed(D * 1000 + K * 10 + norm)
+    N, P1, P2 = 3, 130, 320
+    p1 = torch.randn(N, P1, D, generator=g)
+    p2 = torch.randn(N, P2, D, generator=g)
+    p1[1] = torch.randint(-2, 3, (P1, D), generator=g).float()
+    p2[1] = torch.randint(-2, 3, (P2, D), generator=g).float()
+    p1, p2 = p1.to(dtype), p2.to(dtype)
+    l1 = torch.tensor([P1, 77, 0])
+    l2 = torch.tensor([P2, max(1, K // 2), 5])
+    ei, _ = O.knn_fwd(np_(p1), np_(p2), np_(l1), np_(l2), norm=norm, K=K, version=version)
+    gd = torch.rand(N, P1, K, generator=g).to(dtype)
+    idx = torch.from_numpy(ei)
+    g1, g2 = torch.ops.torch_point_ops_knn.knn_backward(
+        p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev), idx.to(dev), norm, gd.to(dev))
+    e1, e2 = O.knn_bwd(np_(p1), np_(p2), np_(l1), np_(l2), ei, norm, np_(gd), accum_f64=True)
+    tol = 2e-2 if dtype == torch.float16 else (1e-5 if dtype == torch.float32 else 1e-12)
+    for got, ref in ((np_(g1), e1), (np_(g2), e2)):
+        ref64 = ref.astype(np.float64)
+        assert np.abs(got.astype(np.float64) - ref64).max() <= tol * max(np.abs(ref64).max(), 1e-30)
+        if dtype != torch.float16:  # untouched rows and points stay exactly zero
+            assert (got[ref64 == 0] == 0).all()
+
+
+@pytest.mark.parametrize("case", ["one_row", "range", "nonfinite"])
+def test_backward_accumulation_edge_cases(tpo, O, dev, case):
+    """grad_p2 through the bucketed fixed-point accumulation: 48000 terms on
+    one reference row (the scale must keep the row sum in range), terms
+    spanning 1e-18 .. 1e+18 in one bucket, and infinite / NaN terms (their
+    buckets summed in floating point); finite buckets give the same bits on
+    every call."""
+    g = torch.Generator().manual_seed(len(case))
+    N, P1, P2, D, K = 2, 3000, 700, 3, 16
+    p1 = torch.randn(N, P1, D, generator=g)
+    p2 = torch.randn(N, P2, D, generator=g)
+    idx = torch.randint(0, P2, (N, P1, K), generator=g)
+    gd = torch.rand(N, P1, K, generator=g)
+    if case == "one_row":
+        idx[0] = 7
+    elif case == "range":
+        gd[0, :, :8] *= 1e-18
+        gd[0, :, 8:] *= 1e18
+        idx[0] = torch.randint(0, 40, (P1, K), generator=g)
+    else:
+        p1[1, 5, 0] = float("inf")
+        p1[1, 9, 2] = float("nan")
+    l1 = torch.tensor([P1, P1 - 100])
+    l2 = torch.tensor([P2, P2])
+    args = (p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev), idx.to(dev), 2, gd.to(dev))
+    g1, g2 = torch.ops.torch_point_ops_knn.knn_backward(*args)
+    h1, h2 = torch.ops.torch_point_ops_knn.knn_backward(*args)
+    # finite terms are summed exactly (fixed point): the same bits each call;
+    # a bucket with a non-finite term sums in floating point, order unspecified
+    same = slice(None) if case != "nonfinite" else slice(0, 1)
+    assert torch.equal(g2[same], h2[same])
+    e1, e2 = O.knn_bwd(np_(p1), np_(p2), np_(l1), np_(l2), np_(idx), 2, np_(gd), accum_f64=True)
+    for got, ref in ((np_(g1), e1), (np_(g2), e2)):
+        ref64, got64 = ref.astype(np.float64), got.astype(np.float64)
+        fin = np.isfinite(ref64)
+        assert np.array_equal(np.isnan(got64), np.isnan(ref64))
+        assert np.array_equal(got64[np.isinf(ref64)], ref64[np.isinf(ref64)])
+        for n in range(N):  # per cloud: cloud 0 of "range" is 1e36 times cloud 1
+            f = fin[n]
+            scale = max(np.abs(ref64[n][f]).max(), 1e-30)
+            assert np.abs(got64[n][f] - ref64[n][f]).max() <= 1e-5 * scale
+
+
 # ---- the reference test suite's checks (tests/test_knn.py) ----
 
 def torch_reference_knn(p1, p2, K):

@@ -27,4 +27,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* tpo_last_error(void) { return tpo::g_err; }
 
-extern "C" int tpo_abi_version(void) { return (2 << 16) | 3; }
+extern "C" int tpo_abi_version(void) { return (2 << 16) | 4; }

@@ -1,4 +1,5 @@
-// knn.hip -- K nearest neighbours (forward/backward) for gfx950.
+// knn.hip -- K nearest neighbours (forward) for gfx950; the backward is in
+// knn_bwd.hip.
 //
 // Forward (replaces KNearestNeighborKernelV0..V3, knn.cu:16-227).
 //   One query per lane; the wave's 64 queries belong to one cloud, so the
@@ -22,10 +23,6 @@
 //   versions 2/3 with (0, 0); rows >= lengths1 are (0, 0).
 //   K > 32 (versions 0/1 only) keeps the slots in the output rows, like the
 //   reference's global-memory MinK.
-// Backward (replaces KNearestNeighborBackwardKernel, knn.cu:400-466).
-//   One thread per query row sums its K contributions to grad_p1 in
-//   registers (plain stores, every row written) and scatters -diff onto
-//   grad_p2 with hardware atomics (grad_p2 zero-filled first).
 #include <utility>
 
 #include "knn_common.hpp"
@@ -49,13 +46,6 @@ void launch_knn_grid(const void* p1, const void* p2, const int64_t* l1, const in
 
 namespace tpo {
 namespace {
-
-template <typename T>
-__global__ __launch_bounds__(256) void fill_kernel(T* __restrict__ p, int64_t n, T v) {
-  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n;
-       t += (int64_t)gridDim.x * blockDim.x)
-    p[t] = v;
-}
 
 // Per cloud, the valid queries (row < lengths1) in Morton order of a 16^3
 // grid over their bounding box.  The order only decides which queries share
@@ -787,49 +777,6 @@ __global__ __launch_bounds__(256) void knn_fwd_global_kernel(
   }
 }
 
-template <typename T, int NORM>
-__global__ __launch_bounds__(256) void knn_bwd_kernel(
-    const T* __restrict__ p1, const T* __restrict__ p2, const int64_t* __restrict__ len1,
-    const int64_t* __restrict__ idxs, const T* __restrict__ gd, int64_t N, int64_t P1, int64_t P2,
-    int64_t D, int64_t K, T* __restrict__ gp1, T* __restrict__ gp2) {
-  const int64_t total = N * P1;
-  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
-       t += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t n = t / P1, q = t - n * P1;
-    int64_t l1 = len1[n];
-    l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
-    const bool active = q < l1;
-    for (int64_t d = 0; d < D; ++d) {
-      T acc = (T)0;
-      if (active) {
-        const T v1 = p1[t * D + d];
-        for (int64_t k = 0; k < K; ++k) {
-          const int64_t r = idxs[t * K + k];
-          if (r < 0 || r >= P2) continue;  // -1 padding (knn.cu:439); others invalid
-          const T g = gd[t * K + k];
-          const T v2 = p2[(n * P2 + r) * D + d];
-          T diff;
-          if (NORM == 1) {  // knn.cu:445-448
-            const T sign = v1 > v2 ? (T)1 : (v1 == v2 ? (T)0 : (T)-1);
-            diff = (T)(g * sign);
-          } else {
-            diff = (T)((T)((T)2 * g) * (T)(v1 - v2));
-          }
-          acc = (T)(acc + diff);
-          atomic_add(gp2 + (n * P2 + r) * D + d, (T)(-diff));
-        }
-      }
-      gp1[t * D + d] = acc;
-    }
-  }
-}
-
-unsigned grid_for(int64_t n) {
-  int64_t g = (n + 255) / 256;
-  if (g > 1 << 20) g = 1 << 20;
-  return (unsigned)(g < 1 ? 1 : g);
-}
-
 template <typename T, int DT, int NORM, int KC>
 void launch_fwd_kc(const void* p1, const void* p2, const int64_t* l1, const int64_t* l2,
                    const int32_t* order, int N, int P1, int P2, int D, int K, int pad,
@@ -889,22 +836,6 @@ void launch_fwd(const void* p1, const void* p2, const int64_t* l1, const int64_t
                 int sorted2, int64_t* idxs, void* dists, hipStream_t s) {
   if (norm == 1) launch_fwd_norm<T, 1>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
   else launch_fwd_norm<T, 2>(p1, p2, l1, l2, order, N, P1, P2, D, K, pad, sorted2, idxs, dists, s);
-}
-
-template <typename T>
-void launch_bwd(const void* p1, const void* p2, const int64_t* l1, const int64_t* idxs,
-                const void* gd, int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K, int norm,
-                void* gp1, void* gp2, hipStream_t s) {
-  hipLaunchKernelGGL(fill_kernel<T>, dim3(grid_for(N * P2 * D)), dim3(256), 0, s, (T*)gp2,
-                     N * P2 * D, (T)0);
-  if (norm == 1)
-    hipLaunchKernelGGL((knn_bwd_kernel<T, 1>), dim3(grid_for(N * P1)), dim3(256), 0, s,
-                       (const T*)p1, (const T*)p2, l1, idxs, (const T*)gd, N, P1, P2, D, K,
-                       (T*)gp1, (T*)gp2);
-  else
-    hipLaunchKernelGGL((knn_bwd_kernel<T, 2>), dim3(grid_for(N * P1)), dim3(256), 0, s,
-                       (const T*)p1, (const T*)p2, l1, idxs, (const T*)gd, N, P1, P2, D, K,
-                       (T*)gp1, (T*)gp2);
 }
 
 // dispatch.cuh:114-147
@@ -1021,21 +952,3 @@ extern "C" int tpo_knn_fwd_sorted(int dtype, const void* p1, const void* p2,
                       dists, version_out, workspace, workspace_bytes, stream, true);
 }
 
-extern "C" int tpo_knn_bwd(int dtype, const void* p1, const void* p2, const int64_t* lengths1,
-                           const int64_t* lengths2, const int64_t* idxs, int norm,
-                           const void* grad_dists, int64_t N, int64_t P1, int64_t P2, int64_t D,
-                           int64_t K, void* grad_p1, void* grad_p2, void* stream) {
-  (void)lengths2;
-  if (N < 0 || P1 < 0 || P2 < 0 || D < 1 || K < 0)
-    return set_error(TPO_ERR_ARG, "tpo_knn_bwd: bad sizes");
-  if (norm != 1 && norm != 2) return set_error(TPO_ERR_ARG, "Norm must be 1 or 2.");
-  if (N == 0 || (P1 == 0 && P2 == 0)) return TPO_OK;
-  hipStream_t s = (hipStream_t)stream;
-  switch (dtype) {
-    case TPO_F32: launch_bwd<float>(p1, p2, lengths1, idxs, grad_dists, N, P1, P2, D, K, norm, grad_p1, grad_p2, s); break;
-    case TPO_F64: launch_bwd<double>(p1, p2, lengths1, idxs, grad_dists, N, P1, P2, D, K, norm, grad_p1, grad_p2, s); break;
-    case TPO_F16: launch_bwd<half_t>(p1, p2, lengths1, idxs, grad_dists, N, P1, P2, D, K, norm, grad_p1, grad_p2, s); break;
-    default: return set_error(TPO_ERR_DTYPE, "tpo_knn_bwd: unsupported dtype %d", dtype);
-  }
-  return check_launch("tpo_knn_bwd");
-}

@@ -391,9 +391,15 @@ std::tuple<at::Tensor, at::Tensor> knn_backward_hip(const at::Tensor& p1_in,
   const at::Tensor idxs = idxs_in.contiguous();
   const at::Tensor gd = grad_dists_in.to(p1.scalar_type()).contiguous();
   const int dt = dtype_code(p1, "knn_backward");
-  check_rc(tpo_knn_bwd(dt, p1.data_ptr(), p2.data_ptr(), l1.data_ptr<int64_t>(),
-                       l2.data_ptr<int64_t>(), idxs.data_ptr<int64_t>(), (int)norm, gd.data_ptr(),
-                       N, P1, P2, D, K, g1.data_ptr(), g2.data_ptr(), stream_of(p1)),
+  // grad_p2 without global atomics: the entry terms are grouped by reference
+  // rows in the workspace (tpo_knn_bwd_ws)
+  const int64_t wsb = tpo_knn_bwd_workspace_size(dt, N, P1, P2, D, K);
+  at::Tensor ws;
+  if (wsb > 0) ws = at::empty({wsb}, p1.options().dtype(at::kByte));
+  check_rc(tpo_knn_bwd_ws(dt, p1.data_ptr(), p2.data_ptr(), l1.data_ptr<int64_t>(),
+                          l2.data_ptr<int64_t>(), idxs.data_ptr<int64_t>(), (int)norm,
+                          gd.data_ptr(), N, P1, P2, D, K, g1.data_ptr(), g2.data_ptr(),
+                          wsb > 0 ? ws.data_ptr() : nullptr, wsb, stream_of(p1)),
            "knn_backward");
   return {g1, g2};
 }
