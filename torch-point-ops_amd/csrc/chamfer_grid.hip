@@ -46,7 +46,8 @@
 // points is rebuilt on the remaining points (the cut sides' boundary cells
 // unbounded); a cloud still crowded into few cells runs the dense block
 // inside the search kernel; a query whose box would hold too many cells
-// joins a wave-wide scan of the reference cloud.  Results are identical to
+// scans coarse 8^3 cells nearest first while a cell can hold a nearer point.
+// Results are identical to
 // the reference's in every case; only the work depends on the data.  Each
 // wave records the number of points it evaluated
 // (tpo_chamfer_pairs_evaluated sums them).
@@ -928,30 +929,102 @@ __global__ __launch_bounds__(WG, 8) void chamfer_grid_search_kernel(
     dout[o] = (T)__uint_as_float((uint32_t)(kb >> 32));
     iout[o] = (int)(uint32_t)kb;
   }
-  // far queries: the wave scans every reference point (sorted order, same
-  // key), one query at a time
-  for (uint64_t fm = __ballot(far); fm; fm &= fm - 1) {
-    const int l = __builtin_ctzll(fm);
-    const float4 qf = wq[l];
-    const float4 ql = make_float4(0.f, qf.x, qf.y, qf.z);
-    unsigned long long k = kInit;
-    for (int j = lane; j < nr; j += 64) {
-      const float4 p = rs[j];
-      const unsigned long long key =
-          ((unsigned long long)__float_as_uint(cg_dist<T>(p, ql)) << 32) | __float_as_uint(p.x);
-      k = key < k ? key : k;
-    }
+  // far queries (nothing in the cell's 3x3x3 neighbourhood, or a box of too
+  // many cells): one query at a time over the coarse grid of 8^3 cells
+  // (Morton order nests the cells: a coarse cell is the run of its 64 fine
+  // 32^3 cells).  Each lane bounds 8 coarse cells from below as the walk
+  // bounds cells; the wave scans the open cell with the smallest bound (its
+  // run of sorted points, 64 a round, a point a lane) and closes it, while
+  // that bound is at or below the query's best.  A skipped cell holds no
+  // point whose distance is at most the best, so neither a smaller distance
+  // nor a tie with a lower index is missed.  Same keys as the walk.
+  if (const uint64_t farm = __ballot(far)) {
+    float csc[3];
+    int gac[3];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const unsigned long long x = __shfl_xor(k, o);
-      k = x < k ? x : k;
+    for (int a = 0; a < 3; ++a) {
+      csc[a] = U(__builtin_ldexpf(h[9 + a], 2));
+      gac[a] = gs[a] > 0.f ? 8 : 1;
     }
-    if (lane == l) {
-      const int o = __float_as_int(qf.w);
-      dout[o] = (T)__uint_as_float((uint32_t)(k >> 32));
-      iout[o] = (int)(uint32_t)k;
+    // distance from x to coarse cell c's slab along axis a, as axis_gap
+    auto gap = [&](int a, int c, float x) {
+      const float clo = (cut >> a) & 1u && c == 0
+                            ? -__builtin_inff()
+                            : (gac[a] > 1 ? glo[a] + (float)c * csc[a] : glo[a]) - eps[a];
+      const float chi = (cut >> (3 + a)) & 1u && c == gac[a] - 1
+                            ? __builtin_inff()
+                            : (gac[a] > 1 ? glo[a] + (float)(c + 1) * csc[a] : ghi[a]) + eps[a];
+      return fmaxf(fmaxf(clo - x, x - chi), 0.f);
+    };
+    // bit k: coarse cell lane + 64 k holds points
+    uint32_t busy = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int c = lane + 64 * k, cx = c & 7, cy = (c >> 3) & 7, cz = c >> 6;
+      const uint32_t code = cg_code(cx, cy, cz);
+      if (cx < gac[0] && cy < gac[1] && cz < gac[2] &&
+          cstart[(code + 1) << 6] > cstart[code << 6])
+        busy |= 1u << k;
     }
-    examined += nr;
+    for (uint64_t fm = farm; fm; fm &= fm - 1) {
+      const int l = __builtin_ctzll(fm);
+      const float4 qf = wq[l];
+      const float4 ql = make_float4(0.f, qf.x, qf.y, qf.z);
+      unsigned long long key = wkey[l];
+      uint32_t open = busy;  // bit k: not scanned yet for this query
+      for (;;) {
+        const float bd = __uint_as_float((uint32_t)(key >> 32));
+        float m = __builtin_inff();
+        int mk = -1;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int c = lane + 64 * k;
+          const float b = fmaxf(sq3(gap(0, c & 7, qf.x), gap(1, (c >> 3) & 7, qf.y),
+                                    gap(2, c >> 6, qf.z)) * Mg::lb - Mg::abs, 0.f);
+          if ((open >> k) & 1u && (mk < 0 || b < m)) {  // an infinite bound is a bound too
+            m = b;
+            mk = k;
+          }
+        }
+        // (bound, lane, cell) of the lane's nearest open cell; all ones when
+        // it has none, above any open cell's key
+        unsigned long long pk = mk < 0 ? ~0ull
+                                       : (unsigned long long)__float_as_uint(m) << 32 |
+                                             (uint32_t)(lane << 3 | mk);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const unsigned long long x = __shfl_xor(pk, o);
+          pk = x < pk ? x : pk;
+        }
+        // every round closes one open cell: at most 512 rounds.  No open cell
+        // left, or the nearest above the best (an infinite best -- half
+        // distances can overflow -- takes every cell): done
+        if (pk == ~0ull || __uint_as_float((uint32_t)(pk >> 32)) > bd) break;
+        const int wl = (int)(pk >> 3) & 63, wk = (int)pk & 7;
+        if (lane == wl) open &= ~(1u << wk);
+        const int c = __builtin_amdgcn_readfirstlane(wl + 64 * wk);
+        const uint32_t code = cg_code(c & 7, (c >> 3) & 7, c >> 6);
+        const int s0 = cstart[code << 6], s1 = cstart[(code + 1) << 6];
+        examined += s1 - s0;
+        unsigned long long kk = kInit;
+        for (int j = s0 + lane; j < s1; j += 64) {
+          const float4 p = rs[j];
+          const unsigned long long k2 =
+              ((unsigned long long)__float_as_uint(cg_dist<T>(p, ql)) << 32) | __float_as_uint(p.x);
+          kk = k2 < kk ? k2 : kk;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const unsigned long long x = __shfl_xor(kk, o);
+          kk = x < kk ? x : kk;
+        }
+        key = kk < key ? kk : key;
+      }
+      if (lane == l) {
+        dout[__float_as_int(qf.w)] = (T)__uint_as_float((uint32_t)(key >> 32));
+        iout[__float_as_int(qf.w)] = (int)(uint32_t)key;
+      }
+    }
   }
   // points evaluated by this wave (a wave-uniform count)
   if (lane == 0) stats[(size_t)bid * (WG / 64) + w] = examined;
