@@ -26,7 +26,7 @@ INCLUDE = os.path.join(REPO, "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["capi.hip", "chamfer.hip", "chamfer_grid.hip", "knn.hip", "knn_bwd.hip", "knn_grid.hip", "knn_bf16.hip", "fps.hip", "gather.hip", "emd.hip"]
+HIP_SOURCES = ["capi.hip", "chamfer.hip", "chamfer_grid.hip", "knn.hip", "knn_hd.hip", "knn_bwd.hip", "knn_grid.hip", "knn_bf16.hip", "fps.hip", "gather.hip", "emd.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
