@@ -207,10 +207,12 @@ __device__ __forceinline__ void knn_sort_row(T (&d)[KC], int (&ix)[KC], uint32_t
     }
 }
 
-// lane L of each 16-lane row, broadcast over the row (gfx950 DPP row_newbcast)
+// lane L of each 16-lane row, broadcast over the row (gfx950 DPP row_newbcast).
+// Every lane reads a lane of its own row, so no old value is needed: without
+// one the move folds into the VALU op that uses it whatever the schedule.
 template <int L>
 __device__ __forceinline__ float row_bcast(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x150 + L, 0xF, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + L, 0xF,
+                                                            0xF, true));
 }
 }  // namespace tpo

@@ -49,15 +49,23 @@ __device__ __forceinline__ float f4_at(const float4& v) {
   else return v.w;
 }
 // knn.cu:148-158 over dimensions 0 .. DT-1 in order; dimension d of the
-// reference is lane (d % 64) / 4 of the row, VGPR (d / 64, d % 4)
-template <int NORM, int DT, int... D>
+// reference is lane (d % 64) / 4 of the row, VGPR (d / 64, d % 4).  The
+// differences are taken two at a time: a DPP subtraction whose destination
+// the previous VALU op wrote needs two wait states (its old-value operand),
+// and two live differences keep consecutive subtractions in different VGPRs.
+template <int NORM, int DT, int D0>
+__device__ __forceinline__ void hd_pair(float& acc, const float (&qr)[DT], const float4 (&rv)[DT / 64]) {
+  constexpr int D1 = D0 + 1;
+  const float x0 = qr[D0] - row_bcast<(D0 % 64) / 4>(f4_at<D0 % 4>(rv[D0 / 64]));
+  const float x1 = qr[D1] - row_bcast<(D1 % 64) / 4>(f4_at<D1 % 4>(rv[D1 / 64]));
+  acc = NORM == 2 ? knn_acc2(acc, x0, D0 == 0) : knn_acc1(acc, x0, D0 == 0);
+  acc = NORM == 2 ? knn_acc2(acc, x1, false) : knn_acc1(acc, x1, false);
+}
+template <int NORM, int DT, int... P>
 __device__ __forceinline__ float hd_dist(const float (&qr)[DT], const float4 (&rv)[DT / 64],
-                                         std::integer_sequence<int, D...>) {
+                                         std::integer_sequence<int, P...>) {
   float acc = 0.f;
-  ((acc = NORM == 2
-              ? knn_acc2(acc, qr[D] - row_bcast<(D % 64) / 4>(f4_at<D % 4>(rv[D / 64])), D == 0)
-              : knn_acc1(acc, qr[D] - row_bcast<(D % 64) / 4>(f4_at<D % 4>(rv[D / 64])), D == 0)),
-   ...);
+  (hd_pair<NORM, DT, 2 * P>(acc, qr, rv), ...);
   return acc;
 }
 
@@ -136,7 +144,7 @@ __global__ __launch_bounds__(256) void knn_hd_slice_kernel(
 #pragma unroll
     for (int g = 0; g < G; ++g) rv[g] = *reinterpret_cast<const float4*>(rp + (size_t)j * DT + 64 * g);
   };
-  constexpr auto dims = std::make_integer_sequence<int, DT>{};
+  constexpr auto dims = std::make_integer_sequence<int, DT / 2>{};
   // the fill: references 0 .. K-1 (K < L2 here)
   float sd[KC];
 #pragma unroll
@@ -169,9 +177,19 @@ __global__ __launch_bounds__(256) void knn_hd_slice_kernel(
   for (int u = 0; u < HD_J; ++u) load_ref(rb[u], min(a + u, b - 1));
   for (int base = a; base < b; base += 32) {
     uint32_t mask = 0;
+    // the last walk's candidate stores count on vmcnt too: settle them here,
+    // so that within the chunk each reference waits only for its own loads
+    // (issued HD_J - 1 distances earlier) and not for the newest ones
+    __builtin_amdgcn_s_waitcnt(0);
     for (int u0 = 0; u0 < 32; u0 += HD_J) {
 #pragma unroll
       for (int u = 0; u < HD_J; ++u) {
+        // an ordering point: the loads issued so far stay above it and this
+        // reference's distance below, so each buffer is reloaded right after
+        // its distance instead of all HD_J at the end of the step
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          asm volatile("" : "+v"(rb[u][g].x), "+v"(rb[u][g].y), "+v"(rb[u][g].z), "+v"(rb[u][g].w) :: "memory");
         float d = hd_dist<NORM>(qr, rb[u], dims);
         // the next reference for this buffer (clamped into the slice)
         load_ref(rb[u], min(base + u0 + HD_J + u, b - 1));
@@ -199,6 +217,31 @@ __global__ __launch_bounds__(256) void knn_hd_slice_kernel(
   if (q < P1) cnt[cs] = act ? count : 0;
 }
 
+// The merge runs one wave per query row.  The replay's K slots live one per
+// lane (lanes 0 .. K-1) as a list ordered by (value, slot descending), NaN
+// values first: the last lane then holds the slot that first_max picks (the
+// first slot holding the largest value; a NaN never becomes the maximum
+// unless it sits in slot 0, and then the threshold is NaN and nothing is
+// ever inserted).  Inserting (d, j) below the threshold puts it into the
+// last element's slot: the lanes whose key exceeds the new one shift up one
+// lane (DPP wave_shr) and the new entry lands in the gap.  Candidates come
+// 64 at a time, one per lane; a ballot against the threshold finds the next
+// insertion in index order, and is taken again after each one.
+
+// order key of a distance: the compare-equal floats share one (-0 as +0),
+// NaN below every number
+__device__ __forceinline__ uint32_t hd_ord(float v) {
+  const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+  return v != v ? 0u : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+}
+__device__ __forceinline__ int hd_shr1(int x) {  // lane i takes lane i-1 (lane 0: 0)
+  return __builtin_amdgcn_mov_dpp(x, 0x138, 0xF, 0xF, true);
+}
+__device__ __forceinline__ int hd_lane(int x, int l) { return __builtin_amdgcn_readlane(x, l); }
+__device__ __forceinline__ float hd_lane(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
 template <int DT, int NORM, int KC, bool SORT>
 __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
     const float* __restrict__ p1, const float* __restrict__ p2, const int64_t* __restrict__ len1,
@@ -206,51 +249,82 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
     const int32_t* __restrict__ cnt, const float* __restrict__ cd,
     const int32_t* __restrict__ ci, const float* __restrict__ fd, int64_t* __restrict__ idxs,
     float* __restrict__ dists) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= (int64_t)N * P1) return;
-  const int n = (int)(t / P1), q = (int)(t - (int64_t)n * P1);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  if (row >= (int64_t)N * P1) return;  // the whole wave
+  const int lane = lane_id();
+  const int n = (int)(row / P1), q = (int)(row - (int64_t)n * P1);
   int64_t l1 = len1[n], l2 = len2[n];
   l1 = l1 < 0 ? 0 : (l1 > P1 ? P1 : l1);
   l2 = l2 < 0 ? 0 : (l2 > P2 ? P2 : l2);
   const int L2 = (int)l2;
-  const size_t row = (size_t)t;
   int64_t* __restrict__ io = idxs + row * K;
   float* __restrict__ dout = dists + row * K;
   if (q >= l1) {  // never written by the reference: its zeros
-    for (int s = 0; s < K; ++s) {
-      io[s] = 0;
-      dout[s] = 0.f;
+    if (lane < K) {
+      io[lane] = 0;
+      dout[lane] = 0.f;
     }
     return;
   }
-  // the query stays in memory (a register copy would be live through the
-  // whole replay): distances here are the fill's and an overflowed slice's
   const float4* __restrict__ qp = reinterpret_cast<const float4*>(p1 + row * DT);
   const float* __restrict__ rp = p2 + (size_t)n * P2 * DT;
   auto dist = [&](int j) { return hd_dist_mem<NORM, DT>(qp, reinterpret_cast<const float4*>(rp + (size_t)j * DT)); };
-  float sd[KC];
-  int si[KC];
+  // lane s < K: slot s of the fill (with more than K references the first
+  // slice stored its distances)
   const int fill = L2 < K ? L2 : K;
-#pragma unroll
-  for (int s = 0; s < KC; ++s) {
-    if (s < fill) {
-      // with more than K references the first slice stored them
-      sd[s] = L2 > K ? fd[row * K + s] : dist(s);
-      si[s] = s;
-    } else {
-      sd[s] = Lim<float>::inf();
-      si[s] = -1;
-    }
+  float v = Lim<float>::inf();
+  int ix = -1;
+  if (lane < fill) {
+    v = L2 > K ? fd[row * K + lane] : dist(lane);
+    ix = lane;
   }
-  const int size = fill;
-  if (L2 > K) {
-    float thr;
-    int ms;
-    first_max<float, KC>(sd, K, thr, ms);
-    auto replay = [&](float d, int j) {
-      if (d < thr) {
-        mink_put<float, KC>(sd, si, ms, d, j);
-        first_max<float, KC>(sd, K, thr, ms);
+  if (L2 > K && hd_lane(v, 0) == hd_lane(v, 0)) {
+    // the fill as the ordered list: lane s moves to its rank
+    int slot = lane;
+    uint64_t key = ((uint64_t)hd_ord(v) << 32) | (uint32_t)(63 - lane);
+    int rank = 0;
+#pragma unroll
+    for (int t = 0; t < KC; ++t) {
+      if (t < K) {
+        const uint64_t kt = ((uint64_t)(uint32_t)hd_lane((int)(key >> 32), t) << 32) |
+                            (uint32_t)hd_lane((int)(uint32_t)key, t);
+        rank += kt < key ? 1 : 0;
+      }
+    }
+    const int to = 4 * (lane < K ? rank : lane);
+    v = __int_as_float(__builtin_amdgcn_ds_permute(to, __float_as_int(v)));
+    ix = __builtin_amdgcn_ds_permute(to, ix);
+    slot = __builtin_amdgcn_ds_permute(to, slot);
+    key = ((uint64_t)hd_ord(v) << 32) | (uint32_t)(63 - slot);
+    float thr = hd_lane(v, K - 1);
+    auto insert = [&](float d, int j) {
+      const int sr = hd_lane(slot, K - 1);
+      const uint64_t kn = ((uint64_t)hd_ord(d) << 32) | (uint32_t)(63 - sr);
+      const bool gt = lane < K && key > kn;
+      const bool gtp = hd_shr1(gt ? 1 : 0) != 0;
+      const float vp = __int_as_float(hd_shr1(__float_as_int(v)));
+      const int ixp = hd_shr1(ix), slp = hd_shr1(slot);
+      const uint32_t klo = (uint32_t)hd_shr1((int)(uint32_t)key), khi = (uint32_t)hd_shr1((int)(key >> 32));
+      if (gtp) {
+        v = vp;
+        ix = ixp;
+        slot = slp;
+        key = ((uint64_t)khi << 32) | klo;
+      } else if (gt) {
+        v = d;
+        ix = j;
+        slot = sr;
+        key = kn;
+      }
+      thr = hd_lane(v, K - 1);
+    };
+    // one candidate per lane, in index order across the lanes
+    auto batch = [&](float di, int ji, bool ok) {
+      uint64_t m = __ballot(ok && di < thr);
+      while (m != 0) {
+        const int e = __builtin_ctzll(m);
+        insert(hd_lane(di, e), hd_lane(ji, e));
+        m &= __ballot(ok && di < thr) & ~((2ull << e) - 1ull);
       }
     };
     for (int sl = 0; sl < S; ++sl) {
@@ -258,69 +332,62 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
       if (a >= b) break;
       const int c = cnt[row * S + sl];
       if (c <= HD_CAP) {
-        // 16 candidates a step, loaded together (the list holds HD_CAP
-        // entries, a multiple of 16, so a step never reads past it); the
-        // step's mask against the threshold at its start is a superset of
-        // its insertions, each re-checked against the current threshold
-        const float4* __restrict__ cdp = reinterpret_cast<const float4*>(cd + (row * S + sl) * HD_CAP);
-        const int4* __restrict__ cip = reinterpret_cast<const int4*>(ci + (row * S + sl) * HD_CAP);
-        for (int k0 = 0; k0 < c; k0 += 16) {
-          float dv[16];
-          int iv[16];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const float4 d4 = cdp[k0 / 4 + v];
-            const int4 i4 = cip[k0 / 4 + v];
-            dv[4 * v] = d4.x, dv[4 * v + 1] = d4.y, dv[4 * v + 2] = d4.z, dv[4 * v + 3] = d4.w;
-            iv[4 * v] = i4.x, iv[4 * v + 1] = i4.y, iv[4 * v + 2] = i4.z, iv[4 * v + 3] = i4.w;
-          }
-          uint32_t m = 0;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) m |= (k0 + e < c && dv[e] < thr ? 1u : 0u) << e;
-          while (m != 0) {
-            const int e = __builtin_ctz(m);
-            m &= m - 1;
-            float d = dv[0];
-            int j = iv[0];
-#pragma unroll
-            for (int x = 1; x < 16; ++x) {
-              d = x == e ? dv[x] : d;
-              j = x == e ? iv[x] : j;
-            }
-            replay(d, j);
-          }
+        const float* __restrict__ cdp = cd + (row * S + sl) * HD_CAP;
+        const int32_t* __restrict__ cip = ci + (row * S + sl) * HD_CAP;
+        for (int k0 = 0; k0 < c; k0 += 64) {
+          const int k = min(k0 + lane, c - 1);  // lanes past the list repeat its last entry
+          batch(cdp[k], cip[k], k0 + lane < c);
         }
       } else {  // the slice's list overflowed: recompute it in order
-        for (int j = a; j < b; ++j) replay(dist(j), j);
+        for (int j0 = a; j0 < b; j0 += 64) {
+          const int j = min(j0 + lane, b - 1);
+          batch(dist(j), j, j0 + lane < b);
+        }
       }
     }
+    // back to slot order: lane s takes slot s
+    const int back = 4 * (lane < K ? slot : lane);
+    v = __int_as_float(__builtin_amdgcn_ds_permute(back, __float_as_int(v)));
+    ix = __builtin_amdgcn_ds_permute(back, ix);
   }
+  const int size = fill;
   const int64_t pad_i = pad_sentinel ? -1 : 0;
   const float pad_d = pad_sentinel ? Lim<float>::inf() : 0.f;
   if constexpr (SORT) {
-#pragma unroll
-    for (int s = 0; s < KC; ++s) {
-      if (s >= size) {
-        sd[s] = Lim<float>::inf();
-        si[s] = (int)pad_i;
+    // knn_sort_row's network with position p in lane p: an exchange of
+    // positions (a, a + stride) runs in both lanes, which agree on it
+    float d = lane < size ? v : Lim<float>::inf();
+    int x = lane < size ? ix : (int)pad_i;
+    int va = lane < K ? 1 : 0;
+    auto cas = [&](int stride, bool up) {
+      const float pd = __shfl_xor(d, stride);
+      const int px = __shfl_xor(x, stride), pv = __shfl_xor(va, stride);
+      const bool lo = (lane & stride) == 0;
+      const float da = lo ? d : pd, db = lo ? pd : d;
+      const bool vA = (lo ? va : pv) != 0, vB = (lo ? pv : va) != 0;
+      const bool lt = !knn_isnan(da) && (knn_isnan(db) || da < db);
+      const bool sw = ((lt && vA) || !vB) == up;
+      if ((lane | stride) < KC && sw) {
+        d = pd;
+        x = px;
+        va = pv;
       }
-    }
-    knn_sort_row<float, KC>(sd, si, K >= 32 ? 0xffffffffu : (1u << K) - 1u);
+    };
 #pragma unroll
-    for (int s = 0; s < KC; ++s) {
-      if (s < K) {
-        io[s] = (int64_t)si[s];
-        dout[s] = s < size ? sd[s] : 0.f;
-      }
+    for (int sz = 2; sz < 32; sz *= 2)
+#pragma unroll
+      for (int stride = sz / 2; stride > 0; stride /= 2) cas(stride, (lane & sz) != 0);
+#pragma unroll
+    for (int stride = 16; stride > 0; stride /= 2) cas(stride, false);
+    if (lane < K) {
+      io[lane] = (int64_t)x;
+      dout[lane] = lane < size ? d : 0.f;
     }
     return;
   }
-#pragma unroll
-  for (int s = 0; s < KC; ++s) {
-    if (s < K) {
-      io[s] = s < size ? (int64_t)si[s] : pad_i;
-      dout[s] = s < size ? sd[s] : pad_d;
-    }
+  if (lane < K) {
+    io[lane] = lane < size ? (int64_t)ix : pad_i;
+    dout[lane] = lane < size ? v : pad_d;
   }
 }
 
@@ -356,7 +423,7 @@ void launch_hd_kc(const void* p1, const void* p2, const int64_t* l1, const int64
   hipLaunchKernelGGL((knn_hd_slice_kernel<DT, NORM, KC>), dim3(N * nqb * S), dim3(256), 0, s,
                      (const float*)p1, (const float*)p2, l1, l2, P1, P2, K, nqb, S, slen, cnt, cd,
                      ci, fd);
-  const unsigned mg = (unsigned)(((int64_t)N * P1 + 255) / 256);
+  const unsigned mg = (unsigned)(((int64_t)N * P1 + 3) / 4);  // a wave per row
   if (sort)
     hipLaunchKernelGGL((knn_hd_merge_kernel<DT, NORM, KC, true>), dim3(mg), dim3(256), 0, s,
                        (const float*)p1, (const float*)p2, l1, l2, N, P1, P2, K, S, slen, pad, cnt,
