@@ -14,12 +14,14 @@ namespace {
 // A long reference cloud and few queries (config 5's shape in float: 16384
 // queries, 65536 references of 128 dimensions) leave most of the GPU idle
 // with one lane per query.  The references [K, lengths2) are cut into S
-// slices, and a workgroup per (cloud, 256 queries, slice) runs its own MinK
-// seeded with the K fill references (0 .. K-1) over its slice only.  That
-// local MinK keeps the K smallest values of a subset of every prefix the
-// real process has seen, so its threshold is never below the real one: every
-// reference the real process inserts is inserted locally too, and the local
-// insertions (distance, index) of a slice are a superset of the real ones.
+// slices, and a workgroup per (cloud, 256 queries, slice) keeps, over its
+// slice only, the K smallest distances of the K fill references (0 .. K-1)
+// and of the slice so far.  Those are K values of the real process's prefix,
+// so their largest is at least the prefix's K-th smallest value, which the
+// real threshold never exceeds (a NaN fill slot only removes a slot from the
+// real process): every reference the real process inserts passes the local
+// threshold, and the local candidates (distance, index) of a slice are a
+// superset of the real insertions.
 // The merge replays MinK over the fill and the slices' candidates in index
 // order; a candidate that is no real insertion fails the replay's test (the
 // replay's state equals the real state at every real insertion), so the
@@ -146,26 +148,30 @@ __global__ __launch_bounds__(256) void knn_hd_slice_kernel(
   };
   constexpr auto dims = std::make_integer_sequence<int, DT / 2>{};
   // the fill: references 0 .. K-1 (K < L2 here)
-  float sd[KC];
+  // the local threshold: the K smallest distances of the fill and of the
+  // slice so far (NaN as +inf), sorted ascending in srt[KC - K .. KC - 1]
+  // behind KC - K entries of -inf, so that srt[KC - 1] is the threshold.
+  // Keeping d (below the threshold) drops the largest: entry s becomes the
+  // median of entries s - 1, s and d, one v_med3 each.
+  float srt[KC];
+#pragma unroll
+  for (int t = 0; t < KC; ++t) srt[t] = t < KC - K ? -Lim<float>::inf() : Lim<float>::inf();
+  auto keep = [&](float d) {
+#pragma unroll
+    for (int t = KC - 1; t > 0; --t) srt[t] = __builtin_amdgcn_fmed3f(srt[t - 1], srt[t], d);
+    srt[0] = fminf(srt[0], d);
+  };
 #pragma unroll
   for (int t = 0; t < KC; ++t) {
     if (t < K) {
       float4 rv[G];
       load_ref(rv, t);
-      sd[t] = hd_dist<NORM>(qr, rv, dims);
-    } else {
-      sd[t] = Lim<float>::inf();
+      const float d = hd_dist<NORM>(qr, rv, dims);
+      if (sl == 0 && act) fd[row * K + t] = d;  // the merge's fill
+      keep(d == d ? d : Lim<float>::inf());
     }
   }
-  if (sl == 0 && act) {  // the merge's fill
-#pragma unroll
-    for (int t = 0; t < KC; ++t)
-      if (t < K) fd[row * K + t] = sd[t];
-  }
-  float thr;
-  int ms;
-  first_max<float, KC>(sd, K, thr, ms);
-  if (!act) thr = -Lim<float>::inf();  // no candidates
+  float thr = act ? srt[KC - 1] : -Lim<float>::inf();  // an idle lane has no candidates
   int count = 0;
   float* __restrict__ cdp = cd + cs * HD_CAP;
   int32_t* __restrict__ cip = ci + cs * HD_CAP;
@@ -209,8 +215,8 @@ __global__ __launch_bounds__(256) void knn_hd_slice_kernel(
           cip[count] = base + u;
         }
         ++count;
-        mink_put<float, KC>(sd, ms, d);
-        first_max<float, KC>(sd, K, thr, ms);
+        keep(d);
+        thr = srt[KC - 1];
       }
     }
   }
