@@ -285,9 +285,9 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
     ix = lane;
   }
   if (L2 > K && hd_lane(v, 0) == hd_lane(v, 0)) {
-    // the fill as the ordered list: lane s moves to its rank
-    int slot = lane;
-    uint64_t key = ((uint64_t)hd_ord(v) << 32) | (uint32_t)(63 - lane);
+    // the fill as the ordered list: lane s moves to its rank.  An entry is
+    // (value, slot << 26 | index) (references fewer than 2^26).
+    const uint64_t key = ((uint64_t)hd_ord(v) << 32) | (uint32_t)(63 - lane);
     int rank = 0;
 #pragma unroll
     for (int t = 0; t < KC; ++t) {
@@ -299,29 +299,20 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
     }
     const int to = 4 * (lane < K ? rank : lane);
     v = __int_as_float(__builtin_amdgcn_ds_permute(to, __float_as_int(v)));
-    ix = __builtin_amdgcn_ds_permute(to, ix);
-    slot = __builtin_amdgcn_ds_permute(to, slot);
-    key = ((uint64_t)hd_ord(v) << 32) | (uint32_t)(63 - slot);
+    int pk = __builtin_amdgcn_ds_permute(to, (lane << 26) | ix);
     float thr = hd_lane(v, K - 1);
+    // (d, j) takes the last entry's slot; the entries after it in the order
+    // (a larger value, or an equal one in a lower slot) move up one lane
     auto insert = [&](float d, int j) {
-      const int sr = hd_lane(slot, K - 1);
-      const uint64_t kn = ((uint64_t)hd_ord(d) << 32) | (uint32_t)(63 - sr);
-      const bool gt = lane < K && key > kn;
-      const bool gtp = hd_shr1(gt ? 1 : 0) != 0;
+      const int sr = hd_lane(pk, K - 1) & ~0x3ffffff;
       const float vp = __int_as_float(hd_shr1(__float_as_int(v)));
-      const int ixp = hd_shr1(ix), slp = hd_shr1(slot);
-      const uint32_t klo = (uint32_t)hd_shr1((int)(uint32_t)key), khi = (uint32_t)hd_shr1((int)(key >> 32));
-      if (gtp) {
-        v = vp;
-        ix = ixp;
-        slot = slp;
-        key = ((uint64_t)khi << 32) | klo;
-      } else if (gt) {
-        v = d;
-        ix = j;
-        slot = sr;
-        key = kn;
-      }
+      const int pp = hd_shr1(pk);
+      // bitwise, not short-circuit: no branches in the wave-wide step
+      const bool in = lane < K;
+      const bool gt = in & ((v > d) | ((v == d) & (pk < sr)));
+      const bool gtp = in & (lane > 0) & ((vp > d) | ((vp == d) & (pp < sr)));
+      v = gtp ? vp : (gt ? d : v);
+      pk = gtp ? pp : (gt ? (sr | j) : pk);
       thr = hd_lane(v, K - 1);
     };
     // one candidate per lane, in index order across the lanes
@@ -352,9 +343,9 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
       }
     }
     // back to slot order: lane s takes slot s
-    const int back = 4 * (lane < K ? slot : lane);
+    const int back = 4 * (lane < K ? (pk >> 26) : lane);
     v = __int_as_float(__builtin_amdgcn_ds_permute(back, __float_as_int(v)));
-    ix = __builtin_amdgcn_ds_permute(back, ix);
+    ix = __builtin_amdgcn_ds_permute(back, pk) & 0x3ffffff;
   }
   const int size = fill;
   const int64_t pad_i = pad_sentinel ? -1 : 0;
@@ -398,12 +389,12 @@ __global__ __launch_bounds__(256) void knn_hd_merge_kernel(
 }
 
 // S slices for the sliced high-D path, or 0 when it does not apply: float,
-// D 64 or 128, 2 <= K <= 32, too few query workgroups to fill the GPU, and
-// slices of at least 1024 references.
+// D 64 or 128, 2 <= K <= 32, at most 2^26 references, too few query
+// workgroups to fill the GPU, and slices of at least 1024 references.
 }  // namespace
 
 int hd_slices(int dtype, int64_t N, int64_t P1, int64_t P2, int64_t D, int64_t K) {
-  if (dtype != TPO_F32 || (D != 64 && D != 128) || K < 2 || K > 32) return 0;
+  if (dtype != TPO_F32 || (D != 64 && D != 128) || K < 2 || K > 32 || P2 > (1 << 26)) return 0;
   const int64_t wgs = N * ((P1 + 255) / 256);
   if (wgs <= 0 || wgs >= 256) return 0;
   int64_t S = 512 / wgs;
