@@ -587,9 +587,12 @@ def profile_run(tpo, torch, reps=5):
     feats, go = (t.to(dev) for t in workloads.gather_c4())
     src = torch.randn(64 << 20, device=dev)  # 256 MiB of float32
     dst = torch.empty_like(src)
+    kidx, kd = torch.ops.torch_point_ops_knn.knn_forward(k1, k2, l1, l2, 2, 16, -1)
+    kg = torch.randn_like(kd)
     for _ in range(reps):
         torch.autograd.grad(tpo.ChamferDistance("mean")(p1, p2), (p1, p2))
         torch.ops.torch_point_ops_knn.knn_forward(k1, k2, l1, l2, 2, 16, -1)
+        torch.ops.torch_point_ops_knn.knn_backward(k1, k2, l1, l2, kidx, 2, kg)
         torch.ops.torch_point_ops_knn.knn_forward(h1, h2, hl1, hl2, 2, 32, -1)
         torch.ops.torch_point_ops_knn.knn_forward(h1f, h2f, hl1, hl2, 2, 32, -1)
         idx = tpo.furthest_point_sampling(pts, 4096)
