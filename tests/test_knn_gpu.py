@@ -15,9 +15,15 @@ def np_(t):
 
 
 def assert_same(got, ref):
+    """Bit for bit (so -0.0 and +0.0 differ); any NaN matches any NaN, since
+    the bits of a NaN the oracle makes on the CPU are the CPU's."""
     got, ref = np.asarray(got), np.asarray(ref)
     assert got.shape == ref.shape and got.dtype == ref.dtype
-    same = (got == ref) | (np.isnan(got) & np.isnan(ref)) if got.dtype.kind == "f" else got == ref
+    if got.dtype.kind == "f":
+        u = np.dtype(f"u{got.dtype.itemsize}")
+        same = (got.view(u) == ref.view(u)) | (np.isnan(got) & np.isnan(ref))
+    else:
+        same = got == ref
     assert same.all(), f"{np.sum(~same)} of {got.size} differ"
 
 
@@ -93,12 +99,30 @@ def _hd_inputs(case, g, D):
         r = p2.norm(dim=-1)
         p2 = torch.gather(p2, 1, r.argsort(dim=1, descending=True)[..., None].expand(-1, -1, D))
         p1 = p1 * 1e-3
+    if case == "nonfinite":
+        p2[0, 0, 5] = float("nan")       # fill slot 0: the threshold is NaN, nothing is inserted
+        p2[1, 3, 0] = float("nan")       # another fill slot: never the maximum
+        p2[1, 4, 7] = float("inf")       # an infinite fill distance: evicted first
+        p2[0, 8000:8010, 1] = float("nan")
+        p2[1, 5000, 2] = float("inf")
+        p2[1, 12345, 9] = -float("inf")
+        p1[1, 7, 0] = float("nan")       # a NaN query: every distance NaN
+        p1[0, 9, 3] = float("inf")
+    if case == "duplicates":
+        # exact copies of queries among the references: distance 0 (-0.0 under
+        # norm 1), in the fill and repeated across slices, so equal values
+        # meet in the merge's order and its first-maximum slot rule
+        for n in range(N):
+            for q in range(0, 40, 3):
+                for j in (q % 7, 100 + 37 * q, 5000 + 91 * q, 15000 + 11 * q):
+                    p2[n, j] = p1[n, q]
     l1 = torch.tensor([P1, 211])
     l2 = torch.tensor([P2, 9000]) if case != "short" else torch.tensor([P2, 20])
     return p1, p2, l1, l2
 
 
-@pytest.mark.parametrize("case", ["random", "lattice", "descending", "short"])
+@pytest.mark.parametrize("case", ["random", "lattice", "descending", "short", "nonfinite",
+                                  "duplicates"])
 @pytest.mark.parametrize("D,K,norm", [(128, 32, 2), (128, 9, 1), (64, 16, 2)])
 def test_high_d_sliced_forward_bit_exact(tpo, O, dev, case, D, K, norm):
     g = torch.Generator().manual_seed(D + K + norm + len(case))
@@ -111,7 +135,8 @@ def test_high_d_sliced_forward_bit_exact(tpo, O, dev, case, D, K, norm):
     a, b, la, lb = p1.to(dev), p2.to(dev), l1.to(dev), l2.to(dev)
     si, sd = tpo.knn_points(a, b, la, lb, norm=norm, K=K)
     wi, wd = _module_sort(torch.from_numpy(ei).to(dev), torch.from_numpy(ed).to(dev), lb, K)
-    assert torch.equal(si, wi) and torch.equal(sd, wd)
+    assert_same(np_(si), np_(wi))
+    assert_same(np_(sd), np_(wd))
 
 
 def _long_cloud_inputs(case, g):

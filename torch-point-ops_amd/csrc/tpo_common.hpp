@@ -62,7 +62,9 @@ __device__ __forceinline__ half_t knn_acc2(half_t acc, half_t d, bool first) {
 template <typename T>
 __device__ __forceinline__ T knn_acc1(T acc, T d, bool first) {
   T a = d > (T)0 ? d : (T)(-d);
-  return first ? a : (T)(acc + a);
+  // the sum starts at +0 (knn.cu:149): for d = +0 the first term is
+  // 0 + (-0) = +0, so equal points are at +0, never -0
+  return first ? (T)((T)0 + a) : (T)(acc + a);
 }
 
 // ------------------------------------------------------------ launch helpers
