@@ -86,10 +86,14 @@ def test_gather_vs_oracle(tpo, O, dev, dtype):
     ref = O.gather_bwd(np_(go), np_(idx), 777, accum_f64=True)
     tol = 1e-2 if dtype == torch.float16 else 1e-6
     assert np.abs(np_(gp).astype(np.float64) - ref).max() <= tol * np.abs(ref).max()
-    # unique indices: every value is exactly 0 + g
+    # unique indices: every value is exactly 0 + g, bit for bit (a gradient
+    # of -0.0 lands as +0.0, as the reference's atomicAdd into zeros leaves it)
     uidx = torch.stack([torch.randperm(777, generator=g)[:130] for _ in range(3)])
+    go[:, :, ::7] = -0.0
     gp = torch.ops.torch_point_ops_fps.gather_points_backward(go.to(dev), uidx.to(dev), 777)
-    assert np.array_equal(np_(gp), O.gather_bwd(np_(go), np_(uidx), 777))
+    want = O.gather_bwd(np_(go), np_(uidx), 777)
+    u = np.dtype(f"u{want.dtype.itemsize}")
+    assert np.array_equal(np_(gp).view(u), want.view(u))
 
 
 def test_gather_config4(tpo, O, dev):
