@@ -553,6 +553,96 @@ def cpu_gather(O, np, idx, threads):
                        f"backward, fps.cpp restated, one thread")
 
 
+def ref_cpu_child():
+    """Child process (bench.py --ref-cpu-child): times the reference's own CPU
+    kernels, compiled from knn.cpp and fps.cpp into oracle/_ref/ (where the
+    reference checkout was present at build time), on the same samples as the
+    restated baselines, and prints one JSON line.  They register the product's
+    torch.library namespaces, so this process imports nothing else of the
+    repository; the reference runs them single-threaded (no parallel loops),
+    and so does this process (one intra-op thread)."""
+    import torch
+
+    import workloads
+
+    ref = os.path.join(REPO, "oracle", "_ref")
+    libs = [os.path.join(ref, f) for f in ("knn_ref.so", "fps_ref.so")]
+    if not all(os.path.exists(f) for f in libs):
+        print(json.dumps({"missing": "oracle/_ref not built"}), flush=True)
+        return
+    for f in libs:
+        torch.ops.load_library(f)
+    torch.set_num_threads(1)
+    res = {}
+    # knn_forward (knn.cpp:30-99): the first 16 queries of every config-3 cloud
+    p1, p2, l1, l2 = workloads.knn_c3()
+    q = 16
+    a = p1[:, :q].contiguous()
+    ln1 = torch.clamp(l1, max=q)
+    t0 = time.perf_counter()
+    idx, _ = torch.ops.torch_point_ops_knn.knn_forward(a, p2, ln1, l2, 2, 16, -1)
+    sec = time.perf_counter() - t0
+    pairs = float((ln1 * l2).sum())
+    res["knn_c3"] = dict(value=pairs / sec / 1e9, unit="G pair-dists/s", cores=1, kind="reference",
+                         sample=f"{q} queries per cloud x 8 clouds of config 3, the reference's "
+                                f"knn.cpp forward (oracle/_ref), one thread")
+    # knn_backward (knn.cpp:104-164): the first 256 query rows
+    q = 256
+    a = p1[:, :q].contiguous()
+    ln1 = torch.clamp(l1, max=q)
+    idx, d = torch.ops.torch_point_ops_knn.knn_forward(a, p2, ln1, l2, 2, 16, -1)
+    g = torch.rand(d.shape, generator=torch.Generator().manual_seed(0))
+    t0 = time.perf_counter()
+    torch.ops.torch_point_ops_knn.knn_backward(a, p2, ln1, l2, idx, 2, g)
+    sec = time.perf_counter() - t0
+    res["knn_c3_backward"] = dict(value=float(ln1.sum()) * 16 / sec / 1e9, unit="G neighbour-slots/s",
+                                  cores=1, kind="reference",
+                                  sample=f"{q} query rows per cloud x 8 clouds of config 3, K=16, the "
+                                         f"reference's knn.cpp backward (oracle/_ref), one thread")
+    # fps_forward (fps.cpp:18-88): 2 clouds of config 4, the first 512 samples
+    pts = workloads.fps_c4()
+    nc, m = 2, 512
+    t0 = time.perf_counter()
+    fidx = torch.ops.torch_point_ops_fps.fps_forward(pts[:nc].contiguous(), m)
+    sec = time.perf_counter() - t0
+    res["fps_c4"] = dict(value=nc * pts.shape[1] * (m - 1) / sec / 1e9, unit="G point-updates/s",
+                         cores=1, kind="reference",
+                         sample=f"{nc} clouds of config 4, first {m} samples, the reference's "
+                                f"fps.cpp (oracle/_ref), one thread")
+    # gather_points forward and backward (fps.cpp:91-141): 2 clouds of config 4
+    feats, go = workloads.gather_c4()
+    full = torch.ops.torch_point_ops_fps.fps_forward(pts[:nc].contiguous(), 4096)
+    f, gg = feats[:nc].contiguous(), go[:nc].contiguous()
+    t0 = time.perf_counter()
+    torch.ops.torch_point_ops_fps.gather_points_forward(f, full)
+    t1 = time.perf_counter()
+    torch.ops.torch_point_ops_fps.gather_points_backward(gg, full, f.shape[2])
+    t2 = time.perf_counter()
+    B, C, N = f.shape
+    M = full.shape[1]
+    res["gather_c4"] = dict(value=round((B * M * 8 + 2 * B * C * M * 4) / (t1 - t0) / 1e9, 3),
+                            unit="GB/s (forward)",
+                            bwd_GBs=round((B * C * N * 4 + B * C * M * 4 + B * M * 8) / (t2 - t1) / 1e9, 3),
+                            cores=1, kind="reference",
+                            sample=f"{nc} of 16 clouds of config 4 (C=64, 65536 -> 4096), the "
+                                   f"reference's fps.cpp gather forward and backward (oracle/_ref), "
+                                   f"one thread")
+    del fidx
+    print(json.dumps(res), flush=True)
+
+
+def cpu_reference_kernels():
+    """The reference's own CPU kernels, timed in a child process (they cannot
+    share a process with the product's operators)."""
+    import subprocess
+
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--ref-cpu-child"],
+                       capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return {"error": (r.stderr or "")[-300:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def cpu_emd(O, threads):
     """The oracle's restatement of emd.cu's approxmatch + matchcost (the
     reference has no CPU kernel), one cloud per thread."""
@@ -626,9 +716,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-run", action="store_true",
                     help="run the fixed kernel sequence for rocprofv3 and exit")
+    ap.add_argument("--ref-cpu-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--profile-emd", action="store_true",
                     help="run EMD forward + backward (B=16, N=M=2048) for rocprofv3 and exit")
     args = ap.parse_args()
+    if args.ref_cpu_child:
+        ref_cpu_child()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs on a single MI355X "
               "(the sharding design is described in DESIGN.md); use --gpus 1", file=sys.stderr)
@@ -817,6 +911,14 @@ def main():
             sec["gather_c4"]["cpu_baseline"] = cpu_gather(O, np, fp["idx"], threads)
             sec["knn_c5_bf16"]["cpu_baseline"] = cpu_knn_c5(O, np, threads)
             sec["knn_c5_bf16"]["cpu_baseline_torch"] = cpu_knn_c5_torch(torch, threads)
+            ref = cpu_reference_kernels()
+            if "knn_c3" in ref:
+                sec["knn_c3"]["cpu_baseline_reference"] = ref["knn_c3"]
+                sec["knn_c3"]["cpu_baseline_reference_backward"] = ref["knn_c3_backward"]
+                sec["fps_c4"]["cpu_baseline_reference"] = ref["fps_c4"]
+                sec["gather_c4"]["cpu_baseline_reference"] = ref["gather_c4"]
+            else:
+                sec["cpu_baseline_reference_unavailable"] = ref
     if sec:
         out["secondary"] = sec
     out["host"] = {"cpu": cpu_model(), "cores": threads,
