@@ -88,17 +88,21 @@ __global__ __launch_bounds__(256) void gather_bwd_dense_kernel(const T* __restri
     const bool hit = p != 0x7fffffff;
     const T* __restrict__ src = go + b * C * M + (hit ? p : 0);
     T* __restrict__ dst = gp + b * C * N + n;
-    // 0 + g, as the reference's atomicAdd into zeros gives (+0 for g = -0)
+    // 0 + g, as the reference's atomicAdd into zeros gives (+0 for g = -0).
+    // The empty asm keeps the adds after all four (conditional) loads: left
+    // alone, the compiler moves each add into its load's branch, where it
+    // waits for that load before the next one is issued.
     int64_t c = 0;
     for (; c + 4 <= C; c += 4) {
-      T v0 = hit ? (T)((T)0 + src[(c + 0) * M]) : (T)0;
-      T v1 = hit ? (T)((T)0 + src[(c + 1) * M]) : (T)0;
-      T v2 = hit ? (T)((T)0 + src[(c + 2) * M]) : (T)0;
-      T v3 = hit ? (T)((T)0 + src[(c + 3) * M]) : (T)0;
-      dst[(c + 0) * N] = v0;
-      dst[(c + 1) * N] = v1;
-      dst[(c + 2) * N] = v2;
-      dst[(c + 3) * N] = v3;
+      T v0 = hit ? src[(c + 0) * M] : (T)0;
+      T v1 = hit ? src[(c + 1) * M] : (T)0;
+      T v2 = hit ? src[(c + 2) * M] : (T)0;
+      T v3 = hit ? src[(c + 3) * M] : (T)0;
+      asm volatile("" : "+v"(v0), "+v"(v1), "+v"(v2), "+v"(v3));
+      dst[(c + 0) * N] = (T)((T)0 + v0);
+      dst[(c + 1) * N] = (T)((T)0 + v1);
+      dst[(c + 2) * N] = (T)((T)0 + v2);
+      dst[(c + 3) * N] = (T)((T)0 + v3);
     }
     for (; c < C; ++c) dst[c * N] = hit ? (T)((T)0 + src[c * M]) : (T)0;
   }
