@@ -31,6 +31,9 @@
 //     their last level's exp(0 * d) is 0 * d + 1 exactly;
 //   * pass 3 of level j and pass 1 of level j-1 need the same inputs, so they
 //     share one sweep (two exponentials per pair): 21 dependent sweeps;
+//     levels j and j-1 differ by a factor 4, so in float32 both exponentials
+//     share one argument reduction (4x splits exactly as 4h + 4l): one more
+//     exp2 and fma give exp(4x) bit for bit;
 //   * match is not accumulated in HBM level by level: the per-level ratioL
 //     and ratioR are kept, and one final pass forms
 //     match[l][k] = sum_j e_j(k,l) * ratioL_j[k] * ratioR_j[l] in level order
@@ -89,6 +92,22 @@ __device__ __forceinline__ float emd_exp(float x) {
   return __builtin_fmaf(r, l * 0.693147180559945309f, r);
 }
 __device__ __forceinline__ double emd_exp(double x) { return exp(x); }
+// emd_exp(x) and emd_exp(4x) from one reduction: scaling by 4 is exact, so
+// 4x splits as 4h + 4l and the second value takes one more exp2 and fma, bit
+// for bit what emd_exp(4x) returns (for 4x below -150, where that clamps,
+// exp2(4h) is +0 as well).
+__device__ __forceinline__ void emd_exp_x4(float x, float& e1, float& e4) {
+  x = x < -150.f ? -150.f : x;
+  constexpr float L1 = 1.44269502162933349609375f;
+  constexpr float L2 = 1.925962989e-8f;
+  const float h = x * L1;
+  const float l = __builtin_fmaf(x, L2, __builtin_fmaf(x, L1, -h));
+  const float t = l * 0.693147180559945309f;
+  const float r = __builtin_amdgcn_exp2f(h);
+  const float r4 = __builtin_amdgcn_exp2f(4.f * h);
+  e1 = __builtin_fmaf(r, t, r);
+  e4 = __builtin_fmaf(r4, 4.f * t, r4);
+}
 template <typename T, typename V>
 __device__ __forceinline__ V emd_e(V level, V d) {
   // the last level: exp(0 * d) = 1 for finite d, NaN otherwise, = 0 * d + 1
@@ -329,6 +348,11 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
   __shared__ EmdPt<V> s_pt[NW][C];  // (x, y, z, wa)
   __shared__ V s_wb[NS == 2 ? NW : 1][C];
   const V zb = emd_zero_below<T, V>();
+  // float32, two levels a factor 4 apart (every fused sweep but the last):
+  // both exponentials come from one argument reduction (emd_exp_x4).
+  // float16 clamps each argument at -20, which breaks the scaling; float64
+  // keeps its library exp.
+  const bool pow4 = std::is_same<T, float>::value && NS == 2 && lb != (V)0 && la == (V)4 * lb;
   const EmdPt<V>* op = (const EmdPt<V>*)other;
   EmdPt<V> nr;
   V nb = (V)0;
@@ -355,6 +379,28 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
       d[u] = sq3(pt[u].x - x, pt[u].y - y, pt[u].z - z);
       nza |= !(la * d[u] < zb);  // NaN counts as non-zero
       if constexpr (NS == 2) nzb |= !(lb * d[u] < zb);
+    }
+    if constexpr (NS == 2 && std::is_same<T, float>::value) {
+      if (pow4) {
+        // la = 4 lb < 0, so la d <= lb d: a batch whose lb terms all vanish
+        // has vanishing la terms too, and both exponentials share one
+        // reduction (the same values as two emd_e calls)
+        if (__builtin_amdgcn_ballot_w64(nzb) != 0) {
+          if (__builtin_amdgcn_ballot_w64(nza) != 0) {
+#pragma unroll
+            for (int u = 0; u < UB; ++u) {
+              V e1, e4;
+              emd_exp_x4(lb * d[u], e1, e4);
+              sb = emd_fma(e1, pb[u], sb);
+              sa = emd_fma(e4, pt[u].w, sa);
+            }
+          } else {
+#pragma unroll
+            for (int u = 0; u < UB; ++u) sb = emd_fma(emd_e<T>(lb, d[u]), pb[u], sb);
+          }
+        }
+        return;
+      }
     }
     if (std::is_same<T, half_t>::value || __builtin_amdgcn_ballot_w64(nza) != 0) {
 #pragma unroll
@@ -495,11 +541,31 @@ __global__ __launch_bounds__(EMD_THREADS) void emd_match_kernel(
   for (int l = l0; l < l1; ++l) {
     const V d = sq3(q[4 * l] - x, q[4 * l + 1] - y, q[4 * l + 2] - z);
     V mt = (V)0;
+    auto add = [&](int t, V e) {
+      const V w = (e * r[t]) * rrb[t * m + l];  // emd.cu:170
+      mt = emd_st<T, V>(mt + emd_st<T, V>(w));  // emd.cu:171
+    };
+    if constexpr (std::is_same<T, float>::value) {
+      // levels 2i and 2i+1 (a factor 4 apart) share one argument reduction;
+      // the additions stay in level order.  When only the steeper level
+      // vanishes in every lane its terms are exactly +0 and leave mt as is.
 #pragma unroll
-    for (int t = 0; t < EMD_LEVELS; ++t) {
-      if (emd_wave_zero<T>(emd_level<V>(t), d)) continue;  // w = +0: mt + 0 == mt
-      const V w = (emd_e<T>(emd_level<V>(t), d) * r[t]) * rrb[t * m + l];  // emd.cu:170
-      mt = emd_st<T, V>(mt + emd_st<T, V>(w));                             // emd.cu:171
+      for (int t = 0; t < EMD_LEVELS - 2; t += 2) {
+        if (emd_wave_zero<T>(emd_level<V>(t + 1), d)) continue;  // both levels vanish
+        V e1, e4;
+        emd_exp_x4(emd_level<V>(t + 1) * d, e1, e4);
+        add(t, e4);
+        add(t + 1, e1);
+      }
+#pragma unroll
+      for (int t = EMD_LEVELS - 2; t < EMD_LEVELS; ++t)
+        if (!emd_wave_zero<T>(emd_level<V>(t), d)) add(t, emd_e<T>(emd_level<V>(t), d));
+    } else {
+#pragma unroll
+      for (int t = 0; t < EMD_LEVELS; ++t) {
+        if (emd_wave_zero<T>(emd_level<V>(t), d)) continue;  // w = +0: mt + 0 == mt
+        add(t, emd_e<T>(emd_level<V>(t), d));
+      }
     }
     if (own) match[(b * m + l) * (int64_t)n + k] = (T)mt;
     cs = emd_fma(d, mt, cs);  // emd.cu:212-213
