@@ -96,6 +96,31 @@ def test_gather_vs_oracle(tpo, O, dev, dtype):
     assert np.array_equal(np_(gp).view(u), want.view(u))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
+@pytest.mark.parametrize("C,N,M", [(1, 3000, 900), (3, 5000, 2000), (5, 9001, 4100),
+                                   (64, 4000, 300), (2, 40000, 20000)])
+def test_gather_backward_paths(tpo, O, dev, dtype, C, N, M):
+    """The backward's channel blocks of 1 to 16 rows staged in LDS (the parts
+    of one block split the positions), and rows too long for LDS (M = 20000:
+    the dense pass), with repeated indices (added by atomics) and without
+    (bit for bit, -0 gradients landing as +0)."""
+    g = torch.Generator().manual_seed(C * 7 + M)
+    B = 2
+    go = torch.randn(B, C, M, generator=g).to(dtype)
+    idx = torch.randint(0, N, (B, M), generator=g)
+    idx[:, 1::5] = idx[:, 0::5][:, : idx[:, 1::5].shape[1]]  # every fifth sample repeats
+    gp = torch.ops.torch_point_ops_fps.gather_points_backward(go.to(dev), idx.to(dev), N)
+    ref = O.gather_bwd(np_(go), np_(idx), N, accum_f64=True)
+    tol = 1e-2 if dtype == torch.float16 else 1e-6
+    assert np.abs(np_(gp).astype(np.float64) - ref).max() <= tol * np.abs(ref).max()
+    uidx = torch.stack([torch.randperm(N, generator=g)[:M] for _ in range(B)])
+    go[:, :, ::7] = -0.0
+    gp = torch.ops.torch_point_ops_fps.gather_points_backward(go.to(dev), uidx.to(dev), N)
+    want = O.gather_bwd(np_(go), np_(uidx), N)
+    u = np.dtype(f"u{want.dtype.itemsize}")
+    assert np.array_equal(np_(gp).view(u), want.view(u))
+
+
 def test_gather_config4(tpo, O, dev):
     pts = workloads.fps_c4()
     idx = tpo.furthest_point_sampling(pts.to(dev), 4096)
