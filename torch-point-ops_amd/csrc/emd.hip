@@ -21,7 +21,7 @@
 // Design for MI355X (the reference runs one 512-thread block per cloud):
 //   * each pass is a grid-wide sweep: a 512-thread workgroup owns 64 points
 //     (one per lane) and its eight waves each sum over an eighth of the other
-//     cloud, read with wave-uniform (scalar) loads, combined in fixed order;
+//     cloud, staged through LDS, combined in fixed order;
 //   * exponentials that are +0 in all 64 lanes (arguments below the float
 //     or double underflow, the steep levels on distant points) are skipped
 //     with a wave-uniform branch, which changes no sum; each cloud's points
@@ -39,6 +39,8 @@
 //     match[l][k] = sum_j e_j(k,l) * ratioL_j[k] * ratioR_j[l] in level order
 //     (each addition rounded as the reference's +=), writes it once and fuses
 //     matchcost's sum of d * match into the same pass;
+//   * the backward reads match once: a tile's column sums (grad_xyz1) stay
+//     in registers and its row sums (grad_xyz2) are reduced across the wave;
 //   * every sum has a fixed order, so results are deterministic.
 // The summation orders differ from the reference's sequential loops and the
 // exponential is ROCm's, so parity is to a tolerance, not bit-exact.
@@ -148,16 +150,34 @@ __device__ __forceinline__ V wave_sum(V v) {
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// The wave's sum in lane 63 (float; the other lanes hold partial sums), by
+// DPP adds in a fixed order: pairs, quads, 8 (half-row mirror), 16 (row
+// mirror), then rows 0+1 and 2+3 (row_bcast:15) and all four (row_bcast:31).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWMASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_total63(float v) {
+  v = dpp_add<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_add<0x140, 0xf>(v);  // row_mirror
+  v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+  v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+__device__ __forceinline__ double wave_total63(double v) { return wave_sum(v); }
 
 // Workspace, array-major over the clouds (opmath values):
 //   p1[B][n][4], p2[B][m][4]   coordinates (x, y, z, 0)
 //   reml[B][n], remr[B][m]     remaining mass
 //   rl[B][10][n], rr[B][10][m] ratioL / ratioR of every level
 //   cost[B][gy][gx]            matchcost partials of the final pass
-//   g1[B][nchunk][n][3]        grad_xyz1 partials of the backward
+//   g1[B][nchunk][n][3]        grad_xyz1 partials of the backward (per row tile)
+//   g2[B][gx][m][3]            grad_xyz2 partials of the backward (per column tile)
 //   ord1[B][n], ord2[B][m]     int32: each cloud's points in Morton order
 struct EmdLayout {
-  int64_t p1, p2, reml, remr, rl, rr, cost, g1, ord1, ord2, total;
+  int64_t p1, p2, reml, remr, rl, rr, cost, g1, g2, ord1, ord2, total;
   int gx, gy, nchunk;
 };
 template <typename V>
@@ -177,6 +197,7 @@ inline EmdLayout emd_layout(int64_t B, int64_t n, int64_t m) {
   L.rr = o; o += al(B * EMD_LEVELS * m * s);
   L.cost = o; o += al(B * (int64_t)L.gx * L.gy * s);
   L.g1 = o; o += al(B * (int64_t)L.nchunk * n * 3 * s);
+  L.g2 = o; o += al(B * (int64_t)L.gx * m * 3 * s);
   L.ord1 = o; o += al(B * n * 4);
   L.ord2 = o; o += al(B * m * 4);
   L.total = o;
@@ -603,83 +624,129 @@ __global__ void emd_zero_kernel(T* __restrict__ p, int64_t count) {
 
 // ---------------------------------------------------------------- backward
 
-// grad_xyz2[l] = grad_cost * sum_k (p2_l - p1_k) * 2 match[l][k]
-// (emd.cu:261-303): one wave per row of match.
+// Both gradients' partials in one pass over match (emd.cu:234-303):
+//   grad_xyz1[k] = grad_cost * sum_l (p1_k - p2_l) * 2 match[l][k]
+//   grad_xyz2[l] = grad_cost * sum_k (p2_l - p1_k) * 2 match[l][k]
+// Workgroup (column tile of 4 * 64 columns, row tile of EMD_G1_ROWS rows,
+// cloud): lane j of every wave holds columns 4j .. 4j + 3 of the tile (one
+// 4-wide load a row), and wave w takes rows w, w + 4, ... of the row tile.
+// A column's sum over the wave's rows stays in registers, the waves' sums
+// added in wave order at the end (grad_xyz1 partials per row tile); a row's
+// sum over the tile's columns is reduced across the wave (grad_xyz2 partials
+// per column tile).  Every sum has a fixed order.
+constexpr int EMD_GT_COLS = 256;
 template <typename T>
-__global__ __launch_bounds__(EMD_THREADS) void emd_grad2_kernel(
-    const T* __restrict__ grad_cost, const T* __restrict__ xyz1, const T* __restrict__ xyz2,
-    const T* __restrict__ match, int n, int m, T* __restrict__ grad2) {
-  typedef typename EmdV<T>::type V;
-  const int64_t b = blockIdx.y;
-  const int l = blockIdx.x * (EMD_THREADS / 64) + wave_id();
-  if (l >= m) return;
-  const V x2 = (V)xyz2[(b * m + l) * 3], y2 = (V)xyz2[(b * m + l) * 3 + 1],
-          z2 = (V)xyz2[(b * m + l) * 3 + 2];
-  const T* row = match + (b * m + l) * (int64_t)n;
-  const T* p = xyz1 + b * n * 3;
-  V ax = (V)0, ay = (V)0, az = (V)0;
-  for (int k = lane_id(); k < n; k += 64) {
-    const V d = (V)row[k] * (V)2;
-    ax = emd_fma(x2 - (V)p[3 * k], d, ax);
-    ay = emd_fma(y2 - (V)p[3 * k + 1], d, ay);
-    az = emd_fma(z2 - (V)p[3 * k + 2], d, az);
-  }
-  ax = wave_sum(ax);
-  ay = wave_sum(ay);
-  az = wave_sum(az);
-  if (lane_id() == 0) {
-    const V g = (V)grad_cost[b];
-    grad2[(b * m + l) * 3] = (T)(ax * g);
-    grad2[(b * m + l) * 3 + 1] = (T)(ay * g);
-    grad2[(b * m + l) * 3 + 2] = (T)(az * g);
-  }
-}
-
-// grad_xyz1 partials over EMD_G1_ROWS rows of match (emd.cu:234-257).
-template <typename T>
-__global__ __launch_bounds__(EMD_THREADS) void emd_grad1_part_kernel(
+__global__ __launch_bounds__(EMD_THREADS) void emd_grad_part_kernel(
     const T* __restrict__ xyz1, const T* __restrict__ xyz2, const T* __restrict__ match, int n,
-    int m, typename EmdV<T>::type* __restrict__ part) {
+    int m, bool vec, typename EmdV<T>::type* __restrict__ part1,
+    typename EmdV<T>::type* __restrict__ part2) {
   typedef typename EmdV<T>::type V;
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  constexpr int NW = EMD_THREADS / 64;
+  __shared__ V s_col[NW - 1][EMD_GT_COLS][3];
   const int64_t b = blockIdx.z;
-  const int k = blockIdx.x * EMD_THREADS + threadIdx.x;
-  if (k >= n) return;
-  const V x1 = (V)xyz1[(b * n + k) * 3], y1 = (V)xyz1[(b * n + k) * 3 + 1],
-          z1 = (V)xyz1[(b * n + k) * 3 + 2];
+  const int w = wave_id(), lane = lane_id();
+  const int k0 = blockIdx.x * EMD_GT_COLS + 4 * lane;
   const int l0 = blockIdx.y * EMD_G1_ROWS, l1 = min(m, l0 + EMD_G1_ROWS);
-  const T* q = xyz2 + b * m * 3;
-  V ax = (V)0, ay = (V)0, az = (V)0;
-#pragma unroll 4
-  for (int l = l0; l < l1; ++l) {
-    const V d = (V)match[(b * m + l) * (int64_t)n + k] * (V)2;
-    ax = emd_fma(x1 - (V)q[3 * l], d, ax);
-    ay = emd_fma(y1 - (V)q[3 * l + 1], d, ay);
-    az = emd_fma(z1 - (V)q[3 * l + 2], d, az);
+  V x1[4], y1[4], z1[4];
+  bool okc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    okc[q] = k0 + q < n;
+    const int64_t kk = b * n + (okc[q] ? k0 + q : n - 1);
+    x1[q] = (V)xyz1[kk * 3];
+    y1[q] = (V)xyz1[kk * 3 + 1];
+    z1[q] = (V)xyz1[kk * 3 + 2];
   }
-  V* o = part + ((b * gridDim.y + blockIdx.y) * n + k) * 3;
-  o[0] = ax;
-  o[1] = ay;
-  o[2] = az;
+  V ax[4] = {}, ay[4] = {}, az[4] = {};
+  for (int l = l0 + w; l < l1; l += NW) {
+    const T* __restrict__ row = match + (b * m + l) * (int64_t)n;
+    V d[4];
+    if (vec) {  // n % 4 == 0 and match aligned: the 4 columns are all in or all out
+      const T4 v = okc[0] ? *reinterpret_cast<const T4*>(row + k0) : T4{};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) d[q] = (V)v[q] * (V)2;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) d[q] = okc[q] ? (V)row[k0 + q] * (V)2 : (V)0;
+    }
+    const V x2 = (V)xyz2[(b * m + l) * 3], y2 = (V)xyz2[(b * m + l) * 3 + 1],
+            z2 = (V)xyz2[(b * m + l) * 3 + 2];
+    V rx = (V)0, ry = (V)0, rz = (V)0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (!okc[q]) continue;
+      const V dx = x1[q] - x2, dy = y1[q] - y2, dz = z1[q] - z2;
+      ax[q] = emd_fma(dx, d[q], ax[q]);
+      ay[q] = emd_fma(dy, d[q], ay[q]);
+      az[q] = emd_fma(dz, d[q], az[q]);
+      rx = emd_fma(-dx, d[q], rx);
+      ry = emd_fma(-dy, d[q], ry);
+      rz = emd_fma(-dz, d[q], rz);
+    }
+    rx = wave_total63(rx);
+    ry = wave_total63(ry);
+    rz = wave_total63(rz);
+    if (lane == 63) {
+      V* __restrict__ o = part2 + ((b * gridDim.x + blockIdx.x) * m + l) * 3;
+      o[0] = rx;
+      o[1] = ry;
+      o[2] = rz;
+    }
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      s_col[w - 1][4 * lane + q][0] = ax[q];
+      s_col[w - 1][4 * lane + q][1] = ay[q];
+      s_col[w - 1][4 * lane + q][2] = az[q];
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (!okc[q]) continue;
+#pragma unroll
+      for (int v = 0; v < NW - 1; ++v) {
+        ax[q] += s_col[v][4 * lane + q][0];
+        ay[q] += s_col[v][4 * lane + q][1];
+        az[q] += s_col[v][4 * lane + q][2];
+      }
+      V* __restrict__ o = part1 + ((b * gridDim.y + blockIdx.y) * n + k0 + q) * 3;
+      o[0] = ax[q];
+      o[1] = ay[q];
+      o[2] = az[q];
+    }
+  }
 }
 
+// grad_xyz1 (blockIdx.z = 0: n points, nchunk row-tile partials) and
+// grad_xyz2 (blockIdx.z = 1: m points, ncol column-tile partials):
+// grad_cost[b] times the sum of the partials, added in order
 template <typename T>
-__global__ __launch_bounds__(EMD_THREADS) void emd_grad1_final_kernel(
-    const T* __restrict__ grad_cost, const typename EmdV<T>::type* __restrict__ part, int n,
-    int nchunk, T* __restrict__ grad1) {
+__global__ __launch_bounds__(EMD_THREADS) void emd_grad_final_kernel(
+    const T* __restrict__ grad_cost, const typename EmdV<T>::type* __restrict__ part1,
+    const typename EmdV<T>::type* __restrict__ part2, int n, int m, int nchunk, int ncol,
+    T* __restrict__ grad1, T* __restrict__ grad2) {
   typedef typename EmdV<T>::type V;
   const int64_t b = blockIdx.y;
+  const bool second = blockIdx.z != 0;
+  const int cnt = second ? m : n, parts = second ? ncol : nchunk;
+  const V* __restrict__ part = second ? part2 : part1;
+  T* __restrict__ grad = second ? grad2 : grad1;
   const int k = blockIdx.x * EMD_THREADS + threadIdx.x;
-  if (k >= n) return;
+  if (k >= cnt) return;
   V a[3] = {(V)0, (V)0, (V)0};
-  for (int c = 0; c < nchunk; ++c) {
-    const V* o = part + ((b * nchunk + c) * n + k) * 3;
+  for (int c = 0; c < parts; ++c) {
+    const V* o = part + ((b * parts + c) * cnt + k) * 3;
     a[0] += o[0];
     a[1] += o[1];
     a[2] += o[2];
   }
   const V g = (V)grad_cost[b];
 #pragma unroll
-  for (int c = 0; c < 3; ++c) grad1[(b * n + k) * 3 + c] = (T)(a[c] * g);
+  for (int c = 0; c < 3; ++c) grad[(b * cnt + k) * 3 + c] = (T)(a[c] * g);
 }
 
 // ---------------------------------------------------------------- host side
@@ -736,17 +803,18 @@ int emd_bwd_impl(const void* grad_cost, const void* xyz1, const void* xyz2, cons
                  hipStream_t s) {
   typedef typename EmdV<T>::type V;
   const EmdLayout L = emd_layout<V>(B, n, m);
-  V* part = (V*)(ws + L.g1);
+  V* part1 = (V*)(ws + L.g1);
+  V* part2 = (V*)(ws + L.g2);
   const int nn = (int)n, mm = (int)m;
   const unsigned bb = (unsigned)B;
-  hipLaunchKernelGGL(emd_grad2_kernel<T>, dim3((unsigned)((m + 3) / 4), bb), dim3(EMD_THREADS), 0,
-                     s, (const T*)grad_cost, (const T*)xyz1, (const T*)xyz2, (const T*)match, nn, mm,
-                     (T*)grad2);
-  hipLaunchKernelGGL(emd_grad1_part_kernel<T>, dim3((unsigned)L.gx, (unsigned)L.nchunk, bb),
+  const bool vec = (n % 4) == 0 && (reinterpret_cast<uintptr_t>(match) % (4 * sizeof(T))) == 0;
+  hipLaunchKernelGGL(emd_grad_part_kernel<T>, dim3((unsigned)L.gx, (unsigned)L.nchunk, bb),
                      dim3(EMD_THREADS), 0, s, (const T*)xyz1, (const T*)xyz2, (const T*)match, nn,
-                     mm, part);
-  hipLaunchKernelGGL(emd_grad1_final_kernel<T>, dim3((unsigned)L.gx, bb), dim3(EMD_THREADS), 0, s,
-                     (const T*)grad_cost, part, nn, L.nchunk, (T*)grad1);
+                     mm, vec, part1, part2);
+  hipLaunchKernelGGL(emd_grad_final_kernel<T>,
+                     dim3((unsigned)((std::max(n, m) + EMD_THREADS - 1) / EMD_THREADS), bb, 2),
+                     dim3(EMD_THREADS), 0, s, (const T*)grad_cost, part1, part2, nn, mm, L.nchunk,
+                     L.gx, (T*)grad1, (T*)grad2);
   return check_launch("tpo_emd_bwd");
 }
 
