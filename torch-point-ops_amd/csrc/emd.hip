@@ -128,13 +128,21 @@ template <typename T, typename V>
 __device__ __forceinline__ V emd_zero_below() {
   return std::is_same<T, double>::value ? (V)-760 : (V)-120;
 }
+// A distance above this makes exp(level * d) exactly +0 (level < 0):
+// level * d is then below zb within a few ulps, far inside the margin between
+// zb and the underflow point; never for level 0.  Testing d against it saves
+// the product level * d.
+template <typename T, typename V>
+__device__ __forceinline__ V emd_zero_dist(V level) {
+  return level < (V)0 ? emd_zero_below<T, V>() / level : (V)__builtin_inf();
+}
 // True when exp(level * d) is +0 in every lane of the wave, so the wave can
 // skip the exponential and its products (wave-uniform branch).  A NaN
-// argument is never "below", so NaN still propagates.
+// distance is never "above", so NaN still propagates.
 template <typename T, typename V>
 __device__ __forceinline__ bool emd_wave_zero(V level, V d) {
   if constexpr (std::is_same<T, half_t>::value) return false;
-  return __builtin_amdgcn_ballot_w64(!(level * d < emd_zero_below<T, V>())) == 0;
+  return __builtin_amdgcn_ballot_w64(!(d > emd_zero_dist<T, V>(level))) == 0;
 }
 // fminf(x, 1.0f) / fmaxf(0.0f, x) of emd.cu:134,136,178 (float functions)
 template <typename V>
@@ -368,7 +376,7 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
   constexpr int C = 64, U = 8;
   __shared__ EmdPt<V> s_pt[NW][C];  // (x, y, z, wa)
   __shared__ V s_wb[NS == 2 ? NW : 1][C];
-  const V zb = emd_zero_below<T, V>();
+  const V ta = emd_zero_dist<T, V>(la), tb = emd_zero_dist<T, V>(lb);
   // float32, two levels a factor 4 apart (every fused sweep but the last):
   // both exponentials come from one argument reduction (emd_exp_x4).
   // float16 clamps each argument at -20, which breaks the scaling; float64
@@ -398,8 +406,8 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
       pt[u] = s_pt[w][base + u];
       if constexpr (NS == 2) pb[u] = s_wb[w][base + u];
       d[u] = sq3(pt[u].x - x, pt[u].y - y, pt[u].z - z);
-      nza |= !(la * d[u] < zb);  // NaN counts as non-zero
-      if constexpr (NS == 2) nzb |= !(lb * d[u] < zb);
+      nza |= !(d[u] > ta);  // NaN counts as non-zero
+      if constexpr (NS == 2) nzb |= !(d[u] > tb);
     }
     if constexpr (NS == 2 && std::is_same<T, float>::value) {
       if (pow4) {
