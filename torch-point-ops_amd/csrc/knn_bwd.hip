@@ -228,18 +228,22 @@ __global__ __launch_bounds__(KB1_THREADS) void knn_bwd_entry_kernel(
   }
 }
 
-// Reads the records of (cloud n, bucket j) -- a lane per entry workgroup,
-// U records in flight -- and calls f(row, v) for each (v: its D terms).
+// Reads the records of (cloud n, bucket j) -- L lanes per entry workgroup
+// (every thread busy when the cloud has KB2_THREADS / L of them), each taking
+// every L-th group of U records, U in flight -- and calls f(row, v) for each
+// (v: its D terms).
 template <typename A, typename F>
 __device__ __forceinline__ void kb_for_records(const A* __restrict__ rec,
                                                const int4* __restrict__ t, int n, int cpc, int D,
                                                F&& f) {
   const int rw = kb_record_words(D);
-  for (int c = threadIdx.x; c < cpc; c += KB2_THREADS) {
+  const int L = cpc * 4 <= KB2_THREADS ? 4 : (cpc * 2 <= KB2_THREADS ? 2 : 1);
+  const int sub = (int)threadIdx.x % L;
+  constexpr int U = 4;
+  for (int c = (int)threadIdx.x / L; c < cpc; c += KB2_THREADS / L) {
     const int4 cs = t[c];
     const A* __restrict__ src = rec + ((int64_t)(n * cpc + c) * KB1_THREADS + cs.y) * rw;
-    constexpr int U = 4;
-    for (int i0 = 0; i0 < cs.x; i0 += U) {
+    for (int i0 = sub * U; i0 < cs.x; i0 += L * U) {
       int row[U];
       A v[U][7];
 #pragma unroll
