@@ -173,6 +173,47 @@ struct CgMargin<half_t> {
   static constexpr float lb = 0.997f, abs = 0x1p-20f, inv = 1.003f;
 };
 
+// Wave reductions of the sort by DPP steps whose result reaches lane 63:
+// pairs, quads, 8 (half-row mirror), 16 (row mirror: after these four every
+// lane holds its row's result), then rows 0-1 and 2-3 (row_bcast:15) and all
+// four (row_bcast:31).  A lane that a step does not write keeps its value.
+template <int CTRL, int RM>
+__device__ __forceinline__ uint32_t cg_dpp_keep(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, RM, 0xf, false);
+}
+template <typename F>
+__device__ __forceinline__ uint32_t cg_row_reduce(uint32_t v, F&& op) {
+  v = op(v, cg_dpp_keep<0xB1, 0xf>(v));   // quad_perm [1,0,3,2]
+  v = op(v, cg_dpp_keep<0x4E, 0xf>(v));   // quad_perm [2,3,0,1]
+  v = op(v, cg_dpp_keep<0x141, 0xf>(v));  // row_half_mirror
+  v = op(v, cg_dpp_keep<0x140, 0xf>(v));  // row_mirror
+  return v;
+}
+template <typename F>
+__device__ __forceinline__ uint32_t cg_wave_reduce63(uint32_t v, F&& op) {
+  v = cg_row_reduce(v, op);
+  v = op(v, cg_dpp_keep<0x142, 0xa>(v));  // row_bcast:15 into rows 1, 3
+  v = op(v, cg_dpp_keep<0x143, 0xc>(v));  // row_bcast:31 into rows 2, 3
+  return v;
+}
+// fminf / fmaxf on float bits (NaN ignored, as those functions do)
+struct CgFmin {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
+    return __float_as_uint(fminf(__uint_as_float(a), __uint_as_float(b)));
+  }
+};
+struct CgFmax {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }
+};
+struct CgAdd {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; }
+};
+struct CgMaxU {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
+};
+
 // PPT > 0: every thread keeps its (at most PPT) points in registers across the
 // passes (n <= 1024 * PPT); PPT == 0: the passes reload from memory.
 template <typename TI, int PPT>
@@ -248,13 +289,11 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     }
   }
 #pragma unroll
-  for (int a = 0; a < 3; ++a)
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      lo[a] = fminf(lo[a], __shfl_xor(lo[a], m));
-      hi[a] = fmaxf(hi[a], __shfl_xor(hi[a], m));
-    }
-  if (lane == 0)
+  for (int a = 0; a < 3; ++a) {
+    lo[a] = __uint_as_float(cg_wave_reduce63(__float_as_uint(lo[a]), CgFmin{}));
+    hi[a] = __uint_as_float(cg_wave_reduce63(__float_as_uint(hi[a]), CgFmax{}));
+  }
+  if (lane == 63)
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
       red[a][w] = lo[a];
@@ -267,11 +306,11 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   float glo[3], ghi[3], gs[3];
 #pragma unroll
   for (int a = 0; a < 3; ++a) {
-    float x = __builtin_inff(), z = -__builtin_inff();
-    for (int v = 0; v < 16; ++v) {
-      x = fminf(x, red[a][v]);
-      z = fmaxf(z, red[3 + a][v]);
-    }
+    // the 16 waves' values, one a lane of each row, reduced within the row
+    float x = __uint_as_float(cg_row_reduce(__float_as_uint(red[a][lane & 15]), CgFmin{}));
+    float z = __uint_as_float(cg_row_reduce(__float_as_uint(red[3 + a][lane & 15]), CgFmax{}));
+    x = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+    z = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(z)));
     if (!is_finite(x) || !is_finite(z)) x = z = 0.f;  // empty or all-NaN axis
     glo[a] = x;
     ghi[a] = z;
@@ -287,24 +326,31 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
   // cell count (the atomics' returned ranks, maximised)
   auto histogram = [&]() {
     uint32_t mr = 0;
-    for (int i = 0; i < iters; ++i) {
-      const int k = tid + 1024 * i;
-      if (k >= n) break;
-      float x, y, z;
-      point(i, k, x, y, z);
-      const int h = cg_hidx(code_of(x, y, z));
-      const uint32_t r = atomicAdd(&cnt[h], 1u);
-      mr = max(mr, r + 1);
-      if constexpr (PPT > 0) {
-        rk[i] = r;
-        hx[i] = (uint32_t)h;
-      } else {
+    if constexpr (PPT > 0) {
+      // all of a thread's atomics are issued before any returned rank is
+      // used, so their LDS round trips overlap; a slot past the cloud (a copy
+      // of the last point) adds 0
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        hx[i] = (uint32_t)cg_hidx(code_of(px[i], py[i], pz[i]));
+        rk[i] = atomicAdd(&cnt[hx[i]], tid + 1024 * i < n ? 1u : 0u);
+      }
+#pragma unroll
+      for (int i = 0; i < PPT; ++i)
+        if (tid + 1024 * i < n) mr = max(mr, rk[i] + 1);
+    } else {
+      for (int i = 0; i < iters; ++i) {
+        const int k = tid + 1024 * i;
+        if (k >= n) break;
+        float x, y, z;
+        point(i, k, x, y, z);
+        const uint32_t r = atomicAdd(&cnt[cg_hidx(code_of(x, y, z))], 1u);
+        mr = max(mr, r + 1);
         rank[k] = (int32_t)r;
       }
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mr = max(mr, (uint32_t)__shfl_xor((int)mr, m));
-    if (lane == 0) atomicMax(&s_maxc, mr);
+    mr = cg_wave_reduce63(mr, CgMaxU{});
+    if (lane == 63) atomicMax(&s_maxc, mr);
     __syncthreads();
   };
   histogram();
@@ -409,7 +455,31 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
     {
       // sums of count^2 over the cells of 32^3, 16^3 and 8^3 (Morton order
       // nests them: 8 consecutive cells form a 16^3 cell, this thread's 32
-      // and its neighbour's an 8^3 cell), in float, reduced in a fixed order
+      // and its neighbour's an 8^3 cell), reduced in a fixed order; with the
+      // points in registers (n <= 8192) in integers, every sum below 2^26
+      if constexpr (PPT > 0) {
+        uint32_t q0 = 0, q1 = 0;
+#pragma unroll
+        for (int i = 0; i < CPT; i += 8) {
+          uint32_t c8 = 0;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            q0 += v[i + k] * v[i + k];
+            c8 += v[i + k];
+          }
+          q1 += c8 * c8;
+        }
+        const uint32_t c64 = sum + cg_dpp_keep<0xB1, 0xf>(sum);  // this thread's and its pair's
+        uint32_t q2 = (lane & 1) ? 0u : c64 * c64;
+        q0 = cg_wave_reduce63(q0, CgAdd{});
+        q1 = cg_wave_reduce63(q1, CgAdd{});
+        q2 = cg_wave_reduce63(q2, CgAdd{});
+        if (lane == 63) {
+          s_sq[0][w] = (float)q0;
+          s_sq[1][w] = (float)q1;
+          s_sq[2][w] = (float)q2;
+        }
+      } else {
       float sq0 = 0.f, sq1 = 0.f;
 #pragma unroll
       for (int i = 0; i < CPT; i += 8) {
@@ -433,6 +503,7 @@ __global__ __launch_bounds__(1024) void chamfer_grid_sort_kernel(
         s_sq[0][w] = sq0;
         s_sq[1][w] = sq1;
         s_sq[2][w] = sq2;
+      }
       }
     }
     uint32_t incl = sum;
