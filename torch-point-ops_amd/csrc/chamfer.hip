@@ -437,7 +437,7 @@ static int64_t loss_parts(int64_t n) {
 }
 
 // Loss from the chunk sums, by one wave: parts [0, p1) sum dist1,
-// [p1, p1 + p2) dist2.  Lane 0 writes, as torch.mean / torch.sum of each
+// [p1, p1 + p2) dist2.  Lane 63 writes, as torch.mean / torch.sum of each
 // array followed by their sum (chamfer.py:20-23; torch's mean scales the
 // accumulated sum by 1 / numel in the accumulation type, and an empty
 // array's mean is NaN):
@@ -451,12 +451,9 @@ __device__ void chamfer_loss_finish(const double* part, int p1, int p2, int mean
   A a1 = (A)0, a2 = (A)0;
   for (int k = lane; k < p1; k += 64) a1 += (A)part[k];
   for (int k = lane; k < p2; k += 64) a2 += (A)part[p1 + k];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    a1 += __shfl_xor(a1, o);
-    a2 += __shfl_xor(a2, o);
-  }
-  if (lane == 0) {
+  a1 = wave_add63(a1);
+  a2 = wave_add63(a2);
+  if (lane == 63) {
     if (mean) {
       a1 *= (A)1 / (A)count1;
       a2 *= (A)1 / (A)count2;
@@ -491,9 +488,8 @@ __global__ __launch_bounds__(256) void chamfer_loss_part_kernel(
   A a = (A)0;
 #pragma unroll 8
   for (int64_t i = lo + threadIdx.x; i < hi; i += 256) a += (A)d[i];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = a;
+  a = wave_add63(a);
+  if ((threadIdx.x & 63) == 63) s_red[threadIdx.x >> 6] = a;
   __syncthreads();
   if (threadIdx.x == 0) part[k] = (double)(((s_red[0] + s_red[1]) + s_red[2]) + s_red[3]);
   if constexpr (LAST) {

@@ -39,6 +39,29 @@ __device__ __forceinline__ T ref_d(T qx, T qy, T qz, const T* __restrict__ r) {
   return sq3((T)(r[0] - qx), (T)(r[1] - qy), (T)(r[2] - qz));
 }
 
+// The wave's sum in lane 63 (the other lanes hold partial sums), in a fixed
+// order by DPP adds: pairs, quads, 8 (half-row mirror), 16 (row mirror), then
+// rows 0+1 and 2+3 (row_bcast:15) and all four (row_bcast:31).  double: the
+// same sum by lane swaps, in every lane.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float ch_dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWMASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_add63(float v) {
+  v = ch_dpp_add<0xB1, 0xf>(v);
+  v = ch_dpp_add<0x4E, 0xf>(v);
+  v = ch_dpp_add<0x141, 0xf>(v);
+  v = ch_dpp_add<0x140, 0xf>(v);
+  v = ch_dpp_add<0x142, 0xa>(v);
+  v = ch_dpp_add<0x143, 0xc>(v);
+  return v;
+}
+__device__ __forceinline__ double wave_add63(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 // Wave minima of NaN-free values.
 __device__ __forceinline__ float wave_min(float v) {
 #pragma unroll
