@@ -127,10 +127,10 @@ def test_emd_sizes_and_errors(lib):
     lib.tpo_emd_workspace_size.argtypes = [ctypes.c_int, I, I, I]
     lib.tpo_emd_workspace_size.restype = I
     # float/half: p1, p2 (4 floats a point), remain, 10 levels of ratios,
-    # 8 x 64 cost partials and 16 chunks of grad_xyz1 partials per cloud,
-    # plus the int32 point orders
+    # 8 x 64 cost partials, 16 row tiles of grad_xyz1 partials and 8 column
+    # tiles of grad_xyz2 partials per cloud, plus the int32 point orders
     B, n, m = 16, 2048, 2048
-    vals = B * (n * 4 + m * 4 + n + m + 10 * n + 10 * m + 8 * 64 + 16 * n * 3)
+    vals = B * (n * 4 + m * 4 + n + m + 10 * n + 10 * m + 8 * 64 + 16 * n * 3 + 8 * m * 3)
     assert lib.tpo_emd_workspace_size(0, B, n, m) == 4 * vals + 4 * B * (n + m)
     assert lib.tpo_emd_workspace_size(2, B, n, m) == 4 * vals + 4 * B * (n + m)
     assert lib.tpo_emd_workspace_size(1, B, n, m) == 8 * vals + 4 * B * (n + m)
