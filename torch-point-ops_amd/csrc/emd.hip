@@ -175,6 +175,35 @@ __device__ __forceinline__ float wave_total63(float v) {
   return v;
 }
 __device__ __forceinline__ double wave_total63(double v) { return wave_sum(v); }
+// Wave minimum / maximum in every lane (float: DPP into lane 63, whose value
+// is read back; double: lane swaps).  The masked-off rows of a row_bcast step
+// take the identity (+inf / -inf).
+template <int CTRL, int ROWMASK, bool MAX>
+__device__ __forceinline__ float dpp_minmax(float v) {
+  const float id = MAX ? -__builtin_inff() : __builtin_inff();
+  const float o = __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(id), __float_as_int(v), CTRL, ROWMASK, 0xf, false));
+  return MAX ? fmaxf(v, o) : fminf(v, o);
+}
+template <bool MAX>
+__device__ __forceinline__ float wave_minmax(float v) {
+  v = dpp_minmax<0xB1, 0xf, MAX>(v);
+  v = dpp_minmax<0x4E, 0xf, MAX>(v);
+  v = dpp_minmax<0x141, 0xf, MAX>(v);
+  v = dpp_minmax<0x140, 0xf, MAX>(v);
+  v = dpp_minmax<0x142, 0xa, MAX>(v);
+  v = dpp_minmax<0x143, 0xc, MAX>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+template <bool MAX>
+__device__ __forceinline__ double wave_minmax(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const double u = __shfl_xor(v, o, 64);
+    v = MAX ? fmax(v, u) : fmin(v, u);
+  }
+  return v;
+}
 
 // Workspace, array-major over the clouds (opmath values):
 //   p1[B][n][4], p2[B][m][4]   coordinates (x, y, z, 0)
@@ -236,13 +265,15 @@ __global__ __launch_bounds__(EMD_THREADS) void emd_prep_kernel(
   }
 }
 
-// The points of one cloud (blockIdx.y: 0 = xyz1, 1 = xyz2) listed by the
-// cell of a 16^3 grid over its bounding box, in Morton order of the cells
-// (counting sort in LDS; the order inside a cell is whatever the atomics
-// give).  A sweep's wave then holds 64 nearby points, so the steep levels'
-// exponentials vanish in all of its lanes at once.  Which wave a point sits
-// in changes no result: its sums run over the other cloud in a fixed order
-// and a skipped term is exactly zero.
+// The points of one cloud (blockIdx.y + first: 0 = xyz1, 1 = xyz2) listed so
+// that every run of 64 (one sweep wave's own points) lies close together:
+// the steep levels' exponentials then vanish in all of a wave's lanes at
+// once, and far points of the other cloud drop out of the wave's sweep.
+// Which wave a point sits in changes no result: its sums run over the other
+// cloud in a fixed order and a skipped term is exactly zero.
+// Clouds of more than EMD_KD_MAX points: the cell of a 16^3 grid over the
+// bounding box, in Morton order of the cells (counting sort in LDS; the order
+// inside a cell is whatever the atomics give).
 constexpr int EMD_ORDER_THREADS = 1024;
 constexpr int EMD_OGRID = 16;
 constexpr int EMD_OCELLS = EMD_OGRID * EMD_OGRID * EMD_OGRID;
@@ -257,12 +288,12 @@ __device__ __forceinline__ uint32_t emd_spread3(uint32_t v) {  // 4 bits -> ever
 template <typename T>
 __global__ __launch_bounds__(EMD_ORDER_THREADS) void emd_order_kernel(
     const T* __restrict__ xyz1, const T* __restrict__ xyz2, int n, int m, int* __restrict__ ord1,
-    int* __restrict__ ord2) {
+    int* __restrict__ ord2, int first) {
   __shared__ uint32_t s_cnt[EMD_OCELLS];
   __shared__ float s_box[6][EMD_ORDER_THREADS / 64];
   __shared__ uint32_t s_part[EMD_ORDER_THREADS / 64];
   const int64_t b = blockIdx.x;
-  const bool two = blockIdx.y != 0;
+  const bool two = blockIdx.y + first != 0;
   const int N = two ? m : n;
   const T* P = two ? xyz2 + b * m * 3 : xyz1 + b * n * 3;
   int* ord = two ? ord2 + b * m : ord1 + b * n;
@@ -343,19 +374,286 @@ __global__ __launch_bounds__(EMD_ORDER_THREADS) void emd_order_kernel(
   for (int k = tid; k < N; k += EMD_ORDER_THREADS) ord[atomicAdd(&s_cnt[cell_of(k)], 1u)] = k;
 }
 
+// Clouds of at most EMD_KD_MAX points: the leaves of a k-d tree whose leaves
+// are the runs of 64 (the last one shorter).  A node of g runs splits into
+// floor(g / 2) runs and the rest, across its longest extent, at the rank
+// 64 floor(g / 2) along that axis.  Morton runs jump between distant cells at
+// the octant borders, and a wave holding such a run reaches most of the
+// other cloud; the tree's leaves are compact boxes.
+//   Three arrays list the points ordered by x, y and z: keys are the
+// coordinate quantised to 20 bits over the cloud's box, then the point (one
+// 32-bit word), placed by a counting sort on the top EMD_KD_BBITS bits (the
+// order inside a bin is whatever the atomics give: a split then errs by at
+// most a bin, 1/512 of the box).  Each node is a segment of each array; its
+// extents are read off its first and last keys, its split marks the points
+// of the lower part along its axis, and a stable partition by that mark
+// (prefix sums of the marks) orders its segment of the other two arrays the
+// same way, so every node stays one segment in all three.  The x array's
+// final order is the list.
+constexpr int EMD_KD_MAX = 4096;
+constexpr int EMD_KD_NODES = EMD_KD_MAX / 64;
+constexpr int EMD_KD_QBITS = 20;
+constexpr int EMD_KD_BBITS = 9;
+constexpr int EMD_KD_BINS = 1 << EMD_KD_BBITS;
+
+// inclusive prefix sum over the 64 lanes (all active): row_shr 1, 2, 4, 8
+// within rows of 16 (lanes without a source read 0), then row_bcast:15 into
+// rows 1, 3 and row_bcast:31 into rows 2, 3
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ int emd_dpp0(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWMASK, 0xf, true);
+}
+__device__ __forceinline__ int emd_wave_scan(int v) {
+  v += emd_dpp0<0x111, 0xf>(v);
+  v += emd_dpp0<0x112, 0xf>(v);
+  v += emd_dpp0<0x114, 0xf>(v);
+  v += emd_dpp0<0x118, 0xf>(v);
+  v += emd_dpp0<0x142, 0xa>(v);
+  v += emd_dpp0<0x143, 0xc>(v);
+  return v;
+}
+// sum of the per-wave totals tot[0 .. w) (w = this wave; at most 64 waves)
+__device__ __forceinline__ int emd_waves_before(const int* tot, int nw, int w) {
+  const int lane = lane_id();
+  const int t = lane < nw ? tot[lane] : 0;
+  return __builtin_amdgcn_readlane(emd_wave_scan(t) - t, w);
+}
+
+template <typename T>
+__global__ __launch_bounds__(EMD_ORDER_THREADS) void emd_kd_order_kernel(
+    const T* __restrict__ xyz1, const T* __restrict__ xyz2, int n, int m, int* __restrict__ ord1,
+    int* __restrict__ ord2, int first) {
+  constexpr int TH = EMD_ORDER_THREADS, NWV = TH / 64;
+  constexpr int PER = EMD_KD_MAX / TH;  // consecutive positions a thread (one run of 64)
+  static_assert(EMD_KD_BINS <= TH, "one bin of each axis a thread");
+  __shared__ __align__(16) uint32_t s_key[3][EMD_KD_MAX];
+  __shared__ __align__(16) uint8_t s_flag[EMD_KD_MAX];
+  __shared__ int s_cnt[3][EMD_KD_BINS];
+  __shared__ float s_box[6][NWV];
+  __shared__ int s_wsum[3][NWV];
+  __shared__ int s_nstart[2][EMD_KD_NODES], s_ngrp[2][EMD_KD_NODES], s_nn[2];
+  __shared__ int s_nlow[EMD_KD_NODES], s_naxis[EMD_KD_NODES], s_nbase[3][EMD_KD_NODES];
+  __shared__ uint8_t s_nog[EMD_KD_NODES];  // node of each run of 64
+  const int64_t b = blockIdx.x;
+  const bool two = blockIdx.y + first != 0;
+  const int N = two ? m : n;
+  const T* P = two ? xyz2 + b * m * 3 : xyz1 + b * n * 3;
+  int* ord = two ? ord2 + b * m : ord1 + b * n;
+  const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+  if (N <= 0 || N > EMD_KD_MAX) return;
+  const int i0 = tid * PER;  // this thread's positions i0 .. i0 + PER - 1
+  // ---- this thread's points (positions = point indices here), the box ----
+  float pc[PER][3];
+  float lo[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
+  float hi[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      pc[u][c] = i0 + u < N ? (float)P[3 * (i0 + u) + c] : 0.f;
+      if (i0 + u < N) {
+        lo[c] = fminf(lo[c], pc[u][c]);
+        hi[c] = fmaxf(hi[c], pc[u][c]);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    lo[c] = wave_minmax<false>(lo[c]);
+    hi[c] = wave_minmax<true>(hi[c]);
+    if (lane == 0) {
+      s_box[c][w] = lo[c];
+      s_box[3 + c][w] = hi[c];
+    }
+  }
+  if (tid < EMD_KD_BINS) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) s_cnt[c][tid] = 0;
+  }
+  __syncthreads();
+  float scl[3], unit[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    float a = __builtin_inff(), z = -__builtin_inff();
+    for (int v = 0; v < NWV; ++v) {
+      a = fminf(a, s_box[c][v]);
+      z = fmaxf(z, s_box[3 + c][v]);
+    }
+    const float ext = z - a;
+    const bool ok = ext > 0.f && ext < __builtin_inff();
+    lo[c] = a;
+    scl[c] = ok ? (float)(1 << EMD_KD_QBITS) / ext : 0.f;
+    unit[c] = ok ? ext / (float)(1 << EMD_KD_QBITS) : 0.f;
+  }
+  // ---- keys, and the three counting sorts at once ----
+  uint32_t kv[3][PER];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const float f = (pc[u][c] - lo[c]) * scl[c];
+      const float q = f == f ? fminf(fmaxf(f, 0.f), (float)((1 << EMD_KD_QBITS) - 1)) : 0.f;
+      kv[c][u] = ((uint32_t)q << 12) | (uint32_t)(i0 + u);
+      if (i0 + u < N) atomicAdd(&s_cnt[c][kv[c][u] >> (32 - EMD_KD_BBITS)], 1);
+    }
+  }
+  __syncthreads();
+  {  // exclusive prefix sums of the bins: thread t < EMD_KD_BINS holds bin t of each axis
+    int v[3], incl[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      v[c] = tid < EMD_KD_BINS ? s_cnt[c][tid] : 0;
+      incl[c] = emd_wave_scan(v[c]);
+      if (lane == 63) s_wsum[c][w] = incl[c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const int off = incl[c] - v[c] + emd_waves_before(s_wsum[c], NWV, w);
+      if (tid < EMD_KD_BINS) s_cnt[c][tid] = off;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      if (i0 + u < N) s_key[c][atomicAdd(&s_cnt[c][kv[c][u] >> (32 - EMD_KD_BBITS)], 1)] = kv[c][u];
+    }
+  }
+  // ---- the tree, a level at a time ----
+  const int G = (N + 63) >> 6;  // runs of 64
+  if (tid == 0) {
+    s_nstart[0][0] = 0;
+    s_ngrp[0][0] = G;
+    s_nn[0] = 1;
+  }
+  __syncthreads();
+  int cur = 0;
+  for (int lev = 0; (1 << lev) < G; ++lev) {
+    if (w == 0) {  // a lane per node: its axis and split, and the next level's nodes
+      const int nn = s_nn[cur];
+      int st = 0, g = 0, low = 0, ax = 0, nch = 0;
+      if (lane < nn) {
+        st = s_nstart[cur][lane];
+        g = s_ngrp[cur][lane];
+        nch = 1;
+        if (g >= 2) {
+          const int e = min(st + 64 * g, N) - 1;
+          float best = -1.f;
+#pragma unroll
+          for (int c = 0; c < 3; ++c) {
+            const int d = (int)(s_key[c][e] >> 12) - (int)(s_key[c][st] >> 12);
+            const float ext = (float)(d < 0 ? -d : d) * unit[c];
+            if (ext > best) {
+              best = ext;
+              ax = c;
+            }
+          }
+          low = 64 * (g >> 1);
+          nch = 2;
+        }
+      }
+      const int incl = emd_wave_scan(nch);
+      const int pos = incl - nch, nx = cur ^ 1;
+      if (lane < nn) {
+        s_nlow[lane] = low;
+        s_naxis[lane] = ax;
+        for (int q = 0; q < g; ++q) s_nog[(st >> 6) + q] = (uint8_t)lane;
+        s_nstart[nx][pos] = st;
+        s_ngrp[nx][pos] = nch == 2 ? g >> 1 : g;
+        if (nch == 2) {
+          s_nstart[nx][pos + 1] = st + low;
+          s_ngrp[nx][pos + 1] = g - (g >> 1);
+        }
+      }
+      if (lane == 63) s_nn[nx] = incl;
+    }
+    __syncthreads();
+    // this thread's node (its PER positions lie in one run of 64)
+    const bool act = i0 < N;
+    const int nd = act ? s_nog[i0 >> 6] : 0;
+    const int low = act ? s_nlow[nd] : 0, ax = s_naxis[nd], st = s_nstart[cur][nd];
+    const bool split = low > 0;
+    // mark the points of each node's lower part along its axis
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const uint4 q4 = act ? *reinterpret_cast<const uint4*>(&s_key[c][i0]) : make_uint4(0, 0, 0, 0);
+      kv[c][0] = q4.x;
+      kv[c][1] = q4.y;
+      kv[c][2] = q4.z;
+      kv[c][3] = q4.w;
+    }
+    if (split) {  // the axis array's keys again, read from LDS (no indexed registers)
+      const uint4 q4 = *reinterpret_cast<const uint4*>(&s_key[ax][i0]);
+      const uint32_t ka[PER] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+      for (int u = 0; u < PER; ++u)
+        if (i0 + u < N) s_flag[ka[u] & 0xfff] = (uint8_t)(i0 + u - st < low);
+    }
+    __syncthreads();
+    // stable partition of each splitting node's segment in the other two
+    // arrays: prefix sums of the marks in array order, then every key to its
+    // new position
+    int f[3][PER], excl[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      int run = 0;
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        f[c][u] = i0 + u < N ? (int)s_flag[kv[c][u] & 0xfff] : 0;
+        run += f[c][u];
+      }
+      const int incl = emd_wave_scan(run);
+      if (lane == 63) s_wsum[c][w] = incl;
+      excl[c] = incl - run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      excl[c] += emd_waves_before(s_wsum[c], NWV, w);
+      if (act && i0 == st) s_nbase[c][nd] = excl[c];  // the node's first position
+    }
+    __syncthreads();
+    if (split) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c) {
+        if (c == ax) continue;
+        const int base = s_nbase[c][nd];
+        int e = excl[c];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          const int i = i0 + u;
+          if (i < N) {
+            const int lb = e - base;  // marked points before i in the node
+            s_key[c][f[c][u] ? st + lb : st + low + (i - st - lb)] = kv[c][u];
+          }
+          e += f[c][u];
+        }
+      }
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+  for (int i = tid; i < N; i += TH) ord[i] = (int)(s_key[0][i] & 0xfff);
+}
+
 // One point of the coordinate arrays (x, y, z, unused), read whole.
 template <typename V>
 struct __attribute__((aligned(4 * sizeof(V)))) EmdPt {
   V x, y, z, w;
 };
 
-// Sums over the "other" cloud for one own point per lane; the waves of the
+// Sums over the "other" cloud for one own point per lane (own: the lane's
+// point is real; the sums of the other lanes are not used); the waves of the
 // workgroup take an equal share of the other points each.  NS = 1 sums
-// e(la)*wa; NS = 2 also sums e(lb)*wb with the same distances.
-template <typename T, int NS>
+// e(la)*wa; NS = 2 also sums e(lb)*wb with the same distances.  PR: leave
+// out the points far from every own point of the wave (below).
+template <typename T, int NS, bool PR>
 __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restrict__ other, int cnt,
-                                          typename EmdV<T>::type x, typename EmdV<T>::type y,
-                                          typename EmdV<T>::type z, typename EmdV<T>::type la,
+                                          bool own, typename EmdV<T>::type x,
+                                          typename EmdV<T>::type y, typename EmdV<T>::type z,
+                                          typename EmdV<T>::type la,
                                           const typename EmdV<T>::type* __restrict__ wa,
                                           typename EmdV<T>::type lb,
                                           const typename EmdV<T>::type* __restrict__ wb,
@@ -382,6 +680,36 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
   // float16 clamps each argument at -20, which breaks the scaling; float64
   // keeps its library exp.
   const bool pow4 = std::is_same<T, float>::value && NS == 2 && lb != (V)0 && la == (V)4 * lb;
+  // Far points.  The wave's own points are neighbours in space (the sweep
+  // takes them in Morton order), so many points of the other cloud lie
+  // farther from the box of the wave's real own points than the zero
+  // distance of every level summed here (with a relative margin of 2^-10, far
+  // above the rounding of the box distance and of d): each of their terms is
+  // exactly +0 in every real lane, and they are left out of the batches.  The
+  // remaining points are summed in the same order, so the sums keep their
+  // bits (for the finite weights these sweeps carry).  A wave with a
+  // non-finite own coordinate leaves nothing out, nor does float16 (its
+  // exponentials never vanish); a non-finite point of the other cloud is
+  // always kept, so NaN still propagates.
+  V reach = NS == 2 ? (ta > tb ? ta : tb) : ta;  // +inf for level 0
+  if constexpr (std::is_same<T, half_t>::value) reach = (V)__builtin_inf();
+  bool prune = false;
+  V olo[3], ohi[3];
+  if constexpr (PR) {
+    const bool fin = __builtin_isfinite(x) && __builtin_isfinite(y) && __builtin_isfinite(z);
+    if (__builtin_amdgcn_ballot_w64(own && !fin) != 0) reach = (V)__builtin_inf();
+    prune = reach < (V)__builtin_inf();
+  }
+  if (prune) {
+    const V inf = (V)__builtin_inf();
+    olo[0] = wave_minmax<false>(own ? x : inf);
+    olo[1] = wave_minmax<false>(own ? y : inf);
+    olo[2] = wave_minmax<false>(own ? z : inf);
+    ohi[0] = wave_minmax<true>(own ? x : -inf);
+    ohi[1] = wave_minmax<true>(own ? y : -inf);
+    ohi[2] = wave_minmax<true>(own ? z : -inf);
+    reach *= (V)1 + (V)1 / (V)1024;
+  }
   const EmdPt<V>* op = (const EmdPt<V>*)other;
   EmdPt<V> nr;
   V nb = (V)0;
@@ -395,7 +723,8 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
       nr = EmdPt<V>{(V)0, (V)0, (V)0, (V)0};
     }
   };
-  auto batch = [&](int base, auto ucnt) {
+  // UB points of the chunk, the u-th at slot ix(u), in increasing slots
+  auto batch = [&](auto ix, auto ucnt) {
     constexpr int UB = decltype(ucnt)::value;
     EmdPt<V> pt[UB];
     V pb[UB];
@@ -403,8 +732,8 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
     bool nza = false, nzb = false;
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
-      pt[u] = s_pt[w][base + u];
-      if constexpr (NS == 2) pb[u] = s_wb[w][base + u];
+      pt[u] = s_pt[w][ix(u)];
+      if constexpr (NS == 2) pb[u] = s_wb[w][ix(u)];
       d[u] = sq3(pt[u].x - x, pt[u].y - y, pt[u].z - z);
       nza |= !(d[u] > ta);  // NaN counts as non-zero
       if constexpr (NS == 2) nzb |= !(d[u] > tb);
@@ -451,11 +780,62 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (c0 + C < q1) fetch(c0 + C);
     const int cn = min(C, q1 - c0);
-    int u0 = 0;
-    for (; u0 + U <= cn; u0 += U) batch(u0, std::integral_constant<int, U>{});
-    for (; u0 < cn; ++u0) batch(u0, std::integral_constant<int, 1>{});
+    if constexpr (!PR) {
+      if (c0 + C < q1) fetch(c0 + C);
+      int u0 = 0;
+      for (; u0 + U <= cn; u0 += U)
+        batch([u0](int u) { return u0 + u; }, std::integral_constant<int, U>{});
+      for (; u0 < cn; ++u0) batch([u0](int) { return u0; }, std::integral_constant<int, 1>{});
+      __builtin_amdgcn_wave_barrier();
+      continue;
+    }
+    const uint64_t all = cn == C ? ~0ull : (1ull << cn) - 1;
+    uint64_t near = all;
+    if (prune) {  // lane i tests point c0 + i of the chunk, still in nr
+      V g[3];
+      const V pc[3] = {nr.x, nr.y, nr.z};
+#pragma unroll
+      for (int c = 0; c < 3; ++c) {
+        const V a = olo[c] - pc[c], e = pc[c] - ohi[c];
+        g[c] = a > e ? a : e;
+        g[c] = g[c] > (V)0 ? g[c] : (V)0;
+      }
+      const V lb2 = g[0] * g[0] + g[1] * g[1] + g[2] * g[2];
+      const bool pf = __builtin_isfinite(pc[0]) && __builtin_isfinite(pc[1]) &&
+                      __builtin_isfinite(pc[2]);
+      near &= __builtin_amdgcn_ballot_w64(!(lb2 > reach) || !pf);
+    }
+    if (c0 + C < q1) fetch(c0 + C);
+    const int nn = __builtin_popcountll(near);
+    if (nn + U > cn) {  // (nearly) every point: consecutive slots
+      int u0 = 0;
+      for (; u0 + U <= cn; u0 += U)
+        batch([u0](int u) { return u0 + u; }, std::integral_constant<int, U>{});
+      for (; u0 < cn; ++u0) batch([u0](int) { return u0; }, std::integral_constant<int, 1>{});
+    } else {  // the near points only, in increasing slots
+      auto take = [&](auto ucnt) {
+        constexpr int UB = decltype(ucnt)::value;
+        int sl[UB];
+#pragma unroll
+        for (int u = 0; u < UB; ++u) {
+          sl[u] = __builtin_ctzll(near);
+          near &= near - 1;
+        }
+        batch([&sl](int u) { return sl[u]; }, ucnt);
+      };
+      int r = nn;
+      for (; r >= U; r -= U) take(std::integral_constant<int, U>{});
+      if (r >= 4) {
+        take(std::integral_constant<int, 4>{});
+        r -= 4;
+      }
+      if (r >= 2) {
+        take(std::integral_constant<int, 2>{});
+        r -= 2;
+      }
+      if (r >= 1) take(std::integral_constant<int, 1>{});
+    }
     __builtin_amdgcn_wave_barrier();
   }
   if (w > 0) {
@@ -476,7 +856,7 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
 
 // Step s = 0..10 over the xyz1 points: pass 3 of level s-1 (s >= 1), then
 // pass 1 of level s (s <= 9).  MODE 1: pass 1 only; 2: pass 3 only; 3: both.
-template <typename T, int MODE>
+template <typename T, int MODE, bool PR>
 __global__ __launch_bounds__(EMD_SWEEP_THREADS) void emd_rows_kernel(
     const typename EmdV<T>::type* __restrict__ p1, const typename EmdV<T>::type* __restrict__ p2,
     const typename EmdV<T>::type* __restrict__ remr, const typename EmdV<T>::type* __restrict__ rr,
@@ -497,10 +877,14 @@ __global__ __launch_bounds__(EMD_SWEEP_THREADS) void emd_rows_kernel(
   const V* w3 = rr + (b * EMD_LEVELS + (s >= 1 ? s - 1 : 0)) * m;  // ratioR of level s-1
   const V* w1 = remr + b * m;
   V sums[2];
-  if constexpr (MODE == 1) emd_sweep<T, 1>(other, m, x, y, z, emd_level<V>(s), w1, (V)0, w1, sums);
-  if constexpr (MODE == 2) emd_sweep<T, 1>(other, m, x, y, z, emd_level<V>(s - 1), w3, (V)0, w3, sums);
+  const bool own = k < n;
+  if constexpr (MODE == 1)
+    emd_sweep<T, 1, PR>(other, m, own, x, y, z, emd_level<V>(s), w1, (V)0, w1, sums);
+  if constexpr (MODE == 2)
+    emd_sweep<T, 1, PR>(other, m, own, x, y, z, emd_level<V>(s - 1), w3, (V)0, w3, sums);
   if constexpr (MODE == 3)
-    emd_sweep<T, 2>(other, m, x, y, z, emd_level<V>(s - 1), w3, emd_level<V>(s), w1, sums);
+    emd_sweep<T, 2, PR>(other, m, own, x, y, z, emd_level<V>(s - 1), w3, emd_level<V>(s), w1,
+                        sums);
   if (wave_id() != 0 || k >= n) return;
   const V eps = emd_eps<T, V>();
   V rem = reml[b * n + k];
@@ -516,7 +900,7 @@ __global__ __launch_bounds__(EMD_SWEEP_THREADS) void emd_rows_kernel(
 }
 
 // Pass 2 of level t over the xyz2 points (emd.cu:98-138).
-template <typename T>
+template <typename T, bool PR>
 __global__ __launch_bounds__(EMD_SWEEP_THREADS) void emd_cols_kernel(
     const typename EmdV<T>::type* __restrict__ p1, const typename EmdV<T>::type* __restrict__ p2,
     const typename EmdV<T>::type* __restrict__ rl, typename EmdV<T>::type* __restrict__ remr,
@@ -535,8 +919,8 @@ __global__ __launch_bounds__(EMD_SWEEP_THREADS) void emd_cols_kernel(
   // d(k,l) takes the differences p2 - p1 as the rows pass does; squaring
   // makes the sign irrelevant, so the same values result.
   V sums[2];
-  emd_sweep<T, 1>(p1 + b * n * 4, n, x, y, z, emd_level<V>(t), rl + (b * EMD_LEVELS + t) * n, (V)0,
-                  nullptr, sums);
+  emd_sweep<T, 1, PR>(p1 + b * n * 4, n, l < m, x, y, z, emd_level<V>(t),
+                      rl + (b * EMD_LEVELS + t) * n, (V)0, nullptr, sums);
   if (wave_id() != 0 || l >= m) return;
   const V eps = emd_eps<T, V>();
   const V rem = remr[b * m + l];
@@ -781,23 +1165,53 @@ int emd_fwd_impl(const void* xyz1, const void* xyz2, int64_t B, int64_t n, int64
   hipLaunchKernelGGL(emd_prep_kernel<T>, dim3((unsigned)((std::max(n, m) + 255) / 256), bb),
                      dim3(EMD_THREADS), 0, s, (const T*)xyz1, (const T*)xyz2, nn, mm, mult_l, mult_r,
                      p1, p2, reml, remr);
-  hipLaunchKernelGGL(emd_order_kernel<T>, dim3(bb, 2), dim3(EMD_ORDER_THREADS), 0, s,
-                     (const T*)xyz1, (const T*)xyz2, nn, mm, ord1, ord2);
-  const dim3 grow((unsigned)((n + 63) / 64), bb), gcol((unsigned)((m + 63) / 64), bb);
-  for (int st = 0; st <= EMD_LEVELS; ++st) {
-    if (st == 0)
-      hipLaunchKernelGGL((emd_rows_kernel<T, 1>), grow, dim3(EMD_SWEEP_THREADS), 0, s, p1, p2, remr, rr,
-                         reml, rl, ord1, nn, mm, st);
-    else if (st == EMD_LEVELS)
-      hipLaunchKernelGGL((emd_rows_kernel<T, 2>), grow, dim3(EMD_SWEEP_THREADS), 0, s, p1, p2, remr, rr,
-                         reml, rl, ord1, nn, mm, st);
-    else
-      hipLaunchKernelGGL((emd_rows_kernel<T, 3>), grow, dim3(EMD_SWEEP_THREADS), 0, s, p1, p2, remr, rr,
-                         reml, rl, ord1, nn, mm, st);
-    if (st < EMD_LEVELS)
-      hipLaunchKernelGGL(emd_cols_kernel<T>, gcol, dim3(EMD_SWEEP_THREADS), 0, s, p1, p2, rl, remr, rr,
-                         ord2, nn, mm, st);
+  {  // the k-d order for clouds that fit it, else the Morton order
+    const bool kd1 = n <= EMD_KD_MAX, kd2 = m <= EMD_KD_MAX;
+    auto order = [&](bool kd, unsigned clouds, int first) {
+      if (kd)
+        hipLaunchKernelGGL(emd_kd_order_kernel<T>, dim3(bb, clouds), dim3(EMD_ORDER_THREADS), 0, s,
+                           (const T*)xyz1, (const T*)xyz2, nn, mm, ord1, ord2, first);
+      else
+        hipLaunchKernelGGL(emd_order_kernel<T>, dim3(bb, clouds), dim3(EMD_ORDER_THREADS), 0, s,
+                           (const T*)xyz1, (const T*)xyz2, nn, mm, ord1, ord2, first);
+    };
+    if (kd1 == kd2) {
+      order(kd1, 2, 0);
+    } else {
+      order(kd1, 1, 0);
+      order(kd2, 1, 1);
+    }
   }
+  const dim3 grow((unsigned)((n + 63) / 64), bb), gcol((unsigned)((m + 63) / 64), bb);
+  // Far points are left out of the steep levels' sweeps (levels -4^7 ..
+  // -4^3, those whose zero distance reaches a small part of a cloud of unit
+  // scale); float16's exponentials never vanish.
+  constexpr bool prunable = !std::is_same<T, half_t>::value;
+  constexpr int EMD_PRUNE_STEPS = 5;
+#define EMD_ROWS(MODE, PR)                                                                 \
+  hipLaunchKernelGGL((emd_rows_kernel<T, MODE, PR>), grow, dim3(EMD_SWEEP_THREADS), 0, s, p1, \
+                     p2, remr, rr, reml, rl, ord1, nn, mm, st)
+#define EMD_COLS(PR)                                                                     \
+  hipLaunchKernelGGL((emd_cols_kernel<T, PR>), gcol, dim3(EMD_SWEEP_THREADS), 0, s, p1, p2, rl, \
+                     remr, rr, ord2, nn, mm, st)
+  for (int st = 0; st <= EMD_LEVELS; ++st) {
+    const bool pr = prunable && st < EMD_PRUNE_STEPS;
+    if (st == 0) {
+      if (pr) EMD_ROWS(1, prunable);
+      else EMD_ROWS(1, false);
+    } else if (st == EMD_LEVELS) {
+      EMD_ROWS(2, false);
+    } else {
+      if (pr) EMD_ROWS(3, prunable);
+      else EMD_ROWS(3, false);
+    }
+    if (st < EMD_LEVELS) {
+      if (pr) EMD_COLS(prunable);
+      else EMD_COLS(false);
+    }
+  }
+#undef EMD_ROWS
+#undef EMD_COLS
   hipLaunchKernelGGL(emd_match_kernel<T>, dim3((unsigned)L.gx, (unsigned)L.gy, bb),
                      dim3(EMD_THREADS), 0, s, p1, p2, rl, rr, nn, mm, (T*)match, cp);
   hipLaunchKernelGGL(emd_cost_kernel<T>, dim3(bb), dim3(EMD_THREADS), 0, s, cp, L.gx * L.gy,
