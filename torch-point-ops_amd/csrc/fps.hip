@@ -16,7 +16,7 @@
 //   * no participating point at all -> the sample is index 0.
 //
 // Design (one 1024-thread workgroup per cloud; no inter-workgroup sync):
-//   1. The workgroup sorts its cloud into a workspace by Morton cell of a
+//   1. The workgroup sorts its cloud into a workspace by Hilbert cell of a
 //      16^3 grid (counting sort in LDS) and cuts the sorted order into
 //      buckets of S = 64 points (S grows for N > 65536 so there are <= 1024).
 //   2. Each lane owns one bucket: its bounding box and the bucket's best
@@ -41,7 +41,7 @@ namespace {
 
 constexpr int FPS_THREADS = 1024;
 constexpr int FPS_WAVES = FPS_THREADS / 64;
-constexpr int FPS_GRID = 16;  // Morton grid per axis (4096 cells)
+constexpr int FPS_GRID = 16;  // cell grid per axis (4096 cells)
 constexpr int FPS_CELLS = FPS_GRID * FPS_GRID * FPS_GRID;
 
 // candidate/value type: float holds every binary16 and binary32 value exactly
@@ -101,6 +101,36 @@ __device__ __forceinline__ uint32_t spread3(uint32_t v) {  // 4 bits -> every th
   v = (v | (v << 4)) & 0x0c3;
   v = (v | (v << 2)) & 0x249;
   return v;
+}
+// Position of cell (x, y, z) of the 16^3 grid along a 3-D Hilbert curve
+// (Skilling's transform of the axes to the curve's transposed index, then
+// the bits interleaved, x's first).  Consecutive cells along the curve are
+// neighbours, so a run of points in this order is one compact region; a
+// Morton run can jump between distant cells at an octant border, and its box
+// then lies within reach of many more samples.
+__device__ __forceinline__ uint32_t hilbert3_16(uint32_t x, uint32_t y, uint32_t z) {
+  uint32_t X[3] = {x, y, z};
+#pragma unroll
+  for (uint32_t q = FPS_GRID / 2; q > 1; q >>= 1) {
+    const uint32_t p = q - 1;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (X[i] & q) {
+        X[0] ^= p;
+      } else {
+        const uint32_t t = (X[0] ^ X[i]) & p;
+        X[0] ^= t;
+        X[i] ^= t;
+      }
+    }
+  }
+  X[1] ^= X[0];
+  X[2] ^= X[1];
+  uint32_t t = 0;
+#pragma unroll
+  for (uint32_t q = FPS_GRID / 2; q > 1; q >>= 1)
+    if (X[2] & q) t ^= q - 1;
+  return (spread3(X[0] ^ t) << 2) | (spread3(X[1] ^ t) << 1) | spread3(X[2] ^ t);
 }
 
 // ------------------------------------------------------------ candidates
@@ -253,7 +283,7 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
   const T* __restrict__ P = pts + (size_t)b * N * 3;
   int64_t* __restrict__ out = idx_out + (size_t)b * m;
 
-  // ---- 1. bounding box of the cloud (for the Morton grid only) ----
+  // ---- 1. bounding box of the cloud (for the cell grid only) ----
   float lo[3] = {__builtin_inff(), __builtin_inff(), __builtin_inff()};
   float hi[3] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
   for (int k = tid; k < N; k += FPS_THREADS) {
@@ -295,7 +325,7 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
     gscale[c] = (ext > 0.f && ext < __builtin_inff()) ? (float)FPS_GRID / ext : 0.f;
   }
 
-  // ---- 2. counting sort by Morton cell ----
+  // ---- 2. counting sort by the cells' Hilbert order ----
   auto cell_of = [&](int k) -> uint32_t {
     uint32_t cc[3];
 #pragma unroll
@@ -305,7 +335,7 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
       i = i < 0 ? 0 : (i > FPS_GRID - 1 ? FPS_GRID - 1 : i);
       cc[c] = (uint32_t)i;
     }
-    return spread3(cc[0]) | (spread3(cc[1]) << 1) | (spread3(cc[2]) << 2);
+    return hilbert3_16(cc[0], cc[1], cc[2]);
   };
   for (int k = tid; k < N; k += FPS_THREADS) atomicAdd(&s_cnt[cell_of(k)], 1u);
   __syncthreads();
@@ -359,7 +389,7 @@ __global__ __launch_bounds__(FPS_THREADS) void fps_kernel(const T* __restrict__ 
   }
 
   // ---- 3. bucket summaries ----
-  // Lane l of wave w owns bucket sb = l * 16 + w: buckets adjacent in Morton
+  // Lane l of wave w owns bucket sb = l * 16 + w: buckets adjacent in Hilbert
   // order (hence in space) belong to different waves, so the few buckets a new
   // sample touches are spread over the workgroup instead of queueing in one wave.
   typedef typename FpsCand<T>::type C;
