@@ -64,7 +64,6 @@ constexpr int CG_GRID = 32;  // cells per axis
 constexpr int CG_CELLS = CG_GRID * CG_GRID * CG_GRID;
 constexpr int CG_CSTRIDE = CG_CELLS + 4;  // cell-start ints per cloud (16-byte rows)
 constexpr int CG_WG = 256;    // queries per search workgroup
-constexpr int CG_UNROLL = 2;  // points of a cell loaded together
 constexpr int CG_OCC = 2;     // mean own-cell occupancy the search resolution aims at
 
 __host__ __device__ inline int64_t cg_pad(int64_t n) { return (n + 63) & ~(int64_t)63; }

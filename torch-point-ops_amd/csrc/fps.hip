@@ -96,42 +96,6 @@ __host__ __device__ inline FpsLayout fps_layout(int64_t n) {
   return L;
 }
 
-__device__ __forceinline__ uint32_t spread3(uint32_t v) {  // 4 bits -> every third bit
-  v &= 0xf;
-  v = (v | (v << 4)) & 0x0c3;
-  v = (v | (v << 2)) & 0x249;
-  return v;
-}
-// Position of cell (x, y, z) of the 16^3 grid along a 3-D Hilbert curve
-// (Skilling's transform of the axes to the curve's transposed index, then
-// the bits interleaved, x's first).  Consecutive cells along the curve are
-// neighbours, so a run of points in this order is one compact region; a
-// Morton run can jump between distant cells at an octant border, and its box
-// then lies within reach of many more samples.
-__device__ __forceinline__ uint32_t hilbert3_16(uint32_t x, uint32_t y, uint32_t z) {
-  uint32_t X[3] = {x, y, z};
-#pragma unroll
-  for (uint32_t q = FPS_GRID / 2; q > 1; q >>= 1) {
-    const uint32_t p = q - 1;
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      if (X[i] & q) {
-        X[0] ^= p;
-      } else {
-        const uint32_t t = (X[0] ^ X[i]) & p;
-        X[0] ^= t;
-        X[i] ^= t;
-      }
-    }
-  }
-  X[1] ^= X[0];
-  X[2] ^= X[1];
-  uint32_t t = 0;
-#pragma unroll
-  for (uint32_t q = FPS_GRID / 2; q > 1; q >>= 1)
-    if (X[2] & q) t ^= q - 1;
-  return (spread3(X[0] ^ t) << 2) | (spread3(X[1] ^ t) << 1) | spread3(X[2] ^ t);
-}
 
 // ------------------------------------------------------------ candidates
 // A candidate is (running-min value, rank); the better one has the larger
@@ -197,14 +161,7 @@ __device__ __forceinline__ int lane_of(C mine, C c) {
   return hit ? __builtin_ctzll(hit) : 0;
 }
 
-// Best candidate of the whole wave: the largest value word, then the largest
-// rank word among the lanes holding that value.
-__device__ __forceinline__ CandF wave_best(CandF c) {
-  const uint32_t hi = (uint32_t)(c.k >> 32);
-  const uint32_t mh = wave_umax(hi);
-  const uint32_t ml = wave_umax(hi == mh ? (uint32_t)c.k : 0u);
-  return {((uint64_t)mh << 32) | ml};
-}
+// Best candidate of the whole wave (double values: (value, rank) pairs).
 __device__ __forceinline__ CandD wave_best(CandD c) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {

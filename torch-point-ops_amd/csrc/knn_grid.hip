@@ -63,39 +63,6 @@ __device__ __forceinline__ int kg_axis(float x, float lo, float gs) {
   return (int)f;
 }
 
-// Index of cell (x, y, z) of the 16^3 grid along a 3-D Hilbert curve, by
-// Skilling's transpose method ("Programming the Hilbert curve", AIP Conf.
-// Proc. 707, 2004): undo the excess work from the top bit down, Gray-encode,
-// then interleave the bits (x first) from the top.
-__device__ __forceinline__ int kg_hilbert(int x, int y, int z) {
-  uint32_t X[3] = {(uint32_t)x, (uint32_t)y, (uint32_t)z};
-#pragma unroll
-  for (uint32_t Q = 8; Q > 1; Q >>= 1) {
-    const uint32_t P = Q - 1;
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      if (X[i] & Q) {
-        X[0] ^= P;
-      } else {
-        const uint32_t t = (X[0] ^ X[i]) & P;
-        X[0] ^= t;
-        X[i] ^= t;
-      }
-    }
-  }
-  X[1] ^= X[0];
-  X[2] ^= X[1];
-  uint32_t t = 0;
-#pragma unroll
-  for (uint32_t Q = 8; Q > 1; Q >>= 1)
-    if (X[2] & Q) t ^= Q - 1;
-  uint32_t h = 0;
-#pragma unroll
-  for (int b = 3; b >= 0; --b)
-#pragma unroll
-    for (int i = 0; i < 3; ++i) h = (h << 1) | (((X[i] ^ t) >> b) & 1u);
-  return (int)h;
-}
 
 // knn.cu:148-158 for D = 3
 template <int NORM>
@@ -198,7 +165,7 @@ __device__ void kg_bin(const float* __restrict__ P, int L, float* __restrict__ h
     const int ci[3] = {kg_axis(x, glo[0], gs[0]), kg_axis(y, glo[1], gs[1]),
                        kg_axis(z, glo[2], gs[2])};
     if constexpr (HILBERT) {
-      return kg_hilbert(ci[0], ci[1], ci[2]);
+      return (int)hilbert3_16(ci[0], ci[1], ci[2]);
     } else {
       return (ci[0] * KG_G + ci[1]) * KG_G + ci[2];
     }

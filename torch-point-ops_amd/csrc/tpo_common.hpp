@@ -112,6 +112,42 @@ __device__ __forceinline__ void atomic_add(half_t* p, half_t v) {
   (void)__builtin_amdgcn_global_atomic_fadd_v2f16((__attribute__((address_space(1))) h2*)w, val);
 }
 
+// Index of cell (x, y, z) of a 16^3 grid along a 3-D Hilbert curve, by
+// Skilling's transpose method ("Programming the Hilbert curve", AIP Conf.
+// Proc. 707, 2004): undo the excess work from the top bit down, Gray-encode,
+// then interleave the bits (x first) from the top.  Consecutive indices are
+// neighbouring cells, so a run of points in this order is one compact region
+// (a Morton run can jump between distant cells at an octant border).
+__device__ __forceinline__ uint32_t hilbert3_16(uint32_t x, uint32_t y, uint32_t z) {
+  uint32_t X[3] = {x, y, z};
+#pragma unroll
+  for (uint32_t Q = 8; Q > 1; Q >>= 1) {
+    const uint32_t P = Q - 1;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (X[i] & Q) {
+        X[0] ^= P;
+      } else {
+        const uint32_t t = (X[0] ^ X[i]) & P;
+        X[0] ^= t;
+        X[i] ^= t;
+      }
+    }
+  }
+  X[1] ^= X[0];
+  X[2] ^= X[1];
+  uint32_t t = 0;
+#pragma unroll
+  for (uint32_t Q = 8; Q > 1; Q >>= 1)
+    if (X[2] & Q) t ^= Q - 1;
+  uint32_t h = 0;
+#pragma unroll
+  for (int b = 3; b >= 0; --b)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) h = (h << 1) | (((X[i] ^ t) >> b) & 1u);
+  return h;
+}
+
 }  // namespace tpo
 
 // ------------------------------------------------------------ host helpers
