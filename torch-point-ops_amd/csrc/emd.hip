@@ -723,28 +723,35 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
       nr = EmdPt<V>{(V)0, (V)0, (V)0, (V)0};
     }
   };
-  // UB points of the chunk, the u-th at slot ix(u), in increasing slots
-  auto batch = [&](auto ix, auto ucnt) {
+  // UB points of the chunk, the u-th at slot ix(u), in increasing slots.
+  // ZT: with the zero tests (the exponentials of a batch whose terms all
+  // vanish are skipped; float16's never vanish); returns whether a test
+  // skipped anything.
+  auto batch = [&](auto ix, auto ucnt, auto ztc) -> bool {
     constexpr int UB = decltype(ucnt)::value;
+    constexpr bool ZT = decltype(ztc)::value && !std::is_same<T, half_t>::value;
     EmdPt<V> pt[UB];
     V pb[UB];
     V d[UB];
-    bool nza = false, nzb = false;
+    bool nza = !ZT, nzb = !ZT;
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
       pt[u] = s_pt[w][ix(u)];
       if constexpr (NS == 2) pb[u] = s_wb[w][ix(u)];
       d[u] = sq3(pt[u].x - x, pt[u].y - y, pt[u].z - z);
-      nza |= !(d[u] > ta);  // NaN counts as non-zero
-      if constexpr (NS == 2) nzb |= !(d[u] > tb);
+      if constexpr (ZT) {
+        nza |= !(d[u] > ta);  // NaN counts as non-zero
+        if constexpr (NS == 2) nzb |= !(d[u] > tb);
+      }
     }
+    bool skipped = false;
     if constexpr (NS == 2 && std::is_same<T, float>::value) {
       if (pow4) {
         // la = 4 lb < 0, so la d <= lb d: a batch whose lb terms all vanish
         // has vanishing la terms too, and both exponentials share one
         // reduction (the same values as two emd_e calls)
-        if (__builtin_amdgcn_ballot_w64(nzb) != 0) {
-          if (__builtin_amdgcn_ballot_w64(nza) != 0) {
+        if (!ZT || __builtin_amdgcn_ballot_w64(nzb) != 0) {
+          if (!ZT || __builtin_amdgcn_ballot_w64(nza) != 0) {
 #pragma unroll
             for (int u = 0; u < UB; ++u) {
               V e1, e4;
@@ -755,22 +762,34 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
           } else {
 #pragma unroll
             for (int u = 0; u < UB; ++u) sb = emd_fma(emd_e<T>(lb, d[u]), pb[u], sb);
+            skipped = true;
           }
+        } else {
+          skipped = true;
         }
-        return;
+        return skipped;
       }
     }
-    if (std::is_same<T, half_t>::value || __builtin_amdgcn_ballot_w64(nza) != 0) {
+    if (!ZT || __builtin_amdgcn_ballot_w64(nza) != 0) {
 #pragma unroll
       for (int u = 0; u < UB; ++u) sa = emd_fma(emd_e<T>(la, d[u]), pt[u].w, sa);
+    } else {
+      skipped = true;
     }
     if constexpr (NS == 2) {
-      if (std::is_same<T, half_t>::value || __builtin_amdgcn_ballot_w64(nzb) != 0) {
+      if (!ZT || __builtin_amdgcn_ballot_w64(nzb) != 0) {
 #pragma unroll
         for (int u = 0; u < UB; ++u) sb = emd_fma(emd_e<T>(lb, d[u]), pb[u], sb);
+      } else {
+        skipped = true;
       }
     }
+    return skipped;
   };
+  // Unpruned sweeps keep the zero tests while they pay: after a chunk in
+  // which no batch vanished, the rest of the wave's share is summed without
+  // them (the same terms; a vanishing term is +0 either way).
+  bool zt = true;
   if (q0 < q1) fetch(q0);
   for (int c0 = q0; c0 < q1; c0 += C) {
     // the previous chunk's reads were issued before this write (LDS runs a
@@ -784,9 +803,22 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
     if constexpr (!PR) {
       if (c0 + C < q1) fetch(c0 + C);
       int u0 = 0;
-      for (; u0 + U <= cn; u0 += U)
-        batch([u0](int u) { return u0 + u; }, std::integral_constant<int, U>{});
-      for (; u0 < cn; ++u0) batch([u0](int) { return u0; }, std::integral_constant<int, 1>{});
+      if (zt) {
+        bool skipped = false;
+        for (; u0 + U <= cn; u0 += U)
+          skipped |= batch([u0](int u) { return u0 + u; }, std::integral_constant<int, U>{},
+                           std::true_type{});
+        for (; u0 < cn; ++u0)
+          skipped |= batch([u0](int) { return u0; }, std::integral_constant<int, 1>{},
+                           std::true_type{});
+        zt = skipped;
+      } else {
+        for (; u0 + U <= cn; u0 += U)
+          batch([u0](int u) { return u0 + u; }, std::integral_constant<int, U>{},
+                std::false_type{});
+        for (; u0 < cn; ++u0)
+          batch([u0](int) { return u0; }, std::integral_constant<int, 1>{}, std::false_type{});
+      }
       __builtin_amdgcn_wave_barrier();
       continue;
     }
@@ -811,8 +843,9 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
     if (nn + U > cn) {  // (nearly) every point: consecutive slots
       int u0 = 0;
       for (; u0 + U <= cn; u0 += U)
-        batch([u0](int u) { return u0 + u; }, std::integral_constant<int, U>{});
-      for (; u0 < cn; ++u0) batch([u0](int) { return u0; }, std::integral_constant<int, 1>{});
+        batch([u0](int u) { return u0 + u; }, std::integral_constant<int, U>{}, std::true_type{});
+      for (; u0 < cn; ++u0)
+        batch([u0](int) { return u0; }, std::integral_constant<int, 1>{}, std::true_type{});
     } else {  // the near points only, in increasing slots
       auto take = [&](auto ucnt) {
         constexpr int UB = decltype(ucnt)::value;
@@ -822,7 +855,7 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
           sl[u] = __builtin_ctzll(near);
           near &= near - 1;
         }
-        batch([&sl](int u) { return sl[u]; }, ucnt);
+        batch([&sl](int u) { return sl[u]; }, ucnt, std::true_type{});
       };
       int r = nn;
       for (; r >= U; r -= U) take(std::integral_constant<int, U>{});
