@@ -25,7 +25,10 @@
 //   * exponentials that are +0 in all 64 lanes (arguments below the float
 //     or double underflow, the steep levels on distant points) are skipped
 //     with a wave-uniform branch, which changes no sum; each cloud's points
-//     are listed in Morton order so a wave's 64 points are neighbours;
+//     are listed as k-d tree leaves (Morton cells above 4096 points) so a
+//     wave's 64 points are neighbours, and at the steep levels the points of
+//     the other cloud beyond reach of the wave's box are left out altogether;
+//     flat levels drop the zero tests once they stop paying;
 //   * the float paths' exp is a two-term Cody-Waite reduction on the
 //     hardware exp2 (at most 1.24 ulp from exp over [-87, 0], measured);
 //     their last level's exp(0 * d) is 0 * d + 1 exactly;
@@ -212,7 +215,7 @@ __device__ __forceinline__ double wave_minmax(double v) {
 //   cost[B][gy][gx]            matchcost partials of the final pass
 //   g1[B][nchunk][n][3]        grad_xyz1 partials of the backward (per row tile)
 //   g2[B][gx][m][3]            grad_xyz2 partials of the backward (per column tile)
-//   ord1[B][n], ord2[B][m]     int32: each cloud's points in Morton order
+//   ord1[B][n], ord2[B][m]     int32: each cloud's points in sweep order
 struct EmdLayout {
   int64_t p1, p2, reml, remr, rl, rr, cost, g1, g2, ord1, ord2, total;
   int gx, gy, nchunk;
@@ -681,7 +684,7 @@ __device__ __forceinline__ void emd_sweep(const typename EmdV<T>::type* __restri
   // keeps its library exp.
   const bool pow4 = std::is_same<T, float>::value && NS == 2 && lb != (V)0 && la == (V)4 * lb;
   // Far points.  The wave's own points are neighbours in space (the sweep
-  // takes them in Morton order), so many points of the other cloud lie
+  // takes them as k-d tree leaves), so many points of the other cloud lie
   // farther from the box of the wave's real own points than the zero
   // distance of every level summed here (with a relative margin of 2^-10, far
   // above the rounding of the box distance and of d): each of their terms is
