@@ -131,10 +131,17 @@ constexpr int GATHER_ROWS_LDS = 65536;  // LDS bytes for the staged rows
 constexpr int GATHER_ROWS_PARTS = 2;
 constexpr int GATHER_ROWS_THREADS = 1024;
 constexpr int GATHER_ROWS_UN = 4;  // positions per thread and step (independent loads)
-template <typename T, int CB>
+// LMAP: the part's position map is built in LDS after the rows (16-bit
+// sample numbers, 0xffff for none; M < 65536, at most GATHER_MAP_SPAN
+// positions a part), so the backward needs no fill and no inverse launch.
+// The map takes the sample of any one plain store among those sharing a
+// position; the others are added with atomics, as with the global map.
+constexpr int64_t GATHER_MAP_SPAN = 32768;
+template <typename T, int CB, bool LMAP>
 __global__ __launch_bounds__(GATHER_ROWS_THREADS) void gather_bwd_rows_kernel(
     const T* __restrict__ go, const int64_t* __restrict__ idx, const int32_t* __restrict__ pos,
-    int64_t B, int64_t C, int64_t N, int64_t M, int parts, T* __restrict__ gp) {
+    int64_t B, int64_t C, int64_t N, int64_t M, int parts, int64_t map_off,
+    T* __restrict__ gp) {
   extern __shared__ __align__(16) unsigned char g_rows[];
   T* __restrict__ rows = reinterpret_cast<T*>(g_rows);
   constexpr int NT = GATHER_ROWS_THREADS, UN = GATHER_ROWS_UN;
@@ -153,22 +160,36 @@ __global__ __launch_bounds__(GATHER_ROWS_THREADS) void gather_bwd_rows_kernel(
   for (int64_t i = threadIdx.x; i < vec; i += NT)
     reinterpret_cast<uint4*>(rows)[i] = reinterpret_cast<const uint4*>(src)[i];
   for (int64_t i = vec * 16 / (int64_t)sizeof(T) + threadIdx.x; i < cnt; i += NT) rows[i] = src[i];
-  __syncthreads();
   const int64_t n0 = N * part / parts, n1 = N * (part + 1) / parts;
   const int32_t* __restrict__ pb = pos + b * N;
+  const int64_t* __restrict__ ib = idx + b * M;
+  uint16_t* __restrict__ lmap = reinterpret_cast<uint16_t*>(g_rows + map_off);
+  if constexpr (LMAP) {
+    const int64_t words = (n1 - n0 + 7) / 8;  // the region is padded to 16 bytes
+    for (int64_t i = threadIdx.x; i < words; i += NT)
+      reinterpret_cast<uint4*>(lmap)[i] = make_uint4(~0u, ~0u, ~0u, ~0u);
+    __syncthreads();
+    for (int64_t j = threadIdx.x; j < M; j += NT) {
+      const int64_t a = ib[j];
+      if (a >= n0 && a < n1) lmap[a - n0] = (uint16_t)j;
+    }
+  }
+  __syncthreads();
+  constexpr int32_t NONE = LMAP ? 0xffff : 0x7fffffff;
   T* __restrict__ dst = gp + (b * C + c0) * N;
   for (int64_t nb = n0 + threadIdx.x; nb < n1; nb += (int64_t)NT * UN) {
     int32_t p[UN];
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
       const int64_t n = nb + (int64_t)NT * u;
-      p[u] = n < n1 ? pb[n] : 0x7fffffff;
+      if constexpr (LMAP) p[u] = n < n1 ? (int32_t)lmap[n - n0] : NONE;
+      else p[u] = n < n1 ? pb[n] : NONE;
     }
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
       const int64_t n = nb + (int64_t)NT * u;
       if (n >= n1) break;
-      const bool hit = p[u] != 0x7fffffff;
+      const bool hit = p[u] != NONE;
       const T* __restrict__ r = rows + (hit ? p[u] : 0);
       // 0 + g, as the reference's atomicAdd into zeros gives (+0 for g = -0)
 #pragma unroll
@@ -180,10 +201,10 @@ __global__ __launch_bounds__(GATHER_ROWS_THREADS) void gather_bwd_rows_kernel(
   // positions: added with atomics (the reference's accumulation) once the
   // workgroup's own writes of those positions are done.
   __syncthreads();
-  const int64_t* __restrict__ ib = idx + b * M;
   for (int64_t j = threadIdx.x; j < M; j += NT) {
     const int64_t a = ib[j];
-    if (a < n0 || a >= n1 || pb[a] == (int32_t)j) continue;
+    if (a < n0 || a >= n1) continue;
+    if (LMAP ? lmap[a - n0] == (uint16_t)j : pb[a] == (int32_t)j) continue;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
       if (c < cn) atomic_add(dst + c * N + a, rows[c * M + j]);
@@ -254,27 +275,44 @@ static void fwd(const void* pts, const int64_t* idx, int64_t B, int64_t C, int64
 template <typename T>
 static void bwd(const void* go, const int64_t* idx, int64_t B, int64_t C, int64_t N, int64_t M,
                 void* gp, int32_t* pos, hipStream_t s) {
-  hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for((B * N + 3) / 4)), dim3(256), 0, s, pos, B * N,
-                     (int32_t)0x7fffffff);
-  if (M > 0)
-    hipLaunchKernelGGL(gather_inverse_kernel, dim3(grid_for(B * M)), dim3(256), 0, s, idx, B, N,
-                       M, pos);
   // rows of cb channels staged in LDS where one row fits, else the dense pass
   const int64_t rowb = std::max<int64_t>(1, M * (int64_t)sizeof(T));
   int cb = 1;
   while (cb < 16 && cb < C && 2 * cb * rowb <= GATHER_ROWS_LDS) cb *= 2;
   const int64_t groups = B * ((C + cb - 1) / cb);
-  if (M > 0 && rowb <= GATHER_ROWS_LDS && groups * GATHER_ROWS_PARTS < (1 << 24)) {
+  const bool rows = M > 0 && rowb <= GATHER_ROWS_LDS && groups * GATHER_ROWS_PARTS < (1 << 24);
+  // the part's position map in LDS beside the rows where it fits
+  const int64_t span = (N + GATHER_ROWS_PARTS - 1) / GATHER_ROWS_PARTS;
+  const bool lmap = rows && M < 0xffff && span <= GATHER_MAP_SPAN;
+  if (!lmap) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for((B * N + 3) / 4)), dim3(256), 0, s, pos,
+                       B * N, (int32_t)0x7fffffff);
+    if (M > 0)
+      hipLaunchKernelGGL(gather_inverse_kernel, dim3(grid_for(B * M)), dim3(256), 0, s, idx, B, N,
+                         M, pos);
+  }
+  if (rows) {
     const dim3 g((unsigned)((groups * GATHER_ROWS_PARTS + 7) & ~(int64_t)7));
     const dim3 blk(GATHER_ROWS_THREADS);
-    const unsigned lds = (unsigned)(cb * rowb);
+    const int64_t map_off = (cb * rowb + 15) / 16 * 16;
+    const unsigned lds = (unsigned)(lmap ? map_off + (span + 7) / 8 * 16 : cb * rowb);
+#define GATHER_ROWS(CBV)                                                                        \
+  do {                                                                                          \
+    if (lmap)                                                                                   \
+      hipLaunchKernelGGL((gather_bwd_rows_kernel<T, CBV, true>), g, blk, lds, s, (const T*)go,  \
+                         idx, pos, B, C, N, M, GATHER_ROWS_PARTS, map_off, (T*)gp);             \
+    else                                                                                        \
+      hipLaunchKernelGGL((gather_bwd_rows_kernel<T, CBV, false>), g, blk, lds, s, (const T*)go, \
+                         idx, pos, B, C, N, M, GATHER_ROWS_PARTS, map_off, (T*)gp);             \
+  } while (0)
     switch (cb) {
-      case 1: hipLaunchKernelGGL((gather_bwd_rows_kernel<T, 1>), g, blk, lds, s, (const T*)go, idx, pos, B, C, N, M, GATHER_ROWS_PARTS, (T*)gp); break;
-      case 2: hipLaunchKernelGGL((gather_bwd_rows_kernel<T, 2>), g, blk, lds, s, (const T*)go, idx, pos, B, C, N, M, GATHER_ROWS_PARTS, (T*)gp); break;
-      case 4: hipLaunchKernelGGL((gather_bwd_rows_kernel<T, 4>), g, blk, lds, s, (const T*)go, idx, pos, B, C, N, M, GATHER_ROWS_PARTS, (T*)gp); break;
-      case 8: hipLaunchKernelGGL((gather_bwd_rows_kernel<T, 8>), g, blk, lds, s, (const T*)go, idx, pos, B, C, N, M, GATHER_ROWS_PARTS, (T*)gp); break;
-      default: hipLaunchKernelGGL((gather_bwd_rows_kernel<T, 16>), g, blk, lds, s, (const T*)go, idx, pos, B, C, N, M, GATHER_ROWS_PARTS, (T*)gp); break;
+      case 1: GATHER_ROWS(1); break;
+      case 2: GATHER_ROWS(2); break;
+      case 4: GATHER_ROWS(4); break;
+      case 8: GATHER_ROWS(8); break;
+      default: GATHER_ROWS(16); break;
     }
+#undef GATHER_ROWS
   } else {
     hipLaunchKernelGGL(gather_bwd_dense_kernel<T>, dim3(grid_for(B * N)), dim3(256), 0, s,
                        (const T*)go, pos, B, C, N, M, (T*)gp);
