@@ -98,12 +98,15 @@ def test_gather_vs_oracle(tpo, O, dev, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
 @pytest.mark.parametrize("C,N,M", [(1, 3000, 900), (3, 5000, 2000), (5, 9001, 4100),
-                                   (64, 4000, 300), (2, 40000, 20000)])
+                                   (64, 4000, 300), (2, 20001, 4096), (2, 40000, 20000)])
 def test_gather_backward_paths(tpo, O, dev, dtype, C, N, M):
     """The backward's channel blocks of 1 to 16 rows staged in LDS (the parts
-    of one block split the positions), and rows too long for LDS (M = 20000:
-    the dense pass), with repeated indices (added by atomics) and without
-    (bit for bit, -0 gradients landing as +0)."""
+    of one block split the positions), with the position map built in LDS a
+    chunk of 8192 positions at a time (M <= 4096; N = 20001: parts of 10000
+    and 10001 positions, a full chunk and a ragged one) or in global memory
+    (M = 4100), and rows too long for LDS (M = 20000: the dense pass), with
+    repeated indices (added by atomics) and without (bit for bit, -0
+    gradients landing as +0)."""
     g = torch.Generator().manual_seed(C * 7 + M)
     B = 2
     go = torch.randn(B, C, M, generator=g).to(dtype)

@@ -131,12 +131,15 @@ constexpr int GATHER_ROWS_LDS = 65536;  // LDS bytes for the staged rows
 constexpr int GATHER_ROWS_PARTS = 2;
 constexpr int GATHER_ROWS_THREADS = 1024;
 constexpr int GATHER_ROWS_UN = 4;  // positions per thread and step (independent loads)
-// LMAP: the part's position map is built in LDS after the rows (16-bit
-// sample numbers, 0xffff for none; M < 65536, at most GATHER_MAP_SPAN
-// positions a part), so the backward needs no fill and no inverse launch.
-// The map takes the sample of any one plain store among those sharing a
-// position; the others are added with atomics, as with the global map.
-constexpr int64_t GATHER_MAP_SPAN = 32768;
+// LMAP: the part's positions are taken GATHER_MAP_CHUNK at a time, each
+// chunk with a position map in LDS (16-bit sample numbers, 0xffff for none)
+// built from the thread's GATHER_MAP_JR samples held in registers (M <=
+// GATHER_MAP_JR * 1024), so the backward needs no fill and no inverse launch,
+// and 64 KB of rows + 16 KB of map let two workgroups share a CU.  The map
+// takes the sample of any one plain store among those sharing a position; the
+// others are added with atomics, as with the global map.
+constexpr int64_t GATHER_MAP_CHUNK = 8192;
+constexpr int GATHER_MAP_JR = 4;
 template <typename T, int CB, bool LMAP>
 __global__ __launch_bounds__(GATHER_ROWS_THREADS) void gather_bwd_rows_kernel(
     const T* __restrict__ go, const int64_t* __restrict__ idx, const int32_t* __restrict__ pos,
@@ -163,33 +166,77 @@ __global__ __launch_bounds__(GATHER_ROWS_THREADS) void gather_bwd_rows_kernel(
   const int64_t n0 = N * part / parts, n1 = N * (part + 1) / parts;
   const int32_t* __restrict__ pb = pos + b * N;
   const int64_t* __restrict__ ib = idx + b * M;
-  uint16_t* __restrict__ lmap = reinterpret_cast<uint16_t*>(g_rows + map_off);
+  T* __restrict__ dst = gp + (b * C + c0) * N;
   if constexpr (LMAP) {
-    const int64_t words = (n1 - n0 + 7) / 8;  // the region is padded to 16 bytes
-    for (int64_t i = threadIdx.x; i < words; i += NT)
-      reinterpret_cast<uint4*>(lmap)[i] = make_uint4(~0u, ~0u, ~0u, ~0u);
-    __syncthreads();
-    for (int64_t j = threadIdx.x; j < M; j += NT) {
-      const int64_t a = ib[j];
-      if (a >= n0 && a < n1) lmap[a - n0] = (uint16_t)j;
+    uint16_t* __restrict__ lmap = reinterpret_cast<uint16_t*>(g_rows + map_off);
+    constexpr int JR = GATHER_MAP_JR;
+    int64_t aj[JR];
+    bool rep[JR];  // the sample repeats a position another sample's store takes
+#pragma unroll
+    for (int r = 0; r < JR; ++r) {
+      const int64_t j = threadIdx.x + (int64_t)NT * r;
+      aj[r] = j < M ? ib[j] : -1;
+      rep[r] = false;
     }
+    for (int64_t cs = n0; cs < n1; cs += GATHER_MAP_CHUNK) {
+      const int64_t ce = min(cs + GATHER_MAP_CHUNK, n1);
+      for (int i = threadIdx.x; i < GATHER_MAP_CHUNK / 8; i += NT)
+        reinterpret_cast<uint4*>(lmap)[i] = make_uint4(~0u, ~0u, ~0u, ~0u);
+      __syncthreads();  // (first chunk: the rows are staged too)
+#pragma unroll
+      for (int r = 0; r < JR; ++r)
+        if (aj[r] >= cs && aj[r] < ce) lmap[aj[r] - cs] = (uint16_t)(threadIdx.x + NT * r);
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < JR; ++r)
+        if (aj[r] >= cs && aj[r] < ce)
+          rep[r] = lmap[aj[r] - cs] != (uint16_t)(threadIdx.x + NT * r);
+      for (int64_t nb = cs + threadIdx.x; nb < ce; nb += (int64_t)NT * UN) {
+        int32_t p[UN];
+#pragma unroll
+        for (int u = 0; u < UN; ++u) {
+          const int64_t n = nb + (int64_t)NT * u;
+          p[u] = n < ce ? (int32_t)lmap[n - cs] : 0xffff;
+        }
+#pragma unroll
+        for (int u = 0; u < UN; ++u) {
+          const int64_t n = nb + (int64_t)NT * u;
+          if (n >= ce) break;
+          const bool hit = p[u] != 0xffff;
+          const T* __restrict__ r = rows + (hit ? p[u] : 0);
+          // 0 + g, as the reference's atomicAdd into zeros gives (+0 for g = -0)
+#pragma unroll
+          for (int c = 0; c < CB; ++c)
+            if (c < cn) dst[c * N + n] = hit ? (T)((T)0 + r[c * M]) : (T)0;
+        }
+      }
+      __syncthreads();  // the next chunk's fill waits for this chunk's map reads
+    }
+    // repeated samples, added once every plain store of the part is done (the
+    // last barrier above)
+#pragma unroll
+    for (int r = 0; r < JR; ++r) {
+      if (!rep[r]) continue;
+      const int64_t a = aj[r], j = threadIdx.x + (int64_t)NT * r;
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+        if (c < cn) atomic_add(dst + c * N + a, rows[c * M + j]);
+    }
+    return;
   }
   __syncthreads();
-  constexpr int32_t NONE = LMAP ? 0xffff : 0x7fffffff;
-  T* __restrict__ dst = gp + (b * C + c0) * N;
   for (int64_t nb = n0 + threadIdx.x; nb < n1; nb += (int64_t)NT * UN) {
     int32_t p[UN];
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
       const int64_t n = nb + (int64_t)NT * u;
-      if constexpr (LMAP) p[u] = n < n1 ? (int32_t)lmap[n - n0] : NONE;
-      else p[u] = n < n1 ? pb[n] : NONE;
+      p[u] = n < n1 ? pb[n] : 0x7fffffff;
     }
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
       const int64_t n = nb + (int64_t)NT * u;
       if (n >= n1) break;
-      const bool hit = p[u] != NONE;
+      const bool hit = p[u] != 0x7fffffff;
       const T* __restrict__ r = rows + (hit ? p[u] : 0);
       // 0 + g, as the reference's atomicAdd into zeros gives (+0 for g = -0)
 #pragma unroll
@@ -203,8 +250,7 @@ __global__ __launch_bounds__(GATHER_ROWS_THREADS) void gather_bwd_rows_kernel(
   __syncthreads();
   for (int64_t j = threadIdx.x; j < M; j += NT) {
     const int64_t a = ib[j];
-    if (a < n0 || a >= n1) continue;
-    if (LMAP ? lmap[a - n0] == (uint16_t)j : pb[a] == (int32_t)j) continue;
+    if (a < n0 || a >= n1 || pb[a] == (int32_t)j) continue;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
       if (c < cn) atomic_add(dst + c * N + a, rows[c * M + j]);
@@ -281,9 +327,8 @@ static void bwd(const void* go, const int64_t* idx, int64_t B, int64_t C, int64_
   while (cb < 16 && cb < C && 2 * cb * rowb <= GATHER_ROWS_LDS) cb *= 2;
   const int64_t groups = B * ((C + cb - 1) / cb);
   const bool rows = M > 0 && rowb <= GATHER_ROWS_LDS && groups * GATHER_ROWS_PARTS < (1 << 24);
-  // the part's position map in LDS beside the rows where it fits
-  const int64_t span = (N + GATHER_ROWS_PARTS - 1) / GATHER_ROWS_PARTS;
-  const bool lmap = rows && M < 0xffff && span <= GATHER_MAP_SPAN;
+  // the position map in LDS beside the rows, a chunk at a time
+  const bool lmap = rows && M <= (int64_t)GATHER_MAP_JR * GATHER_ROWS_THREADS;
   if (!lmap) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for((B * N + 3) / 4)), dim3(256), 0, s, pos,
                        B * N, (int32_t)0x7fffffff);
@@ -295,7 +340,7 @@ static void bwd(const void* go, const int64_t* idx, int64_t B, int64_t C, int64_
     const dim3 g((unsigned)((groups * GATHER_ROWS_PARTS + 7) & ~(int64_t)7));
     const dim3 blk(GATHER_ROWS_THREADS);
     const int64_t map_off = (cb * rowb + 15) / 16 * 16;
-    const unsigned lds = (unsigned)(lmap ? map_off + (span + 7) / 8 * 16 : cb * rowb);
+    const unsigned lds = (unsigned)(lmap ? map_off + GATHER_MAP_CHUNK * 2 : cb * rowb);
 #define GATHER_ROWS(CBV)                                                                        \
   do {                                                                                          \
     if (lmap)                                                                                   \
