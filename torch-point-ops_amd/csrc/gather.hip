@@ -126,8 +126,10 @@ __global__ __launch_bounds__(256) void gather_bwd_dense_kernel(const T* __restri
 // different rows of memory (a line per value).
 constexpr int GATHER_ROWS_LDS = 65536;  // LDS bytes for the staged rows
 // Workgroups sharing one channel block of a cloud (each stages the rows and
-// takes a part of the positions): 2 measured best at config 4 (59 us for the
-// whole backward, 65 with 4, 85 with 8; 128 KB rows: 69 us with one part).
+// takes a part of the positions): 2 measured best at config 4.  With the
+// position map in global memory: 59 us for the whole backward, 65 with 4, 85
+// with 8; 128 KB rows: 69 us with one part.  With the chunked map in LDS:
+// 45 us, 57 with 4 parts, 55 with 2-channel blocks (3 workgroups a CU).
 constexpr int GATHER_ROWS_PARTS = 2;
 constexpr int GATHER_ROWS_THREADS = 1024;
 constexpr int GATHER_ROWS_UN = 4;  // positions per thread and step (independent loads)
